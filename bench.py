@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the JLUST sparse hot path on one MI355X.
+
+    python bench.py [--config 2] [--steps K] [--warmup W] [--gpus 1]
+
+A step is one call of the operator over the configuration's synthetic input,
+already resident in HBM (one C ABI call; for SpMV that is the merge-path
+kernel plus its carry fix-up, for SpMM the B re-layout plus the product).
+Prints ONE JSON line: the metric of BASELINE.json (effective GB/s from the
+reference's compulsory-byte formula, benchmark/bench_suitesparse.jl:170-172,
+plus GFLOP/s), a `roofline` object for the step's dominant kernel and a
+`cpu_baseline` measured on this host with the oracle (a C restatement of
+JLUST's CPU path; Julia/JLUST itself is not available on the GPU box).
+
+Default workload: config 2 (CSR SpMV fp64, power-law 4M x 4M, ~64M nnz).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "SpMV/SpMM/SDDMM effective GB/s (% of MI355X HBM peak) + GFLOP/s"
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F32_PEAK_TFLOPS = 157.3   # MI355X dense fp32 matrix
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=None)
+    p.add_argument("--warmup", type=int, default=None)
+    p.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    p.add_argument("--cpu-seconds", type=float, default=10.0,
+                   help="CPU work budget of the cpu_baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--plan", action="store_true",
+                   help="SpMV through a prepared plan (partition computed once, outside the loop)")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="only run a 1 GiB device copy (PMC byte-counter calibration)")
+    p.add_argument("--gather-ceiling", action="store_true",
+                   help="only measure random-gather bandwidth (8 B and 512 B rows) per source size")
+    return p.parse_args()
+
+
+def gather_ceiling():
+    """Random-gather throughput on this GPU: out[i] = src[idx[i]] with uniform
+    random idx, for the operand sizes the configs gather from (x: 8-byte
+    elements; B rows: 512-byte rows).  Reported as useful gathered bytes/s and
+    as gathers/s; torch.index_select is the gather kernel."""
+    import torch
+    res = []
+    g = torch.Generator(device="cuda").manual_seed(0)
+    for elem_bytes, sizes_mb in ((8, (4, 32, 256, 512)), (512, (32, 256, 512, 1024))):
+        for mb in sizes_mb:
+            if elem_bytes == 8:
+                src = torch.randn(mb * 2**20 // 8, dtype=torch.float64, device="cuda")
+                count = 64 * 2**20
+            else:
+                src = torch.randn(mb * 2**20 // 512, 128, dtype=torch.float32, device="cuda")
+                count = 8 * 2**20
+            idx = torch.randint(0, src.shape[0], (count,), generator=g, device="cuda")
+            out = torch.index_select(src, 0, idx)
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 5
+            s.record()
+            for _ in range(reps):
+                torch.index_select(src, 0, idx, out=out)
+            e.record()
+            torch.cuda.synchronize()
+            t = s.elapsed_time(e) / reps * 1e-3
+            res.append({"elem_bytes": elem_bytes, "source_MB": mb, "gathers": count,
+                        "ms": round(t * 1e3, 4), "gathered_GBps": round(count * elem_bytes / t / 1e9, 1),
+                        "Ggathers_per_s": round(count / t / 1e9, 2)})
+            del src, idx, out
+    return res
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def dev(a):
+    import torch
+    if a.ndim == 2:
+        return torch.from_numpy(np.ascontiguousarray(a.T)).cuda().t()
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def build_step(cfg, use_plan=False):
+    """Returns (step_fn, dominant_kernel_name, bound, algorithmic units)."""
+    import torch
+    import jlust_amd as J
+    kind = cfg["kind"]
+    m, n = cfg["m"], cfg["n"]
+    if kind == "csr_spmv":
+        A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (m, n))
+        x = dev(cfg["x"])
+        y = torch.empty(m, dtype=A.dtype, device="cuda")
+        if use_plan:
+            h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+            return (lambda: J.execute(h, x, y)), "csr_spmv_merge_kernel", "hbm", (A, x, y, h)
+        return (lambda: J.execute(J.SpMVOp, A, x, y)), "csr_spmv_merge_kernel", "hbm", (A, x, y)
+    if kind == "csr_spmm":
+        A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (m, n))
+        B = dev(cfg["B"])
+        C = J.dense_matrix(m, cfg["k"], dtype=A.dtype)
+        return (lambda: J.execute(J.SpMMOp, A, B, C)), "csr_spmm_kernel", "hbm", (A, B, C)
+    if kind == "csr_sddmm":
+        S = dev(cfg["mask"])
+        out = torch.empty_like(S)
+        Cs = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), out, (m, n))
+        A, B = dev(cfg["A"]), dev(cfg["B"])
+        return (lambda: J.execute(J.SDDMMOp, A, B, Cs, mask=S)), "csr_sddmm_kernel", "hbm", \
+            (S, out, Cs, A, B)
+    if kind == "bsr_spmm":
+        A = J.bsr_tensor(dev(cfg["browptr"]), dev(cfg["bcolind"]), dev(cfg["val"]), (m, n))
+        B = dev(cfg["B"])
+        C = J.dense_matrix(m, cfg["k"], dtype=torch.float32)
+        return (lambda: J.execute(J.SpMMOp, A, B, C)), "bsr16_spmm_mfma_kernel", "mfma", (A, B, C)
+    raise ValueError(kind)
+
+
+def cpu_baseline(cfg, budget_s):
+    """Time the oracle (C restatement of JLUST's CPU path, OpenMP over 64-row
+    chunks) on a bounded sample of the same workload on this host."""
+    from oracle import oracle as O
+    from jlust_amd import workloads as W
+    nt = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or O.default_threads()
+    kind = cfg["kind"]
+    rows_frac = 1.0
+    if kind == "csr_spmv":
+        fn = lambda: O.csr_spmv(cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"], nthreads=nt)
+        sample = "full matrix, repeated"
+        sub = cfg
+    else:
+        # A contiguous block of rows (block-rows for BSR), sized from a probe.
+        m_units = cfg["mb"] if kind == "bsr_spmm" else cfg["m"]
+        probe = max(1, m_units // 2000)
+
+        def make_sub(units):
+            if kind == "bsr_spmm":
+                bp = cfg["browptr"][:units + 1]
+                q1 = int(bp[-1]) - 1
+                return dict(cfg, browptr=bp, bcolind=cfg["bcolind"][:q1],
+                            val=cfg["val"][:q1 * 256], mb=units, m=units * 16)
+            rp = cfg["rowptr"][:units + 1]
+            p1 = int(rp[-1]) - 1
+            d = dict(cfg, rowptr=rp, colind=cfg["colind"][:p1], m=units)
+            if kind == "csr_spmm":
+                d["val"] = cfg["val"][:p1]
+            else:
+                d["mask"] = cfg["mask"][:p1]
+                d["A"] = np.asfortranarray(cfg["A"][:units])
+            return d
+
+        def runner(d):
+            if kind == "csr_spmm":
+                return lambda: O.csr_spmm(d["rowptr"], d["colind"], d["val"], d["B"], nthreads=nt)
+            if kind == "csr_sddmm":
+                return lambda: O.csr_sddmm(d["rowptr"], d["colind"], d["A"], d["B"],
+                                           mask=d["mask"], nthreads=nt)
+            return lambda: O.bsr_spmm(d["browptr"], d["bcolind"], d["val"], 16, d["B"],
+                                      nthreads=nt)
+        t0 = time.perf_counter()
+        runner(make_sub(probe))()
+        tp = max(time.perf_counter() - t0, 1e-4)
+        units = int(min(m_units, max(probe, probe * (budget_s / 4) / tp)))
+        sub = make_sub(units)
+        fn = runner(sub)
+        rows_frac = units / m_units
+        sample = f"first {units} of {m_units} {'block-rows' if kind == 'bsr_spmm' else 'rows'}"
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    tmin = min(times)
+    nbytes = W.algorithmic_bytes(sub) if kind != "csr_spmv" else W.algorithmic_bytes(cfg)
+    return {"value": round(nbytes / tmin / 1e9, 3), "unit": "GB/s", "cores": nt,
+            "kind": "port",
+            "sample": f"{sample}; min of {len(times)} runs; oracle/jlust_cpu.c "
+                      f"(C restatement of JLUST EmitterBackend CPU path, -O3 -ffp-contract=off, "
+                      f"OpenMP {nt} threads, 64-row chunks); host nproc={os.cpu_count()}",
+            "seconds_per_run": round(tmin, 6), "rows_fraction": round(rows_frac, 6),
+            "gflops": round(W.flops(sub) / tmin / 1e9, 3) if kind != "csr_spmv" else
+            round(W.flops(cfg) / tmin / 1e9, 3)}
+
+
+def traffic_for(workload):
+    path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+    try:
+        with open(path) as f:
+            d = json.load(f)
+        e = d.get(workload)
+        return None if e is None else int(e["traffic_bytes"])
+    except (OSError, ValueError, KeyError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if args.calibrate_copy:
+        a = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"calibrate_copy_bytes": a.numel() * 4}), flush=True)
+        return
+    if args.gather_ceiling:
+        print(json.dumps({"gather_ceiling": gather_ceiling()}), flush=True)
+        return
+    from jlust_amd import workloads as W
+
+    steps = args.steps if args.steps is not None else (200 if args.config in (1, 2) else 30)
+    warmup = args.warmup if args.warmup is not None else 5
+    t0 = time.perf_counter()
+    cfg = W.make(args.config)
+    log(f"generated {cfg['name']} in {time.perf_counter() - t0:.1f}s")
+    step, kname, bound, keep = build_step(cfg, use_plan=args.plan)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    if torch.distributed.is_available() and torch.distributed.is_initialized():
+        torch.distributed.barrier()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for s, e in ev:
+        s.record(stream)
+        step()
+        e.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    per_launch_ms = np.array([s.elapsed_time(e) for s, e in ev])
+    ms_per_step = wall * 1e3 / steps
+    log(f"{steps} steps: wall {ms_per_step:.4f} ms/step, event mean "
+        f"{per_launch_ms.mean():.4f} ms, min {per_launch_ms.min():.4f} ms")
+
+    nbytes = W.algorithmic_bytes(cfg)
+    nflops = W.flops(cfg)
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    k_ms = float(per_launch_ms.mean())
+    if bound == "hbm":
+        achieved = nbytes / (k_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5)}
+    else:
+        achieved = nflops / (k_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 5)}
+    roof["traffic"] = traffic_for(cfg["name"])
+    roof["kernel"] = kname
+    roof["per_launch_ms"] = round(k_ms, 6)
+    roof["per_launch_ms_min"] = round(float(per_launch_ms.min()), 6)
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("timing the CPU baseline (oracle) ...")
+        cpu = cpu_baseline(cfg, args.cpu_seconds)
+
+    nnz_key = "nnzb" if cfg["kind"] == "bsr_spmm" else "nnz"
+    nnz_val = int((cfg["browptr"] if cfg["kind"] == "bsr_spmm" else cfg["rowptr"])[-1]) - 1
+    out = {
+        "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f64" if np.dtype(cfg["dtype"]) == np.float64 else "f32",
+        "data": "synthetic (seeded generator, jlust_amd/csrc/workloads.c)",
+        "config": {"workload": cfg["name"], "baseline_config": cfg["config"], "m": cfg["m"],
+                   "n": cfg["n"], nnz_key: nnz_val, "seed": cfg["seed"],
+                   "index": "Int32, 1-based", "plan": bool(args.plan)},
+        "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 3),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 3),
+        "algorithmic_bytes": int(nbytes), "flops": int(nflops),
+        "roofline": roof, "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    del keep
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,226 @@
+/*
+ * jlust_hip.h -- C ABI of libjlust_hip.so, the MI355X (gfx950) sparse hot path
+ * of JLUST: CSR/COO SpMV, CSR SpMM, CSR SDDMM and BSR SpMM.
+ *
+ * This is the surface a JLUST `ext/HIPExt` package extension reaches through
+ * `ccall` (or any FFI: Python ctypes in this repository's host mirror).
+ * Each entry point replaces one `execute(::EmitterBackend, ::Op{...}, ...)`
+ * method of the reference; the citation above each declaration names it.
+ *
+ * Conventions (all entry points):
+ *  - Plain device pointers and sizes only.  Every array is owned by the caller
+ *    and must stay alive until the stream work completes (the Julia side keeps
+ *    it alive through the USTensor `owner` field, src/tensor.jl:42).
+ *  - Index arrays are Int32 and carry the tensor's index origin
+ *    (`origin` = 1 for OneBased, 0 for ZeroBased, src/tensor.jl:3-5); kernels
+ *    subtract it at use, like `_origin_off` (ext/KernelAbstractionsExt/ops/
+ *    _walker.jl:125-128).
+ *  - Dense matrices are column-major (Julia arrays) with a leading dimension
+ *    `ld*` >= their row count, so views (`SubArray` columns) work.
+ *  - alpha and beta are given in the value type T (the reference casts them to
+ *    T first, ext/KernelAbstractionsExt/ops/spmv.jl:377-378).  beta == 0 makes
+ *    the output write-only: it is never read, so NaN/Inf in it do not
+ *    propagate (the reference's Tiled/ColFirst SpMM and its SDDMM read it
+ *    anyway; that difference is documented in DESIGN.md).
+ *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
+ *    returns without synchronising.  Entry points are reentrant.  The library
+ *    keeps one scratch buffer per (device, stream) for the SpMV/SpMM partial
+ *    results, so concurrent calls must use different streams.
+ *  - Return value: a jlust_status code.  A message for the last failure on the
+ *    calling thread is available from jlust_hip_last_error().
+ *  - There is no CPU fallback: with no usable GPU every compute entry point
+ *    returns JLUST_STATUS_NO_DEVICE.
+ */
+#ifndef JLUST_HIP_H
+#define JLUST_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define JLUST_HIP_ABI_VERSION 1
+
+typedef void *jlust_stream_t;                 /* hipStream_t */
+typedef struct jlust_spmv_plan *jlust_spmv_plan_t;
+
+/*
+ * Status codes.  The Julia side maps them onto the reference's exception
+ * types (src/errors.jl:1-9):
+ *   INVALID_ARGUMENT       -> IncompatibleExtents / ArgumentError
+ *   UNSUPPORTED_VALUE_TYPE -> UnsupportedValueType
+ *   UNSUPPORTED_FORMAT     -> UnsupportedFormat
+ *   NONCANONICAL_STORAGE   -> NonCanonicalStorage
+ *   INDEX_ORIGIN           -> IndexOriginMismatch
+ */
+enum jlust_status {
+    JLUST_STATUS_SUCCESS = 0,
+    JLUST_STATUS_INVALID_ARGUMENT = 1,
+    JLUST_STATUS_UNSUPPORTED_VALUE_TYPE = 2,
+    JLUST_STATUS_UNSUPPORTED_FORMAT = 3,
+    JLUST_STATUS_NONCANONICAL_STORAGE = 4,
+    JLUST_STATUS_INDEX_ORIGIN = 5,
+    JLUST_STATUS_HIP_ERROR = 6,
+    JLUST_STATUS_NO_DEVICE = 7,
+    JLUST_STATUS_OUT_OF_MEMORY = 8
+};
+
+/* ---------------------------------------------------------------- library */
+
+/* ABI version (JLUST_HIP_ABI_VERSION of the build). */
+int jlust_hip_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *jlust_hip_last_error(void);
+
+/* Name of the current device's ISA, e.g. "gfx950", into buf. */
+int jlust_hip_device_arch(char *buf, size_t len);
+
+/*
+ * Host-side structural check of a CSR pattern already copied to the host:
+ * rowptr monotone from `origin` to nnz+origin, column indices within
+ * [origin, n+origin), and (if require_sorted) strictly increasing per row.
+ * Mirrors `validate_storage` (src/backends.jl:309-316), which the reference
+ * limits to the value-buffer length; this opt-in deep check reports
+ * JLUST_STATUS_NONCANONICAL_STORAGE.  No GPU needed.
+ */
+int jlust_hip_check_csr(int64_t m, int64_t n, int64_t nnz, int32_t origin,
+                        const int32_t *rowptr_host, const int32_t *colind_host,
+                        int require_sorted);
+
+/* ----------------------------------------------------------------- SpMV */
+
+/*
+ * y = alpha*A*x + beta*y, A m x n CSR (rowptr[m+1], colind[nnz], val[nnz]).
+ * Replaces execute(::EmitterBackend, ::Op{:SpMV,Tuple{CSR,Dense,Dense}}, ...)
+ * (ext/KernelAbstractionsExt/ops/spmv.jl:371-504, CSR branch :449-502).
+ * nnz-balanced merge-path tiles, so any row-length distribution is balanced.
+ */
+int jlust_hip_csr_spmv_f64_i32(int64_t m, int64_t n, int64_t nnz,
+                               int32_t origin, const int32_t *rowptr,
+                               const int32_t *colind, const double *val,
+                               double alpha, const double *x, double beta,
+                               double *y, jlust_stream_t stream);
+int jlust_hip_csr_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz,
+                               int32_t origin, const int32_t *rowptr,
+                               const int32_t *colind, const float *val,
+                               float alpha, const float *x, float beta,
+                               float *y, jlust_stream_t stream);
+
+/*
+ * Prepared SpMV: analysis once (the merge-path partition of the pattern),
+ * execute many times, refresh the value pointer without re-analysis.
+ * Replaces prepare(::EmitterBackend, SpMVOp, u_A) / execute(h, ...)
+ * (ext/KernelAbstractionsExt/ops/spmv.jl:518-544) and the cuSPARSE handle
+ * contract prepare -> execute(h) -> update_values! (ext/CUDAExt/ops/
+ * spmv.jl:7-83, src/ops.jl:179-188).  value_type: 0 = f64, 1 = f32.
+ * The plan records the pointers given here; they must outlive the plan.
+ */
+int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
+                                   int32_t origin, int value_type,
+                                   const int32_t *rowptr,
+                                   const int32_t *colind, const void *val,
+                                   jlust_stream_t stream,
+                                   jlust_spmv_plan_t *plan_out);
+int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan,
+                                          const void *val);
+int jlust_hip_csr_spmv_plan_execute_f64(jlust_spmv_plan_t plan, double alpha,
+                                        const double *x, double beta,
+                                        double *y, jlust_stream_t stream);
+int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float alpha,
+                                        const float *x, float beta, float *y,
+                                        jlust_stream_t stream);
+int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan);
+
+/*
+ * COO SpMV (rows[nnz], cols[nnz] as stored by coo_tensor, src/interop.jl:
+ * 248-260): y = beta*y (zero-filled when beta == 0), then y += alpha*A*x.
+ * Replaces the COO branch of execute(::EmitterBackend, ::Op{:SpMV}, ...)
+ * (ext/KernelAbstractionsExt/ops/spmv.jl:407-448).  Rows need not be sorted;
+ * sorted rows reduce atomic traffic (one add per row run per tile).
+ */
+int jlust_hip_coo_spmv_f64_i32(int64_t m, int64_t n, int64_t nnz,
+                               int32_t origin, const int32_t *rows,
+                               const int32_t *cols, const double *val,
+                               double alpha, const double *x, double beta,
+                               double *y, jlust_stream_t stream);
+int jlust_hip_coo_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz,
+                               int32_t origin, const int32_t *rows,
+                               const int32_t *cols, const float *val,
+                               float alpha, const float *x, float beta,
+                               float *y, jlust_stream_t stream);
+
+/* ----------------------------------------------------------------- SpMM */
+
+/*
+ * C = alpha*A*B + beta*C, A m x n CSR, B n x k (ldb), C m x k (ldc), both
+ * column-major.  skip_empty_rows leaves rows with no stored entry untouched
+ * (the reference's guarded 2-D path, ext/KernelAbstractionsExt/ops/
+ * spmm.jl:203,340).  Replaces execute(::EmitterBackend, ::Op{:SpMM}, ...)
+ * (spmm.jl:397-423).
+ */
+int jlust_hip_csr_spmm_f64_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                               int32_t origin, const int32_t *rowptr,
+                               const int32_t *colind, const double *val,
+                               double alpha, const double *B, int64_t ldb,
+                               double beta, double *C, int64_t ldc,
+                               int skip_empty_rows, jlust_stream_t stream);
+int jlust_hip_csr_spmm_f32_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                               int32_t origin, const int32_t *rowptr,
+                               const int32_t *colind, const float *val,
+                               float alpha, const float *B, int64_t ldb,
+                               float beta, float *C, int64_t ldc,
+                               int skip_empty_rows, jlust_stream_t stream);
+
+/* ---------------------------------------------------------------- SDDMM */
+
+/*
+ * Cval[p] = alpha*dot(A[i,:], B[:,j]) + beta*Cval[p] for each stored (i, j)
+ * of the CSR pattern C (m x n); A m x K (lda), B K x n (ldb), column-major.
+ * When mask != NULL the dot term is multiplied by mask[p]:
+ * Cval[p] = mask[p]*(alpha*dot) + beta*Cval[p]; mask may alias Cval.
+ * Replaces execute(::EmitterBackend, ::Op{:SDDMM}, A, B, C; alpha, beta)
+ * (ext/KernelAbstractionsExt/ops/sddmm.jl:49-65; body :23-30).
+ */
+int jlust_hip_csr_sddmm_f64_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                int32_t origin, const int32_t *rowptr,
+                                const int32_t *colind, double alpha,
+                                const double *A, int64_t lda, const double *B,
+                                int64_t ldb, double beta, double *Cval,
+                                const double *mask, jlust_stream_t stream);
+int jlust_hip_csr_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                int32_t origin, const int32_t *rowptr,
+                                const int32_t *colind, float alpha,
+                                const float *A, int64_t lda, const float *B,
+                                int64_t ldb, float beta, float *Cval,
+                                const float *mask, jlust_stream_t stream);
+
+/* ------------------------------------------------------------------ BSR */
+
+/*
+ * C = alpha*A*B + beta*C, A an mb x nb grid of bs x bs blocks in BSR
+ * (browptr[mb+1], bcolind[nnzb], val[nnzb*bs*bs] block-major; row-major
+ * inside a block when row_major_blocks != 0 = Formats.BSRRight, else
+ * column-major = BSRLeft; src/named_formats.jl:106-128, storage as in
+ * ext/CUDAExt/CUDAExt.jl:144-156).  B (nb*bs) x k (ldb), C (mb*bs) x k (ldc),
+ * column-major.  bs == 16 runs on fp32 MFMA; other block sizes return
+ * JLUST_STATUS_UNSUPPORTED_FORMAT.  The reference routes BSR SpMM through the
+ * generic execute(::EmitterBackend, ::Op{:SpMM}) (KernelAbstractionsExt.jl:
+ * 35-37), which does not compute it correctly; this entry point implements
+ * the operator's definition.
+ */
+int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs,
+                               int64_t nnzb, int32_t origin,
+                               const int32_t *browptr, const int32_t *bcolind,
+                               const float *val, int row_major_blocks,
+                               int64_t k, float alpha, const float *B,
+                               int64_t ldb, float beta, float *C, int64_t ldc,
+                               jlust_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* JLUST_HIP_H */

@@ -1,0 +1,106 @@
+"""Loader and ctypes signatures for libjlust_hip.so (include/jlust_hip.h).
+
+torch is imported before the library is opened: torch ships its own
+libamdhip64.so.7 (same SONAME as ROCm's), so the library then binds to the HIP
+runtime torch already loaded and device pointers are shared with torch's
+allocator.  There is no fallback: if the library is missing the import of the
+compute path fails loudly.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the HIP library, see module docstring)
+
+from . import errors
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libjlust_hip.so")
+
+_P = ctypes.c_void_p
+_I32 = ctypes.c_int32
+_I64 = ctypes.c_int64
+_INT = ctypes.c_int
+_D = ctypes.c_double
+_F = ctypes.c_float
+
+# Every symbol include/jlust_hip.h declares, with (restype, argtypes).
+SIGNATURES = {
+    "jlust_hip_version": (_INT, []),
+    "jlust_hip_last_error": (ctypes.c_char_p, []),
+    "jlust_hip_device_arch": (_INT, [ctypes.c_char_p, ctypes.c_size_t]),
+    "jlust_hip_check_csr": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _INT]),
+    "jlust_hip_csr_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P, _P]),
+    "jlust_hip_csr_spmv_f32_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _F, _P, _P]),
+    "jlust_hip_csr_spmv_plan_create": (_INT, [_I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
+                                              ctypes.POINTER(_P)]),
+    "jlust_hip_csr_spmv_plan_update_values": (_INT, [_P, _P]),
+    "jlust_hip_csr_spmv_plan_execute_f64": (_INT, [_P, _D, _P, _D, _P, _P]),
+    "jlust_hip_csr_spmv_plan_execute_f32": (_INT, [_P, _F, _P, _F, _P, _P]),
+    "jlust_hip_csr_spmv_plan_destroy": (_INT, [_P]),
+    "jlust_hip_coo_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P, _P]),
+    "jlust_hip_coo_spmv_f32_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _F, _P, _P]),
+    "jlust_hip_csr_spmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _I64,
+                                          _D, _P, _I64, _INT, _P]),
+    "jlust_hip_csr_spmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _I64,
+                                          _F, _P, _I64, _INT, _P]),
+    "jlust_hip_csr_sddmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _D, _P, _I64, _P,
+                                           _I64, _D, _P, _P, _P]),
+    "jlust_hip_csr_sddmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _F, _P, _I64, _P,
+                                           _I64, _F, _P, _P, _P]),
+    "jlust_hip_bsr_spmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _INT, _I64, _F,
+                                          _P, _I64, _F, _P, _I64, _P]),
+}
+
+STATUS = {
+    0: "SUCCESS", 1: "INVALID_ARGUMENT", 2: "UNSUPPORTED_VALUE_TYPE", 3: "UNSUPPORTED_FORMAT",
+    4: "NONCANONICAL_STORAGE", 5: "INDEX_ORIGIN", 6: "HIP_ERROR", 7: "NO_DEVICE",
+    8: "OUT_OF_MEMORY",
+}
+
+_lib = None
+
+
+def lib():
+    """Open libjlust_hip.so once; raise if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m jlust_amd.build` "
+                "(the sparse operators have no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        if L.jlust_hip_version() != 1:
+            raise RuntimeError("libjlust_hip.so ABI version mismatch")
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().jlust_hip_last_error().decode(errors="replace")
+
+
+def check(status: int, what: str, fmt=None, backend=None, T=None):
+    """Raise the JLUST exception that corresponds to a C ABI status code."""
+    if status == 0:
+        return
+    msg = f"{what}: {last_error()}"
+    if status == 1:
+        raise errors.IncompatibleExtents(msg)
+    if status == 2:
+        raise errors.UnsupportedValueType(T, backend, msg)
+    if status == 3:
+        raise errors.UnsupportedFormat(fmt, backend, msg)
+    if status == 4:
+        raise errors.NonCanonicalStorage(msg)
+    if status == 5:
+        raise errors.IndexOriginMismatch("origin", msg)
+    if status == 7:
+        raise errors.NoDevice(msg)
+    if status == 8:
+        raise MemoryError(msg)
+    raise errors.HIPError(f"{STATUS.get(status, status)}: {msg}")

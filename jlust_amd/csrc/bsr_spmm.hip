@@ -1,0 +1,182 @@
+// bsr_spmm.hip -- BSR (16 x 16 blocks) SpMM C = alpha*A*B + beta*C on the
+// gfx950 fp32 matrix cores (v_mfma_f32_16x16x4_f32).
+//
+// JLUST's BSR layout: Formats.BSRRight/BSRLeft (src/named_formats.jl:106-128),
+// block-row pointers and block-column indices at level 2, values block-major,
+// row-major inside a block for BSRRight (ext/CUDAExt/CUDAExt.jl:144-156).
+// The reference sends BSR SpMM to execute(::EmitterBackend, ::Op{:SpMM})
+// (KernelAbstractionsExt.jl:35-37), which does not compute it; this kernel
+// implements the definition C[16R+r, c] = alpha*sum_q sum_s V_q[r][s] *
+// B[16*bcol_q + s, c] + beta*C.
+//
+// One wave owns one block-row and all k columns of C for it (V is read
+// once).  A 16 x 16 block times a 16 x 16 slab of B is four MFMA 16x16x4
+// steps.  The contraction index is split as s = 4*g + step (g = lane / 16),
+// so every lane needs 4 consecutive s of its row (A) and of its column (B):
+//   A operand: lane (i = lane % 16, g) holds V_q[i][4g .. 4g+3]  (one float4
+//              of a row-major block);
+//   B operand: lane (j = lane % 16, g) holds B[16*bcol + 4g .. +3, c0 + j]
+//              (one float4 of a column-major B column);
+//   result:    lane (j, g) holds C rows 16R + 4g .. +3 of column c0 + j, so
+//              the epilogue is one float4 load/store per 16-column tile.
+// Block-rows are mapped XCD-major: the 8 XCDs each take one contiguous band
+// of block-rows, so the +-bandwidth window of B a band reuses stays in that
+// XCD's L2.
+#include "common.hpp"
+
+namespace jlust {
+namespace {
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int BSR_BS = 16;
+constexpr int BSR_WAVES = 4;                 // block-rows per workgroup
+constexpr int BSR_TILES = 16;                // 16-column tiles per pass (256 columns)
+constexpr int NUM_XCD = 8;
+
+// VEC: B, C 16-byte aligned with ld % 4 == 0 (float4 access).
+template <bool ROW_MAJOR, bool VEC>
+__global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_mfma_kernel(
+    int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
+    const int32_t *__restrict__ bcolind, const float *__restrict__ val, int64_t k, float alpha,
+    const float *__restrict__ B, int64_t ldb, float beta, int beta_zero, float *__restrict__ C,
+    int64_t ldc, int64_t ngroups)
+{
+    // XCD-major remap of the workgroup index (grid padded to a multiple of 8).
+    const int64_t per_xcd = (int64_t)gridDim.x / NUM_XCD;
+    const int64_t grp = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+    if (grp >= ngroups) return;
+    const int64_t R = grp * BSR_WAVES + (threadIdx.x >> 6);
+    if (R >= mb) return;
+
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 15;       // block row (A operand) / column in tile (B, C)
+    const int g = lane >> 4;       // group of 4 in the contraction / C row group
+    const int64_t q0 = (int64_t)browptr[R] - origin;
+    const int64_t q1 = (int64_t)browptr[R + 1] - origin;
+    const int64_t crow = R * BSR_BS + 4 * g;
+
+    for (int64_t c0 = 0; c0 < k; c0 += 16 * BSR_TILES) {
+        floatx4 acc[BSR_TILES];
+#pragma unroll
+        for (int t = 0; t < BSR_TILES; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+        for (int64_t q = q0; q < q1; ++q) {
+            const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
+            const float *vb = val + q * (BSR_BS * BSR_BS);
+            floatx4 a;
+            if (ROW_MAJOR) {
+                a = *reinterpret_cast<const floatx4 *>(vb + i * BSR_BS + 4 * g);
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) a[u] = vb[(4 * g + u) * BSR_BS + i];
+            }
+            floatx4 b[BSR_TILES];
+#pragma unroll
+            for (int t = 0; t < BSR_TILES; ++t) {
+                const int64_t col = c0 + 16 * t + i;
+                if (col < k) {
+                    const float *src = B + brow + col * ldb;
+                    if (VEC) {
+                        b[t] = *reinterpret_cast<const floatx4 *>(src);
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) b[t][u] = src[u];
+                    }
+                } else {
+                    b[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+                }
+            }
+#pragma unroll
+            for (int t = 0; t < BSR_TILES; ++t) {
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[t][0], acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[t][1], acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[t][2], acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[t][3], acc[t], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < BSR_TILES; ++t) {
+            const int64_t col = c0 + 16 * t + i;
+            if (col >= k) continue;
+            float *dst = C + crow + col * ldc;
+            floatx4 out = acc[t] * alpha;
+            if (!beta_zero) {
+                floatx4 old;
+                if (VEC) old = *reinterpret_cast<const floatx4 *>(dst);
+                else
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) old[u] = dst[u];
+                out += beta * old;
+            }
+            if (VEC) {
+                *reinterpret_cast<floatx4 *>(dst) = out;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) dst[u] = out[u];
+            }
+        }
+    }
+}
+
+int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
+             const int32_t *browptr, const int32_t *bcolind, const float *val,
+             int row_major_blocks, int64_t k, float alpha, const float *B, int64_t ldb,
+             float beta, float *C, int64_t ldc, jlust_stream_t stream)
+{
+    clear_error();
+    if (mb < 0 || nb < 0 || bs <= 0 || nnzb < 0 || k < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: negative extent or block size");
+    if (bs != BSR_BS)
+        return fail(JLUST_STATUS_UNSUPPORTED_FORMAT,
+                    "bsr_spmm: block size %lld x %lld (the MFMA path supports 16 x 16)",
+                    (long long)bs, (long long)bs);
+    if (mb * bs > INT32_MAX || nb * bs > INT32_MAX || nnzb > INT32_MAX)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: extents exceed the Int32 index range");
+    if (int st = check_origin(origin)) return st;
+    const int64_t mrows = mb * bs, nrows = nb * bs;
+    if (ldb < (nrows > 0 ? nrows : 1) || ldc < (mrows > 0 ? mrows : 1))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "bsr_spmm: leading dimensions too small (ldb=%lld < %lld or ldc=%lld < %lld)",
+                    (long long)ldb, (long long)nrows, (long long)ldc, (long long)mrows);
+    if ((mb > 0 && !browptr) || bad_ptr(bcolind, nnzb) || bad_ptr(val, nnzb) ||
+        bad_ptr(B, (nnzb > 0 && k > 0) ? nrows : 0) || bad_ptr(C, mrows * k))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: null device pointer");
+    if (int st = require_device(nullptr)) return st;
+    if (mb == 0 || k == 0) return JLUST_STATUS_SUCCESS;
+
+    const bool vec = (ldb % 4 == 0) && (ldc % 4 == 0) && ((uintptr_t)B % 16 == 0) &&
+                     ((uintptr_t)C % 16 == 0);
+    const bool vals_aligned = ((uintptr_t)val % 16 == 0);
+    const int64_t ngroups = (mb + BSR_WAVES - 1) / BSR_WAVES;
+    const int64_t grid = (ngroups + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+    hipStream_t s = (hipStream_t)stream;
+    const int bz = beta == 0.f;
+#define JLUST_BSR_LAUNCH(RM, V)                                                                   \
+    hipLaunchKernelGGL((bsr16_spmm_mfma_kernel<RM, V>), dim3((unsigned)grid), dim3(64 * BSR_WAVES), \
+                       0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, bz, C, ldc, \
+                       ngroups)
+    const bool rm = row_major_blocks && vals_aligned;
+    if (row_major_blocks && !vals_aligned)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: block values must be 16-byte aligned");
+    if (rm && vec) JLUST_BSR_LAUNCH(true, true);
+    else if (rm) JLUST_BSR_LAUNCH(true, false);
+    else if (vec) JLUST_BSR_LAUNCH(false, true);
+    else JLUST_BSR_LAUNCH(false, false);
+#undef JLUST_BSR_LAUNCH
+    return check_launch("bsr16_spmm_mfma_kernel");
+}
+
+}  // namespace
+}  // namespace jlust
+
+extern "C" int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb,
+                                          int32_t origin, const int32_t *browptr,
+                                          const int32_t *bcolind, const float *val,
+                                          int row_major_blocks, int64_t k, float alpha,
+                                          const float *B, int64_t ldb, float beta, float *C,
+                                          int64_t ldc, jlust_stream_t stream)
+{
+    return jlust::bsr_spmm(mb, nb, bs, nnzb, origin, browptr, bcolind, val, row_major_blocks, k,
+                           alpha, B, ldb, beta, C, ldc, stream);
+}

@@ -1,0 +1,67 @@
+// common.hpp -- internals shared by the libjlust_hip.so translation units:
+// status/error plumbing for the C ABI, argument checks, per-(device, stream)
+// scratch buffers, device properties and wave64 helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/jlust_hip.h"
+
+namespace jlust {
+
+// ----------------------------------------------------------------- errors
+
+// Records `msg` as this thread's last error and returns `code`.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+void clear_error();
+
+// Maps a failed HIP call onto JLUST_STATUS_HIP_ERROR / OUT_OF_MEMORY.
+int hip_fail(hipError_t e, const char *what);
+
+#define JLUST_HIP_TRY(expr)                                      \
+    do {                                                         \
+        hipError_t _e = (expr);                                  \
+        if (_e != hipSuccess) return ::jlust::hip_fail(_e, #expr); \
+    } while (0)
+
+// Checks that a GPU is present and current; JLUST_STATUS_NO_DEVICE otherwise.
+int require_device(int *device_out);
+
+// Checks a kernel launch (hipGetLastError) and turns failures into a status.
+int check_launch(const char *kernel);
+
+// ------------------------------------------------------------- arguments
+
+inline bool bad_ptr(const void *p, int64_t count) { return count > 0 && p == nullptr; }
+
+int check_origin(int32_t origin);
+
+// ---------------------------------------------------------------- devices
+
+struct DeviceInfo {
+    int cu_count = 0;          // compute units
+    int wave_size = 64;
+    size_t lds_per_block = 0;  // bytes
+    char arch[64] = {0};
+};
+const DeviceInfo &device_info(int device);
+
+// ---------------------------------------------------------------- scratch
+
+// Returns a device buffer of at least `bytes` owned by the library and
+// private to (current device, stream).  It grows on demand (the old buffer is
+// released after the stream drains) and lives until process exit.
+int scratch(jlust_stream_t stream, size_t bytes, void **out);
+
+// ------------------------------------------------------------ device code
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+template <typename T>
+__device__ __forceinline__ T ld_nt(const T *p) { return __builtin_nontemporal_load(p); }
+
+}  // namespace jlust

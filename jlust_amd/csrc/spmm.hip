@@ -1,0 +1,237 @@
+// spmm.hip -- CSR SpMM C = alpha*A*B + beta*C for gfx950 (wave64).
+//
+// Replaces execute(::EmitterBackend, ::Op{:SpMM}, ...)
+// (ext/KernelAbstractionsExt/ops/spmm.jl:397-423).  Per output the reference
+// sums val[k]*B[col[k], c] sequentially over the row and writes
+// alpha*acc + beta*C (spmm.jl:272-279 for the Tiled strategy used at k > 32).
+//
+// B and C are column-major (Julia layout).  Gathering a row B[j, :] straight
+// from column-major B touches k cache lines 4*ldb bytes apart for k useful
+// values, so the kernel first re-lays B out row-major (Bt, n x ldt) in the
+// library's scratch buffer with an LDS-tiled transpose: one coalesced read
+// and one coalesced write of B.  Then:
+//   - a block owns SPMM_ROWS consecutive rows; each wave walks one row at a
+//     time, its 64 lanes covering a 64*VEC-column chunk (VEC consecutive
+//     columns per lane, one vector load per lane per nonzero, so one nonzero
+//     reads a contiguous 64*VEC*sizeof(T)-byte slice of Bt);
+//   - the row's col/val are read 64 at a time with one coalesced load and
+//     broadcast lane by lane (v_readlane), several B slices in flight;
+//   - results are staged in LDS and written to column-major C column by
+//     column (SPMM_ROWS consecutive values per column), so C writes are
+//     coalesced too.
+#include "common.hpp"
+
+namespace jlust {
+namespace {
+
+constexpr int SPMM_BLOCK = 256;
+constexpr int SPMM_ROWS = 32;
+constexpr int SPMM_UNROLL = 8;
+
+template <typename T>
+__device__ __forceinline__ T bcast(T v, int lane);
+template <>
+__device__ __forceinline__ float bcast<float>(float v, int lane)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+template <>
+__device__ __forceinline__ double bcast<double>(double v, int lane)
+{
+    const long long b = __double_as_longlong(v);
+    const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), lane);
+    const int hi = __builtin_amdgcn_readlane((int)(b >> 32), lane);
+    return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+__device__ __forceinline__ int bcast_i(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
+
+template <typename T, int VEC> struct Vec;
+template <typename T> struct Vec<T, 1> { T v[1]; };
+template <typename T> struct alignas(2 * sizeof(T)) Vec<T, 2> { T v[2]; };
+template <typename T> struct alignas(4 * sizeof(T)) Vec<T, 4> { T v[4]; };
+
+// Bt[j*ldt + c] = B[j + c*ldb] for j < n, c < k (64 x 64 tiles through LDS).
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(int64_t n, int64_t k,
+                                                        const T *__restrict__ B, int64_t ldb,
+                                                        T *__restrict__ Bt, int64_t ldt)
+{
+    __shared__ T tile[64][65];
+    const int tx = threadIdx.x & 63;
+    const int ty = threadIdx.x >> 6;
+    const int64_t j0 = (int64_t)blockIdx.x * 64;
+    const int64_t c0 = (int64_t)blockIdx.y * 64;
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const int cc = ty + 4 * s;
+        const int64_t j = j0 + tx, c = c0 + cc;
+        if (j < n && c < k) tile[cc][tx] = B[j + c * ldb];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < 16; ++s) {
+        const int jj = ty + 4 * s;
+        const int64_t j = j0 + jj, c = c0 + tx;
+        if (j < n && c < k) Bt[j * ldt + c] = tile[tx][jj];
+    }
+}
+
+template <typename T, int VEC>
+__global__ __launch_bounds__(SPMM_BLOCK) void csr_spmm_kernel(
+    int64_t m, int64_t k, int32_t origin, const int32_t *__restrict__ rowptr,
+    const int32_t *__restrict__ colind, const T *__restrict__ val, const T *__restrict__ Bt,
+    int64_t ldt, T alpha, T beta, int beta_zero, T *__restrict__ C, int64_t ldc,
+    int skip_empty_rows)
+{
+    constexpr int KC = 64 * VEC;              // columns per chunk
+    constexpr int NW = SPMM_BLOCK / 64;
+    __shared__ T s_c[SPMM_ROWS][KC + 1];
+    __shared__ int s_empty[SPMM_ROWS];
+    using V = Vec<T, VEC>;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int64_t row0 = (int64_t)blockIdx.x * SPMM_ROWS;
+    const int nrows = (int)min((int64_t)SPMM_ROWS, m - row0);
+
+    for (int64_t c0 = 0; c0 < k; c0 += KC) {
+        const int64_t cl = c0 + (int64_t)lane * VEC;     // first column of this lane
+        const bool full = cl + VEC <= k;
+        for (int rr = wave; rr < nrows; rr += NW) {
+            const int64_t row = row0 + rr;
+            const int64_t lo = (int64_t)rowptr[row] - origin;
+            const int64_t hi = (int64_t)rowptr[row + 1] - origin;
+            if (lane == 0 && c0 == 0) s_empty[rr] = hi <= lo;
+            T acc[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) acc[e] = T(0);
+            for (int64_t p0 = lo; p0 < hi; p0 += 64) {
+                const int cnt = (int)min((int64_t)64, hi - p0);
+                int cidx = 0;
+                T cv = T(0);
+                if (lane < cnt) {
+                    cidx = colind[p0 + lane] - origin;
+                    cv = val[p0 + lane];
+                }
+                int q = 0;
+                for (; q + SPMM_UNROLL <= cnt; q += SPMM_UNROLL) {
+                    V b[SPMM_UNROLL];
+                    T a[SPMM_UNROLL];
+#pragma unroll
+                    for (int u = 0; u < SPMM_UNROLL; ++u) {
+                        const int64_t j = bcast_i(cidx, q + u);
+                        a[u] = bcast(cv, q + u);
+                        if (full) {
+                            b[u] = *reinterpret_cast<const V *>(Bt + j * ldt + cl);
+                        } else {
+#pragma unroll
+                            for (int e = 0; e < VEC; ++e)
+                                b[u].v[e] = cl + e < k ? Bt[j * ldt + cl + e] : T(0);
+                        }
+                    }
+#pragma unroll
+                    for (int u = 0; u < SPMM_UNROLL; ++u)
+#pragma unroll
+                        for (int e = 0; e < VEC; ++e) acc[e] += a[u] * b[u].v[e];
+                }
+                for (; q < cnt; ++q) {
+                    const int64_t j = bcast_i(cidx, q);
+                    const T a = bcast(cv, q);
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e)
+                        if (cl + e < k) acc[e] += a * Bt[j * ldt + cl + e];
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) s_c[rr][lane * VEC + e] = acc[e];
+        }
+        __syncthreads();
+        // Column-major write-out: SPMM_ROWS consecutive rows per column.
+        const int ncols = (int)min((int64_t)KC, k - c0);
+        for (int idx = tid; idx < SPMM_ROWS * ncols; idx += SPMM_BLOCK) {
+            const int rr = idx % SPMM_ROWS;
+            const int cc = idx / SPMM_ROWS;
+            if (rr >= nrows) continue;
+            if (skip_empty_rows && s_empty[rr]) continue;
+            T *dst = C + (row0 + rr) + (c0 + cc) * ldc;
+            const T s = alpha * s_c[rr][cc];
+            *dst = beta_zero ? s : s + beta * *dst;
+        }
+        __syncthreads();
+    }
+}
+
+template <typename T>
+int csr_spmm(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
+             const int32_t *rowptr, const int32_t *colind, const T *val, T alpha, const T *B,
+             int64_t ldb, T beta, T *C, int64_t ldc, int skip_empty_rows, jlust_stream_t stream)
+{
+    clear_error();
+    if (m < 0 || n < 0 || k < 0 || nnz < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_spmm: negative extent");
+    if (m > INT32_MAX || n > INT32_MAX || nnz > INT32_MAX)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_spmm: extents exceed the Int32 index range");
+    if (int st = check_origin(origin)) return st;
+    if (ldb < (n > 0 ? n : 1) || ldc < (m > 0 ? m : 1))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "csr_spmm: leading dimensions too small (ldb=%lld < n=%lld or ldc=%lld < m=%lld)",
+                    (long long)ldb, (long long)n, (long long)ldc, (long long)m);
+    if ((m > 0 && !rowptr) || bad_ptr(colind, nnz) || bad_ptr(val, nnz) ||
+        bad_ptr(B, (nnz > 0 && k > 0) ? n : 0) || bad_ptr(C, m * k))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_spmm: null device pointer");
+    if (nnz > 0 && n == 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_spmm: nnz > 0 with n == 0");
+    if (int st = require_device(nullptr)) return st;
+    if (m == 0 || k == 0) return JLUST_STATUS_SUCCESS;
+    hipStream_t s = (hipStream_t)stream;
+
+    const int vec = (sizeof(T) == 4) ? (k <= 64 ? 1 : k <= 128 ? 2 : 4) : (k <= 64 ? 1 : 2);
+    const int64_t ldt = (k + 3) / 4 * 4;       // keeps every row of Bt 16-byte aligned
+    void *ws = nullptr;
+    const int64_t nt = n > 0 ? n : 1;
+    if (int st = scratch(stream, sizeof(T) * (size_t)(nt * ldt), &ws)) return st;
+    T *Bt = (T *)ws;
+    if (n > 0) {
+        dim3 grid((unsigned)((n + 63) / 64), (unsigned)((k + 63) / 64));
+        hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, s, n, k, B, ldb, Bt, ldt);
+        if (int st = check_launch("transpose_kernel")) return st;
+    }
+    const dim3 grid((unsigned)((m + SPMM_ROWS - 1) / SPMM_ROWS));
+    const int bz = beta == T(0);
+    if (vec == 1)
+        hipLaunchKernelGGL((csr_spmm_kernel<T, 1>), grid, dim3(SPMM_BLOCK), 0, s, m, k, origin,
+                           rowptr, colind, val, Bt, ldt, alpha, beta, bz, C, ldc, skip_empty_rows);
+    else if (vec == 2)
+        hipLaunchKernelGGL((csr_spmm_kernel<T, 2>), grid, dim3(SPMM_BLOCK), 0, s, m, k, origin,
+                           rowptr, colind, val, Bt, ldt, alpha, beta, bz, C, ldc, skip_empty_rows);
+    else
+        hipLaunchKernelGGL((csr_spmm_kernel<T, 4>), grid, dim3(SPMM_BLOCK), 0, s, m, k, origin,
+                           rowptr, colind, val, Bt, ldt, alpha, beta, bz, C, ldc, skip_empty_rows);
+    return check_launch("csr_spmm_kernel");
+}
+
+}  // namespace
+}  // namespace jlust
+
+using namespace jlust;
+
+extern "C" int jlust_hip_csr_spmm_f64_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                                          int32_t origin, const int32_t *rowptr,
+                                          const int32_t *colind, const double *val, double alpha,
+                                          const double *B, int64_t ldb, double beta, double *C,
+                                          int64_t ldc, int skip_empty_rows, jlust_stream_t stream)
+{
+    return csr_spmm<double>(m, n, k, nnz, origin, rowptr, colind, val, alpha, B, ldb, beta, C,
+                            ldc, skip_empty_rows, stream);
+}
+
+extern "C" int jlust_hip_csr_spmm_f32_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                                          int32_t origin, const int32_t *rowptr,
+                                          const int32_t *colind, const float *val, float alpha,
+                                          const float *B, int64_t ldb, float beta, float *C,
+                                          int64_t ldc, int skip_empty_rows, jlust_stream_t stream)
+{
+    return csr_spmm<float>(m, n, k, nnz, origin, rowptr, colind, val, alpha, B, ldb, beta, C,
+                           ldc, skip_empty_rows, stream);
+}

@@ -1,0 +1,318 @@
+"""HIPBackend: execute/prepare for SpMV, SpMM and SDDMM over libjlust_hip.so.
+
+The checks mirror what the reference raises before it launches
+(validate_storage, src/backends.jl:309-316; the error types of
+src/errors.jl): value type, index type, device, extents, buffer lengths.
+Every compute call goes to the C ABI on torch's current stream; there is no
+CPU path here.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+from .errors import (DeviceMismatch, IncompatibleExtents, NonCanonicalStorage,
+                     UnsupportedFormat, UnsupportedIndexType, UnsupportedValueType)
+from .formats import bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped
+from .ops import AbstractKernelHandle, HIPBackend, Op, SDDMMOp, SpMMOp, SpMVOp
+from .tensor import USTensor, leading_dim, nnz, nonzeros
+
+_BE = HIPBackend()
+_VALUE_TYPES = {torch.float64: "f64", torch.float32: "f32"}
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _dense_fmt(fmt) -> bool:
+    return fmt.is_dense
+
+
+# ---------------------------------------------------------------- capability
+
+def supports(op: Op) -> bool:
+    """Capability table (the counterpart of KernelAbstractionsExt.jl:31-41)."""
+    f = op.formats
+    if op.tag == "SpMV" and len(f) == 3:
+        return (is_csr_shaped(f[0]) or is_coo_shaped(f[0])) and _dense_fmt(f[1]) and \
+            _dense_fmt(f[2]) and f[1].ndims == 1 and f[2].ndims == 1
+    if op.tag == "SpMM" and len(f) == 3:
+        a_ok = is_csr_shaped(f[0]) or (is_bsr(f[0]) and bsr_blocksize(f[0])[:2] == (16, 16))
+        return a_ok and _dense_fmt(f[1]) and _dense_fmt(f[2]) and f[1].ndims == 2 and \
+            f[2].ndims == 2
+    if op.tag == "SDDMM" and len(f) == 3:
+        return _dense_fmt(f[0]) and _dense_fmt(f[1]) and is_csr_shaped(f[2])
+    return False
+
+
+# --------------------------------------------------------------------- checks
+
+def _value_suffix(u: USTensor) -> str:
+    s = _VALUE_TYPES.get(nonzeros(u).dtype)
+    if s is None:
+        raise UnsupportedValueType(nonzeros(u).dtype, _BE)
+    return s
+
+
+def _check_index(u: USTensor, *bufs):
+    for b in bufs:
+        if b.dtype != torch.int32:
+            raise UnsupportedIndexType(b.dtype, _BE)
+        if not b.is_contiguous():
+            raise NonCanonicalStorage(f"{u.format} index buffers must be contiguous")
+
+
+def _check_same_device(*ts):
+    devs = {t.device for t in ts if t is not None}
+    if len(devs) != 1:
+        raise DeviceMismatch(f"operands on several devices: {sorted(map(str, devs))}")
+    dev = devs.pop()
+    if dev.type != "cuda":
+        raise DeviceMismatch(f"HIPBackend needs GPU buffers, got {dev}")
+    return dev
+
+
+def _check_values(u: USTensor, T):
+    v = nonzeros(u)
+    if v.dtype != T:
+        raise UnsupportedValueType(v.dtype, _BE, f"operands must share the value type {T}")
+    if not v.is_contiguous():
+        raise NonCanonicalStorage("value buffers must be contiguous")
+
+
+def _csr_parts(u: USTensor):
+    rowptr, colind = u.pos_buffers[1], u.crd_buffers[1]
+    if rowptr is None or colind is None:
+        raise NonCanonicalStorage(f"{u.format}: missing level-2 pos/crd buffer")
+    _check_index(u, rowptr, colind)
+    m, n = u.extents
+    if rowptr.numel() != m + 1:
+        raise NonCanonicalStorage(f"rowptr has {rowptr.numel()} entries, expected m+1 = {m + 1}")
+    if colind.numel() != nnz(u):
+        raise NonCanonicalStorage(
+            f"val buffer length {nnz(u)} != nnz {colind.numel()} (backend=HIPBackend)")
+    return rowptr, colind
+
+
+# -------------------------------------------------------------------- execute
+
+def execute(op: Op, *ts, alpha=1.0, beta=0.0, input_fn=None, output_fn=None,
+            skip_empty_rows=False, mask=None):
+    if input_fn is not None or output_fn is not None:
+        raise UnsupportedFormat(op.formats, _BE,
+                                "input_fn/output_fn closures are not supported by the HIP kernels")
+    if not supports(op):
+        raise UnsupportedFormat(op.formats, _BE)
+    if op.tag == "SpMV":
+        return _spmv(*ts, alpha=alpha, beta=beta)
+    if op.tag == "SpMM":
+        return _spmm(*ts, alpha=alpha, beta=beta, skip_empty_rows=skip_empty_rows)
+    return _sddmm(*ts, alpha=alpha, beta=beta, mask=mask)
+
+
+def _vec_checks(u_A, u_x, u_y):
+    T = nonzeros(u_A).dtype
+    x, y = nonzeros(u_x), nonzeros(u_y)
+    _check_values(u_x, T)
+    _check_values(u_y, T)
+    m, n = u_A.extents
+    if x.numel() != n or y.numel() != m:
+        raise IncompatibleExtents(
+            f"SpMV: A is {m}x{n}, x has {x.numel()} entries, y has {y.numel()}")
+    return x, y
+
+
+def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
+    suf = _value_suffix(u_A)
+    x, y = _vec_checks(u_A, u_x, u_y)
+    m, n = u_A.extents
+    L = _lib.lib()
+    if is_csr_shaped(u_A.format):
+        rowptr, colind = _csr_parts(u_A)
+        dev = _check_same_device(rowptr, colind, nonzeros(u_A), x, y)
+        with torch.cuda.device(dev):
+            st = getattr(L, f"jlust_hip_csr_spmv_{suf}_i32")(
+                m, n, nnz(u_A), u_A.origin.offset, _ptr(rowptr), _ptr(colind),
+                _ptr(nonzeros(u_A)), float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
+        _lib.check(st, "csr_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
+        return u_y
+    rows, cols = u_A.crd_buffers[0], u_A.crd_buffers[1]
+    _check_index(u_A, rows, cols)
+    if rows.numel() != nnz(u_A) or cols.numel() != nnz(u_A):
+        raise NonCanonicalStorage("COO coordinate buffers must have nnz entries")
+    dev = _check_same_device(rows, cols, nonzeros(u_A), x, y)
+    with torch.cuda.device(dev):
+        st = getattr(L, f"jlust_hip_coo_spmv_{suf}_i32")(
+            m, n, nnz(u_A), u_A.origin.offset, _ptr(rows), _ptr(cols), _ptr(nonzeros(u_A)),
+            float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
+    _lib.check(st, "coo_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
+    return u_y
+
+
+def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_rows=False):
+    suf = _value_suffix(u_A)
+    T = nonzeros(u_A).dtype
+    B, C = nonzeros(u_B), nonzeros(u_C)
+    if B.dtype != T or C.dtype != T:
+        raise UnsupportedValueType(B.dtype if B.dtype != T else C.dtype, _BE)
+    m, n = u_A.extents
+    if B.shape[0] != n or C.shape[0] != m or B.shape[1] != C.shape[1]:
+        raise IncompatibleExtents(
+            f"SpMM: A is {m}x{n}, B is {tuple(B.shape)}, C is {tuple(C.shape)}")
+    for t, nm in ((B, "B"), (C, "C")):
+        if t.shape[0] > 1 and t.shape[1] > 0 and t.stride(0) != 1:
+            raise NonCanonicalStorage(f"SpMM: {nm} must be column-major (stride(0) == 1)")
+    k = B.shape[1]
+    L = _lib.lib()
+    if is_bsr(u_A.format):
+        b1, b2, row_major = bsr_blocksize(u_A.format)
+        if suf != "f32":
+            raise UnsupportedValueType(T, _BE, "BSR SpMM runs on fp32 MFMA")
+        browptr, bcolind = u_A.pos_buffers[1], u_A.crd_buffers[1]
+        _check_index(u_A, browptr, bcolind)
+        mb, nb = -(-m // b1), -(-n // b2)
+        if m % b1 or n % b2:
+            raise IncompatibleExtents(f"BSR extents {m}x{n} are not multiples of {b1}x{b2}")
+        if browptr.numel() != mb + 1 or nnz(u_A) != bcolind.numel() * b1 * b2:
+            raise NonCanonicalStorage("BSR: browptr must have mb+1 entries and val nnzb*b1*b2")
+        dev = _check_same_device(browptr, bcolind, nonzeros(u_A), B, C)
+        with torch.cuda.device(dev):
+            st = L.jlust_hip_bsr_spmm_f32_i32(
+                mb, nb, b1, bcolind.numel(), u_A.origin.offset, _ptr(browptr), _ptr(bcolind),
+                _ptr(nonzeros(u_A)), int(row_major), k, float(alpha), _ptr(B), leading_dim(B),
+                float(beta), _ptr(C), leading_dim(C), _stream(dev))
+        _lib.check(st, "bsr_spmm", u_A.format, _BE, T)
+        return u_C
+    rowptr, colind = _csr_parts(u_A)
+    dev = _check_same_device(rowptr, colind, nonzeros(u_A), B, C)
+    with torch.cuda.device(dev):
+        st = getattr(L, f"jlust_hip_csr_spmm_{suf}_i32")(
+            m, n, k, nnz(u_A), u_A.origin.offset, _ptr(rowptr), _ptr(colind),
+            _ptr(nonzeros(u_A)), float(alpha), _ptr(B), leading_dim(B), float(beta), _ptr(C),
+            leading_dim(C), int(bool(skip_empty_rows)), _stream(dev))
+    _lib.check(st, "csr_spmm", u_A.format, _BE, T)
+    return u_C
+
+
+def _sddmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, mask=None):
+    suf = _value_suffix(u_C)
+    T = nonzeros(u_C).dtype
+    A, B = nonzeros(u_A), nonzeros(u_B)
+    if A.dtype != T or B.dtype != T:
+        raise UnsupportedValueType(A.dtype if A.dtype != T else B.dtype, _BE)
+    m, n = u_C.extents
+    if A.dim() != 2 or B.dim() != 2 or A.shape[0] != m or B.shape[1] != n or \
+            A.shape[1] != B.shape[0]:
+        raise IncompatibleExtents(
+            f"SDDMM: C is {m}x{n}, A is {tuple(A.shape)}, B is {tuple(B.shape)}")
+    for t, nm in ((A, "A"), (B, "B")):
+        if t.shape[0] > 1 and t.shape[1] > 0 and t.stride(0) != 1:
+            raise NonCanonicalStorage(f"SDDMM: {nm} must be column-major (stride(0) == 1)")
+    K = A.shape[1]
+    rowptr, colind = _csr_parts(u_C)
+    mk = None
+    if mask is not None:
+        mk = nonzeros(mask) if isinstance(mask, USTensor) else mask
+        if mk.dtype != T or mk.numel() != nnz(u_C) or not mk.is_contiguous():
+            raise IncompatibleExtents("SDDMM: mask must hold nnz(C) contiguous values of C's type")
+    dev = _check_same_device(rowptr, colind, nonzeros(u_C), A, B, mk)
+    with torch.cuda.device(dev):
+        st = getattr(_lib.lib(), f"jlust_hip_csr_sddmm_{suf}_i32")(
+            m, n, K, nnz(u_C), u_C.origin.offset, _ptr(rowptr), _ptr(colind), float(alpha),
+            _ptr(A), leading_dim(A), _ptr(B), leading_dim(B), float(beta), _ptr(nonzeros(u_C)),
+            _ptr(mk), _stream(dev))
+    _lib.check(st, "csr_sddmm", u_C.format, _BE, T)
+    return u_C
+
+
+# -------------------------------------------------------------------- handles
+
+class HIPSpMVHandle(AbstractKernelHandle):
+    """Prepared CSR SpMV: the merge-path partition is computed once
+    (prepare(::EmitterBackend, SpMVOp, A), ext/KernelAbstractionsExt/ops/
+    spmv.jl:518-544; the cuSPARSE handle contract, ext/CUDAExt/ops/spmv.jl:7-83)."""
+
+    def __init__(self, u_A: USTensor):
+        if not is_csr_shaped(u_A.format):
+            raise UnsupportedFormat(u_A.format, _BE, "prepared SpMV needs CSR")
+        suf = _value_suffix(u_A)
+        rowptr, colind = _csr_parts(u_A)
+        self.dev = _check_same_device(rowptr, colind, nonzeros(u_A))
+        self.u_A = u_A                      # keeps the buffers alive (GC anchor)
+        self.T = nonzeros(u_A).dtype
+        self.suf = suf
+        self._plan = ctypes.c_void_p(0)
+        m, n = u_A.extents
+        with torch.cuda.device(self.dev):
+            st = _lib.lib().jlust_hip_csr_spmv_plan_create(
+                m, n, nnz(u_A), u_A.origin.offset, 0 if suf == "f64" else 1, _ptr(rowptr),
+                _ptr(colind), _ptr(nonzeros(u_A)), _stream(self.dev), ctypes.byref(self._plan))
+        _lib.check(st, "csr_spmv_plan_create", u_A.format, _BE, self.T)
+
+    def execute(self, u_x: USTensor, u_y: USTensor, alpha=1.0, beta=0.0):
+        x, y = _vec_checks(self.u_A, u_x, u_y)
+        _check_same_device(nonzeros(self.u_A), x, y)
+        with torch.cuda.device(self.dev):
+            st = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_{self.suf}")(
+                self._plan, float(alpha), _ptr(x), float(beta), _ptr(y), _stream(self.dev))
+        _lib.check(st, "csr_spmv_plan_execute", self.u_A.format, _BE, self.T)
+        return u_y
+
+    def update_values(self, u_A: USTensor):
+        if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):
+            raise IncompatibleExtents("update_values!: the sparsity structure must not change")
+        _check_values(u_A, self.T)
+        st = _lib.lib().jlust_hip_csr_spmv_plan_update_values(self._plan, _ptr(nonzeros(u_A)))
+        _lib.check(st, "csr_spmv_plan_update_values", u_A.format, _BE, self.T)
+        self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
+                            self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+        return self
+
+    def __del__(self):
+        plan, self._plan = getattr(self, "_plan", None), None
+        if plan is not None and plan.value:
+            try:
+                _lib.lib().jlust_hip_csr_spmv_plan_destroy(plan)
+            except Exception:
+                pass
+
+
+class HIPOpHandle(AbstractKernelHandle):
+    """Prepared SpMM / SDDMM: holds A (or the mask pattern C) and dispatches to
+    the plain entry points, the contract of the cuSPARSE SpMM/SDDMM handles
+    (ext/CUDAExt/ops/spmm.jl:8-70, sddmm.jl:10-76)."""
+
+    def __init__(self, optype, u_A: USTensor, **kw):
+        self.optype, self.u_A, self.kw = optype, u_A, kw
+        _value_suffix(u_A)
+
+    def execute(self, *ts, **kw):
+        from .ops import execute as _execute
+        if self.optype.tag == "SDDMM":
+            a, b, c = ts if len(ts) == 3 else (*ts, self.u_A)
+            return _execute(self.optype, a, b, c, backend=_BE, **kw)
+        return _execute(self.optype, self.u_A, *ts, backend=_BE, **kw)
+
+    def update_values(self, u_A: USTensor):
+        if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):
+            raise IncompatibleExtents("update_values!: the sparsity structure must not change")
+        self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
+                            self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+        return self
+
+
+def prepare(optype, u_A: USTensor, **kw):
+    if optype is SpMVOp or getattr(optype, "tag", None) == "SpMV":
+        if is_csr_shaped(u_A.format):
+            return HIPSpMVHandle(u_A)
+        return HIPOpHandle(SpMVOp, u_A)
+    if optype.tag in ("SpMM", "SDDMM"):
+        return HIPOpHandle(SpMMOp if optype.tag == "SpMM" else SDDMMOp, u_A, **kw)
+    raise UnsupportedFormat(u_A.format, _BE, f"prepare: {optype} is not supported")

@@ -1,0 +1,157 @@
+"""Operator tags, backends and the generic dispatcher (src/ops.jl,
+src/backends.jl, src/convenience.jl).
+
+`execute(SpMVOp, A, x, y; alpha, beta)` builds the operator instance from the
+operand formats, resolves the backend with `default_backend` (from C for
+SDDMM, src/convenience.jl:23-27) and calls the backend's `execute`.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Tuple
+
+from .errors import UnsupportedFormat
+from .formats import TensorFormat
+from .tensor import USTensor, device_of, nonzeros, ust
+
+
+# ------------------------------------------------------------------- op tags
+
+@dataclass(frozen=True)
+class Op:
+    """Op{Tag, Formats} (src/ops.jl:24-31): the tag plus operand formats."""
+    tag: str
+    formats: Tuple[TensorFormat, ...]
+
+    def __repr__(self):
+        return f"{self.tag}Op({', '.join(map(repr, self.formats))})"
+
+
+@dataclass(frozen=True)
+class OpType:
+    """The UnionAll alias Op{:Tag}; calling it with formats makes an Op."""
+    tag: str
+
+    def __call__(self, *formats: TensorFormat) -> Op:
+        return Op(self.tag, tuple(formats))
+
+    def __repr__(self):
+        return f"{self.tag}Op"
+
+
+SpMVOp = OpType("SpMV")      # src/ops.jl:50
+SpMMOp = OpType("SpMM")      # src/ops.jl:54
+SDDMMOp = OpType("SDDMM")    # src/ops.jl:74
+
+
+# ------------------------------------------------------------------ backends
+
+class AbstractUSTBackend:
+    def __repr__(self):
+        return f"{type(self).__name__}()"
+
+    def __eq__(self, other):
+        return type(self) is type(other)
+
+    def __hash__(self):
+        return hash(type(self))
+
+
+class AbstractKernelHandle:
+    """A prepared operator (src/backends.jl:97)."""
+
+
+class HIPBackend(AbstractUSTBackend):
+    """Hand-written gfx950 kernels in libjlust_hip.so, reached through its C ABI.
+    The counterpart of EmitterBackend / CUSPARSEBackend (src/backends.jl:176-181)."""
+
+
+def supports_backend(backend, op: Op) -> bool:
+    """src/backends.jl:111; the HIP capability table is in hip_backend."""
+    if isinstance(backend, HIPBackend):
+        from . import hip_backend
+        return hip_backend.supports(op)
+    return False
+
+
+def default_backend(u: USTensor, optype: OpType):
+    """src/backends.jl:195 and the GPU policy of ext/CUDAExt/CUDAExt.jl:232-241:
+    tensors in GPU memory go to HIPBackend.  This package ships no CPU backend
+    (JLUST's CPU path is EmitterBackend on KernelAbstractions), so host-memory
+    tensors are an error rather than a silent fallback."""
+    dev = device_of(u)
+    if dev.type == "cuda":
+        return HIPBackend()
+    raise UnsupportedFormat(u.format, "HIPBackend",
+                            f"{optype} operands live in host memory ({dev}); move them with "
+                            "materialize(u, HIPDevice())")
+
+
+# ---------------------------------------------------------------- dispatcher
+
+def _wrap(a):
+    return a if isinstance(a, (USTensor, AbstractKernelHandle)) else ust(a)
+
+
+def execute(optype, *args, backend=None, **kw):
+    """execute(OpType, tensors...; backend, kw...)   (src/convenience.jl:15-39)
+    execute(handle, tensors...; kw...)             (handle-driven call)."""
+    if isinstance(optype, AbstractKernelHandle):
+        return optype.execute(*[_wrap(a) for a in args], **kw)
+    if args and isinstance(args[0], AbstractKernelHandle):
+        return args[0].execute(*[_wrap(a) for a in args[1:]], **kw)
+    if isinstance(optype, AbstractUSTBackend):          # execute(backend, op, tensors...)
+        be, op, tensors = optype, args[0], [_wrap(a) for a in args[1:]]
+        return _backend_execute(be, op, tensors, kw)
+    tensors = [_wrap(a) for a in args]
+    if not isinstance(optype, OpType):
+        raise TypeError(f"execute: expected an op type such as SpMVOp, got {optype!r}")
+    primary = tensors[2] if optype.tag == "SDDMM" else tensors[0]
+    be = backend if backend is not None else default_backend(primary, optype)
+    op = optype(*[t.format for t in tensors])
+    return _backend_execute(be, op, tensors, kw)
+
+
+def _backend_execute(be, op: Op, tensors, kw):
+    if isinstance(be, HIPBackend):
+        from . import hip_backend
+        return hip_backend.execute(op, *tensors, **kw)
+    raise UnsupportedFormat(op.formats, be, "no such backend in jlust_amd")
+
+
+def prepare(backend, optype: OpType, u_A: USTensor, **kw):
+    """prepare(backend, OpType, A; kw...) -> handle (src/ops.jl:179)."""
+    if not isinstance(backend, HIPBackend):
+        raise UnsupportedFormat(u_A.format, backend, "prepare is implemented for HIPBackend")
+    from . import hip_backend
+    return hip_backend.prepare(optype, u_A, **kw)
+
+
+def update_values_(handle, u_A: USTensor):
+    """update_values!(handle, A) (src/ops.jl:188): new values, same pattern."""
+    return handle.update_values(u_A)
+
+
+def mul_(Y, A: USTensor, X, alpha=None, beta=None):
+    """LinearAlgebra.mul!(y, A, x[, alpha, beta]) and mul!(C, A, B[, alpha, beta])
+    (src/convenience.jl:46-53): returns Y."""
+    kw = {}
+    if alpha is not None or beta is not None:
+        kw = dict(alpha=1 if alpha is None else alpha, beta=0 if beta is None else beta)
+    xt = X.val if isinstance(X, USTensor) else X
+    optype = SpMVOp if xt.dim() == 1 else SpMMOp
+    execute(optype, A, ust(X), ust(Y), **kw)
+    return Y
+
+
+def matmul(A: USTensor, x):
+    """Base.:*(A, x) (src/convenience.jl:55-59): a new y of A's value type."""
+    import torch
+    xt = x.val if isinstance(x, USTensor) else x
+    if xt.dim() == 1:
+        y = torch.empty(A.extents[0], dtype=nonzeros(A).dtype, device=nonzeros(A).device)
+    else:
+        from .tensor import dense_matrix
+        y = dense_matrix(A.extents[0], xt.shape[1], dtype=nonzeros(A).dtype,
+                         device=nonzeros(A).device)
+    return mul_(y, A, x)

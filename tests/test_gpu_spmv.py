@@ -1,0 +1,207 @@
+"""GPU parity of CSR SpMV (and its prepared plan) against the CPU oracle.
+
+Bar: |y - y_ref| <= 1e-12 (fp64) / 1e-5 (fp32) x (|alpha||A||x| + |beta||y0|)
+elementwise, y_ref from oracle/ (C restatement of JLUST's CPU walker).
+"""
+import json
+import os
+import zlib
+
+import numpy as np
+import pytest
+
+from tests._util import assert_within, dev, host, random_csr, sample_rows
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.load(open(os.path.join(os.path.dirname(__file__), "golden",
+                                     "reference_fixtures.json")))
+
+
+@pytest.fixture(scope="module")
+def J():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import jlust_amd
+    return jlust_amd
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+def run_spmv(J, rowptr, colind, val, x, m, n, origin=1, alpha=1.0, beta=0.0, y0=None):
+    import torch
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n),
+                     origin=J.OneBased() if origin == 1 else J.ZeroBased())
+    y = dev(y0) if y0 is not None else torch.full((m,), float("nan"), dtype=A.dtype,
+                                                   device="cuda")
+    J.execute(J.SpMVOp, A, dev(x), y, alpha=alpha, beta=beta)
+    return host(y)
+
+
+@pytest.mark.parametrize("case", [c for c in GOLDEN["spmv"] if c["format"] == "CSR"],
+                         ids=lambda c: c["name"])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_reference_fixture(J, case, dtype):
+    y = run_spmv(J, np.array(case["rowptr"], np.int32), np.array(case["colind"], np.int32),
+                 np.array(case["val"], dtype), np.array(case["x"], dtype), case["m"], case["n"],
+                 origin=case["origin"])
+    np.testing.assert_array_equal(y, np.array(case["y"], dtype))
+
+
+def test_mul_bang_and_star(J):
+    c = GOLDEN["spmv"][0]
+    A = J.csr_tensor(dev(np.array(c["rowptr"], np.int32)), dev(np.array(c["colind"], np.int32)),
+                     dev(np.array(c["val"])), (3, 3))
+    x = dev(np.array(c["x"]))
+    y = J.matmul(A, x)
+    np.testing.assert_array_equal(host(y), c["y"])
+    y2 = dev(np.ones(3))
+    J.mul_(y2, A, x, 2.0, 3.0)
+    np.testing.assert_array_equal(host(y2), 2 * np.array(c["y"]) + 3.0)
+
+
+SHAPES = [
+    ("tiny", dict(m=5, n=7, density=0.5)),
+    ("empty_rows", dict(m=3000, n=500, density=0.002)),
+    ("one_row_long", dict(m=1, n=300_000, lengths=[250_000])),
+    ("long_rows_mix", dict(m=4000, n=100_000, lengths=np.r_[np.full(3990, 3), np.full(10, 20_000)])),
+    ("all_empty", dict(m=10_000, n=10, lengths=np.zeros(10_000, np.int64))),
+    ("dense_rows", dict(m=300, n=300, density=0.9)),
+    ("uniform_medium", dict(m=50_000, n=50_000, lengths=np.full(50_000, 16))),
+]
+
+
+@pytest.mark.parametrize("name,kw", SHAPES, ids=[s[0] for s in SHAPES])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("origin", [1, 0])
+def test_random_shapes(J, O, name, kw, dtype, origin):
+    m, n = kw["m"], kw["n"]
+    rowptr, colind, val = random_csr(m, n, density=kw.get("density"), lengths=kw.get("lengths"),
+                                     seed=zlib.crc32(name.encode()) % 1000, origin=origin, dtype=dtype)
+    x = np.random.default_rng(1).uniform(-1, 1, n).astype(dtype)
+    y = run_spmv(J, rowptr, colind, val, x, m, n, origin=origin)
+    ref = O.csr_spmv(rowptr, colind, val, x, origin=origin)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x, origin=origin)
+    assert_within(y, ref, absref, dtype, name)
+
+
+@pytest.mark.parametrize("alpha,beta", [(2.5, 0.0), (1.0, 1.0), (-0.5, 2.0), (0.0, 3.0)])
+def test_alpha_beta(J, O, alpha, beta):
+    m, n = 20_000, 20_000
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(3).integers(0, 40, m),
+                                     seed=5)
+    x = np.random.default_rng(4).uniform(-1, 1, n)
+    y0 = np.random.default_rng(5).uniform(-1, 1, m)
+    y = run_spmv(J, rowptr, colind, val, x, m, n, alpha=alpha, beta=beta, y0=y0)
+    ref = O.csr_spmv(rowptr, colind, val, x, alpha=alpha, beta=beta, y0=y0)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x, alpha=alpha, beta=beta, y0=y0)
+    assert_within(y, ref, absref, np.float64, f"alpha={alpha} beta={beta}")
+
+
+def test_beta_zero_is_write_only(J):
+    """beta == 0 never reads y: NaN in y does not leak (spmv.jl:167-168)."""
+    c = GOLDEN["spmv"][0]
+    y = run_spmv(J, np.array(c["rowptr"], np.int32), np.array(c["colind"], np.int32),
+                 np.array(c["val"]), np.array(c["x"]), 3, 3,
+                 y0=np.full(3, np.nan), beta=0.0)
+    np.testing.assert_array_equal(y, c["y"])
+
+
+def test_deterministic(J):
+    import torch
+    from jlust_amd import workloads as W
+    cfg = W.make(2, scale=8)
+    A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (cfg["m"], cfg["n"]))
+    x = dev(cfg["x"])
+    y1 = torch.empty(cfg["m"], dtype=torch.float64, device="cuda")
+    y2 = torch.empty_like(y1)
+    J.execute(J.SpMVOp, A, x, y1)
+    J.execute(J.SpMVOp, A, x, y2)
+    assert torch.equal(y1, y2)
+
+
+@pytest.mark.parametrize("config", [1, 2])
+def test_benchmark_config_full(J, O, config):
+    """Full BASELINE configs 1 and 2 against the oracle, every row."""
+    from jlust_amd import workloads as W
+    cfg = W.make(config)
+    y = run_spmv(J, cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"], cfg["m"], cfg["n"])
+    ref = O.csr_spmv(cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"])
+    absref = O.csr_spmv_absref(cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"])
+    assert_within(y, ref, absref, np.float64, cfg["name"])
+
+
+def test_plan_execute_and_update_values(J, O):
+    import torch
+    from jlust_amd import workloads as W
+    cfg = W.make(2, scale=16)
+    m, n = cfg["m"], cfg["n"]
+    A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (m, n))
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    x = dev(cfg["x"])
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    J.execute(J.SpMVOp, h, x, y)
+    ref = O.csr_spmv(cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"])
+    absref = O.csr_spmv_absref(cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"])
+    assert_within(host(y), ref, absref, np.float64, "plan")
+    # update_values!: same pattern, new values; plan keeps its partition.
+    val2 = -2.0 * cfg["val"]
+    A2 = J.csr_tensor(A.pos_buffers[1], A.crd_buffers[1], dev(val2), (m, n))
+    J.update_values_(h, A2)
+    J.execute(h, x, y, alpha=1.0, beta=0.0)
+    ref2 = O.csr_spmv(cfg["rowptr"], cfg["colind"], val2, cfg["x"])
+    absref2 = O.csr_spmv_absref(cfg["rowptr"], cfg["colind"], val2, cfg["x"])
+    assert_within(host(y), ref2, absref2, np.float64, "plan after update_values!")
+
+
+def test_power_law_sampled_rows_f32(J, O):
+    """fp32 on the power-law pattern (scaled config 2)."""
+    from jlust_amd import workloads as W
+    cfg = W.make(2, scale=4)
+    val = cfg["val"].astype(np.float32)
+    x = cfg["x"].astype(np.float32)
+    y = run_spmv(J, cfg["rowptr"], cfg["colind"], val, x, cfg["m"], cfg["n"])
+    rows = np.random.default_rng(0).choice(cfg["m"], 20_000, replace=False)
+    rp, ci, v, _ = sample_rows(cfg["rowptr"], cfg["colind"], val, rows)
+    ref = O.csr_spmv(rp, ci, v, x)
+    absref = O.csr_spmv_absref(rp, ci, v, x)
+    assert_within(y[rows], ref, absref, np.float32, "powerlaw f32")
+
+
+def test_errors(J):
+    import torch
+    c = GOLDEN["spmv"][0]
+    A = J.csr_tensor(dev(np.array(c["rowptr"], np.int32)), dev(np.array(c["colind"], np.int32)),
+                     dev(np.array(c["val"])), (3, 3))
+    with pytest.raises(J.IncompatibleExtents):
+        J.execute(J.SpMVOp, A, dev(np.ones(4)), dev(np.zeros(3)))
+    with pytest.raises(J.UnsupportedValueType):
+        J.execute(J.SpMVOp, A, dev(np.ones(3, np.float32)), dev(np.zeros(3, np.float32)))
+    with pytest.raises(J.UnsupportedFormat):
+        J.execute(J.SpMVOp, A, dev(np.ones(3)), dev(np.zeros(3)), input_fn=lambda v: 2 * v)
+    A64 = J.csr_tensor(dev(np.array(c["rowptr"], np.int64)), dev(np.array(c["colind"], np.int64)),
+                       dev(np.array(c["val"])), (3, 3))
+    with pytest.raises(J.UnsupportedIndexType):
+        J.execute(J.SpMVOp, A64, dev(np.ones(3)), dev(np.zeros(3)))
+    Ah = J.csr_tensor(torch.tensor(c["rowptr"], dtype=torch.int32),
+                      torch.tensor(c["colind"], dtype=torch.int32), torch.tensor(c["val"]), (3, 3))
+    with pytest.raises(J.UnsupportedFormat):
+        J.execute(J.SpMVOp, Ah, torch.ones(3, dtype=torch.float64),
+                  torch.zeros(3, dtype=torch.float64))
+    # C ABI argument checks (status codes -> exceptions)
+    L = J._lib.lib()
+    st = L.jlust_hip_csr_spmv_f64_i32(-1, 3, 5, 1, None, None, None, 1.0, None, 0.0, None, None)
+    assert st == 1 and "negative" in J._lib.last_error()
+    st = L.jlust_hip_csr_spmv_f64_i32(3, 3, 5, 2, None, None, None, 1.0, None, 0.0, None, None)
+    assert st == 5
+
+
+def test_device_arch(J):
+    import ctypes
+    buf = ctypes.create_string_buffer(64)
+    assert J._lib.lib().jlust_hip_device_arch(buf, 64) == 0
+    assert buf.value.decode().startswith("gfx950")
