@@ -4,8 +4,12 @@
     python bench.py [--config 2] [--steps K] [--warmup W] [--gpus 1]
 
 A step is one call of the operator over the configuration's synthetic input,
-already resident in HBM (one C ABI call; for SpMV that is the merge-path
-kernel plus its carry fix-up, for SpMM the B re-layout plus the product).
+already resident in HBM (one C ABI call).  SpMV runs, as JLUST's
+prepare/execute handles do, through a plan prepared once outside the timed
+region (for x wider than one XCD's L2 the column-sliced merge kernel, its
+carry fix-up and the slice reduction); the plain per-call entry point (merge
+kernel plus carry fix-up, nothing cached) is timed in the same run and
+reported as `plain_call`.  SpMM's step includes the B re-layout.
 Prints ONE JSON line: the metric of BASELINE.json (effective GB/s from the
 reference's compulsory-byte formula, benchmark/bench_suitesparse.jl:170-172,
 plus GFLOP/s), a `roofline` object for the step's dominant kernel and a
@@ -42,8 +46,9 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU work budget of the cpu_baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--plan", action="store_true",
-                   help="SpMV through a prepared plan (partition computed once, outside the loop)")
+    p.add_argument("--no-plan", action="store_true",
+                   help="SpMV: time only the plain per-call entry point (default: a prepared plan, "
+                        "as JLUST's prepare/execute handle API, with the plain call timed beside it)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="only run a 1 GiB device copy (PMC byte-counter calibration)")
     p.add_argument("--gather-ceiling", action="store_true",
@@ -198,6 +203,29 @@ def cpu_baseline(cfg, budget_s):
             round(W.flops(cfg) / tmin / 1e9, 3)}
 
 
+def timed(step, steps, warmup):
+    """W untimed steps, then exactly K steps bracketed by synchronize();
+    returns (wall ms per step, per-step event durations in ms)."""
+    import torch
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    if torch.distributed.is_available() and torch.distributed.is_initialized():
+        torch.distributed.barrier()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    for s, e in ev:
+        s.record(stream)
+        step()
+        e.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    return wall * 1e3 / steps, np.array([s.elapsed_time(e) for s, e in ev])
+
+
 def traffic_for(workload):
     path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     try:
@@ -234,26 +262,19 @@ def main():
     t0 = time.perf_counter()
     cfg = W.make(args.config)
     log(f"generated {cfg['name']} in {time.perf_counter() - t0:.1f}s")
-    step, kname, bound, keep = build_step(cfg, use_plan=args.plan)
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-
-    stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
-    if torch.distributed.is_available() and torch.distributed.is_initialized():
-        torch.distributed.barrier()
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    for s, e in ev:
-        s.record(stream)
-        step()
-        e.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    per_launch_ms = np.array([s.elapsed_time(e) for s, e in ev])
-    ms_per_step = wall * 1e3 / steps
+    use_plan = cfg["kind"] == "csr_spmv" and not args.no_plan
+    step, kname, bound, keep = build_step(cfg, use_plan=use_plan)
+    ms_per_step, per_launch_ms = timed(step, steps, warmup)
+    plain = None
+    if use_plan:
+        pstep, pkname, _, pkeep = build_step(cfg, use_plan=False)
+        p_ms, p_launch = timed(pstep, steps, warmup)
+        plain = {"value": round(W.algorithmic_bytes(cfg) / (p_ms * 1e-3) / 1e9, 3),
+                 "ms_per_step": round(p_ms, 6), "kernel": pkname,
+                 "per_launch_ms": round(float(p_launch.mean()), 6)}
+        del pkeep
+        kname = "csr_spmv_sliced_kernel" if cfg["n"] * np.dtype(cfg["dtype"]).itemsize > (4 << 20) \
+            else kname
     log(f"{steps} steps: wall {ms_per_step:.4f} ms/step, event mean "
         f"{per_launch_ms.mean():.4f} ms, min {per_launch_ms.min():.4f} ms")
 
@@ -269,7 +290,7 @@ def main():
         achieved = nflops / (k_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 5)}
-    roof["traffic"] = traffic_for(cfg["name"])
+    roof["traffic"] = traffic_for(cfg["name"] + (":plan" if use_plan else ""))
     roof["kernel"] = kname
     roof["per_launch_ms"] = round(k_ms, 6)
     roof["per_launch_ms_min"] = round(float(per_launch_ms.min()), 6)
@@ -289,11 +310,11 @@ def main():
         "data": "synthetic (seeded generator, jlust_amd/csrc/workloads.c)",
         "config": {"workload": cfg["name"], "baseline_config": cfg["config"], "m": cfg["m"],
                    "n": cfg["n"], nnz_key: nnz_val, "seed": cfg["seed"],
-                   "index": "Int32, 1-based", "plan": bool(args.plan)},
+                   "index": "Int32, 1-based", "plan": bool(use_plan)},
         "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 3),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 3),
         "algorithmic_bytes": int(nbytes), "flops": int(nflops),
-        "roofline": roof, "cpu_baseline": cpu,
+        "roofline": roof, "plain_call": plain, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     del keep

@@ -22,7 +22,7 @@ BUILD = os.path.join(HERE, "_build")
 HIP_LIB = os.path.join(HERE, "libjlust_hip.so")
 WL_LIB = os.path.join(HERE, "libjlust_workloads.so")
 
-HIP_SOURCES = ["capi.hip", "spmv.hip", "coo_spmv.hip", "spmm.hip", "sddmm.hip",
+HIP_SOURCES = ["capi.hip", "scan.hip", "spmv.hip", "coo_spmv.hip", "spmm.hip", "sddmm.hip",
                "bsr_spmm.hip"]
 
 ARCH = os.environ.get("JLUST_HIP_ARCH", "gfx950")

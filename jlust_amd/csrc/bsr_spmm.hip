@@ -9,8 +9,8 @@
 // implements the definition C[16R+r, c] = alpha*sum_q sum_s V_q[r][s] *
 // B[16*bcol_q + s, c] + beta*C.
 //
-// One wave owns one block-row and all k columns of C for it (V is read
-// once).  A 16 x 16 block times a 16 x 16 slab of B is four MFMA 16x16x4
+// One workgroup owns one block-row; its 4 waves split each 256-column pass
+// into 4 x 64 columns (V is read from HBM once, the other waves hit L1).  A 16 x 16 block times a 16 x 16 slab of B is four MFMA 16x16x4
 // steps.  The contraction index is split as s = 4*g + step (g = lane / 16),
 // so every lane needs 4 consecutive s of its row (A) and of its column (B):
 //   A operand: lane (i = lane % 16, g) holds V_q[i][4g .. 4g+3]  (one float4
@@ -30,9 +30,9 @@ namespace {
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int BSR_BS = 16;
-constexpr int BSR_WAVES = 4;                 // block-rows per workgroup
-constexpr int BSR_TILES = 16;                // 16-column tiles per pass (256 columns)
-constexpr int NUM_XCD = 8;
+constexpr int BSR_WAVES = 4;                 // waves per workgroup (one block-row)
+constexpr int BSR_WTILES = 4;                // 16-column tiles per wave per pass
+constexpr int BSR_PASS = 16 * BSR_WTILES * BSR_WAVES;   // 256 columns per pass
 
 // VEC: B, C 16-byte aligned with ld % 4 == 0 (float4 access).
 template <bool ROW_MAJOR, bool VEC>
@@ -40,26 +40,28 @@ __global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_mfma_kernel(
     int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
     const int32_t *__restrict__ bcolind, const float *__restrict__ val, int64_t k, float alpha,
     const float *__restrict__ B, int64_t ldb, float beta, int beta_zero, float *__restrict__ C,
-    int64_t ldc, int64_t ngroups)
+    int64_t ldc)
 {
-    // XCD-major remap of the workgroup index (grid padded to a multiple of 8).
+    // XCD-major remap of the workgroup index (grid padded to a multiple of 8):
+    // XCD x takes block-rows [x*per_xcd, (x+1)*per_xcd).
     const int64_t per_xcd = (int64_t)gridDim.x / NUM_XCD;
-    const int64_t grp = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
-    if (grp >= ngroups) return;
-    const int64_t R = grp * BSR_WAVES + (threadIdx.x >> 6);
+    const int64_t R = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
     if (R >= mb) return;
 
     const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
     const int i = lane & 15;       // block row (A operand) / column in tile (B, C)
     const int g = lane >> 4;       // group of 4 in the contraction / C row group
     const int64_t q0 = (int64_t)browptr[R] - origin;
     const int64_t q1 = (int64_t)browptr[R + 1] - origin;
     const int64_t crow = R * BSR_BS + 4 * g;
 
-    for (int64_t c0 = 0; c0 < k; c0 += 16 * BSR_TILES) {
-        floatx4 acc[BSR_TILES];
+    for (int64_t pass = 0; pass < k; pass += BSR_PASS) {
+        const int64_t c0 = pass + (int64_t)wave * 16 * BSR_WTILES;   // this wave's first column
+        if (c0 >= k) continue;
+        floatx4 acc[BSR_WTILES];
 #pragma unroll
-        for (int t = 0; t < BSR_TILES; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+        for (int t = 0; t < BSR_WTILES; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
 
         for (int64_t q = q0; q < q1; ++q) {
             const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
@@ -71,9 +73,9 @@ __global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_mfma_kernel(
 #pragma unroll
                 for (int u = 0; u < 4; ++u) a[u] = vb[(4 * g + u) * BSR_BS + i];
             }
-            floatx4 b[BSR_TILES];
+            floatx4 b[BSR_WTILES];
 #pragma unroll
-            for (int t = 0; t < BSR_TILES; ++t) {
+            for (int t = 0; t < BSR_WTILES; ++t) {
                 const int64_t col = c0 + 16 * t + i;
                 if (col < k) {
                     const float *src = B + brow + col * ldb;
@@ -88,15 +90,13 @@ __global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_mfma_kernel(
                 }
             }
 #pragma unroll
-            for (int t = 0; t < BSR_TILES; ++t) {
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[0], b[t][0], acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[1], b[t][1], acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[2], b[t][2], acc[t], 0, 0, 0);
-                acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[3], b[t][3], acc[t], 0, 0, 0);
-            }
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int t = 0; t < BSR_WTILES; ++t)
+                    acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[t][u], acc[t], 0, 0, 0);
         }
 #pragma unroll
-        for (int t = 0; t < BSR_TILES; ++t) {
+        for (int t = 0; t < BSR_WTILES; ++t) {
             const int64_t col = c0 + 16 * t + i;
             if (col >= k) continue;
             float *dst = C + crow + col * ldc;
@@ -148,14 +148,12 @@ int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
     const bool vec = (ldb % 4 == 0) && (ldc % 4 == 0) && ((uintptr_t)B % 16 == 0) &&
                      ((uintptr_t)C % 16 == 0);
     const bool vals_aligned = ((uintptr_t)val % 16 == 0);
-    const int64_t ngroups = (mb + BSR_WAVES - 1) / BSR_WAVES;
-    const int64_t grid = (ngroups + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+    const int64_t grid = (mb + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
     hipStream_t s = (hipStream_t)stream;
     const int bz = beta == 0.f;
 #define JLUST_BSR_LAUNCH(RM, V)                                                                   \
     hipLaunchKernelGGL((bsr16_spmm_mfma_kernel<RM, V>), dim3((unsigned)grid), dim3(64 * BSR_WAVES), \
-                       0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, bz, C, ldc, \
-                       ngroups)
+                       0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, bz, C, ldc)
     const bool rm = row_major_blocks && vals_aligned;
     if (row_major_blocks && !vals_aligned)
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: block values must be 16-byte aligned");

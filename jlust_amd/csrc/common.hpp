@@ -57,6 +57,12 @@ const DeviceInfo &device_info(int device);
 // released after the stream drains) and lives until process exit.
 int scratch(jlust_stream_t stream, size_t bytes, void **out);
 
+// out[i] = sum(in[0..i)) over n int32 counts (in == out allowed); stream-ordered.
+// Uses the stream's scratch buffer for chunk sums.
+int exclusive_scan_i32(const int32_t *in, int32_t *out, int64_t n, jlust_stream_t stream);
+
+constexpr int NUM_XCD = 8;   // MI355X: workgroup b runs on XCD b % 8
+
 // ------------------------------------------------------------ device code
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

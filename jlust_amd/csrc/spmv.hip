@@ -5,13 +5,12 @@
 // `acc = 0; for k in row: acc += val[k]*x[col[k]]; y = alpha*acc (+beta*y)`
 // (spmv.jl:154-169, _walker.jl:123-132).
 //
-// Work split: the merge path of (m row ends, nnz nonzeros) is cut into tiles
-// of TILE = BLOCK*IPT items, so every tile costs the same whatever the row
-// lengths (a 10^5-nonzero row spans ~50 tiles; 10^4 empty rows share one).
-// Each block owns `tiles_per_block` consecutive tiles and finds only its first
-// coordinate in global memory (a 64-ary wave-parallel search of rowptr); the
-// next tile starts where the previous one ended, found from the row ends the
-// tile already staged in LDS.  Per tile:
+// Work split (merge_range): the merge path of (m row ends, nnz nonzeros) is
+// cut into tiles of TILE = BLOCK*IPT items, so every tile costs the same
+// whatever the row lengths (a 10^5-nonzero row spans ~50 tiles; 10^4 empty
+// rows share one).  Each block owns consecutive tiles and finds only its
+// first coordinate in global memory (a 64-ary wave-parallel search of
+// rowptr); the next tile starts where the previous one ended.  Per tile:
 //   1. the row ends of rows i0..i0+TILE are staged in LDS (coalesced);
 //   2. every thread locates its IPT-item slice of the tile by binary search in
 //      LDS, and the tile end by the same search;
@@ -24,20 +23,44 @@
 // A row still open at the end of a block leaves (row, partial) in a carry
 // slot; a small second kernel adds each run of equal-row carries into y in
 // block order, so the result is deterministic run to run.
+//
+// Column-sliced plans.  A random gather of x costs a whole 128-byte line from
+// the memory side whenever x does not fit the 4 MB L2 of an XCD (8 XCDs,
+// workgroup b runs on XCD b % 8).  A prepared plan whose x exceeds that
+// re-lays A out as 8 column slices (slice s = columns [s*w, (s+1)*w)): each
+// slice is a CSR matrix over all m rows with local column indices.  The
+// sliced kernel runs slice s on the workgroups with b % 8 == s, so XCD s only
+// gathers from x[s*w : (s+1)*w] and keeps it in its own L2.  Slice s writes a
+// partial y_s; a last pass forms y = alpha*(y_0 + ... + y_7) + beta*y in that
+// fixed order.
+#include <cstdlib>
+#include <cstring>
+
 #include "common.hpp"
 
 namespace jlust {
 namespace {
 
 constexpr int SPMV_BLOCK = 256;
-template <typename T> struct SpmvIpt;
-template <> struct SpmvIpt<double> { static constexpr int value = 8; };
-template <> struct SpmvIpt<float> { static constexpr int value = 8; };
+constexpr size_t SLICE_MIN_X_BYTES = (size_t)4 << 20;   // one XCD's L2
 
-// Smallest i in [max(0, d-nnz), min(d, m)] with (rowptr[i+1]-origin) + i >= d,
+// buf holds the tile's products at [0, nloc) and its finished row sums at
+// [nloc, nloc + rend); nloc + rend is the tile length, so one array suffices.
+// rowend uses [0, tile length]; it has room for every thread's IPT+1 stores.
+template <typename T, int TILE, int NW>
+struct SpmvSmem {
+    T buf[TILE];
+    int32_t rowend[TILE + 64 * NW];
+    int64_t i0;
+    int32_t wkey[NW];
+    T wval[NW];
+    T bs[NW];
+};
+
+// Smallest i in [max(0, d-nnz), min(d, m)] with (rowptr[i+1]-ptr_origin) + i >= d,
 // taking i == m as true: the number of rows finished after the first d items
 // of the merge path.  Called by a whole wave; every lane returns the answer.
-__device__ int64_t wave_merge_search(const int32_t *__restrict__ rowptr, int32_t origin,
+__device__ int64_t wave_merge_search(const int32_t *__restrict__ rowptr, int64_t ptr_origin,
                                      int64_t m, int64_t nnz, int64_t d)
 {
     const int lane = __lane_id();
@@ -46,7 +69,7 @@ __device__ int64_t wave_merge_search(const int32_t *__restrict__ rowptr, int32_t
     while (lo < hi) {
         const int64_t n = hi - lo;
         const int64_t p = lo + (n * lane) / 64;
-        const bool pred = (p >= m) || ((int64_t)rowptr[p + 1] - origin + p >= d);
+        const bool pred = (p >= m) || ((int64_t)rowptr[p + 1] - ptr_origin + p >= d);
         const uint64_t mask = __ballot(pred);
         if (mask & 1ull) return lo;
         const int f = mask ? __builtin_ctzll(mask) : 64;
@@ -57,50 +80,88 @@ __device__ int64_t wave_merge_search(const int32_t *__restrict__ rowptr, int32_t
     return lo;
 }
 
-template <typename T, int BLOCK, int IPT>
-__global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
-    int64_t m, int64_t nnz, int32_t origin, const int32_t *__restrict__ rowptr,
-    const int32_t *__restrict__ colind, const T *__restrict__ val, const T *__restrict__ x,
-    T *__restrict__ y, T alpha, T beta, int beta_zero, int64_t tiles_per_block,
-    const int64_t *__restrict__ start_rows, int64_t *__restrict__ carry_row,
-    T *__restrict__ carry_val)
+// One block's share [dbeg, dend) of the merge path of a CSR matrix whose row
+// pointers hold ptr_origin + (0-based position in colind/val) and whose column
+// indices hold col_origin + (0-based column of x).  start_row < 0: search.
+// Requires m >= 1 and a nonempty nonzero array: colind/val + jmax is the last
+// readable element (jmax < 0 when this range's own nonzeros are empty; the
+// clamped prefetch then reads an element before them), and x[x_safe] is a
+// readable element of x (used with PF only).
+// PF: prefetch the next tile's row ends and col/val into registers while the
+// current tile is processed (pays off when x gathers hit L2; when they go to
+// memory the speculative loads only add traffic).  NT: stream rowptr/col/val
+// with nontemporal loads so they do not evict x from L2.
+template <typename T, int BLOCK, int IPT, bool PF, bool NT>
+__device__ void merge_range(int64_t m, int64_t nnz, int64_t jmax, int64_t x_safe,
+                            int64_t ptr_origin, int32_t col_origin,
+                            const int32_t *__restrict__ rowptr, const int32_t *__restrict__ colind,
+                            const T *__restrict__ val, const T *__restrict__ x, T *__restrict__ y,
+                            T alpha, T beta, int beta_zero, int64_t dbeg, int64_t dend,
+                            int64_t start_row, int64_t *carry_row, T *carry_val,
+                            SpmvSmem<T, BLOCK * IPT, BLOCK / 64> &sm)
 {
     constexpr int TILE = BLOCK * IPT;
     constexpr int NW = BLOCK / 64;
-    __shared__ T s_prod[TILE];
-    __shared__ T s_ysum[TILE];
-    __shared__ int32_t s_rowend[TILE + 1];
-    __shared__ int64_t s_i0;
-    __shared__ int32_t s_wkey[NW];
-    __shared__ T s_wval[NW];
-    __shared__ T s_bs[NW];
-
+    constexpr int RPT = TILE / BLOCK + 1;      // row ends per thread (TILE + 1 per tile)
+    static_assert(RPT * BLOCK <= TILE + 64 * NW, "rowend too small for the row-end stores");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int64_t total = m + nnz;
-    const int64_t dbeg = (int64_t)blockIdx.x * tiles_per_block * TILE;
-    if (dbeg >= total) return;
-    const int64_t dend = min(total, dbeg + tiles_per_block * (int64_t)TILE);
 
-    if (start_rows) {
-        if (tid == 0) s_i0 = start_rows[blockIdx.x];
+    if (start_row >= 0) {
+        if (tid == 0) sm.i0 = start_row;
     } else if (wave == 0) {
-        const int64_t r = wave_merge_search(rowptr, origin, m, nnz, dbeg);
-        if (lane == 0) s_i0 = r;
+        const int64_t r = wave_merge_search(rowptr, ptr_origin, m, nnz, dbeg);
+        if (lane == 0) sm.i0 = r;
     }
     __syncthreads();
-    int64_t i0 = s_i0;
+    int64_t i0 = sm.i0;
     int64_t j0 = dbeg - i0;
     T carry = T(0);
     bool carry_has = false;
 
+    // Loads are issued straight-line (clamped, always in-bounds addresses, no
+    // per-lane branches): a load under an exec-masked branch makes the
+    // compiler wait for every outstanding load before the next one, which
+    // would serialise the gathers.  Row ends are kept raw; validity and the
+    // origin are applied when they are written to LDS.
+    int32_t ren[RPT];
+    int32_t cn[IPT];
+    T vn[IPT];
+    auto load_rowends = [&](int64_t is) {
+#pragma unroll
+        for (int u = 0; u < RPT; ++u) {
+            const int64_t row = min(is + tid + u * BLOCK, m - 1);
+            ren[u] = NT ? __builtin_nontemporal_load(rowptr + row + 1) : rowptr[row + 1];
+        }
+    };
+    // col/val of nonzeros js + q (q = tid + u*BLOCK), clamped to [js, jmax].
+    auto load_nz = [&](int64_t js, int64_t jmax) {
+#pragma unroll
+        for (int u = 0; u < IPT; ++u) {
+            const int64_t k = min(js + tid + u * BLOCK, jmax);
+            cn[u] = NT ? __builtin_nontemporal_load(colind + k) : colind[k];
+            vn[u] = NT ? __builtin_nontemporal_load(val + k) : val[k];
+        }
+    };
+    // Register prefetch (PF): tile t+1's row ends and col/val are issued while
+    // tile t is processed, so the loads are in flight across its barriers.
+    if (PF) {
+        load_rowends(i0);
+        load_nz(j0, jmax);
+    }
+
     for (int64_t d = dbeg; d < dend; d += TILE) {
         const int tlen = (int)min((int64_t)TILE, dend - d);
         // (1) row ends (0-based nonzero index) of rows i0 .. i0+tlen.
-        for (int r = tid; r <= tlen; r += BLOCK) {
-            const int64_t row = i0 + r;
-            s_rowend[r] = row < m ? rowptr[row + 1] - origin : INT32_MAX;
+        if (!PF) load_rowends(i0);
+        // Stored unconditionally (entries past tlen are never read): a
+        // conditional store would let the compiler sink each load under its
+        // branch and serialise them.
+#pragma unroll
+        for (int u = 0; u < RPT; ++u) {
+            const int r = tid + u * BLOCK;
+            sm.rowend[r] = i0 + r < m ? (int32_t)((int64_t)ren[u] - ptr_origin) : INT32_MAX;
         }
         __syncthreads();
 
@@ -109,7 +170,7 @@ __global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
             int lo = 0, hi = dl;
             while (lo < hi) {
                 const int mid = (lo + hi) >> 1;
-                if ((int64_t)s_rowend[mid] - j0 + mid >= dl) hi = mid;
+                if ((int64_t)sm.rowend[mid] - j0 + mid >= dl) hi = mid;
                 else lo = mid + 1;
             }
             return lo;
@@ -121,50 +182,63 @@ __global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
         int jl = dl - r;
         const int r_first = r;
         const int64_t j1 = d + tlen - (i0 + rend);
-        // j1 <= nnz whenever rowptr[m] - origin == nnz; the clamp keeps a
+        // j1 <= nnz whenever the row pointers end at nnz; the clamp keeps a
         // malformed rowptr from reading past the nonzero arrays.
         const int nloc = (int)(min(j1, nnz) - j0);
 
-        // (3) products of the tile's nonzeros into LDS.
-        {
-            int32_t c[IPT];
-            T v[IPT];
-            T xv[IPT];
+        // (3) products of the tile's nonzeros into LDS: gather x (lanes past
+        // the tile's nonzeros gather x[0]), then start the next tile's prefetch.
+        // With PF every lane gathers (x[x_safe] past the tile's nonzeros), so
+        // no branch separates the gathers from the prefetch below.
+        const bool has_nz = PF || __builtin_amdgcn_readfirstlane(nloc) > 0;
+        T xv[IPT];
+        T vcur[IPT];
+        if (has_nz) {
+            if (!PF) load_nz(j0, j0 + nloc - 1);
 #pragma unroll
             for (int u = 0; u < IPT; ++u) {
                 const int q = tid + u * BLOCK;
-                if (q < nloc) {
-                    c[u] = colind[j0 + q];
-                    v[u] = val[j0 + q];
-                }
+                xv[u] = x[q < nloc ? (int64_t)(cn[u] - col_origin) : (PF ? x_safe : 0)];
+                vcur[u] = vn[u];
             }
+        }
+        if (PF) {
+            // Issued after the gathers, so waiting for the gathers leaves the
+            // prefetch in flight (loads return in order).  The block's last
+            // tile re-reads itself (L2-resident) rather than branching: a
+            // conditional prefetch makes the compiler's wait before the LDS
+            // stores below cover the prefetch too.
+            const bool more = d + TILE < dend;
+            load_rowends(more ? i0 + rend : i0);
+            load_nz(more ? j1 : j0, jmax);
+            // Keep the products (which wait for the gathers) below the
+            // prefetch issue.
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        // Stored unconditionally: entries past nloc are scratch until the row
+        // sums of step (4) overwrite them (a conditional store would let the
+        // compiler sink its gather under the branch and wait on the prefetch).
+        if (has_nz) {
 #pragma unroll
-            for (int u = 0; u < IPT; ++u) {
-                const int q = tid + u * BLOCK;
-                if (q < nloc) xv[u] = x[c[u] - origin];
-            }
-#pragma unroll
-            for (int u = 0; u < IPT; ++u) {
-                const int q = tid + u * BLOCK;
-                if (q < nloc) s_prod[q] = v[u] * xv[u];
-            }
+            for (int u = 0; u < IPT; ++u) sm.buf[tid + u * BLOCK] = vcur[u] * xv[u];
         }
         __syncthreads();
 
         // (4) sequential walk of this thread's slice of the merge path.
+        T *ysum = sm.buf + nloc;
         T acc = T(0);
         for (int s = dl; s < dl_next; ++s) {
-            if ((int64_t)jl < (int64_t)s_rowend[r] - j0) {
-                acc += s_prod[jl];
+            if ((int64_t)jl < (int64_t)sm.rowend[r] - j0) {
+                acc += sm.buf[jl];
                 ++jl;
             } else {
-                s_ysum[r] = acc;
+                ysum[r] = acc;
                 acc = T(0);
                 ++r;
             }
         }
         if (tid == 0) {          // partial sum of row i0 left by the previous tile
-            if (r > 0) s_ysum[0] += carry;
+            if (r > 0) ysum[0] += carry;
             else acc += carry;
         }
 
@@ -178,61 +252,135 @@ __global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
             if (lane >= off && k2 == key) sv += v2;
         }
         if (lane == 63) {
-            s_wkey[wave] = key;
-            s_wval[wave] = sv;
+            sm.wkey[wave] = key;
+            sm.wval[wave] = sv;
         }
         __syncthreads();
         if (tid == 0) {
-            T run = s_wval[0];
-            s_bs[0] = run;
+            T run = sm.wval[0];
+            sm.bs[0] = run;
             for (int w = 1; w < NW; ++w) {
-                T b = s_wval[w];
-                if (s_wkey[w] == s_wkey[w - 1]) b += run;
-                s_bs[w] = b;
+                T b = sm.wval[w];
+                if (sm.wkey[w] == sm.wkey[w - 1]) b += run;
+                sm.bs[w] = b;
                 run = b;
             }
         }
         __syncthreads();
-        if (wave > 0 && key == s_wkey[wave - 1]) sv += s_bs[wave - 1];
+        if (wave > 0 && key == sm.wkey[wave - 1]) sv += sm.bs[wave - 1];
         T prev = __shfl_up(sv, 1, 64);
-        if (lane == 0) prev = wave > 0 ? s_bs[wave - 1] : T(0);
-        if (tid > 0 && r > r_first) s_ysum[r_first] += prev;
+        if (lane == 0) prev = wave > 0 ? sm.bs[wave - 1] : T(0);
+        if (tid > 0 && r > r_first) ysum[r_first] += prev;
         __syncthreads();
 
         // (5) finished rows i0 .. i0+rend-1.
         for (int q = tid; q < rend; q += BLOCK) {
             const int64_t row = i0 + q;
-            const T s = alpha * s_ysum[q];
+            const T s = alpha * ysum[q];
             y[row] = beta_zero ? s : s + beta * y[row];
         }
-        if (rend > 0) carry_has = j1 > (int64_t)s_rowend[rend - 1];
+        if (rend > 0) carry_has = j1 > (int64_t)sm.rowend[rend - 1];
         else carry_has = carry_has || (j1 > j0);
-        carry = s_bs[NW - 1];
+        carry = sm.bs[NW - 1];
         i0 += rend;
         j0 = j1;
         __syncthreads();
     }
     if (tid == 0) {
-        carry_row[blockIdx.x] = (i0 < m && carry_has) ? i0 : -1;
-        carry_val[blockIdx.x] = carry;
+        *carry_row = (i0 < m && carry_has) ? i0 : -1;
+        *carry_val = carry;
     }
 }
 
-// Adds each run of equal-row carries (in block order) into y.
-template <typename T>
-__global__ void spmv_carry_fixup_kernel(int64_t nblocks, const int64_t *__restrict__ carry_row,
-                                        const T *__restrict__ carry_val, T *__restrict__ y, T alpha)
+template <typename T, int BLOCK, int IPT, bool PF>
+__global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
+    int64_t m, int64_t nnz, int32_t origin, const int32_t *__restrict__ rowptr,
+    const int32_t *__restrict__ colind, const T *__restrict__ val, const T *__restrict__ x,
+    T *__restrict__ y, T alpha, T beta, int beta_zero, int64_t tiles_per_block,
+    const int64_t *__restrict__ start_rows, int64_t *__restrict__ carry_row,
+    T *__restrict__ carry_val)
 {
-    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b >= nblocks) return;
-    const int64_t r = carry_row[b];
-    if (r < 0) return;
-    if (b > 0 && carry_row[b - 1] == r) return;
-    T s = carry_val[b];
-    for (int64_t u = b + 1; u < nblocks && carry_row[u] == r; ++u) s += carry_val[u];
-    atomicAdd(&y[r], alpha * s);
+    constexpr int TILE = BLOCK * IPT;
+    __shared__ SpmvSmem<T, TILE, BLOCK / 64> sm;
+    const int64_t total = m + nnz;
+    const int64_t dbeg = (int64_t)blockIdx.x * tiles_per_block * TILE;
+    if (dbeg >= total) return;
+    const int64_t dend = min(total, dbeg + tiles_per_block * (int64_t)TILE);
+    merge_range<T, BLOCK, IPT, PF, !PF>(m, nnz, nnz - 1, 0, origin, origin, rowptr, colind, val, x, y, alpha, beta,
+                               beta_zero, dbeg, dend, start_rows ? start_rows[blockIdx.x] : -1,
+                               carry_row + blockIdx.x, carry_val + blockIdx.x, sm);
 }
 
+struct SliceInfo {
+    int64_t off[NUM_XCD + 1];      // slice s occupies [off[s], off[s+1]) of colind/val
+    int64_t tiles[NUM_XCD];        // tiles per block in slice s
+};
+
+// Workgroup b runs slice s = b % 8 (on XCD s); rowptr_all holds 8 row-pointer
+// arrays of m+1 absolute positions; colind_all holds slice-local columns.
+template <typename T, int BLOCK, int IPT, bool NT>
+__global__ __launch_bounds__(BLOCK) void csr_spmv_sliced_kernel(
+    int64_t m, SliceInfo info, const int32_t *__restrict__ rowptr_all,
+    const int32_t *__restrict__ colind_all, const T *__restrict__ val_all,
+    const T *__restrict__ x, int64_t slice_w, T *__restrict__ ypart, int64_t nb,
+    const int64_t *__restrict__ start_rows, int64_t *__restrict__ carry_row,
+    T *__restrict__ carry_val)
+{
+    constexpr int TILE = BLOCK * IPT;
+    __shared__ SpmvSmem<T, TILE, BLOCK / 64> sm;
+    const int s = blockIdx.x % NUM_XCD;
+    const int64_t lb = blockIdx.x / NUM_XCD;
+    const int64_t slot = s * nb + lb;
+    const int64_t off = info.off[s];
+    const int64_t nnz_s = info.off[s + 1] - off;
+    const int64_t total = m + nnz_s;
+    const int64_t dbeg = lb * info.tiles[s] * TILE;
+    if (dbeg >= total) {
+        if (threadIdx.x == 0) carry_row[slot] = -1;
+        return;
+    }
+    const int64_t dend = min(total, dbeg + info.tiles[s] * (int64_t)TILE);
+    merge_range<T, BLOCK, IPT, true, NT>(m, nnz_s, info.off[NUM_XCD] - 1 - off, -s * slice_w, off, 0,
+                               rowptr_all + s * (m + 1), colind_all + off,
+                               val_all + off, x + s * slice_w, ypart + s * m, T(1), T(0), 1,
+                               dbeg, dend, start_rows ? start_rows[slot] : -1, carry_row + slot,
+                               carry_val + slot, sm);
+}
+
+// Adds each run of equal-row carries (in block order) of each segment into
+// y + seg*ystride.  Segment = one merge path (the whole matrix, or a slice).
+template <typename T>
+__global__ void spmv_carry_fixup_kernel(int64_t nb, int64_t nseg, const int64_t *__restrict__ carry_row,
+                                        const T *__restrict__ carry_val, T *__restrict__ y,
+                                        int64_t ystride, T alpha)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nb * nseg) return;
+    const int64_t seg = t / nb, b = t % nb;
+    const int64_t *cr = carry_row + seg * nb;
+    const T *cv = carry_val + seg * nb;
+    const int64_t r = cr[b];
+    if (r < 0) return;
+    if (b > 0 && cr[b - 1] == r) return;
+    T s = cv[b];
+    for (int64_t u = b + 1; u < nb && cr[u] == r; ++u) s += cv[u];
+    atomicAdd(&y[seg * ystride + r], alpha * s);
+}
+
+template <typename T>
+__global__ void slice_reduce_kernel(int64_t m, const T *__restrict__ ypart, T *__restrict__ y,
+                                    T alpha, T beta, int beta_zero)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    T s = __builtin_nontemporal_load(ypart + i);
+#pragma unroll
+    for (int k = 1; k < NUM_XCD; ++k) s += __builtin_nontemporal_load(ypart + k * m + i);
+    const T r = alpha * s;
+    y[i] = beta_zero ? r : r + beta * y[i];
+}
+
+// Start row of each block's first tile: plain (nseg = 1) or per slice.
 __global__ void merge_start_kernel(int64_t m, int64_t nnz, int32_t origin,
                                    const int32_t *__restrict__ rowptr, int64_t items_per_block,
                                    int64_t nblocks, int64_t *__restrict__ start_rows)
@@ -243,28 +391,150 @@ __global__ void merge_start_kernel(int64_t m, int64_t nnz, int32_t origin,
     if (__lane_id() == 0) start_rows[b] = r;
 }
 
+__global__ void sliced_start_kernel(int64_t m, SliceInfo info, const int32_t *__restrict__ rowptr_all,
+                                    int64_t nb, int64_t tile, int64_t *__restrict__ start_rows)
+{
+    const int s = blockIdx.x % NUM_XCD;
+    const int64_t lb = blockIdx.x / NUM_XCD;
+    const int64_t nnz_s = info.off[s + 1] - info.off[s];
+    const int64_t d = lb * info.tiles[s] * tile;
+    int64_t r = -1;
+    if (d < m + nnz_s)
+        r = wave_merge_search(rowptr_all + s * (m + 1), info.off[s], m, nnz_s, d);
+    if (__lane_id() == 0) start_rows[s * nb + lb] = r;
+}
+
+// counts[s*(m+1) + i] = entries of row i in column slice s (the i = m slot is 0).
+__global__ void slice_count_kernel(int64_t m, int32_t origin, const int32_t *__restrict__ rowptr,
+                                   const int32_t *__restrict__ colind, int64_t w,
+                                   int32_t *__restrict__ counts)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i > m) return;
+    int32_t c[NUM_XCD] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (i < m) {
+        for (int64_t p = (int64_t)rowptr[i] - origin; p < (int64_t)rowptr[i + 1] - origin; ++p) {
+            int64_t s = ((int64_t)colind[p] - origin) / w;
+            c[s < NUM_XCD ? s : NUM_XCD - 1]++;
+        }
+    }
+#pragma unroll
+    for (int s = 0; s < NUM_XCD; ++s) counts[s * (m + 1) + i] = c[s];
+}
+
+template <typename T>
+__global__ void slice_scatter_kernel(int64_t m, int32_t origin, const int32_t *__restrict__ rowptr,
+                                     const int32_t *__restrict__ colind, const T *__restrict__ val,
+                                     int64_t w, const int32_t *__restrict__ rowptr_all,
+                                     int32_t *__restrict__ colind_all, T *__restrict__ val_all,
+                                     int32_t *__restrict__ perm)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= m) return;
+    int32_t cur[NUM_XCD];
+#pragma unroll
+    for (int s = 0; s < NUM_XCD; ++s) cur[s] = rowptr_all[s * (m + 1) + i];
+    for (int64_t p = (int64_t)rowptr[i] - origin; p < (int64_t)rowptr[i + 1] - origin; ++p) {
+        const int64_t c = (int64_t)colind[p] - origin;
+        int s = (int)(c / w);
+        if (s >= NUM_XCD) s = NUM_XCD - 1;
+        int32_t q = 0;
+#pragma unroll
+        for (int t = 0; t < NUM_XCD; ++t)
+            if (t == s) q = cur[t]++;
+        colind_all[q] = (int32_t)(c - (int64_t)s * w);
+        val_all[q] = val[p];
+        perm[q] = (int32_t)p;
+    }
+}
+
+template <typename T>
+__global__ void gather_values_kernel(int64_t nnz, const int32_t *__restrict__ perm,
+                                     const T *__restrict__ src, T *__restrict__ dst)
+{
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q < nnz) dst[q] = src[perm[q]];
+}
+
 struct SpmvGrid {
     int64_t tiles_per_block = 1;
     int64_t nblocks = 0;
+    bool pf = false;      // prefetching plain kernel
 };
 
-template <typename T>
-int spmv_grid(int64_t m, int64_t nnz, SpmvGrid *g)
+// Items per thread (tile = 256 * ipt merge items): JLUST_HIP_SPMV_IPT in
+// {4, 8, 16}, default 4.
+int spmv_ipt()
 {
-    constexpr int TILE = SPMV_BLOCK * SpmvIpt<T>::value;
-    int dev = 0;
-    if (int st = require_device(&dev)) return st;
-    static int occ_cache[2][64] = {};
-    int &occ = occ_cache[sizeof(T) == 8 ? 0 : 1][dev & 63];
+    static const int v = [] {
+        const char *e = getenv("JLUST_HIP_SPMV_IPT");
+        const int x = e ? atoi(e) : 4;
+        return (x == 4 || x == 8 || x == 16) ? x : 4;
+    }();
+    return v;
+}
+
+#define JLUST_SPMV_IPT_DISPATCH(ipt, F) ((ipt) == 4 ? F(4) : (ipt) == 16 ? F(16) : F(8))
+
+// Merge-kernel variant: plain (row ends, then col/val, then x, per tile),
+// plain with register prefetch, or column-sliced (prefetching).
+enum SpmvKind { SPMV_PLAIN = 0, SPMV_PLAIN_PF = 1, SPMV_SLICED = 2 };
+
+// JLUST_HIP_SPMV_PF=1 selects the prefetching plain kernel (default off).
+bool spmv_plain_pf()
+{
+    static const bool v = [] {
+        const char *e = getenv("JLUST_HIP_SPMV_PF");
+        return e && e[0] == '1';
+    }();
+    return v;
+}
+
+template <typename T, int IPT, int KIND>
+int spmv_occupancy_ipt(int dev, int *occ_out)
+{
+    static int occ_cache[64] = {};
+    int &occ = occ_cache[dev & 63];
     if (occ == 0) {
         int nb = 0;
-        JLUST_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &nb, csr_spmv_merge_kernel<T, SPMV_BLOCK, SpmvIpt<T>::value>, SPMV_BLOCK, 0));
+        if (KIND == SPMV_SLICED)
+            JLUST_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb, csr_spmv_sliced_kernel<T, SPMV_BLOCK, IPT, false>, SPMV_BLOCK, 0));
+        else
+            JLUST_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb, csr_spmv_merge_kernel<T, SPMV_BLOCK, IPT, KIND == SPMV_PLAIN_PF>, SPMV_BLOCK, 0));
         occ = nb > 0 ? nb : 1;
     }
-    const int64_t target = (int64_t)occ * device_info(dev).cu_count;
+    *occ_out = occ;
+    return JLUST_STATUS_SUCCESS;
+}
+
+template <typename T>
+int spmv_occupancy(int dev, int ipt, int kind, int *occ_out)
+{
+#define F(I)                                                                         \
+    (kind == SPMV_SLICED     ? spmv_occupancy_ipt<T, I, SPMV_SLICED>(dev, occ_out)    \
+     : kind == SPMV_PLAIN_PF ? spmv_occupancy_ipt<T, I, SPMV_PLAIN_PF>(dev, occ_out)  \
+                             : spmv_occupancy_ipt<T, I, SPMV_PLAIN>(dev, occ_out))
+    return JLUST_SPMV_IPT_DISPATCH(ipt, F);
+#undef F
+}
+
+template <typename T>
+int spmv_grid(int64_t m, int64_t nnz, int ipt, SpmvGrid *g)
+{
+    const int64_t TILE = (int64_t)SPMV_BLOCK * ipt;
+    int dev = 0, occ = 1;
+    if (int st = require_device(&dev)) return st;
+    // The prefetching kernel's clamped loads need at least one nonzero.
+    g->pf = spmv_plain_pf() && nnz > 0;
+    if (int st = spmv_occupancy<T>(dev, ipt, g->pf ? SPMV_PLAIN_PF : SPMV_PLAIN, &occ)) return st;
+    int64_t target = (int64_t)occ * device_info(dev).cu_count;
+    if (target < 1) target = 1;
     const int64_t ntiles = (m + nnz + TILE - 1) / TILE;
-    g->tiles_per_block = ntiles / (target > 0 ? target : 1);
+    // Rounded up, so that nblocks <= target: every block is resident at once
+    // and no block runs as a tail after the others.
+    g->tiles_per_block = (ntiles + target - 1) / target;
     if (g->tiles_per_block < 1) g->tiles_per_block = 1;
     g->nblocks = (ntiles + g->tiles_per_block - 1) / g->tiles_per_block;
     return JLUST_STATUS_SUCCESS;
@@ -292,19 +562,28 @@ int check_spmv_args(int64_t m, int64_t n, int64_t nnz, int32_t origin, const voi
 template <typename T>
 int spmv_launch(int64_t m, int64_t nnz, int32_t origin, const int32_t *rowptr,
                 const int32_t *colind, const T *val, T alpha, const T *x, T beta, T *y,
-                const SpmvGrid &g, const int64_t *start_rows, int64_t *carry_row, T *carry_val,
-                hipStream_t stream)
+                const SpmvGrid &g, int ipt, const int64_t *start_rows, int64_t *carry_row,
+                T *carry_val, hipStream_t stream)
 {
-    constexpr int IPT = SpmvIpt<T>::value;
-    hipLaunchKernelGGL((csr_spmv_merge_kernel<T, SPMV_BLOCK, IPT>), dim3((unsigned)g.nblocks),
-                       dim3(SPMV_BLOCK), 0, stream, m, nnz, origin, rowptr, colind, val, x, y,
-                       alpha, beta, (int)(beta == T(0)), g.tiles_per_block, start_rows,
-                       carry_row, carry_val);
+#define G(I, P)                                                                                  \
+    hipLaunchKernelGGL((csr_spmv_merge_kernel<T, SPMV_BLOCK, I, P>), dim3((unsigned)g.nblocks), \
+                       dim3(SPMV_BLOCK), 0, stream, m, nnz, origin, rowptr, colind, val, x, y,  \
+                       alpha, beta, (int)(beta == T(0)), g.tiles_per_block, start_rows,         \
+                       carry_row, carry_val)
+#define F(I) do { if (g.pf) G(I, true); else G(I, false); } while (0)
+    switch (ipt) {
+    case 4: F(4); break;
+    case 16: F(16); break;
+    default: F(8); break;
+    }
+#undef F
+#undef G
     if (int st = check_launch("csr_spmv_merge_kernel")) return st;
     // A single block ends on the last row end, so it never leaves a carry.
     if (g.nblocks > 1) {
         hipLaunchKernelGGL((spmv_carry_fixup_kernel<T>), dim3((unsigned)((g.nblocks + 255) / 256)),
-                           dim3(256), 0, stream, g.nblocks, carry_row, carry_val, y, alpha);
+                           dim3(256), 0, stream, g.nblocks, (int64_t)1, carry_row, carry_val, y,
+                           (int64_t)0, alpha);
         if (int st = check_launch("spmv_carry_fixup_kernel")) return st;
     }
     return JLUST_STATUS_SUCCESS;
@@ -322,14 +601,25 @@ int csr_spmv(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *r
     if (int st = require_device(nullptr)) return st;
     if (m == 0) return JLUST_STATUS_SUCCESS;
     SpmvGrid g;
-    if (int st = spmv_grid<T>(m, nnz, &g)) return st;
+    const int ipt = spmv_ipt();
+    if (int st = spmv_grid<T>(m, nnz, ipt, &g)) return st;
     void *ws = nullptr;
     const size_t rows_bytes = align_up(sizeof(int64_t) * (size_t)g.nblocks, 256);
     if (int st = scratch(stream, rows_bytes + sizeof(T) * (size_t)g.nblocks, &ws)) return st;
     int64_t *carry_row = (int64_t *)ws;
     T *carry_val = (T *)((char *)ws + rows_bytes);
-    return spmv_launch<T>(m, nnz, origin, rowptr, colind, val, alpha, x, beta, y, g, nullptr,
+    return spmv_launch<T>(m, nnz, origin, rowptr, colind, val, alpha, x, beta, y, g, ipt, nullptr,
                           carry_row, carry_val, (hipStream_t)stream);
+}
+
+// Slice or not: JLUST_HIP_SPMV_SLICE=0 never, =1 always, unset = when x is
+// larger than one XCD's L2.
+bool want_slices(int64_t n, size_t tsize)
+{
+    const char *e = getenv("JLUST_HIP_SPMV_SLICE");
+    if (e && e[0] == '0') return false;
+    if (e && e[0] == '1') return n >= NUM_XCD;
+    return (size_t)n * tsize > SLICE_MIN_X_BYTES;
 }
 
 }  // namespace
@@ -344,12 +634,24 @@ struct jlust_spmv_plan {
     const int32_t *rowptr;
     const int32_t *colind;
     const void *val;
-    jlust::SpmvGrid grid;
     int device;
-    void *mem;        // start rows | carry rows | carry values
+    int ipt;         // items per thread of the merge tiles
+    void *mem;       // everything below lives in this allocation
+    // unsliced
+    jlust::SpmvGrid grid;
     int64_t *start_rows;
     int64_t *carry_row;
     void *carry_val;
+    // sliced
+    bool sliced;
+    int64_t slice_w;
+    int64_t nb;                      // blocks per slice
+    jlust::SliceInfo info;
+    int32_t *rowptr_all;
+    int32_t *colind_all;
+    void *val_all;
+    int32_t *perm;
+    void *ypart;
 };
 
 using namespace jlust;
@@ -370,6 +672,54 @@ extern "C" int jlust_hip_csr_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz, int
     return csr_spmv<float>(m, n, nnz, origin, rowptr, colind, val, alpha, x, beta, y, stream);
 }
 
+template <typename T>
+static int plan_build_sliced(jlust_spmv_plan *p, jlust_stream_t stream)
+{
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t m = p->m, nnz = p->nnz;
+    const int64_t lenp = NUM_XCD * (m + 1);
+    const unsigned rblocks = (unsigned)((m + 1 + 255) / 256);
+    hipLaunchKernelGGL(slice_count_kernel, dim3(rblocks), dim3(256), 0, s, m, p->origin, p->rowptr,
+                       p->colind, p->slice_w, p->rowptr_all);
+    if (int st = check_launch("slice_count_kernel")) return st;
+    if (int st = exclusive_scan_i32(p->rowptr_all, p->rowptr_all, lenp, stream)) return st;
+    if (m > 0) {
+        hipLaunchKernelGGL((slice_scatter_kernel<T>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0,
+                           s, m, p->origin, p->rowptr, p->colind, (const T *)p->val, p->slice_w,
+                           p->rowptr_all, p->colind_all, (T *)p->val_all, p->perm);
+        if (int st = check_launch("slice_scatter_kernel")) return st;
+    }
+    // Slice offsets (first entry of each slice's row pointers, plus nnz) to the host.
+    int32_t firsts[NUM_XCD];
+    for (int k = 0; k < NUM_XCD; ++k)
+        JLUST_HIP_TRY(hipMemcpyAsync(&firsts[k], p->rowptr_all + k * (m + 1), sizeof(int32_t),
+                                     hipMemcpyDeviceToHost, s));
+    JLUST_HIP_TRY(hipStreamSynchronize(s));
+    for (int k = 0; k < NUM_XCD; ++k) p->info.off[k] = firsts[k];
+    p->info.off[NUM_XCD] = nnz;
+    const int64_t TILE = (int64_t)SPMV_BLOCK * p->ipt;
+    int64_t maxb = 1;
+    for (int k = 0; k < NUM_XCD; ++k) {
+        const int64_t ntiles = (m + p->info.off[k + 1] - p->info.off[k] + TILE - 1) / TILE;
+        p->info.tiles[k] = ntiles;   // provisional: blocks needed at one tile each
+        if (ntiles > maxb) maxb = ntiles;
+    }
+    int occ = 1;
+    if (int st = spmv_occupancy<T>(p->device, p->ipt, SPMV_SLICED, &occ)) return st;
+    int64_t target = (int64_t)occ * device_info(p->device).cu_count / NUM_XCD;
+    if (target < 1) target = 1;
+    // Rounded up, so that nb <= target (one resident wave of blocks).
+    int64_t tpb = (maxb + target - 1) / target;
+    if (tpb < 1) tpb = 1;
+    p->nb = (maxb + tpb - 1) / tpb;
+    for (int k = 0; k < NUM_XCD; ++k) {
+        const int64_t ntiles = p->info.tiles[k];
+        int64_t t = (ntiles + p->nb - 1) / p->nb;
+        p->info.tiles[k] = t < 1 ? 1 : t;
+    }
+    return JLUST_STATUS_SUCCESS;
+}
+
 extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz, int32_t origin,
                                               int value_type, const int32_t *rowptr,
                                               const int32_t *colind, const void *val,
@@ -386,29 +736,78 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
         return st;
     int dev = 0;
     if (int st = require_device(&dev)) return st;
-    SpmvGrid g;
-    if (m > 0) {
-        int st = value_type == 0 ? spmv_grid<double>(m, nnz, &g) : spmv_grid<float>(m, nnz, &g);
-        if (st) return st;
-    }
     const size_t tsz = value_type == 0 ? sizeof(double) : sizeof(float);
-    const size_t nb = (size_t)(g.nblocks > 0 ? g.nblocks : 1);
-    const size_t sz_rows = align_up(sizeof(int64_t) * nb, 256);
-    void *mem = nullptr;
-    JLUST_HIP_TRY(hipMalloc(&mem, 2 * sz_rows + tsz * nb));
-    auto *p = new jlust_spmv_plan{m, n, nnz, origin, value_type, rowptr, colind, val, g, dev, mem,
-                                  (int64_t *)mem, (int64_t *)((char *)mem + sz_rows),
-                                  (char *)mem + 2 * sz_rows};
-    if (m > 0) {
-        const int tile = SPMV_BLOCK * (value_type == 0 ? SpmvIpt<double>::value : SpmvIpt<float>::value);
-        hipLaunchKernelGGL(merge_start_kernel, dim3((unsigned)g.nblocks), dim3(64), 0,
-                           (hipStream_t)stream, m, nnz, origin, rowptr,
-                           g.tiles_per_block * (int64_t)tile, g.nblocks, p->start_rows);
-        if (int st = check_launch("merge_start_kernel")) {
-            (void)hipFree(mem);
-            delete p;
-            return st;
+    auto *p = new jlust_spmv_plan();
+    p->m = m;
+    p->n = n;
+    p->nnz = nnz;
+    p->origin = origin;
+    p->value_type = value_type;
+    p->rowptr = rowptr;
+    p->colind = colind;
+    p->val = val;
+    p->device = dev;
+    p->ipt = spmv_ipt();
+    // (The sliced kernel's clamped prefetch needs at least one nonzero.)
+    p->sliced = m > 0 && nnz > 0 && want_slices(n, tsz);
+    hipStream_t s = (hipStream_t)stream;
+    int st = JLUST_STATUS_SUCCESS;
+    if (!p->sliced) {
+        if (m > 0) {
+            st = value_type == 0 ? spmv_grid<double>(m, nnz, p->ipt, &p->grid)
+                                 : spmv_grid<float>(m, nnz, p->ipt, &p->grid);
+            if (st) { delete p; return st; }
         }
+        const size_t nb = (size_t)(p->grid.nblocks > 0 ? p->grid.nblocks : 1);
+        const size_t sz_rows = align_up(sizeof(int64_t) * nb, 256);
+        hipError_t e = hipMalloc(&p->mem, 2 * sz_rows + tsz * nb);
+        if (e != hipSuccess) { delete p; return hip_fail(e, "hipMalloc(spmv plan)"); }
+        p->start_rows = (int64_t *)p->mem;
+        p->carry_row = (int64_t *)((char *)p->mem + sz_rows);
+        p->carry_val = (char *)p->mem + 2 * sz_rows;
+        if (m > 0) {
+            hipLaunchKernelGGL(merge_start_kernel, dim3((unsigned)p->grid.nblocks), dim3(64), 0, s, m,
+                               nnz, origin, rowptr,
+                               p->grid.tiles_per_block * (int64_t)(SPMV_BLOCK * p->ipt),
+                               p->grid.nblocks, p->start_rows);
+            st = check_launch("merge_start_kernel");
+        }
+    } else {
+        p->slice_w = (n + NUM_XCD - 1) / NUM_XCD;
+        // Upper bound of blocks per slice: one tile each.
+        const int64_t tile = (int64_t)SPMV_BLOCK * p->ipt;
+        const int64_t nb_max = (m + nnz + tile - 1) / tile + 1;
+        const size_t sz_rp = align_up(sizeof(int32_t) * NUM_XCD * (size_t)(m + 1), 256);
+        const size_t sz_ci = align_up(sizeof(int32_t) * (size_t)(nnz > 0 ? nnz : 1), 256);
+        const size_t sz_v = align_up(tsz * (size_t)(nnz > 0 ? nnz : 1), 256);
+        const size_t sz_y = align_up(tsz * NUM_XCD * (size_t)m, 256);
+        const size_t sz_sr = align_up(sizeof(int64_t) * NUM_XCD * (size_t)nb_max, 256);
+        const size_t sz_cv = align_up(tsz * NUM_XCD * (size_t)nb_max, 256);
+        hipError_t e = hipMalloc(&p->mem, sz_rp + 2 * sz_ci + sz_v + sz_y + 2 * sz_sr + sz_cv);
+        if (e != hipSuccess) { delete p; return hip_fail(e, "hipMalloc(sliced spmv plan)"); }
+        char *b = (char *)p->mem;
+        p->rowptr_all = (int32_t *)b;  b += sz_rp;
+        p->colind_all = (int32_t *)b;  b += sz_ci;
+        p->perm = (int32_t *)b;        b += sz_ci;
+        p->val_all = b;                b += sz_v;
+        p->ypart = b;                  b += sz_y;
+        p->start_rows = (int64_t *)b;  b += sz_sr;
+        p->carry_row = (int64_t *)b;   b += sz_sr;
+        p->carry_val = b;
+        st = value_type == 0 ? plan_build_sliced<double>(p, stream) : plan_build_sliced<float>(p, stream);
+        if (!st && p->nb > nb_max) st = fail(JLUST_STATUS_HIP_ERROR, "spmv plan: block count overflow");
+        if (!st) {
+            hipLaunchKernelGGL(sliced_start_kernel, dim3((unsigned)(NUM_XCD * p->nb)), dim3(64), 0, s,
+                               m, p->info, p->rowptr_all, p->nb, (int64_t)SPMV_BLOCK * p->ipt,
+                               p->start_rows);
+            st = check_launch("sliced_start_kernel");
+        }
+    }
+    if (st) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(p->mem);
+        delete p;
+        return st;
     }
     *plan_out = p;
     return JLUST_STATUS_SUCCESS;
@@ -421,6 +820,21 @@ extern "C" int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan, con
     if (bad_ptr(val, plan->nnz))
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_update_values: null values");
     plan->val = val;
+    if (plan->sliced && plan->nnz > 0) {
+        // The plan's slice-major copy of the values is refreshed in stream order
+        // on the null stream, then waited for, so the caller's next execute on
+        // any stream sees it.
+        const unsigned grid = (unsigned)((plan->nnz + 255) / 256);
+        JLUST_HIP_TRY(hipDeviceSynchronize());      // the new values are complete
+        if (plan->value_type == 0)
+            hipLaunchKernelGGL((gather_values_kernel<double>), dim3(grid), dim3(256), 0, 0, plan->nnz,
+                               plan->perm, (const double *)val, (double *)plan->val_all);
+        else
+            hipLaunchKernelGGL((gather_values_kernel<float>), dim3(grid), dim3(256), 0, 0, plan->nnz,
+                               plan->perm, (const float *)val, (float *)plan->val_all);
+        if (int st = check_launch("gather_values_kernel")) return st;
+        JLUST_HIP_TRY(hipDeviceSynchronize());
+    }
     return JLUST_STATUS_SUCCESS;
 }
 
@@ -443,9 +857,39 @@ static int plan_execute(jlust_spmv_plan_t plan, int want_type, T alpha, const T 
         return fail(JLUST_STATUS_INVALID_ARGUMENT,
                     "spmv_plan_execute: plan belongs to device %d, current device is %d",
                     plan->device, dev);
-    return spmv_launch<T>(plan->m, plan->nnz, plan->origin, plan->rowptr, plan->colind,
-                          (const T *)plan->val, alpha, x, beta, y, plan->grid, plan->start_rows,
-                          plan->carry_row, (T *)plan->carry_val, (hipStream_t)stream);
+    hipStream_t s = (hipStream_t)stream;
+    if (!plan->sliced)
+        return spmv_launch<T>(plan->m, plan->nnz, plan->origin, plan->rowptr, plan->colind,
+                              (const T *)plan->val, alpha, x, beta, y, plan->grid, plan->ipt,
+                              plan->start_rows, plan->carry_row, (T *)plan->carry_val, s);
+    const int64_t m = plan->m;
+    T *ypart = (T *)plan->ypart;
+    static const bool nt = [] {
+        const char *e = getenv("JLUST_HIP_SPMV_SLICED_NT");
+        return e && e[0] == '1';
+    }();
+#define G(I, N)                                                                                  \
+    hipLaunchKernelGGL((csr_spmv_sliced_kernel<T, SPMV_BLOCK, I, N>),                            \
+                       dim3((unsigned)(NUM_XCD * plan->nb)), dim3(SPMV_BLOCK), 0, s, m, plan->info, \
+                       plan->rowptr_all, plan->colind_all, (const T *)plan->val_all, x,         \
+                       plan->slice_w, ypart, plan->nb, plan->start_rows, plan->carry_row,       \
+                       (T *)plan->carry_val)
+#define F(I) do { if (nt) G(I, true); else G(I, false); } while (0)
+    switch (plan->ipt) {
+    case 4: F(4); break;
+    case 16: F(16); break;
+    default: F(8); break;
+    }
+#undef F
+#undef G
+    if (int st = check_launch("csr_spmv_sliced_kernel")) return st;
+    hipLaunchKernelGGL((spmv_carry_fixup_kernel<T>),
+                       dim3((unsigned)((NUM_XCD * plan->nb + 255) / 256)), dim3(256), 0, s, plan->nb,
+                       (int64_t)NUM_XCD, plan->carry_row, (const T *)plan->carry_val, ypart, m, T(1));
+    if (int st = check_launch("spmv_carry_fixup_kernel")) return st;
+    hipLaunchKernelGGL((slice_reduce_kernel<T>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0, s, m,
+                       (const T *)ypart, y, alpha, beta, (int)(beta == T(0)));
+    return check_launch("slice_reduce_kernel");
 }
 
 extern "C" int jlust_hip_csr_spmv_plan_execute_f64(jlust_spmv_plan_t plan, double alpha,

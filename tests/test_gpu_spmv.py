@@ -205,3 +205,73 @@ def test_device_arch(J):
     buf = ctypes.create_string_buffer(64)
     assert J._lib.lib().jlust_hip_device_arch(buf, 64) == 0
     assert buf.value.decode().startswith("gfx950")
+
+
+# ------------------------------------------------- column-sliced SpMV plans
+
+def run_plan(J, rowptr, colind, val, x, m, n, origin=1, alpha=1.0, beta=0.0, y0=None):
+    import torch
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n),
+                     origin=J.OneBased() if origin == 1 else J.ZeroBased())
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    y = dev(y0) if y0 is not None else torch.full((m,), float("nan"), dtype=A.dtype,
+                                                   device="cuda")
+    J.execute(h, dev(x), y, alpha=alpha, beta=beta)
+    return host(y), h, A
+
+
+@pytest.mark.parametrize("name,kw", SHAPES, ids=[s[0] for s in SHAPES])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_plan_sliced_random_shapes(J, O, name, kw, dtype, monkeypatch):
+    """JLUST_HIP_SPMV_SLICE=1 forces the 8-column-slice layout on any n >= 8."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1")
+    m, n = kw["m"], kw["n"]
+    origin = 0 if name in ("empty_rows", "dense_rows") else 1
+    rowptr, colind, val = random_csr(m, n, density=kw.get("density"), lengths=kw.get("lengths"),
+                                     seed=zlib.crc32(name.encode()) % 1000 + 7, origin=origin,
+                                     dtype=dtype)
+    x = np.random.default_rng(2).uniform(-1, 1, n).astype(dtype)
+    y, _, _ = run_plan(J, rowptr, colind, val, x, m, n, origin=origin)
+    ref = O.csr_spmv(rowptr, colind, val, x, origin=origin)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x, origin=origin)
+    assert_within(y, ref, absref, dtype, "sliced " + name)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_plan_sliced_auto_alpha_beta_update(J, O, dtype, monkeypatch):
+    """Scaled config 2 with n = 1M: x is 8 MB (f64) / 4 MB (f32); the plan
+    slices when x exceeds 4 MB."""
+    monkeypatch.delenv("JLUST_HIP_SPMV_SLICE", raising=False)
+    from jlust_amd import workloads as W
+    cfg = W.make(2, scale=4)
+    val = cfg["val"].astype(dtype)
+    x = cfg["x"].astype(dtype)
+    y0 = np.random.default_rng(3).uniform(-1, 1, cfg["m"]).astype(dtype)
+    y, h, A = run_plan(J, cfg["rowptr"], cfg["colind"], val, x, cfg["m"], cfg["n"], alpha=1.5,
+                       beta=-0.5, y0=y0)
+    ref = O.csr_spmv(cfg["rowptr"], cfg["colind"], val, x, 1.5, -0.5, y0)
+    absref = O.csr_spmv_absref(cfg["rowptr"], cfg["colind"], val, x, 1.5, -0.5, y0)
+    assert_within(y, ref, absref, dtype, "sliced auto")
+    val2 = (val * -3.0).astype(dtype)
+    J.update_values_(h, J.csr_tensor(A.pos_buffers[1], A.crd_buffers[1], dev(val2),
+                                     (cfg["m"], cfg["n"])))
+    import torch
+    yt = torch.empty(cfg["m"], dtype=A.dtype, device="cuda")
+    J.execute(h, dev(x), yt)
+    ref2 = O.csr_spmv(cfg["rowptr"], cfg["colind"], val2, x)
+    absref2 = O.csr_spmv_absref(cfg["rowptr"], cfg["colind"], val2, x)
+    assert_within(host(yt), ref2, absref2, dtype, "sliced after update_values!")
+
+
+def test_plan_sliced_full_config2_deterministic(J, O, monkeypatch):
+    monkeypatch.delenv("JLUST_HIP_SPMV_SLICE", raising=False)
+    import torch
+    from jlust_amd import workloads as W
+    cfg = W.make(2)
+    y, h, A = run_plan(J, cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"], cfg["m"], cfg["n"])
+    ref = O.csr_spmv(cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"])
+    absref = O.csr_spmv_absref(cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"])
+    assert_within(y, ref, absref, np.float64, "sliced full config 2")
+    y2 = torch.empty(cfg["m"], dtype=torch.float64, device="cuda")
+    J.execute(h, dev(cfg["x"]), y2)
+    np.testing.assert_array_equal(host(y2), y)
