@@ -44,18 +44,26 @@ namespace {
 constexpr int SPMV_BLOCK = 256;
 constexpr size_t SLICE_MIN_X_BYTES = (size_t)4 << 20;   // one XCD's L2
 
-// buf holds the tile's products at [0, nloc) and its finished row sums at
-// [nloc, nloc + rend); nloc + rend is the tile length, so one array suffices.
-// rowend uses [0, tile length]; it has room for every thread's IPT+1 stores.
+// LDS of one block.  buf: the tile's products at [0, nloc), followed by the
+// finished row sums of the tile at [nloc, nloc + rend) (nloc + rend is the
+// tile length).  diag[r]: merge coordinate of the end of tile row r (local
+// row-end position + r); every thread stores IPT+1 of them.
 template <typename T, int TILE, int NW>
 struct SpmvSmem {
     T buf[TILE];
-    int32_t rowend[TILE + 64 * NW];
+    int32_t diag[TILE + 64 * NW];
     int64_t i0;
+    int32_t wcnt[NW];
     int32_t wkey[NW];
     T wval[NW];
-    T bs[NW];
 };
+
+__device__ __forceinline__ int64_t uniform64(int64_t v)
+{
+    const int32_t lo = __builtin_amdgcn_readfirstlane((int32_t)v);
+    const int32_t hi = __builtin_amdgcn_readfirstlane((int32_t)(v >> 32));
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
 
 // Smallest i in [max(0, d-nnz), min(d, m)] with (rowptr[i+1]-ptr_origin) + i >= d,
 // taking i == m as true: the number of rows finished after the first d items
@@ -80,30 +88,73 @@ __device__ int64_t wave_merge_search(const int32_t *__restrict__ rowptr, int64_t
     return lo;
 }
 
+// ---- wave64 DPP (GFX9 controls): row_shr:n = 0x110+n, row_bcast:15 = 0x142,
+// row_bcast:31 = 0x143, wave_shr:1 = 0x138.  Lanes without a source keep `old`.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int32_t dpp_i32(int32_t old, int32_t v)
+{
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+
+template <int CTRL, int ROW_MASK, typename T>
+__device__ __forceinline__ T dpp_val(T old, T v)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, dpp_i32<CTRL, ROW_MASK>(__builtin_bit_cast(int32_t, old),
+                                                             __builtin_bit_cast(int32_t, v)));
+    } else {
+        const uint64_t o = __builtin_bit_cast(uint64_t, old), x = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = (uint32_t)dpp_i32<CTRL, ROW_MASK>((int32_t)o, (int32_t)x);
+        const uint32_t hi = (uint32_t)dpp_i32<CTRL, ROW_MASK>((int32_t)(o >> 32), (int32_t)(x >> 32));
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
+
+template <int CTRL, int ROW_MASK, typename T>
+__device__ __forceinline__ void seg_scan_step(int32_t key, T &v)
+{
+    const int32_t k2 = dpp_i32<CTRL, ROW_MASK>(-1, key);
+    const T v2 = dpp_val<CTRL, ROW_MASK>(T(0), v);
+    if (k2 == key) v += v2;
+}
+
+// Inclusive scan of v over the wave in lane order, segmented by key (keys are
+// non-decreasing with the lane and never -1).
+template <typename T>
+__device__ __forceinline__ T wave_seg_scan(int32_t key, T v)
+{
+    seg_scan_step<0x111, 0xf>(key, v);
+    seg_scan_step<0x112, 0xf>(key, v);
+    seg_scan_step<0x114, 0xf>(key, v);
+    seg_scan_step<0x118, 0xf>(key, v);
+    seg_scan_step<0x142, 0xa>(key, v);
+    seg_scan_step<0x143, 0xc>(key, v);
+    return v;
+}
+
 // One block's share [dbeg, dend) of the merge path of a CSR matrix whose row
-// pointers hold ptr_origin + (0-based position in colind/val) and whose column
-// indices hold col_origin + (0-based column of x).  start_row < 0: search.
-// Requires m >= 1 and a nonempty nonzero array: colind/val + jmax is the last
-// readable element (jmax < 0 when this range's own nonzeros are empty; the
-// clamped prefetch then reads an element before them), and x[x_safe] is a
-// readable element of x (used with PF only).
+// pointers hold ptr_origin + (0-based position in colind/val); the x value of
+// a stored column c is xs[c - col_origin], and xs[0] is readable.  start_row
+// < 0: search.  Requires m >= 1 and, for PF, a
+// nonempty nonzero array: colind/val + jmax is the last readable element (jmax
+// < 0 when this range's own nonzeros are empty; the clamped prefetch then
+// reads an element before them).  BZ: beta == 0 (y is only written).
 // PF: prefetch the next tile's row ends and col/val into registers while the
-// current tile is processed (pays off when x gathers hit L2; when they go to
-// memory the speculative loads only add traffic).  NT: stream rowptr/col/val
-// with nontemporal loads so they do not evict x from L2.
-template <typename T, int BLOCK, int IPT, bool PF, bool NT>
-__device__ void merge_range(int64_t m, int64_t nnz, int64_t jmax, int64_t x_safe,
-                            int64_t ptr_origin, int32_t col_origin,
-                            const int32_t *__restrict__ rowptr, const int32_t *__restrict__ colind,
-                            const T *__restrict__ val, const T *__restrict__ x, T *__restrict__ y,
-                            T alpha, T beta, int beta_zero, int64_t dbeg, int64_t dend,
-                            int64_t start_row, int64_t *carry_row, T *carry_val,
-                            SpmvSmem<T, BLOCK * IPT, BLOCK / 64> &sm)
+// current tile is processed (pays off when x gathers hit L2).  NT: stream
+// rowptr/col/val with nontemporal loads.
+template <typename T, int BLOCK, int IPT, bool PF, bool NT, bool BZ>
+__device__ __forceinline__ void merge_range(int64_t m, int64_t nnz, int64_t jmax, int64_t ptr_origin,
+                            int32_t col_origin, const int32_t *__restrict__ rowptr,
+                            const int32_t *__restrict__ colind, const T *__restrict__ val,
+                            const T *__restrict__ xs, T *__restrict__ y,
+                            T alpha, T beta, int64_t dbeg, int64_t dend, int64_t start_row,
+                            int64_t *carry_row, T *carry_val, SpmvSmem<T, BLOCK * IPT, BLOCK / 64> &sm)
 {
     constexpr int TILE = BLOCK * IPT;
     constexpr int NW = BLOCK / 64;
-    constexpr int RPT = TILE / BLOCK + 1;      // row ends per thread (TILE + 1 per tile)
-    static_assert(RPT * BLOCK <= TILE + 64 * NW, "rowend too small for the row-end stores");
+    constexpr int RPT = IPT + 1;               // row ends per thread (TILE + 1 per tile)
+    constexpr int BIG = TILE + 1;              // any row end at or past the tile's end
+    static_assert(RPT * BLOCK <= TILE + 64 * NW, "diag too small for the row-end stores");
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
@@ -115,122 +166,153 @@ __device__ void merge_range(int64_t m, int64_t nnz, int64_t jmax, int64_t x_safe
         if (lane == 0) sm.i0 = r;
     }
     __syncthreads();
-    int64_t i0 = sm.i0;
+    int64_t i0 = uniform64(sm.i0);
     int64_t j0 = dbeg - i0;
     T carry = T(0);
     bool carry_has = false;
 
-    // Loads are issued straight-line (clamped, always in-bounds addresses, no
-    // per-lane branches): a load under an exec-masked branch makes the
-    // compiler wait for every outstanding load before the next one, which
-    // would serialise the gathers.  Row ends are kept raw; validity and the
-    // origin are applied when they are written to LDS.
+    // Loads use a block-uniform base plus a 32-bit lane offset clamped into
+    // range, with no per-lane branch: a load under an exec-masked branch makes
+    // the compiler wait for every outstanding load before the next one.
     int32_t ren[RPT];
     int32_t cn[IPT];
     T vn[IPT];
-    auto load_rowends = [&](int64_t is) {
+    // The lane offsets are unsigned and below 2^11, so the compiler can use
+    // scalar-base + 32-bit-offset addressing.
+    auto load_rowends = [&](int64_t is) {      // rowptr[row + 1] of rows is + tid + u*BLOCK
+        const int64_t ib = min(is, m - 1);
+        const uint32_t lim = (uint32_t)min(m - 1 - ib, (int64_t)(RPT * BLOCK));
+        const int32_t *rp = rowptr + ib + 1;
 #pragma unroll
         for (int u = 0; u < RPT; ++u) {
-            const int64_t row = min(is + tid + u * BLOCK, m - 1);
-            ren[u] = NT ? __builtin_nontemporal_load(rowptr + row + 1) : rowptr[row + 1];
+            const uint32_t q = min((uint32_t)(tid + u * BLOCK), lim);
+            ren[u] = NT ? __builtin_nontemporal_load(rp + q) : rp[q];
         }
     };
-    // col/val of nonzeros js + q (q = tid + u*BLOCK), clamped to [js, jmax].
-    auto load_nz = [&](int64_t js, int64_t jmax) {
+    // col (and, with VALS, val) of nonzeros js + tid + u*BLOCK, clamped to jmx.
+    auto load_nz = [&](int64_t js, int64_t jmx, bool cols, bool vals) {
+        const int64_t jb = min(js, jmx);
+        const uint32_t lim = (uint32_t)min(jmx - jb, (int64_t)TILE);
+        const int32_t *cb = colind + jb;
+        const T *vb = val + jb;
 #pragma unroll
         for (int u = 0; u < IPT; ++u) {
-            const int64_t k = min(js + tid + u * BLOCK, jmax);
-            cn[u] = NT ? __builtin_nontemporal_load(colind + k) : colind[k];
-            vn[u] = NT ? __builtin_nontemporal_load(val + k) : val[k];
+            const uint32_t q = min((uint32_t)(tid + u * BLOCK), lim);
+            if (cols) cn[u] = NT ? __builtin_nontemporal_load(cb + q) : cb[q];
+            if (vals) vn[u] = NT ? __builtin_nontemporal_load(vb + q) : vb[q];
         }
     };
-    // Register prefetch (PF): tile t+1's row ends and col/val are issued while
-    // tile t is processed, so the loads are in flight across its barriers.
+    // Row ends are issued before col/val here and in the loop, so the wait for
+    // them at the top of the loop leaves the col/val loads in flight on both
+    // the entry and the loop-back path.
     if (PF) {
         load_rowends(i0);
-        load_nz(j0, jmax);
+        __builtin_amdgcn_sched_barrier(0);
+        load_nz(j0, jmax, true, false);
+        __builtin_amdgcn_sched_barrier(0);
+        load_nz(j0, jmax, false, true);
     }
 
     for (int64_t d = dbeg; d < dend; d += TILE) {
         const int tlen = (int)min((int64_t)TILE, dend - d);
-        // (1) row ends (0-based nonzero index) of rows i0 .. i0+tlen.
+        // (1) merge coordinates of the row ends of rows i0 .. i0+tlen, and the
+        // number rend of rows finished in this tile (diag is increasing, so it
+        // is the count of row ends inside the tile).
         if (!PF) load_rowends(i0);
-        // Stored unconditionally (entries past tlen are never read): a
-        // conditional store would let the compiler sink each load under its
-        // branch and serialise them.
+        {
+            const int32_t base = (int32_t)(ptr_origin + j0);
+            const int32_t rows_left = (int32_t)min(m - i0, (int64_t)(RPT * BLOCK));
+            int cnt = 0;
 #pragma unroll
-        for (int u = 0; u < RPT; ++u) {
-            const int r = tid + u * BLOCK;
-            sm.rowend[r] = i0 + r < m ? (int32_t)((int64_t)ren[u] - ptr_origin) : INT32_MAX;
+            for (int u = 0; u < RPT; ++u) {
+                const int r = tid + u * BLOCK;
+                const int32_t e = min(max(ren[u] - base, 0), BIG);
+                const int32_t dg = (r < rows_left ? e : BIG) + r;
+                sm.diag[r] = dg;
+                cnt += __popcll(__ballot(r < tlen && dg < tlen));
+            }
+            if (lane == 0) sm.wcnt[wave] = cnt;
         }
         __syncthreads();
+        int rend = 0;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) rend += sm.wcnt[w];
+        rend = __builtin_amdgcn_readfirstlane(rend);
+        const int nlt = tlen - rend;                        // nonzeros in the tile
+        const int64_t j1 = j0 + nlt;
+        // The clamp keeps a malformed rowptr from reading past the nonzero arrays.
+        const int nloc = (int)(min(j1, nnz) - j0);
+        // Does the tile end inside row i0+rend (a partial sum carried on)?
+        if (rend > 0) carry_has = sm.diag[rend - 1] < tlen - 1;
+        else carry_has = carry_has || nlt > 0;
 
-        // (2) smallest local row r in [0, dl] whose end lies at or past diagonal dl.
-        auto search = [&](int dl) {
-            int lo = 0, hi = dl;
-            while (lo < hi) {
-                const int mid = (lo + hi) >> 1;
-                if ((int64_t)sm.rowend[mid] - j0 + mid >= dl) hi = mid;
-                else lo = mid + 1;
-            }
-            return lo;
-        };
+        // (2) this thread's slice [dl, dl_next) starts in row r_first: the
+        // smallest r with diag[r] >= dl, which lies in [dl - nlt, dl] and [0, rend].
         const int dl = min(tid * IPT, tlen);
         const int dl_next = min(dl + IPT, tlen);
-        const int rend = search(tlen);
-        int r = search(dl);
-        int jl = dl - r;
-        const int r_first = r;
-        const int64_t j1 = d + tlen - (i0 + rend);
-        // j1 <= nnz whenever the row pointers end at nnz; the clamp keeps a
-        // malformed rowptr from reading past the nonzero arrays.
-        const int nloc = (int)(min(j1, nnz) - j0);
+        int lo = max(0, dl - nlt), hi = min(dl, rend);
+        while (lo < hi) {
+            const int mid = (lo + hi) >> 1;
+            if (sm.diag[mid] >= dl) hi = mid;
+            else lo = mid + 1;
+        }
+        const int r_first = lo;
 
         // (3) products of the tile's nonzeros into LDS: gather x (lanes past
         // the tile's nonzeros gather x[0]), then start the next tile's prefetch.
-        // With PF every lane gathers (x[x_safe] past the tile's nonzeros), so
-        // no branch separates the gathers from the prefetch below.
-        const bool has_nz = PF || __builtin_amdgcn_readfirstlane(nloc) > 0;
+        // With PF every lane gathers, so no branch separates the gathers from
+        // the prefetch.
+        // The next tile's row ends and columns are prefetched right after the
+        // gathers (the current columns are dead once the gathers are issued),
+        // its values after the products (which consume the current ones), so
+        // each prefetch lands in the registers the next iteration reads.
+        const bool has_nz = PF || nloc > 0;
+        const bool more = d + TILE < dend;
+        const int64_t inext = more ? i0 + rend : i0;   // the last tile re-reads itself
+        const int64_t jnext = more ? j1 : j0;          // (L2-resident) rather than branching
         T xv[IPT];
-        T vcur[IPT];
         if (has_nz) {
-            if (!PF) load_nz(j0, j0 + nloc - 1);
+            if (!PF) {           // columns first, so the gathers wait only for them
+                load_nz(j0, j0 + nloc - 1, true, false);
+                __builtin_amdgcn_sched_barrier(0);
+                load_nz(j0, j0 + nloc - 1, false, true);
+                __builtin_amdgcn_sched_barrier(0);
+            }
 #pragma unroll
             for (int u = 0; u < IPT; ++u) {
                 const int q = tid + u * BLOCK;
-                xv[u] = x[q < nloc ? (int64_t)(cn[u] - col_origin) : (PF ? x_safe : 0)];
-                vcur[u] = vn[u];
+                xv[u] = xs[q < nloc ? (uint32_t)(cn[u] - col_origin) : 0u];
             }
+            // All gathers are issued before the products wait for the first.
+            if (!PF) __builtin_amdgcn_sched_barrier(0);
         }
         if (PF) {
             // Issued after the gathers, so waiting for the gathers leaves the
-            // prefetch in flight (loads return in order).  The block's last
-            // tile re-reads itself (L2-resident) rather than branching: a
-            // conditional prefetch makes the compiler's wait before the LDS
-            // stores below cover the prefetch too.
-            const bool more = d + TILE < dend;
-            load_rowends(more ? i0 + rend : i0);
-            load_nz(more ? j1 : j0, jmax);
-            // Keep the products (which wait for the gathers) below the
-            // prefetch issue.
+            // prefetch in flight (loads return in order).
+            load_rowends(inext);
+            __builtin_amdgcn_sched_barrier(0);
+            load_nz(jnext, jmax, true, false);
             __builtin_amdgcn_sched_barrier(0);
         }
         // Stored unconditionally: entries past nloc are scratch until the row
         // sums of step (4) overwrite them (a conditional store would let the
-        // compiler sink its gather under the branch and wait on the prefetch).
+        // compiler sink its gather under the branch).
         if (has_nz) {
 #pragma unroll
-            for (int u = 0; u < IPT; ++u) sm.buf[tid + u * BLOCK] = vcur[u] * xv[u];
+            for (int u = 0; u < IPT; ++u) sm.buf[tid + u * BLOCK] = vn[u] * xv[u];
         }
+        if (PF) load_nz(jnext, jmax, false, true);
         __syncthreads();
 
-        // (4) sequential walk of this thread's slice of the merge path.
+        // (4) sequential walk of this thread's slice of the merge path: merge
+        // item s is nonzero s - r of the tile while s < diag[r], else the end
+        // of row r.
         T *ysum = sm.buf + nloc;
         T acc = T(0);
+        int r = r_first;
         for (int s = dl; s < dl_next; ++s) {
-            if ((int64_t)jl < (int64_t)sm.rowend[r] - j0) {
-                acc += sm.buf[jl];
-                ++jl;
+            if (s < sm.diag[r]) {
+                acc += sm.buf[s - r];
             } else {
                 ysum[r] = acc;
                 acc = T(0);
@@ -242,49 +324,56 @@ __device__ void merge_range(int64_t m, int64_t nnz, int64_t jmax, int64_t x_safe
             else acc += carry;
         }
 
-        // Segmented inclusive scan of (row, partial) over the block, in thread order.
-        int key = r;
-        T sv = acc;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-            const int k2 = __shfl_up(key, off, 64);
-            const T v2 = __shfl_up(sv, off, 64);
-            if (lane >= off && k2 == key) sv += v2;
-        }
+        // Segmented scan of (row, partial) over the block in thread order:
+        // within each wave by DPP, across the NW waves from their totals.
+        T sv = wave_seg_scan<T>(r, acc);
         if (lane == 63) {
-            sm.wkey[wave] = key;
+            sm.wkey[wave] = r;
             sm.wval[wave] = sv;
         }
         __syncthreads();
-        if (tid == 0) {
-            T run = sm.wval[0];
-            sm.bs[0] = run;
-            for (int w = 1; w < NW; ++w) {
-                T b = sm.wval[w];
-                if (sm.wkey[w] == sm.wkey[w - 1]) b += run;
-                sm.bs[w] = b;
-                run = b;
+        T pre = T(0);            // inclusive total of the waves before this one
+        T run = T(0);
+        int32_t pkey = -1, rkey = -1;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const int32_t kw = sm.wkey[w];
+            const T vw = sm.wval[w];
+            run = kw == rkey ? vw + run : vw;
+            rkey = kw;
+            if (w == wave - 1) {
+                pre = run;
+                pkey = kw;
             }
         }
-        __syncthreads();
-        if (wave > 0 && key == sm.wkey[wave - 1]) sv += sm.bs[wave - 1];
-        T prev = __shfl_up(sv, 1, 64);
-        if (lane == 0) prev = wave > 0 ? sm.bs[wave - 1] : T(0);
+        if (r == pkey) sv += pre;
+        // Value of the previous thread (lane 0: the previous waves' total).
+        const T prev = dpp_val<0x138, 0xf>(pre, sv);
         if (tid > 0 && r > r_first) ysum[r_first] += prev;
         __syncthreads();
 
-        // (5) finished rows i0 .. i0+rend-1.
-        for (int q = tid; q < rend; q += BLOCK) {
-            const int64_t row = i0 + q;
-            const T s = alpha * ysum[q];
-            y[row] = beta_zero ? s : s + beta * y[row];
+        // (5) finished rows i0 .. i0+rend-1.  With beta == 0 every thread
+        // stores RPT times (lanes past rend repeat the tile's last row, same
+        // value), so the count of outstanding memory operations is the same
+        // on every path and the next tile's waits stay exact.
+        if (BZ) {
+            if (rend > 0) {
+                T *yt = y + i0;
+#pragma unroll
+                for (int u = 0; u < RPT; ++u) {
+                    const int q = min(tid + u * BLOCK, rend - 1);
+                    yt[q] = alpha * ysum[q];
+                }
+            }
+        } else {
+            for (int q = tid; q < rend; q += BLOCK) {
+                const int64_t row = i0 + q;
+                y[row] = alpha * ysum[q] + beta * y[row];
+            }
         }
-        if (rend > 0) carry_has = j1 > (int64_t)sm.rowend[rend - 1];
-        else carry_has = carry_has || (j1 > j0);
-        carry = sm.bs[NW - 1];
+        carry = run;
         i0 += rend;
         j0 = j1;
-        __syncthreads();
     }
     if (tid == 0) {
         *carry_row = (i0 < m && carry_has) ? i0 : -1;
@@ -292,11 +381,11 @@ __device__ void merge_range(int64_t m, int64_t nnz, int64_t jmax, int64_t x_safe
     }
 }
 
-template <typename T, int BLOCK, int IPT, bool PF>
+template <typename T, int BLOCK, int IPT, bool PF, bool BZ>
 __global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
     int64_t m, int64_t nnz, int32_t origin, const int32_t *__restrict__ rowptr,
     const int32_t *__restrict__ colind, const T *__restrict__ val, const T *__restrict__ x,
-    T *__restrict__ y, T alpha, T beta, int beta_zero, int64_t tiles_per_block,
+    T *__restrict__ y, T alpha, T beta, int64_t tiles_per_block,
     const int64_t *__restrict__ start_rows, int64_t *__restrict__ carry_row,
     T *__restrict__ carry_val)
 {
@@ -306,9 +395,10 @@ __global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
     const int64_t dbeg = (int64_t)blockIdx.x * tiles_per_block * TILE;
     if (dbeg >= total) return;
     const int64_t dend = min(total, dbeg + tiles_per_block * (int64_t)TILE);
-    merge_range<T, BLOCK, IPT, PF, !PF>(m, nnz, nnz - 1, 0, origin, origin, rowptr, colind, val, x, y, alpha, beta,
-                               beta_zero, dbeg, dend, start_rows ? start_rows[blockIdx.x] : -1,
-                               carry_row + blockIdx.x, carry_val + blockIdx.x, sm);
+    merge_range<T, BLOCK, IPT, PF, !PF, BZ>(m, nnz, nnz - 1, origin, origin, rowptr,
+                                            colind, val, x, y, alpha, beta, dbeg, dend,
+                                            start_rows ? start_rows[blockIdx.x] : -1,
+                                            carry_row + blockIdx.x, carry_val + blockIdx.x, sm);
 }
 
 struct SliceInfo {
@@ -340,11 +430,14 @@ __global__ __launch_bounds__(BLOCK) void csr_spmv_sliced_kernel(
         return;
     }
     const int64_t dend = min(total, dbeg + info.tiles[s] * (int64_t)TILE);
-    merge_range<T, BLOCK, IPT, true, NT>(m, nnz_s, info.off[NUM_XCD] - 1 - off, -s * slice_w, off, 0,
-                               rowptr_all + s * (m + 1), colind_all + off,
-                               val_all + off, x + s * slice_w, ypart + s * m, T(1), T(0), 1,
-                               dbeg, dend, start_rows ? start_rows[slot] : -1, carry_row + slot,
-                               carry_val + slot, sm);
+    // An empty slice gathers only xs[0]; its columns may start past x's end.
+    const T *xs = nnz_s > 0 ? x + s * slice_w : x;
+    merge_range<T, BLOCK, IPT, true, NT, true>(m, nnz_s, info.off[NUM_XCD] - 1 - off, off, 0,
+                                               rowptr_all + s * (m + 1), colind_all + off,
+                                               val_all + off, xs, ypart + s * m,
+                                               T(1), T(0), dbeg, dend,
+                                               start_rows ? start_rows[slot] : -1, carry_row + slot,
+                                               carry_val + slot, sm);
 }
 
 // Adds each run of equal-row carries (in block order) of each segment into
@@ -463,18 +556,18 @@ struct SpmvGrid {
 };
 
 // Items per thread (tile = 256 * ipt merge items): JLUST_HIP_SPMV_IPT in
-// {4, 8, 16}, default 4.
+// {4, 8}, default 8.
 int spmv_ipt()
 {
     static const int v = [] {
         const char *e = getenv("JLUST_HIP_SPMV_IPT");
-        const int x = e ? atoi(e) : 4;
-        return (x == 4 || x == 8 || x == 16) ? x : 4;
+        const int x = e ? atoi(e) : 8;
+        return x == 4 ? 4 : 8;
     }();
     return v;
 }
 
-#define JLUST_SPMV_IPT_DISPATCH(ipt, F) ((ipt) == 4 ? F(4) : (ipt) == 16 ? F(16) : F(8))
+#define JLUST_SPMV_IPT_DISPATCH(ipt, F) ((ipt) == 4 ? F(4) : F(8))
 
 // Merge-kernel variant: plain (row ends, then col/val, then x, per tile),
 // plain with register prefetch, or column-sliced (prefetching).
@@ -500,9 +593,18 @@ int spmv_occupancy_ipt(int dev, int *occ_out)
         if (KIND == SPMV_SLICED)
             JLUST_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
                 &nb, csr_spmv_sliced_kernel<T, SPMV_BLOCK, IPT, false>, SPMV_BLOCK, 0));
-        else
+        else {
+            // The grid is sized before beta is known: the smaller occupancy of
+            // the beta == 0 and beta != 0 instances.
+            int nb2 = 0;
             JLUST_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
-                &nb, csr_spmv_merge_kernel<T, SPMV_BLOCK, IPT, KIND == SPMV_PLAIN_PF>, SPMV_BLOCK, 0));
+                &nb, csr_spmv_merge_kernel<T, SPMV_BLOCK, IPT, KIND == SPMV_PLAIN_PF, true>,
+                SPMV_BLOCK, 0));
+            JLUST_HIP_TRY(hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &nb2, csr_spmv_merge_kernel<T, SPMV_BLOCK, IPT, KIND == SPMV_PLAIN_PF, false>,
+                SPMV_BLOCK, 0));
+            nb = nb2 < nb ? nb2 : nb;
+        }
         occ = nb > 0 ? nb : 1;
     }
     *occ_out = occ;
@@ -565,19 +667,17 @@ int spmv_launch(int64_t m, int64_t nnz, int32_t origin, const int32_t *rowptr,
                 const SpmvGrid &g, int ipt, const int64_t *start_rows, int64_t *carry_row,
                 T *carry_val, hipStream_t stream)
 {
-#define G(I, P)                                                                                  \
-    hipLaunchKernelGGL((csr_spmv_merge_kernel<T, SPMV_BLOCK, I, P>), dim3((unsigned)g.nblocks), \
-                       dim3(SPMV_BLOCK), 0, stream, m, nnz, origin, rowptr, colind, val, x, y,  \
-                       alpha, beta, (int)(beta == T(0)), g.tiles_per_block, start_rows,         \
-                       carry_row, carry_val)
+#define H(I, P, B)                                                                                \
+    hipLaunchKernelGGL((csr_spmv_merge_kernel<T, SPMV_BLOCK, I, P, B>), dim3((unsigned)g.nblocks), \
+                       dim3(SPMV_BLOCK), 0, stream, m, nnz, origin, rowptr, colind, val, x, y,    \
+                       alpha, beta, g.tiles_per_block, start_rows, carry_row, carry_val)
+#define G(I, P) do { if (beta == T(0)) H(I, P, true); else H(I, P, false); } while (0)
 #define F(I) do { if (g.pf) G(I, true); else G(I, false); } while (0)
-    switch (ipt) {
-    case 4: F(4); break;
-    case 16: F(16); break;
-    default: F(8); break;
-    }
+    if (ipt == 4) F(4);
+    else F(8);
 #undef F
 #undef G
+#undef H
     if (int st = check_launch("csr_spmv_merge_kernel")) return st;
     // A single block ends on the last row end, so it never leaves a carry.
     if (g.nblocks > 1) {
@@ -875,11 +975,8 @@ static int plan_execute(jlust_spmv_plan_t plan, int want_type, T alpha, const T 
                        plan->slice_w, ypart, plan->nb, plan->start_rows, plan->carry_row,       \
                        (T *)plan->carry_val)
 #define F(I) do { if (nt) G(I, true); else G(I, false); } while (0)
-    switch (plan->ipt) {
-    case 4: F(4); break;
-    case 16: F(16); break;
-    default: F(8); break;
-    }
+    if (plan->ipt == 4) F(4);
+    else F(8);
 #undef F
 #undef G
     if (int st = check_launch("csr_spmv_sliced_kernel")) return st;
