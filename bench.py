@@ -83,10 +83,57 @@ def gather_ceiling():
             e.record()
             torch.cuda.synchronize()
             t = s.elapsed_time(e) / reps * 1e-3
-            res.append({"elem_bytes": elem_bytes, "source_MB": mb, "gathers": count,
-                        "ms": round(t * 1e3, 4), "gathered_GBps": round(count * elem_bytes / t / 1e9, 1),
+            res.append({"kernel": "torch.index_select", "elem_bytes": elem_bytes, "source_MB": mb,
+                        "gathers": count, "ms": round(t * 1e3, 4),
+                        "gathered_GBps": round(count * elem_bytes / t / 1e9, 1),
                         "Ggathers_per_s": round(count / t / 1e9, 2)})
             del src, idx, out
+    res += gather_probe()
+    return res
+
+
+def gather_probe():
+    """8-byte random gathers by jlust_amd/csrc/gather_probe.hip (8 per thread),
+    from the whole source or, XCD-sliced, from source/8 per XCD (the access
+    pattern of the column-sliced SpMV plan)."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "jlust_amd", "libjlust_probe.so"))
+    lib.jlust_probe_gather_f64.restype = ctypes.c_int
+    lib.jlust_probe_gather_f64.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                           ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
+                                           ctypes.c_uint32, ctypes.c_void_p]
+    total = 64 * 2**20
+    nthreads = total // 8
+    idx = torch.empty(total, dtype=torch.int32, device="cuda")
+    out = torch.empty(nthreads, dtype=torch.float64, device="cuda")
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    res = []
+    for sliced in (0, 1):
+        for mb in (1, 4, 8, 32, 256):
+            n = mb * 2**20 // 8
+            rng = n // 8 if sliced else n
+            src = torch.rand(n, dtype=torch.float64, device="cuda")
+            idx.random_(0, rng, generator=g)
+            call = lambda: lib.jlust_probe_gather_f64(src.data_ptr(), n, idx.data_ptr(), out.data_ptr(),
+                                                      nthreads, sliced, rng, stream.cuda_stream)
+            for _ in range(3):
+                assert call() == 0
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 10
+            s.record(stream)
+            for _ in range(reps):
+                call()
+            e.record(stream)
+            torch.cuda.synchronize()
+            t = s.elapsed_time(e) / reps * 1e-3
+            res.append({"kernel": "gather_probe" + (" xcd-sliced" if sliced else ""), "elem_bytes": 8,
+                        "source_MB": mb, "per_xcd_MB": mb / 8 if sliced else mb, "gathers": total,
+                        "ms": round(t * 1e3, 4), "gathered_GBps": round(total * 8 / t / 1e9, 1),
+                        "Ggathers_per_s": round(total / t / 1e9, 2)})
+            del src
     return res
 
 
@@ -131,7 +178,7 @@ def build_step(cfg, use_plan=False):
         A = J.bsr_tensor(dev(cfg["browptr"]), dev(cfg["bcolind"]), dev(cfg["val"]), (m, n))
         B = dev(cfg["B"])
         C = J.dense_matrix(m, cfg["k"], dtype=torch.float32)
-        return (lambda: J.execute(J.SpMMOp, A, B, C)), "bsr16_spmm_mfma_kernel", "mfma", (A, B, C)
+        return (lambda: J.execute(J.SpMMOp, A, B, C)), "bsr16_spmm_rowwave_kernel", "mfma", (A, B, C)
     raise ValueError(kind)
 
 

@@ -119,6 +119,107 @@ __global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_mfma_kernel(
     }
 }
 
+// Row-wave kernel (row-major blocks, B and C float4-aligned).  One wave owns
+// one block-row.  Column-major B with a large ldb puts every column in its own
+// memory page, so loading B in the MFMA operand layout (16 columns per
+// instruction) costs 16 address translations per load.  Here each 16-column
+// tile of B is loaded down the columns instead -- lane l covers block
+// sq = l/8 of the chunk, rows 4*((l/2)%4) .. +3, column 2t + l%2 of load t --
+// so one load touches 2 columns, and is transposed into the MFMA layout
+// through a per-wave LDS area.  Load t lands at t*BSR_LSTRIDE + 16*l bytes;
+// the 32-byte pad per load puts column i of an MFMA operand read at bank
+// 4*i (mod 64), so its 16 lanes hit distinct banks.  The chunk's A operands (up to BSR_QCHUNK blocks) stay in
+// registers for all of k; the next tile's B is loaded while the current
+// tile's MFMAs run.
+constexpr int BSR_QCHUNK = 8;
+constexpr int BSR_LSTRIDE = 1024 + 32;
+
+template <bool BZ>
+__global__ __launch_bounds__(256) void bsr16_spmm_rowwave_kernel(
+    int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
+    const int32_t *__restrict__ bcolind, const float *__restrict__ val, int64_t k, float alpha,
+    const float *__restrict__ B, int64_t ldb, float beta, float *__restrict__ C, int64_t ldc)
+{
+    __shared__ __align__(16) char lds[4][BSR_QCHUNK * BSR_LSTRIDE];
+    // XCD-major remap (grid padded to a multiple of 8): XCD x takes a
+    // contiguous band of block-rows, so the B rows the band shares stay in
+    // that XCD's L2.
+    const int64_t per_xcd = (int64_t)gridDim.x / NUM_XCD;
+    const int64_t wg = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int64_t R = wg * 4 + wave;
+    if (R >= mb) return;                   // whole waves only; no block barrier follows
+
+    char *ws = lds[wave];
+    const int i = lane & 15;               // MFMA: A row / B, C column in the tile
+    const int g = lane >> 4;               // MFMA: contraction group / C row group
+    const int sq = lane >> 3;              // staging: block of the chunk
+    const int srow = 4 * ((lane >> 1) & 3);
+    const int sj = lane & 1;
+    const int64_t crow = R * BSR_BS + 4 * g;
+    const int64_t q0 = (int64_t)browptr[R] - origin;
+    const int64_t q1 = (int64_t)browptr[R + 1] - origin;
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+
+    if (q1 <= q0) {                        // empty block-row: C = beta*C
+        for (int64_t c0 = 0; c0 < k; c0 += 16) {
+            const int64_t col = c0 + i;
+            if (col >= k) continue;
+            floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + col * ldc);
+            *dst = BZ ? zero : beta * *dst;
+        }
+        return;
+    }
+    for (int64_t qb = q0; qb < q1; qb += BSR_QCHUNK) {
+        const int nq = (int)min((int64_t)BSR_QCHUNK, q1 - qb);
+        const bool first = qb == q0;
+        floatx4 a[BSR_QCHUNK];
+#pragma unroll
+        for (int qq = 0; qq < BSR_QCHUNK; ++qq)
+            a[qq] = qq < nq ? *reinterpret_cast<const floatx4 *>(val + (qb + qq) * 256 + i * 16 + 4 * g)
+                            : zero;
+        // Staging lanes past the chunk's blocks repeat its last block (their
+        // LDS slots are never read).
+        const int64_t sb = (int64_t)bcolind[qb + min(sq, nq - 1)] - origin;
+        const float *bsrc = B + sb * BSR_BS + srow;
+        floatx4 st[8];
+        auto load_tile = [&](int64_t c0) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t) {
+                const int64_t col = min(c0 + 2 * t + sj, k - 1);
+                st[t] = *reinterpret_cast<const floatx4 *>(bsrc + col * ldb);
+            }
+        };
+        load_tile(0);
+        for (int64_t c0 = 0; c0 < k; c0 += 16) {
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                *reinterpret_cast<floatx4 *>(ws + t * BSR_LSTRIDE + lane * 16) = st[t];
+            if (c0 + 16 < k) load_tile(c0 + 16);
+            floatx4 acc = zero;
+            const char *rd = ws + (i >> 1) * BSR_LSTRIDE + (g * 2 + (i & 1)) * 16;
+#pragma unroll
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+                if (qq < nq) {
+                    const floatx4 b = *reinterpret_cast<const floatx4 *>(rd + qq * 128);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[qq][u], b[u], acc, 0, 0, 0);
+                }
+            }
+            const int64_t col = c0 + i;
+            if (col < k) {
+                floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + col * ldc);
+                floatx4 out = alpha * acc;
+                if (!first) out += *dst;
+                else if (!BZ) out += beta * *dst;
+                *dst = out;
+            }
+        }
+    }
+}
+
 int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
              const int32_t *browptr, const int32_t *bcolind, const float *val,
              int row_major_blocks, int64_t k, float alpha, const float *B, int64_t ldb,
@@ -157,6 +258,17 @@ int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
     const bool rm = row_major_blocks && vals_aligned;
     if (row_major_blocks && !vals_aligned)
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: block values must be 16-byte aligned");
+    if (rm && vec) {
+        const int64_t wgs = (mb + 3) / 4;
+        const int64_t grid4 = (wgs + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+        if (beta == 0.f)
+            hipLaunchKernelGGL((bsr16_spmm_rowwave_kernel<true>), dim3((unsigned)grid4), dim3(256), 0, s,
+                               mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
+        else
+            hipLaunchKernelGGL((bsr16_spmm_rowwave_kernel<false>), dim3((unsigned)grid4), dim3(256), 0, s,
+                               mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
+        return check_launch("bsr16_spmm_rowwave_kernel");
+    }
     if (rm && vec) JLUST_BSR_LAUNCH(true, true);
     else if (rm) JLUST_BSR_LAUNCH(true, false);
     else if (vec) JLUST_BSR_LAUNCH(false, true);

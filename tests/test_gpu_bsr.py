@@ -157,3 +157,51 @@ def test_bsr_unsupported_block_size(J):
                      dev(np.ones(64, np.float32)), (8, 8), (8, 8))
     with pytest.raises(J.UnsupportedFormat):
         J.execute(J.SpMMOp, A, dev(np.ones((8, 4), np.float32)), J.dense_matrix(8, 4, dtype=torch.float32))
+
+
+@pytest.mark.parametrize("beta", [0.0, -0.5])
+def test_bsr_long_block_rows(J, O, beta):
+    """Block-rows with more blocks than one register chunk (8): the partial
+    products of later chunks are added onto C."""
+    mb, nb, k = 12, 40, 48
+    browptr, bcolind, val = random_bsr(mb, nb, 19, seed=11)
+    B = np.asfortranarray(np.random.default_rng(5).standard_normal((nb * 16, k)).astype(np.float32))
+    C0 = np.asfortranarray(np.random.default_rng(6).standard_normal((mb * 16, k)).astype(np.float32))
+    C = run_bsr(J, browptr, bcolind, val, B, mb, nb, alpha=0.75, beta=beta, C0=C0)
+    ref = O.bsr_spmm(browptr, bcolind, val, 16, B, 0.75, beta, C0)
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
+    absref = O.csr_spmm_absref(rp, ci, v, B, 0.75, beta, C0)
+    assert_within(C, ref, absref, np.float32, f"19 blocks per block-row, beta={beta}")
+
+
+def test_bsr_empty_block_rows_beta(J, O):
+    mb, nb, k = 10, 10, 20
+    browptr = np.array([1, 1, 3, 3, 3, 4, 4, 4, 4, 4, 5], np.int32)
+    bcolind = np.array([1, 10, 5, 2], np.int32)
+    val = np.random.default_rng(0).standard_normal(4 * 256).astype(np.float32)
+    B = np.asfortranarray(np.random.default_rng(1).standard_normal((160, k)).astype(np.float32))
+    C0 = np.asfortranarray(np.random.default_rng(2).standard_normal((160, k)).astype(np.float32))
+    C = run_bsr(J, browptr, bcolind, val, B, mb, nb, alpha=2.0, beta=3.0, C0=C0)
+    ref = O.bsr_spmm(browptr, bcolind, val, 16, B, 2.0, 3.0, C0)
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
+    absref = O.csr_spmm_absref(rp, ci, v, B, 2.0, 3.0, C0)
+    assert_within(C, ref, absref, np.float32, "empty block-rows, beta=3")
+
+
+def test_bsr_unaligned_leading_dims(J, O):
+    """ldb and ldc not multiples of 4: the scalar-access kernel."""
+    import torch
+    mb, nb, k = 9, 11, 24
+    browptr, bcolind, val = random_bsr(mb, nb, 3, seed=21)
+    Bbig = np.asfortranarray(np.random.default_rng(7).standard_normal((nb * 16 + 1, k)).astype(np.float32))
+    A = J.bsr_tensor(dev(browptr), dev(bcolind), dev(val), (mb * 16, nb * 16), (16, 16))
+    Bd = dev(Bbig)[: nb * 16]
+    Cbig = torch.full((k, mb * 16 + 3), float("nan"), dtype=torch.float32, device="cuda").t()
+    Cd = Cbig[: mb * 16]
+    from jlust_amd.tensor import leading_dim
+    assert leading_dim(Bd) == nb * 16 + 1 and leading_dim(Cd) == mb * 16 + 3
+    J.execute(J.SpMMOp, A, Bd, Cd)
+    ref = O.bsr_spmm(browptr, bcolind, val, 16, np.asfortranarray(Bbig[: nb * 16]))
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
+    absref = O.csr_spmm_absref(rp, ci, v, np.asfortranarray(Bbig[: nb * 16]))
+    assert_within(host(Cd), ref, absref, np.float32, "unaligned leading dimensions")
