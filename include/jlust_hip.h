@@ -45,6 +45,7 @@ extern "C" {
 
 typedef void *jlust_stream_t;                 /* hipStream_t */
 typedef struct jlust_spmv_plan *jlust_spmv_plan_t;
+typedef struct jlust_convert *jlust_convert_t;
 
 /*
  * Status codes.  The Julia side maps them onto the reference's exception
@@ -218,6 +219,84 @@ int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs,
                                int64_t k, float alpha, const float *B,
                                int64_t ldb, float beta, float *C, int64_t ldc,
                                jlust_stream_t stream);
+
+/* ----------------------------------------------------------- conversions */
+
+/* Sparse matrix formats of the conversion entry points
+ * (src/named_formats.jl:24-27,106-128). */
+enum jlust_format {
+    JLUST_FORMAT_CSR = 0,   /* (i : dense, j : compressed)                        */
+    JLUST_FORMAT_CSC = 1,   /* (j : dense, i : compressed)                        */
+    JLUST_FORMAT_COO = 2,   /* (i : compressed(nonunique), j : singleton)         */
+    JLUST_FORMAT_DCSR = 3,  /* (i : compressed, j : compressed)                   */
+    JLUST_FORMAT_BSR = 4    /* BSRRight/BSRLeft((b1, b2)): (i/b1 : dense, j/b2 :
+                               compressed, then the in-block levels)            */
+};
+
+/*
+ * A 2-D sparse matrix: the level buffers of a USTensor (src/tensor.jl:33-44)
+ * as device pointers.  Index values are origin-based Int32 (origin 0 or 1).
+ *   CSR : pos2 = rowptr[m+1], crd2 = colind[nnz]
+ *   CSC : pos2 = colptr[n+1], crd2 = rowind[nnz]
+ *   COO : pos1 = {origin, nnz+origin} (may be NULL on input), crd1 = rows, crd2 = cols
+ *   DCSR: pos1 = {origin, nouter+origin}, crd1 = stored rows[nouter],
+ *         pos2 = row segments[nouter+1], crd2 = cols[nnz]
+ *   BSR : pos2 = browptr[m/b1+1], crd2 = bcolind[nouter] (nouter = nnzb),
+ *         nnz = nouter*b1*b2 values, block-major, row-major inside a block
+ *         when row_major_blocks != 0
+ * val holds nnz Float64 or Float32 values (value_type 0 / 1).
+ */
+typedef struct jlust_sparse {
+    int32_t format;
+    int32_t origin;
+    int64_t m, n;
+    int32_t b1, b2, row_major_blocks;
+    int64_t nnz;
+    int64_t nouter;
+    int32_t *pos1, *crd1, *pos2, *crd2;
+    void *val;
+} jlust_sparse;
+
+/*
+ * convert_format(u, fmt) (src/convert.jl:302-388) on the GPU, step 1 of 2:
+ * decomposes src, drops explicit zeros, sorts stably by the target's level
+ * coordinates (unless the target is the identity ordering and the source is
+ * an ordered identity format, convert.jl:331-349) and merges adjacent equal
+ * coordinates on unique levels keeping the first value (convert.jl:232-250).
+ * Reports the target's sizes: *dst_nnz values and *dst_nouter (DCSR stored
+ * rows, BSR blocks; 0 otherwise).  Synchronises `stream`.  The handle owns
+ * the analysed entries until jlust_hip_convert_destroy; src must stay valid
+ * until jlust_hip_convert_fill.  dst_b1/dst_b2/dst_row_major_blocks describe
+ * a BSR target.  Returns NONCANONICAL_STORAGE where the reference asserts
+ * (a CSR target built from rows in decreasing order).
+ */
+int jlust_hip_convert_analyze(const jlust_sparse *src, int32_t dst_format,
+                              int32_t dst_b1, int32_t dst_b2,
+                              int32_t dst_row_major_blocks, int value_type,
+                              jlust_stream_t stream, jlust_convert_t *out,
+                              int64_t *dst_nnz, int64_t *dst_nouter);
+
+/* Step 2: writes the target's buffers (caller-allocated with the sizes from
+ * analyze; origin, extents and format equal to the source's and the analysed
+ * target), stream-ordered. */
+int jlust_hip_convert_fill(jlust_convert_t h, const jlust_sparse *dst,
+                           jlust_stream_t stream);
+
+/* Frees the handle's device memory (after the fills that use it). */
+int jlust_hip_convert_destroy(jlust_convert_t h);
+
+/*
+ * sparse_to_dense (ext/KernelAbstractionsExt/ops/conversion.jl:47-65): the
+ * m x n column-major `dense` (leading dimension ld) is zero-filled and every
+ * stored entry written at its (row, col).  Synchronises `stream`.
+ */
+int jlust_hip_sparse_to_dense(const jlust_sparse *src, int value_type,
+                              void *dense, int64_t ld, jlust_stream_t stream);
+
+/* dst[i] = src[i] + delta (dst == src allowed): the index shift of
+ * materialize's origin change (ext/CUDAExt/CUDAExt.jl:199-220). */
+int jlust_hip_shift_index(int32_t *dst, const int32_t *src, int64_t len,
+                          int32_t delta, jlust_stream_t stream);
 
 #ifdef __cplusplus
 }

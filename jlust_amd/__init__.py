@@ -20,6 +20,8 @@ from .formats import (CompressedLevel, DenseLevel, Formats, SingletonLevel, Tens
 from .ops import (AbstractKernelHandle, AbstractUSTBackend, HIPBackend, Op, OpType, SDDMMOp,
                   SpMMOp, SpMVOp, default_backend, execute, matmul, mul_, prepare,
                   supports_backend, update_values_)
+from .convert import (convert_format, convert_index_type, convert_value_type, csc_tensor,
+                      dcsr_tensor, sparse_to_dense)
 from .tensor import (CPUDevice, HIPDevice, OneBased, USTensor, ZeroBased, bsr_tensor,
                      coo_tensor, coordinates, csr_tensor, dense_matrix, extents, format,
                      has_coordinates, has_positions, index_origin, materialize, nnz, nonzeros,

@@ -221,13 +221,27 @@ def materialize(u: USTensor, device, origin: Optional[AbstractIndexOrigin] = Non
     asked, change the index origin by shifting pos/crd by +-1
     (ext/CUDAExt/CUDAExt.jl:199-220)."""
     tdev = torch.device("cpu") if isinstance(device, CPUDevice) else device.torch
-    mv = lambda b: None if b is None else b.to(tdev)  # noqa: E731
-    pos = tuple(mv(b) for b in u.pos_buffers)
-    crd = tuple(mv(b) for b in u.crd_buffers)
-    val = u.val.to(tdev)
     new_origin = u.origin if origin is None else origin
-    if new_origin != u.origin:
-        shift = new_origin.offset - u.origin.offset
-        pos = tuple(None if b is None else b + shift for b in pos)
-        crd = tuple(None if b is None else b + shift for b in crd)
+    shift = new_origin.offset - u.origin.offset
+    pos, crd = u.pos_buffers, u.crd_buffers
+    if shift:
+        # The index shift runs on the HIP device (jlust_hip_shift_index): on
+        # the source's buffers when they live there, else after the move.
+        from .convert import shift_index
+        sh = lambda b: None if b is None else shift_index(b, shift)  # noqa: E731
+        if u.val.device.type == "cuda":
+            pos, crd = tuple(sh(b) for b in pos), tuple(sh(b) for b in crd)
+            shift = 0
+        elif tdev.type != "cuda":
+            from .errors import UnsupportedFormat
+            raise UnsupportedFormat(u.format.name, "HIPBackend",
+                                    "an origin change runs on the HIP device; move the tensor there")
+    mv = lambda b: None if b is None else b.to(tdev)  # noqa: E731
+    pos = tuple(mv(b) for b in pos)
+    crd = tuple(mv(b) for b in crd)
+    val = u.val.to(tdev)
+    if shift:
+        from .convert import shift_index
+        pos = tuple(None if b is None else shift_index(b, shift) for b in pos)
+        crd = tuple(None if b is None else shift_index(b, shift) for b in crd)
     return USTensor(u.extents, u.format, pos, crd, val, None, new_origin)
