@@ -53,7 +53,69 @@ def parse():
                    help="only run a 1 GiB device copy (PMC byte-counter calibration)")
     p.add_argument("--gather-ceiling", action="store_true",
                    help="only measure random-gather bandwidth (8 B and 512 B rows) per source size")
+    p.add_argument("--convert", action="store_true",
+                   help="only time format conversions (convert_format) at config sizes")
     return p.parse_args()
+
+
+def convert_bench(cpu_seconds):
+    """Format conversions at BASELINE sizes: GPU convert_format (analyse +
+    fill, as a caller sees it) and the numpy restatement of src/convert.jl on
+    the host (the reference's convert_format runs on the CPU only).  Bytes =
+    source buffers + target buffers, each counted once."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    from oracle import convert_oracle as CO
+    res = []
+
+    def nbytes(u):
+        return sum(b.numel() * b.element_size() for b in (*u.pos_buffers, *u.crd_buffers, u.val)
+                   if b is not None)
+
+    def run(name, u, fmt, src_dict, target, extra=()):
+        out = J.convert_format(u, fmt)
+        torch.cuda.synchronize()
+        reps = 5
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            out = J.convert_format(u, fmt)
+        torch.cuda.synchronize()
+        t = (time.perf_counter() - t0) / reps
+        b = nbytes(u) + nbytes(out)
+        t1 = time.perf_counter()
+        CO.convert_format(src_dict, target, *extra)
+        tc = time.perf_counter() - t1
+        res.append({"conversion": name, "nnz_in": int(u.val.numel()), "nnz_out": int(out.val.numel()),
+                    "ms": round(t * 1e3, 3), "GBps": round(b / t / 1e9, 1),
+                    "cpu_numpy_ms": round(tc * 1e3, 1), "speedup_vs_cpu": round(tc / t, 1)})
+        log(f"{name}: {t*1e3:.2f} ms GPU, {tc*1e3:.0f} ms numpy")
+
+    cfg = W.make(2)
+    m, n = cfg["m"], cfg["n"]
+    u = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (m, n))
+    s = dict(format="CSR", origin=1, m=m, n=n, pos2=cfg["rowptr"], crd2=cfg["colind"], val=cfg["val"])
+    run("config2 CSR->CSC", u, J.Formats.CSC, s, "CSC")
+    run("config2 CSR->COO", u, J.Formats.COO, s, "COO")
+    q = J.convert_format(u, J.Formats.COO)
+    sq = dict(format="COO", origin=1, m=m, n=n, crd1=host_np(q.crd_buffers[0]),
+              crd2=host_np(q.crd_buffers[1]), val=host_np(q.val))
+    run("config2 COO->CSR", q, J.Formats.CSR, sq, "CSR")
+    del u, q, s, sq, cfg
+    cfg = W.make(5)
+    b = J.bsr_tensor(dev(cfg["browptr"]), dev(cfg["bcolind"]), dev(cfg["val"]), (cfg["m"], cfg["n"]))
+    sb = dict(format="BSR", origin=1, m=cfg["m"], n=cfg["n"], b1=16, b2=16, row_major=True,
+              pos2=cfg["browptr"], crd2=cfg["bcolind"], val=cfg["val"])
+    run("config5 BSR->CSR", b, J.Formats.CSR, sb, "CSR")
+    c = J.convert_format(b, J.Formats.CSR)
+    sc = dict(format="CSR", origin=1, m=cfg["m"], n=cfg["n"], pos2=host_np(c.pos_buffers[1]),
+              crd2=host_np(c.crd_buffers[1]), val=host_np(c.val))
+    run("config5 CSR->BSR16", c, J.Formats.BSRRight((16, 16)), sc, "BSR", (16, 16, True))
+    return res
+
+
+def host_np(t):
+    return t.detach().cpu().numpy()
 
 
 def gather_ceiling():
@@ -301,6 +363,9 @@ def main():
         return
     if args.gather_ceiling:
         print(json.dumps({"gather_ceiling": gather_ceiling()}), flush=True)
+        return
+    if args.convert:
+        print(json.dumps({"convert": convert_bench(args.cpu_seconds)}), flush=True)
         return
     from jlust_amd import workloads as W
 
