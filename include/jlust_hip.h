@@ -298,6 +298,65 @@ int jlust_hip_sparse_to_dense(const jlust_sparse *src, int value_type,
 int jlust_hip_shift_index(int32_t *dst, const int32_t *src, int64_t len,
                           int32_t delta, jlust_stream_t stream);
 
+/* ------------------------------------------------------- block assembly */
+
+/*
+ * One block of an assembled matrix: a CSR or DCSR matrix (`block`), or, when
+ * block == NULL, a shifted scaled identity of extents diag_m x diag_n whose
+ * row r holds diag_val at column r + diag_shift where that column exists
+ * (Formats.ShiftedDiag, src/named_formats.jl:53-61), placed with its (0, 0)
+ * at (row_off, col_off) of the result (0-based).  When slots != NULL it
+ * receives, for each stored value k of a CSR/DCSR block, the position of
+ * that value in the assembled colind/val.
+ */
+typedef struct jlust_placement {
+    const jlust_sparse *block;
+    int64_t row_off, col_off;
+    int64_t diag_m, diag_n, diag_shift;
+    double diag_val;
+    int32_t *slots;
+} jlust_placement;
+
+/*
+ * The m x n CSR (origin 0) of a block aggregate: row R holds, for each
+ * placement covering R in the given order, that block row's stored entries
+ * in storage order (explicit zeros included) with columns shifted by
+ * col_off.  rowptr[m+1], colind[nnz], val[nnz] are caller-allocated; nnz
+ * must equal the placements' stored values.  Synchronises `stream`.  Invalid
+ * block storage returns NONCANONICAL_STORAGE.  Replaces the host assembly
+ * of _compile_bsm (ext/CUDAExt/ops/block_mul.jl:128-224) and _compile_bbm
+ * (:453-556).
+ */
+int jlust_hip_csr_assemble(int64_t m, int64_t n, int32_t nplacements,
+                           const jlust_placement *placements, int value_type,
+                           int32_t *rowptr, int32_t *colind, void *val,
+                           int64_t nnz, jlust_stream_t stream);
+
+/*
+ * dst[slots[k]] = src[k] for k < len (slots outside [0, dst_len) are
+ * skipped): new values of one block into an assembled matrix, the compiled
+ * view update of update_block_values! (ext/CUDAExt/ops/block_mul.jl:310-336).
+ */
+int jlust_hip_scatter_values(void *dst, int64_t dst_len, const int32_t *slots,
+                             const void *src, int64_t len, int value_type,
+                             jlust_stream_t stream);
+
+/*
+ * y = alpha*A*x + beta*y for the m x n shifted scaled identity A: row r holds
+ * val at column r + shift where that column exists, and nothing else
+ * (Formats.ShiftedDiag, src/named_formats.jl:53-61, whose level yields
+ * (r + shift, val) per row, src/backends.jl:223-227).  beta == 0 writes y
+ * without reading it.
+ */
+int jlust_hip_shifted_diag_spmv_f64(int64_t m, int64_t n, int64_t shift,
+                                    double val, double alpha, const double *x,
+                                    double beta, double *y,
+                                    jlust_stream_t stream);
+int jlust_hip_shifted_diag_spmv_f32(int64_t m, int64_t n, int64_t shift,
+                                    float val, float alpha, const float *x,
+                                    float beta, float *y,
+                                    jlust_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

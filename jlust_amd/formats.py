@@ -12,6 +12,8 @@ expression of the dimension coordinates (i, j):
                       j%b2 : dense(b2))                  named_formats.jl:106-116
   BSRLeft((b1,b2))   same with the two inner levels swapped, :118-128
   DensedRight(N)     N dense levels (plain column-major arrays), :219-227
+  ShiftedDiag(T; shift, val)  (i : dense, j : shifted diagonal): row r holds
+                     val at column r + shift, no buffers, :53-61
 
 Only the level *types* drive operator dispatch (dense outer + compressed
 inner = CSR-shaped, compressed non-unique + singleton = COO-shaped, blocked =
@@ -46,6 +48,17 @@ class CompressedLevel:
 class SingletonLevel:
     def __repr__(self):
         return "SingletonLevel"
+
+
+@dataclass(frozen=True)
+class ShiftedDiagLevel:
+    """src/formats.jl:47-74: row r holds one entry at column r + shift with
+    the constant value val; the level stores no buffers."""
+    shift: int = 0
+    val: float = 1.0
+
+    def __repr__(self):
+        return f"ShiftedDiagLevel(shift={self.shift}, val={self.val})"
 
 
 @dataclass(frozen=True, eq=False)
@@ -120,6 +133,15 @@ class Formats:
                             n, ident, ident, ident)
 
     @staticmethod
+    def ShiftedDiag(dtype=None, shift: int = 0, val=1.0) -> TensorFormat:
+        """src/named_formats.jl:53-61; val is rounded to dtype (Float64 by default)."""
+        import torch
+        dtype = torch.float64 if dtype is None else dtype
+        v = float(torch.tensor(float(val), dtype=dtype).item())
+        return _make2(f"ShiftedDiag(shift={int(shift)},val={v})",
+                      [DenseLevel(), ShiftedDiagLevel(int(shift), v)], "ShiftedDiag", _ident2())
+
+    @staticmethod
     def BSRRight(blocksize) -> TensorFormat:
         b1, b2 = blocksize
         return _make2(
@@ -152,6 +174,13 @@ def is_coo_shaped(fmt: TensorFormat) -> bool:
     lv = fmt.levels
     return len(lv) >= 2 and isinstance(lv[0], CompressedLevel) and not lv[0].unique and \
         isinstance(lv[1], SingletonLevel)
+
+
+def is_shifted_diag(fmt: TensorFormat) -> bool:
+    """(Dense, ShiftedDiag): the shape the block compile recognises
+    (ext/CUDAExt/ops/block_mul.jl:60-69)."""
+    lv = fmt.levels
+    return len(lv) == 2 and isinstance(lv[0], DenseLevel) and isinstance(lv[1], ShiftedDiagLevel)
 
 
 def is_bsr(fmt: TensorFormat) -> bool:

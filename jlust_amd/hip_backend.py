@@ -15,7 +15,7 @@ import torch
 from . import _lib
 from .errors import (DeviceMismatch, IncompatibleExtents, NonCanonicalStorage,
                      UnsupportedFormat, UnsupportedIndexType, UnsupportedValueType)
-from .formats import bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped
+from .formats import bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped, is_shifted_diag
 from .ops import AbstractKernelHandle, HIPBackend, Op, SDDMMOp, SpMMOp, SpMVOp
 from .tensor import USTensor, leading_dim, nnz, nonzeros
 
@@ -41,7 +41,8 @@ def supports(op: Op) -> bool:
     """Capability table (the counterpart of KernelAbstractionsExt.jl:31-41)."""
     f = op.formats
     if op.tag == "SpMV" and len(f) == 3:
-        return (is_csr_shaped(f[0]) or is_coo_shaped(f[0])) and _dense_fmt(f[1]) and \
+        return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_shifted_diag(f[0])) and \
+            _dense_fmt(f[1]) and \
             _dense_fmt(f[2]) and f[1].ndims == 1 and f[2].ndims == 1
     if op.tag == "SpMM" and len(f) == 3:
         a_ok = is_csr_shaped(f[0]) or (is_bsr(f[0]) and bsr_blocksize(f[0])[:2] == (16, 16))
@@ -134,6 +135,14 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     x, y = _vec_checks(u_A, u_x, u_y)
     m, n = u_A.extents
     L = _lib.lib()
+    if is_shifted_diag(u_A.format):
+        lv = u_A.format.levels[1]
+        dev = _check_same_device(x, y)
+        with torch.cuda.device(dev):
+            st = getattr(L, f"jlust_hip_shifted_diag_spmv_{suf}")(
+                m, n, lv.shift, lv.val, float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
+        _lib.check(st, "shifted_diag_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
+        return u_y
     if is_csr_shaped(u_A.format):
         rowptr, colind = _csr_parts(u_A)
         dev = _check_same_device(rowptr, colind, nonzeros(u_A), x, y)

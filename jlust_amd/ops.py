@@ -42,6 +42,10 @@ class OpType:
 SpMVOp = OpType("SpMV")      # src/ops.jl:50
 SpMMOp = OpType("SpMM")      # src/ops.jl:54
 SDDMMOp = OpType("SDDMM")    # src/ops.jl:74
+BlockSpMVOp = OpType("BlockSpMV")    # src/ops.jl (Op{:BlockSpMV})
+BlockSpMMOp = OpType("BlockSpMM")    # src/ops.jl:111
+BBMSpMVOp = OpType("BBMSpMV")        # src/ops.jl:115
+_AGGREGATE_TAGS = ("BlockSpMV", "BlockSpMM", "BBMSpMV")
 
 
 # ------------------------------------------------------------------ backends
@@ -103,6 +107,8 @@ def execute(optype, *args, backend=None, **kw):
     if isinstance(optype, AbstractUSTBackend):          # execute(backend, op, tensors...)
         be, op, tensors = optype, args[0], [_wrap(a) for a in args[1:]]
         return _backend_execute(be, op, tensors, kw)
+    if isinstance(optype, OpType) and optype.tag in _AGGREGATE_TAGS:
+        return _execute_aggregate(optype, *args, backend=backend, **kw)
     tensors = [_wrap(a) for a in args]
     if not isinstance(optype, OpType):
         raise TypeError(f"execute: expected an op type such as SpMVOp, got {optype!r}")
@@ -110,6 +116,22 @@ def execute(optype, *args, backend=None, **kw):
     be = backend if backend is not None else default_backend(primary, optype)
     op = optype(*[t.format for t in tensors])
     return _backend_execute(be, op, tensors, kw)
+
+
+def _execute_aggregate(optype: OpType, A, x, y, backend=None, alpha=1.0, beta=0.0):
+    """execute(BlockSpMVOp, A, x, y), execute(BlockSpMMOp, A, X, Y)
+    (src/block_sparse.jl:259-302) and execute(BBMSpMVOp, M, x, y)
+    (src/block_banded.jl:79-122): the aggregate runs its own products."""
+    from .block_banded import BlockBandedMatrix
+    from .block_sparse import BlockSparseMatrix
+    if backend is not None and not isinstance(backend, HIPBackend):
+        raise UnsupportedFormat(optype.tag, backend, "no such backend in jlust_amd")
+    want = BlockBandedMatrix if optype.tag == "BBMSpMV" else BlockSparseMatrix
+    if not isinstance(A, want):
+        raise TypeError(f"execute({optype!r}, ...): expected a {want.__name__}, got {type(A).__name__}")
+    if optype.tag == "BlockSpMM":
+        return A.spmm(x, y, alpha, beta)
+    return A.spmv(x, y, alpha, beta)
 
 
 def _backend_execute(be, op: Op, tensors, kw):
@@ -139,6 +161,16 @@ def mul_(Y, A: USTensor, X, alpha=None, beta=None):
     if alpha is not None or beta is not None:
         kw = dict(alpha=1 if alpha is None else alpha, beta=0 if beta is None else beta)
     xt = X.val if isinstance(X, USTensor) else X
+    if not isinstance(A, USTensor):          # BlockSparseMatrix / BlockBandedMatrix
+        from .block_banded import BlockBandedMatrix
+        if isinstance(A, BlockBandedMatrix):
+            if xt.dim() != 1:
+                raise TypeError("mul!(Y, ::BlockBandedMatrix, X) takes vectors only")
+            optype = BBMSpMVOp
+        else:
+            optype = BlockSpMVOp if xt.dim() == 1 else BlockSpMMOp
+        execute(optype, A, X, Y, **kw)
+        return Y
     optype = SpMVOp if xt.dim() == 1 else SpMMOp
     execute(optype, A, ust(X), ust(Y), **kw)
     return Y
@@ -148,6 +180,13 @@ def matmul(A: USTensor, x):
     """Base.:*(A, x) (src/convenience.jl:55-59): a new y of A's value type."""
     import torch
     xt = x.val if isinstance(x, USTensor) else x
+    if not isinstance(A, USTensor):          # BlockSparseMatrix / BlockBandedMatrix
+        if xt.dim() == 1:
+            y = torch.empty(A.size(1), dtype=A.dtype, device=xt.device)
+        else:
+            from .tensor import dense_matrix
+            y = dense_matrix(A.size(1), xt.shape[1], dtype=A.dtype, device=xt.device)
+        return mul_(y, A, x)
     if xt.dim() == 1:
         y = torch.empty(A.extents[0], dtype=nonzeros(A).dtype, device=nonzeros(A).device)
     else:

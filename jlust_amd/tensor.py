@@ -171,6 +171,15 @@ def bsr_tensor(browptr, bcolind, nzval, dims, blocksize=(16, 16), row_major_bloc
                     origin)
 
 
+def shifted_diag_tensor(dtype, n_rows: int, n_cols: int, shift: int = 0, val=1.0,
+                        device="cuda") -> USTensor:
+    """src/interop.jl:167-180: a structural shifted scaled identity (row r
+    holds val at column r + shift) with no pos/crd/val storage."""
+    fmt = Formats.ShiftedDiag(dtype, shift=shift, val=val)
+    return USTensor((int(n_rows), int(n_cols)), fmt, (None, None), (None, None),
+                    torch.empty(0, dtype=dtype, device=device), None, OneBased())
+
+
 def ust(a) -> USTensor:
     """Zero-copy dense view of a vector or a column-major matrix
     (src/interop.jl:36-46)."""
