@@ -55,6 +55,9 @@ def parse():
                    help="only measure random-gather bandwidth (8 B and 512 B rows) per source size")
     p.add_argument("--convert", action="store_true",
                    help="only time format conversions (convert_format) at config sizes")
+    p.add_argument("--blocks", action="store_true",
+                   help="only time BlockSparseMatrix / BlockBandedMatrix mul! on a synthetic "
+                        "DCOPF operator of pglib case30000_goc size (T = 24)")
     return p.parse_args()
 
 
@@ -112,6 +115,83 @@ def convert_bench(cpu_seconds):
               crd2=host_np(c.crd_buffers[1]), val=host_np(c.val))
     run("config5 CSR->BSR16", c, J.Formats.BSRRight((16, 16)), sc, "BSR", (16, 16, True))
     return res
+
+
+def blocks_bench(steps, warmup):
+    """mul! of the DCOPF BlockSparseMatrix [Cg 0 -Bbus; 0 -I Bf] and of the
+    T = 24 BlockBandedMatrix with ramp coupling (-R, R), the two block
+    operators of the reference's GPU tour (benchmark/tour_spmv.jl:178-370,
+    sweep_cases.jl:103-166), on synthetic matrices of pglib case30000_goc
+    size.  Per operator: time per call with a sync after each (the
+    reference's @belapsed(mul!; sync)), time per call when calls are queued
+    back to back, the one-off assembly, effective GB/s of the assembled
+    CSR's compulsory bytes, and scipy's CSR matvec of the same matrix on
+    this host."""
+    import torch
+    import scipy.sparse as sps
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    d = W.dcopf(**W.DCOPF_CASE30000)
+    nb, nl, ng, nv, nc = d["n_bus"], d["n_line"], d["n_gen"], d["n_var"], d["n_con"]
+
+    def ucsr(t, m, n, sign=1.0):
+        rp, ci, v = t
+        return J.csr_tensor(dev(rp), dev(ci), dev(sign * v), (m, n))
+    one = np.arange(1, nl + 2, dtype=np.int32)
+    negI = J.csr_tensor(dev(one), dev(one[:-1]), dev(-np.ones(nl)), (nl, nl))
+    BM = J.BlockSparseMatrix([[ucsr(d["Cg"], nb, ng), None, ucsr(d["Bbus"], nb, nb, -1.0)],
+                              [None, negI, ucsr(d["Bf"], nl, nb)]])
+    g1 = np.arange(1, ng + 2, dtype=np.int32)
+    R = J.csr_tensor(dev(g1), dev(g1[:-1]), dev(np.ones(ng)), (ng, nv))
+    negR = J.csr_tensor(dev(g1), dev(g1[:-1]), dev(-np.ones(ng)), (ng, nv))
+    T = 24
+    MS = J.BlockBandedMatrix(BM, negR, R, T, nc, ng, nv)
+    rng = np.random.default_rng(0)
+    out = []
+    for name, A in (("BlockSparseMatrix mul!", BM), ("BlockBandedMatrix mul! (T=24)", MS)):
+        m, n = A.size()
+        x = dev(rng.standard_normal(n))
+        y = torch.empty(m, dtype=torch.float64, device="cuda")
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        J.mul_(y, A, x)
+        torch.cuda.synchronize()
+        t_first = time.perf_counter() - t0
+        for _ in range(warmup):
+            J.mul_(y, A, x)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            J.mul_(y, A, x)
+            torch.cuda.synchronize()
+        t_sync = (time.perf_counter() - t0) / steps
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            J.mul_(y, A, x)
+        torch.cuda.synchronize()
+        t_async = (time.perf_counter() - t0) / steps
+        asm = A.assembled().asm
+        nz = J.nnz(asm)
+        byts = 12 * nz + 4 * (m + 1) + 8 * (m + n)
+        S = sps.csr_matrix((host_np(asm.val), host_np(asm.crd_buffers[1]), host_np(asm.pos_buffers[1])),
+                           shape=(m, n))
+        xh = host_np(x)
+        reps = max(3, min(200, int(0.5 / max(1e-6, (S.nnz + m) * 2e-9))))
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            yh = S @ xh
+        t_cpu = (time.perf_counter() - t0) / reps
+        err = float(np.max(np.abs(yh - host_np(y))) / max(1e-300, float(np.max(np.abs(yh)))))
+        out.append({"op": name, "rows": m, "cols": n, "nnz": nz,
+                    "first_call_ms": round(t_first * 1e3, 2),
+                    "us_per_call_sync": round(t_sync * 1e6, 1),
+                    "us_per_call_queued": round(t_async * 1e6, 1),
+                    "effective_GBps_sync": round(byts / t_sync / 1e9, 1),
+                    "effective_GBps_queued": round(byts / t_async / 1e9, 1),
+                    "cpu_scipy_us": round(t_cpu * 1e6, 1), "max_rel_diff_vs_scipy": err})
+        log(f"{name}: {m}x{n} nnz {nz}: {t_sync*1e6:.1f} us/call synced, {t_async*1e6:.1f} queued, "
+            f"first call {t_first*1e3:.1f} ms, scipy {t_cpu*1e6:.0f} us")
+    return out
 
 
 def host_np(t):
@@ -366,6 +446,9 @@ def main():
         return
     if args.convert:
         print(json.dumps({"convert": convert_bench(args.cpu_seconds)}), flush=True)
+        return
+    if args.blocks:
+        print(json.dumps({"blocks": blocks_bench(args.steps or 200, args.warmup or 10)}), flush=True)
         return
     from jlust_amd import workloads as W
 

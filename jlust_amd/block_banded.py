@@ -99,6 +99,7 @@ class BlockBandedMatrix:
         self.n_diag_rows, self.n_off_rows, self.n_cols = n_diag_rows, n_off_rows, n_cols
         self._check()
         self._asm: Optional[AssembledCSR] = None
+        self._assemblable = all(assemblable(b) for obj in self._matrices() for b in _all_blocks(obj))
         for obj in self._matrices():
             if isinstance(obj, BlockSparseMatrix):
                 obj._listeners.add(self)
@@ -213,7 +214,7 @@ class BlockBandedMatrix:
                 yield from _pieces(pos, ("pos", k, t), ro, (t + k) * self.n_cols)
 
     def assemblable(self) -> bool:
-        return all(assemblable(b) for obj in self._matrices() for b in _all_blocks(obj))
+        return self._assemblable
 
     def _device(self):
         devs = {b.val.device for obj in self._matrices() for b in _all_blocks(obj)}

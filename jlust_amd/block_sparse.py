@@ -128,8 +128,7 @@ class AssembledCSR:
         return self._plan
 
     def spmv(self, x: torch.Tensor, y: torch.Tensor, alpha=1.0, beta=0.0):
-        self.plan().execute(ust(x), ust(y), alpha=alpha, beta=beta)
-        return y
+        return self.plan().execute_tensors(x, y, float(alpha), float(beta))
 
     def spmm(self, X: torch.Tensor, Y: torch.Tensor, alpha=1.0, beta=0.0):
         from .hip_backend import _spmm
@@ -217,6 +216,7 @@ class BlockSparseMatrix:
             self._col_off.append(self._col_off[-1] + s)
         self._T = ref_T
         self._asm: Optional[AssembledCSR] = None
+        self._assemblable = all(assemblable(b) for _, b, _, _ in self.placed_blocks())
         self._listeners = weakref.WeakSet()      # block-banded matrices built on this one
 
     # ------------------------------------------------------------ interface
@@ -251,7 +251,7 @@ class BlockSparseMatrix:
                     yield (i, j), b, self._row_off[i], self._col_off[j]
 
     def assemblable(self) -> bool:
-        return all(assemblable(b) for _, b, _, _ in self.placed_blocks())
+        return self._assemblable
 
     def _device(self):
         devs = {b.val.device for _, b, _, _ in self.placed_blocks()}

@@ -391,14 +391,21 @@ __global__ __launch_bounds__(BLOCK) void csr_spmv_merge_kernel(
 {
     constexpr int TILE = BLOCK * IPT;
     __shared__ SpmvSmem<T, TILE, BLOCK / 64> sm;
+    // XCD-major order: the grid is a multiple of 8 blocks and workgroup b runs
+    // on XCD b % 8, so logical block L = (b % 8) * (grid / 8) + b / 8 gives
+    // each XCD one contiguous eighth of the merge path.  Rows of one eighth
+    // gather from one window of x when the matrix is banded or block
+    // structured, and that window stays in the XCD's own L2.
+    const int64_t per_xcd = gridDim.x / NUM_XCD;
+    const int64_t L = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
     const int64_t total = m + nnz;
-    const int64_t dbeg = (int64_t)blockIdx.x * tiles_per_block * TILE;
+    const int64_t dbeg = L * tiles_per_block * TILE;
     if (dbeg >= total) return;
     const int64_t dend = min(total, dbeg + tiles_per_block * (int64_t)TILE);
     merge_range<T, BLOCK, IPT, PF, !PF, BZ>(m, nnz, nnz - 1, origin, origin, rowptr,
                                             colind, val, x, y, alpha, beta, dbeg, dend,
-                                            start_rows ? start_rows[blockIdx.x] : -1,
-                                            carry_row + blockIdx.x, carry_val + blockIdx.x, sm);
+                                            start_rows ? start_rows[L] : -1,
+                                            carry_row + L, carry_val + L, sm);
 }
 
 struct SliceInfo {
@@ -667,8 +674,10 @@ int spmv_launch(int64_t m, int64_t nnz, int32_t origin, const int32_t *rowptr,
                 const SpmvGrid &g, int ipt, const int64_t *start_rows, int64_t *carry_row,
                 T *carry_val, hipStream_t stream)
 {
+    // Whole XCD groups: logical blocks past g.nblocks return at once.
+    const unsigned launch = (unsigned)((g.nblocks + NUM_XCD - 1) / NUM_XCD * NUM_XCD);
 #define H(I, P, B)                                                                                \
-    hipLaunchKernelGGL((csr_spmv_merge_kernel<T, SPMV_BLOCK, I, P, B>), dim3((unsigned)g.nblocks), \
+    hipLaunchKernelGGL((csr_spmv_merge_kernel<T, SPMV_BLOCK, I, P, B>), dim3(launch),              \
                        dim3(SPMV_BLOCK), 0, stream, m, nnz, origin, rowptr, colind, val, x, y,    \
                        alpha, beta, g.tiles_per_block, start_rows, carry_row, carry_val)
 #define G(I, P) do { if (beta == T(0)) H(I, P, true); else H(I, P, false); } while (0)
@@ -712,14 +721,88 @@ int csr_spmv(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *r
                           carry_row, carry_val, (hipStream_t)stream);
 }
 
+// Counts the entries whose column lies within +-w of their row's diagonal
+// position r*n/m.  Each thread walks LOC_CHUNK consecutive entries from the
+// row found by binary search; one atomic per wave.
+constexpr int LOC_CHUNK = 64;
+
+__global__ __launch_bounds__(256) void locality_kernel(int64_t m, int64_t n, int64_t nnz, int32_t origin,
+                                                       const int32_t *__restrict__ rowptr,
+                                                       const int32_t *__restrict__ colind, int64_t w,
+                                                       unsigned long long *__restrict__ count)
+{
+    const int64_t k0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * LOC_CHUNK;
+    unsigned long long local = 0;
+    if (k0 < nnz) {
+        int64_t lo = 0, hi = m;          // rowptr[lo] <= k0 < rowptr[hi] (relative to origin)
+        while (hi - lo > 1) {
+            const int64_t mid = (lo + hi) >> 1;
+            if ((int64_t)rowptr[mid] - origin <= k0) lo = mid;
+            else hi = mid;
+        }
+        int64_t r = lo;
+        int64_t rend = (int64_t)rowptr[r + 1] - origin;
+        const int64_t k1 = min(nnz, k0 + LOC_CHUNK);
+        for (int64_t k = k0; k < k1; ++k) {
+            while (k >= rend && r < m - 1) {
+                ++r;
+                rend = (int64_t)rowptr[r + 1] - origin;
+            }
+            const int64_t d = r * n / m;
+            const int64_t c = (int64_t)colind[k] - origin;
+            local += (c >= d - w && c <= d + w) ? 1u : 0u;
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) local += __shfl_xor(local, off, 64);
+    if (__lane_id() == 0 && local) atomicAdd(count, local);
+}
+
+// True when at least 90% of the entries gather from within half an XCD L2
+// of x around their row's diagonal position: the rows one XCD runs (an
+// eighth of the merge path, XCD-major) then share one L2-sized window of x,
+// and slicing would only add its reduction pass.  Synchronises `s`.
+template <typename T>
+int mostly_local(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *rowptr,
+                 const int32_t *colind, hipStream_t s, bool *out)
+{
+    *out = false;
+    if (m <= 0 || nnz <= 0) return JLUST_STATUS_SUCCESS;
+    void *ws = nullptr;
+    if (int st = scratch(s, sizeof(unsigned long long), &ws)) return st;
+    auto *cnt = (unsigned long long *)ws;
+    JLUST_HIP_TRY(hipMemsetAsync(cnt, 0, sizeof(*cnt), s));
+    const int64_t threads = (nnz + LOC_CHUNK - 1) / LOC_CHUNK;
+    const int64_t w = (int64_t)(SLICE_MIN_X_BYTES / sizeof(T) / 2);
+    hipLaunchKernelGGL(locality_kernel, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, s, m, n, nnz,
+                       origin, rowptr, colind, w, cnt);
+    if (int st = check_launch("locality_kernel")) return st;
+    unsigned long long h = 0;
+    JLUST_HIP_TRY(hipMemcpyAsync(&h, cnt, sizeof(h), hipMemcpyDeviceToHost, s));
+    JLUST_HIP_TRY(hipStreamSynchronize(s));
+    *out = (double)h >= 0.9 * (double)nnz;
+    return JLUST_STATUS_SUCCESS;
+}
+
 // Slice or not: JLUST_HIP_SPMV_SLICE=0 never, =1 always, unset = when x is
-// larger than one XCD's L2.
-bool want_slices(int64_t n, size_t tsize)
+// larger than one XCD's L2 and the gathers are not mostly local.
+template <typename T>
+int want_slices(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *rowptr,
+                const int32_t *colind, hipStream_t s, bool *out)
 {
     const char *e = getenv("JLUST_HIP_SPMV_SLICE");
-    if (e && e[0] == '0') return false;
-    if (e && e[0] == '1') return n >= NUM_XCD;
-    return (size_t)n * tsize > SLICE_MIN_X_BYTES;
+    *out = false;
+    if (m <= 0 || nnz <= 0) return JLUST_STATUS_SUCCESS;   // the sliced kernel needs a nonzero
+    if (e && e[0] == '0') return JLUST_STATUS_SUCCESS;
+    if (e && e[0] == '1') {
+        *out = n >= NUM_XCD;
+        return JLUST_STATUS_SUCCESS;
+    }
+    if ((size_t)n * sizeof(T) <= SLICE_MIN_X_BYTES) return JLUST_STATUS_SUCCESS;
+    bool local = false;
+    if (int st = mostly_local<T>(m, n, nnz, origin, rowptr, colind, s, &local)) return st;
+    *out = !local;
+    return JLUST_STATUS_SUCCESS;
 }
 
 }  // namespace
@@ -848,10 +931,14 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
     p->val = val;
     p->device = dev;
     p->ipt = spmv_ipt();
-    // (The sliced kernel's clamped prefetch needs at least one nonzero.)
-    p->sliced = m > 0 && nnz > 0 && want_slices(n, tsz);
     hipStream_t s = (hipStream_t)stream;
-    int st = JLUST_STATUS_SUCCESS;
+    // (The sliced kernel's clamped prefetch needs at least one nonzero.)
+    int st = value_type == 0 ? want_slices<double>(m, n, nnz, origin, rowptr, colind, s, &p->sliced)
+                             : want_slices<float>(m, n, nnz, origin, rowptr, colind, s, &p->sliced);
+    if (st) {
+        delete p;
+        return st;
+    }
     if (!p->sliced) {
         if (m > 0) {
             st = value_type == 0 ? spmv_grid<double>(m, nnz, p->ipt, &p->grid)
