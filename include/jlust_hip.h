@@ -153,6 +153,35 @@ int jlust_hip_coo_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz,
                                float alpha, const float *x, float beta,
                                float *y, jlust_stream_t stream);
 
+/*
+ * Elementwise transforms for SpMV's input_fn / output_fn
+ * (execute(::EmitterBackend, ::Op{:SpMV}; input_fn, output_fn),
+ * ext/KernelAbstractionsExt/ops/spmv.jl:371-374): f(v) of one kind.
+ */
+enum jlust_fn_kind {
+    JLUST_FN_IDENTITY = 0,  /* v                        */
+    JLUST_FN_AFFINE = 1,    /* a*v + b (not contracted) */
+    JLUST_FN_ABS = 2,       /* |v|                      */
+    JLUST_FN_SQUARE = 3,    /* v*v                      */
+    JLUST_FN_SQRT = 4,      /* sqrt(v)                  */
+    JLUST_FN_EXP = 5,       /* exp(v)                   */
+    JLUST_FN_LOG = 6,       /* log(v)                   */
+    JLUST_FN_RELU = 7       /* max(v, 0), NaN kept      */
+};
+
+/*
+ * dst[i] = alpha*f(src[i]) + beta*dst[i] for i < n (beta == 0 writes dst
+ * without reading it; dst == src allowed).  With alpha = 1, beta = 0 it is
+ * in_fn.(x); after an SpMV into a row-sum vector t it is the row write
+ * alpha*out_fn(t) + beta*y (spmv.jl:168-169).
+ */
+int jlust_hip_apply_fn_f64(int64_t n, int32_t kind, double a, double b,
+                           const double *src, double alpha, double beta,
+                           double *dst, jlust_stream_t stream);
+int jlust_hip_apply_fn_f32(int64_t n, int32_t kind, float a, float b,
+                           const float *src, float alpha, float beta,
+                           float *dst, jlust_stream_t stream);
+
 /* ----------------------------------------------------------------- SpMM */
 
 /*

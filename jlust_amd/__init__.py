@@ -23,6 +23,8 @@ from .ops import (AbstractKernelHandle, AbstractUSTBackend, BBMSpMVOp, BlockSpMM
 from .block_sparse import (BlockSparseMatrix, BlockStructureError, batch_mul, batch_mul_,
                            update_block_values_)
 from .block_banded import BlockBandedMatrix
+from .elementwise import (ElementwiseFn, abs_fn, affine_fn, exp_fn, identity_fn, log_fn, relu_fn,
+                          sqrt_fn, square_fn)
 from .convert import (convert_format, convert_index_type, convert_value_type, csc_tensor,
                       dcsr_tensor, sparse_to_dense)
 from .tensor import (CPUDevice, HIPDevice, OneBased, USTensor, ZeroBased, bsr_tensor,

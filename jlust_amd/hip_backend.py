@@ -106,16 +106,43 @@ def _csr_parts(u: USTensor):
 
 def execute(op: Op, *ts, alpha=1.0, beta=0.0, input_fn=None, output_fn=None,
             skip_empty_rows=False, mask=None):
-    if input_fn is not None or output_fn is not None:
-        raise UnsupportedFormat(op.formats, _BE,
-                                "input_fn/output_fn closures are not supported by the HIP kernels")
+    from .elementwise import is_identity
     if not supports(op):
         raise UnsupportedFormat(op.formats, _BE)
     if op.tag == "SpMV":
-        return _spmv(*ts, alpha=alpha, beta=beta)
+        return spmv_with_fns(_spmv, *ts, alpha=alpha, beta=beta, input_fn=input_fn,
+                             output_fn=output_fn)
+    if not (is_identity(input_fn) and is_identity(output_fn)):
+        raise UnsupportedFormat(op.formats, _BE, "input_fn/output_fn belong to SpMV")
     if op.tag == "SpMM":
         return _spmm(*ts, alpha=alpha, beta=beta, skip_empty_rows=skip_empty_rows)
     return _sddmm(*ts, alpha=alpha, beta=beta, mask=mask)
+
+
+def spmv_with_fns(spmv, u_A, u_x, u_y, alpha=1.0, beta=0.0, input_fn=None, output_fn=None):
+    """y = alpha*output_fn(A*input_fn.(x)) + beta*y (spmv.jl:371-374) around a
+    plain SpMV `spmv(u_A, u_x, u_y, alpha, beta)`: in_fn.(x) into a new
+    vector, the product into a row-sum vector when output_fn is given, then
+    the row write on the device (jlust_amd/elementwise.py)."""
+    from .elementwise import apply_fn, is_identity
+    if is_identity(input_fn) and is_identity(output_fn):
+        return spmv(u_A, u_x, u_y, alpha, beta)
+    x, y = _vec_checks(u_A, u_x, u_y)
+    if not is_identity(output_fn) and is_coo_shaped(u_A.format):
+        # The reference rejects output_fn where rows are accumulated by atomics
+        # (spmv.jl:394-399); COO's row sums are such atomics here.
+        raise UnsupportedFormat(u_A.format, _BE,
+                                "output_fn is unsupported for COO SpMV; convert A to CSR first")
+    if not is_identity(input_fn):
+        x2 = torch.empty_like(x)
+        apply_fn(input_fn, x, x2)
+        u_x = ust(x2)
+    if is_identity(output_fn):
+        return spmv(u_A, u_x, u_y, alpha, beta)
+    t = torch.empty_like(y)
+    spmv(u_A, u_x, ust(t), 1.0, 0.0)
+    apply_fn(output_fn, t, y, alpha, beta)
+    return u_y
 
 
 def _vec_checks(u_A, u_x, u_y):
@@ -248,9 +275,10 @@ class HIPSpMVHandle(AbstractKernelHandle):
     (prepare(::EmitterBackend, SpMVOp, A), ext/KernelAbstractionsExt/ops/
     spmv.jl:518-544; the cuSPARSE handle contract, ext/CUDAExt/ops/spmv.jl:7-83)."""
 
-    def __init__(self, u_A: USTensor):
+    def __init__(self, u_A: USTensor, input_fn=None, output_fn=None):
         if not is_csr_shaped(u_A.format):
             raise UnsupportedFormat(u_A.format, _BE, "prepared SpMV needs CSR")
+        self.input_fn, self.output_fn = input_fn, output_fn
         suf = _value_suffix(u_A)
         rowptr, colind = _csr_parts(u_A)
         self.dev = _check_same_device(rowptr, colind, nonzeros(u_A))
@@ -266,7 +294,23 @@ class HIPSpMVHandle(AbstractKernelHandle):
                 _ptr(colind), _ptr(nonzeros(u_A)), _stream(self.dev), ctypes.byref(self._plan))
         _lib.check(st, "csr_spmv_plan_create", u_A.format, _BE, self.T)
 
-    def execute(self, u_x: USTensor, u_y: USTensor, alpha=1.0, beta=0.0):
+    def execute(self, *ts, alpha=1.0, beta=0.0):
+        """execute(h, x, y) (the cuSPARSE handle form) or execute(h, A, x, y)
+        (EmitterSpMVHandle, spmv.jl:531-544, which takes A's buffers at each
+        call: an A with other values than the plan's refreshes them first).
+        The handle's input_fn/output_fn apply."""
+        if len(ts) == 3:
+            u_A, u_x, u_y = ts
+            if u_A is not self.u_A and nonzeros(u_A).data_ptr() != nonzeros(self.u_A).data_ptr():
+                self.update_values(u_A)
+        elif len(ts) == 2:
+            u_x, u_y = ts
+        else:
+            raise TypeError("execute(handle, [A,] x, y)")
+        return spmv_with_fns(self._execute_plain, self.u_A, u_x, u_y, alpha, beta,
+                             self.input_fn, self.output_fn)
+
+    def _execute_plain(self, u_A, u_x: USTensor, u_y: USTensor, alpha=1.0, beta=0.0):
         x, y = _vec_checks(self.u_A, u_x, u_y)
         _check_same_device(nonzeros(self.u_A), x, y)
         with torch.cuda.device(self.dev):
@@ -282,8 +326,10 @@ class HIPSpMVHandle(AbstractKernelHandle):
         m, n = self.u_A.extents
         if (x.dtype is not self.T or y.dtype is not self.T or x.device != self.dev or
                 y.device != self.dev or x.numel() != n or y.numel() != m or
-                not x.is_contiguous() or not y.is_contiguous()):
-            return self.execute(ust(x), ust(y), alpha, beta)
+                not x.is_contiguous() or not y.is_contiguous() or
+                self.input_fn is not None or self.output_fn is not None):
+            self.execute(ust(x), ust(y), alpha=alpha, beta=beta)
+            return y
         if self._exec is None:
             self._exec = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_{self.suf}")
         if torch.cuda.current_device() != self.dev.index:
@@ -324,10 +370,16 @@ class HIPOpHandle(AbstractKernelHandle):
         _value_suffix(u_A)
 
     def execute(self, *ts, **kw):
+        """execute(h, x, y) / execute(h, A, x, y) for SpMV and SpMM (A given
+        at the call wins, as EmitterSpMVHandle takes it per call), and
+        execute(h, A, B[, C]) for SDDMM; keywords given at prepare apply."""
         from .ops import execute as _execute
+        kw = {**self.kw, **kw}
         if self.optype.tag == "SDDMM":
             a, b, c = ts if len(ts) == 3 else (*ts, self.u_A)
             return _execute(self.optype, a, b, c, backend=_BE, **kw)
+        if len(ts) == 3:
+            return _execute(self.optype, *ts, backend=_BE, **kw)
         return _execute(self.optype, self.u_A, *ts, backend=_BE, **kw)
 
     def update_values(self, u_A: USTensor):
@@ -340,9 +392,12 @@ class HIPOpHandle(AbstractKernelHandle):
 
 def prepare(optype, u_A: USTensor, **kw):
     if optype is SpMVOp or getattr(optype, "tag", None) == "SpMV":
+        bad = set(kw) - {"input_fn", "output_fn"}
+        if bad:
+            raise TypeError(f"prepare(SpMVOp): unexpected keywords {sorted(bad)}")
         if is_csr_shaped(u_A.format):
-            return HIPSpMVHandle(u_A)
-        return HIPOpHandle(SpMVOp, u_A)
+            return HIPSpMVHandle(u_A, kw.get("input_fn"), kw.get("output_fn"))
+        return HIPOpHandle(SpMVOp, u_A, **kw)
     if optype.tag in ("SpMM", "SDDMM"):
         return HIPOpHandle(SpMMOp if optype.tag == "SpMM" else SDDMMOp, u_A, **kw)
     raise UnsupportedFormat(u_A.format, _BE, f"prepare: {optype} is not supported")

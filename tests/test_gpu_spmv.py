@@ -181,8 +181,12 @@ def test_errors(J):
         J.execute(J.SpMVOp, A, dev(np.ones(4)), dev(np.zeros(3)))
     with pytest.raises(J.UnsupportedValueType):
         J.execute(J.SpMVOp, A, dev(np.ones(3, np.float32)), dev(np.zeros(3, np.float32)))
-    with pytest.raises(J.UnsupportedFormat):
-        J.execute(J.SpMVOp, A, dev(np.ones(3)), dev(np.zeros(3)), input_fn=lambda v: 2 * v)
+    y_fn = dev(np.zeros(3))
+    J.execute(J.SpMVOp, A, dev(np.ones(3)), y_fn, input_fn=lambda v: 2 * v)   # SpMV takes input_fn
+    assert host(y_fn).tolist() == [6.0, 6.0, 18.0]
+    with pytest.raises(J.UnsupportedFormat, match="belong to SpMV"):
+        J.execute(J.SpMMOp, A, J.dense_matrix(3, 2, fill=1.0), J.dense_matrix(3, 2),
+                  input_fn=lambda v: 2 * v)
     A64 = J.csr_tensor(dev(np.array(c["rowptr"], np.int64)), dev(np.array(c["colind"], np.int64)),
                        dev(np.array(c["val"])), (3, 3))
     with pytest.raises(J.UnsupportedIndexType):

@@ -134,3 +134,11 @@ def test_op_construction():
 def test_execute_rejects_non_op():
     with pytest.raises(TypeError):
         J.execute("SpMV", fixture_csr())
+
+
+def test_elementwise_fns_and_prepare_keywords():
+    assert J.affine_fn(2.0) == J.ElementwiseFn(1, 2.0, 0.0) and repr(J.abs_fn) == "abs"
+    from jlust_amd.elementwise import is_identity
+    assert is_identity(None) and is_identity(J.identity_fn) and not is_identity(J.exp_fn)
+    with pytest.raises(TypeError, match="unexpected keywords"):
+        J.prepare(J.HIPBackend(), J.SpMVOp, fixture_csr(), skip_empty_rows=True)
