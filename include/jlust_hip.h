@@ -182,6 +182,34 @@ int jlust_hip_apply_fn_f32(int64_t n, int32_t kind, float a, float b,
                            const float *src, float alpha, float beta,
                            float *dst, jlust_stream_t stream);
 
+/*
+ * Row gathers / scatters of DCSR products (src/named_formats.jl:27): a DCSR
+ * SpMV or SpMM runs as the CSR product over its stored rows into a compact
+ * result t, with t = y[rows] gathered first when beta != 0 and y[rows] = t
+ * scattered after, so rows that are not stored stay untouched as in the
+ * reference (ext/KernelAbstractionsExt/ops/spmv.jl:449-502, n_outer = stored
+ * rows; spmm.jl:397-423).  gather: dst[s + c*ldd] = src[rows[s] - origin +
+ * c*lds]; scatter: dst[rows[s] - origin + c*ldd] = src[s + c*lds], for
+ * s < nrows, c < k; m = rows of the full operand; rows outside [0, m) are
+ * skipped.
+ */
+int jlust_hip_gather_rows_f64(int64_t nrows, int64_t k, int32_t origin,
+                              const int32_t *rows, int64_t m, const double *src,
+                              int64_t lds, double *dst, int64_t ldd,
+                              jlust_stream_t stream);
+int jlust_hip_gather_rows_f32(int64_t nrows, int64_t k, int32_t origin,
+                              const int32_t *rows, int64_t m, const float *src,
+                              int64_t lds, float *dst, int64_t ldd,
+                              jlust_stream_t stream);
+int jlust_hip_scatter_rows_f64(int64_t nrows, int64_t k, int32_t origin,
+                               const int32_t *rows, int64_t m, const double *src,
+                               int64_t lds, double *dst, int64_t ldd,
+                               jlust_stream_t stream);
+int jlust_hip_scatter_rows_f32(int64_t nrows, int64_t k, int32_t origin,
+                               const int32_t *rows, int64_t m, const float *src,
+                               int64_t lds, float *dst, int64_t ldd,
+                               jlust_stream_t stream);
+
 /* ----------------------------------------------------------------- SpMM */
 
 /*

@@ -62,6 +62,10 @@ SIGNATURES = {
     "jlust_hip_shifted_diag_spmv_f32": (_INT, [_I64, _I64, _I64, _F, _F, _P, _F, _P, _P]),
     "jlust_hip_apply_fn_f64": (_INT, [_I64, _I32, _D, _D, _P, _D, _D, _P, _P]),
     "jlust_hip_apply_fn_f32": (_INT, [_I64, _I32, _F, _F, _P, _F, _F, _P, _P]),
+    "jlust_hip_gather_rows_f64": (_INT, [_I64, _I64, _I32, _P, _I64, _P, _I64, _P, _I64, _P]),
+    "jlust_hip_gather_rows_f32": (_INT, [_I64, _I64, _I32, _P, _I64, _P, _I64, _P, _I64, _P]),
+    "jlust_hip_scatter_rows_f64": (_INT, [_I64, _I64, _I32, _P, _I64, _P, _I64, _P, _I64, _P]),
+    "jlust_hip_scatter_rows_f32": (_INT, [_I64, _I64, _I32, _P, _I64, _P, _I64, _P, _I64, _P]),
 }
 
 STATUS = {

@@ -15,9 +15,9 @@ import torch
 from . import _lib
 from .errors import (DeviceMismatch, IncompatibleExtents, NonCanonicalStorage,
                      UnsupportedFormat, UnsupportedIndexType, UnsupportedValueType)
-from .formats import bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped, is_shifted_diag
+from .formats import Formats, bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped, is_shifted_diag
 from .ops import AbstractKernelHandle, HIPBackend, Op, SDDMMOp, SpMMOp, SpMVOp
-from .tensor import USTensor, leading_dim, nnz, nonzeros, ust
+from .tensor import USTensor, dense_matrix, leading_dim, nnz, nonzeros, ust
 
 _BE = HIPBackend()
 _VALUE_TYPES = {torch.float64: "f64", torch.float32: "f32"}
@@ -41,11 +41,13 @@ def supports(op: Op) -> bool:
     """Capability table (the counterpart of KernelAbstractionsExt.jl:31-41)."""
     f = op.formats
     if op.tag == "SpMV" and len(f) == 3:
-        return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_shifted_diag(f[0])) and \
+        return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_shifted_diag(f[0]) or
+                f[0] == Formats.DCSR) and \
             _dense_fmt(f[1]) and \
             _dense_fmt(f[2]) and f[1].ndims == 1 and f[2].ndims == 1
     if op.tag == "SpMM" and len(f) == 3:
-        a_ok = is_csr_shaped(f[0]) or (is_bsr(f[0]) and bsr_blocksize(f[0])[:2] == (16, 16))
+        a_ok = is_csr_shaped(f[0]) or f[0] == Formats.DCSR or \
+            (is_bsr(f[0]) and bsr_blocksize(f[0])[:2] == (16, 16))
         return a_ok and _dense_fmt(f[1]) and _dense_fmt(f[2]) and f[1].ndims == 2 and \
             f[2].ndims == 2
     if op.tag == "SDDMM" and len(f) == 3:
@@ -162,6 +164,8 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     x, y = _vec_checks(u_A, u_x, u_y)
     m, n = u_A.extents
     L = _lib.lib()
+    if u_A.format == Formats.DCSR:
+        return _dcsr_product(u_A, u_x, u_y, alpha, beta)
     if is_shifted_diag(u_A.format):
         lv = u_A.format.levels[1]
         dev = _check_same_device(x, y)
@@ -192,6 +196,52 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     return u_y
 
 
+def _dcsr_product(u_A: USTensor, u_X: USTensor, u_Y: USTensor, alpha, beta):
+    """DCSR SpMV/SpMM: the CSR product over the stored rows into a compact
+    result, with y[rows] gathered first when beta != 0 and scattered back
+    after, so rows that are not stored stay untouched (the walker writes
+    stored rows only, spmv.jl:449-502; dcsr.hip)."""
+    rows, pos, cols = u_A.crd_buffers[0], u_A.pos_buffers[1], u_A.crd_buffers[1]
+    if rows is None or pos is None or cols is None:
+        raise NonCanonicalStorage("DCSR: missing level buffers")
+    _check_index(u_A, rows, pos, cols)
+    nout = rows.numel()
+    if pos.numel() != nout + 1 or cols.numel() != nnz(u_A):
+        raise NonCanonicalStorage(
+            f"DCSR: {nout} stored rows need {nout + 1} segment pointers (got {pos.numel()}) and "
+            f"{nnz(u_A)} columns (got {cols.numel()})")
+    m, n = u_A.extents
+    Y = nonzeros(u_Y)
+    dev = _check_same_device(rows, pos, cols, nonzeros(u_A), nonzeros(u_X), Y)
+    if nout == 0:
+        return u_Y
+    compact = USTensor((nout, n), Formats.CSR, (None, pos), (None, cols), nonzeros(u_A),
+                       u_A.owner, u_A.origin)
+    vec = Y.dim() == 1
+    k = 1 if vec else Y.shape[1]
+    suf = _value_suffix(u_A)
+    t = torch.empty(nout, dtype=Y.dtype, device=dev) if vec else \
+        dense_matrix(nout, k, dtype=Y.dtype, device=dev)
+    ldy = 1 if vec else leading_dim(Y)
+    ldt = 1 if vec else leading_dim(t)
+    L = _lib.lib()
+    o = u_A.origin.offset
+    if beta != 0:
+        with torch.cuda.device(dev):
+            st = getattr(L, f"jlust_hip_gather_rows_{suf}")(nout, k, o, _ptr(rows), m, _ptr(Y), ldy,
+                                                            _ptr(t), ldt, _stream(dev))
+        _lib.check(st, "gather_rows", u_A.format, _BE, Y.dtype)
+    if vec:
+        _spmv(compact, u_X, ust(t), alpha, beta)
+    else:
+        _spmm(compact, u_X, ust(t), alpha, beta)
+    with torch.cuda.device(dev):
+        st = getattr(L, f"jlust_hip_scatter_rows_{suf}")(nout, k, o, _ptr(rows), m, _ptr(t), ldt,
+                                                         _ptr(Y), ldy, _stream(dev))
+    _lib.check(st, "scatter_rows", u_A.format, _BE, Y.dtype)
+    return u_Y
+
+
 def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_rows=False):
     suf = _value_suffix(u_A)
     T = nonzeros(u_A).dtype
@@ -207,6 +257,8 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
             raise NonCanonicalStorage(f"SpMM: {nm} must be column-major (stride(0) == 1)")
     k = B.shape[1]
     L = _lib.lib()
+    if u_A.format == Formats.DCSR:
+        return _dcsr_product(u_A, u_B, u_C, alpha, beta)
     if is_bsr(u_A.format):
         b1, b2, row_major = bsr_blocksize(u_A.format)
         if suf != "f32":

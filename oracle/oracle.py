@@ -145,6 +145,31 @@ def csr_spmv_absref(rowptr, colind, val, x, alpha=1.0, beta=0.0, y0=None,
     return out
 
 
+def dcsr_spmv(outer, inner_pos, inner_crd, val, x, m, alpha=1.0, beta=0.0, y0=None, origin=1):
+    """DCSR SpMV as JLUST's walker runs it (n_outer = stored rows,
+    ext/KernelAbstractionsExt/ops/spmv.jl:449-502): stored row f writes
+    y[outer[f]] = alpha*sum + beta*y0[outer[f]]; rows that are not stored keep
+    y0 (zeros when y0 is None)."""
+    dt = np.asarray(val).dtype
+    outer = np.asarray(outer, np.int64) - origin
+    y = np.zeros(m, dt) if y0 is None else _c(y0, dt).copy()
+    yc = csr_spmv(inner_pos, inner_crd, val, x, alpha, beta, y[outer], origin)
+    y[outer] = yc
+    return y
+
+
+def dcsr_spmm(outer, inner_pos, inner_crd, val, B, m, alpha=1.0, beta=0.0, C0=None, origin=1):
+    """DCSR SpMM: the stored rows' C rows as csr_spmm computes them, the other
+    rows of C0 untouched."""
+    dt = np.asarray(val).dtype
+    outer = np.asarray(outer, np.int64) - origin
+    B = _f(B, dt)
+    C = np.zeros((m, B.shape[1]), dt, order="F") if C0 is None else _f(C0, dt).copy(order="F")
+    Cc, _ = csr_spmm(inner_pos, inner_crd, val, B, alpha, beta, C[outer, :], origin)
+    C[outer, :] = Cc
+    return C
+
+
 def coo_spmv(rows, cols, val, x, m, alpha=1.0, beta=0.0, y0=None, origin=1):
     L = lib()
     dt = np.asarray(val).dtype

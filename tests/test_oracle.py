@@ -322,3 +322,30 @@ def test_planted_mistakes_are_caught():
     np.testing.assert_array_equal(good, np.array(c["y"]) + 2.0)
     bad = O.csr_spmv(c["rowptr"], c["colind"], np.array(c["val"]), np.array(c["x"]), 1.0, -2.0, y0)
     assert not np.array_equal(bad, np.array(c["y"]) + 2.0)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_dcsr_fixtures_and_untouched_rows(dtype):
+    """test_emitter.jl:127-157 and :230-260; rows not stored keep y0 / C0
+    whatever beta is (the walker only visits stored rows)."""
+    c = next(c for c in GOLDEN["spmv"] if c["format"] == "DCSR")
+    y = O.dcsr_spmv(c["outer_crd"], c["inner_pos"], c["inner_crd"], np.array(c["val"], dtype),
+                    np.array(c["x"], dtype), c["m"], origin=c["origin"])
+    np.testing.assert_array_equal(y, np.array(c["y"], dtype))
+    y0 = np.array([10.0, -3.0, 0.5], dtype)
+    y = O.dcsr_spmv(c["outer_crd"], c["inner_pos"], c["inner_crd"], np.array(c["val"], dtype),
+                    np.array(c["x"], dtype), c["m"], alpha=2.0, beta=0.5, y0=y0, origin=c["origin"])
+    D = np.array([[1, 0, 2], [0, 0, 0], [4, 0, 5]], np.float64)
+    want = 2.0 * D @ np.array(c["x"], np.float64) + 0.5 * y0
+    want[1] = y0[1]                                      # absent row untouched, beta or not
+    np.testing.assert_allclose(y, want, rtol=1e-6)
+    s = next(c for c in GOLDEN["spmm"] if c["format"] == "DCSR")
+    B = np.asfortranarray(np.array(s["B"], dtype))
+    C = O.dcsr_spmm(s["outer_crd"], s["inner_pos"], s["inner_crd"], np.array(s["val"], dtype), B,
+                    s["m"], origin=s["origin"])
+    np.testing.assert_array_equal(C, np.array(s["C"], dtype))
+    C0 = np.full((3, 2), 7.0, dtype)
+    C = O.dcsr_spmm(s["outer_crd"], s["inner_pos"], s["inner_crd"], np.array(s["val"], dtype), B,
+                    s["m"], beta=1.0, C0=C0, origin=s["origin"])
+    assert C[1].tolist() == [7.0, 7.0]
+    np.testing.assert_allclose(C[[0, 2]], np.array(s["C"], dtype)[[0, 2]] + 7.0, rtol=1e-6)
