@@ -136,6 +136,27 @@ int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float alpha,
 int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan);
 
 /*
+ * Prepared COO SpMV (rows[nnz], cols[nnz] as coo_tensor stores them,
+ * src/interop.jl:248-260): the entries are put in row order once (a stable
+ * radix sort only when the rows are not already non-decreasing) and every
+ * execute runs the CSR plan over them: y = alpha*A*x + beta*y with no
+ * atomics and a run-to-run identical result.  Returns a plan used with the
+ * jlust_hip_csr_spmv_plan_{execute,update_values,destroy} entry points;
+ * update_values takes values in the caller's COO order.  The plan keeps
+ * `cols` and `val` when the rows were already sorted (they must outlive it),
+ * otherwise row-ordered copies.  A row index outside [origin, m + origin)
+ * returns NONCANONICAL_STORAGE.  Replaces the COO branch of
+ * execute(::EmitterBackend, ::Op{:SpMV}) (ext/KernelAbstractionsExt/ops/
+ * spmv.jl:407-448) under the prepare/execute/update_values! handle contract
+ * (ext/CUDAExt/ops/spmv.jl:7-83).  Synchronises `stream`.
+ */
+int jlust_hip_coo_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
+                                   int32_t origin, int value_type,
+                                   const int32_t *rows, const int32_t *cols,
+                                   const void *val, jlust_stream_t stream,
+                                   jlust_spmv_plan_t *plan_out);
+
+/*
  * COO SpMV (rows[nnz], cols[nnz] as stored by coo_tensor, src/interop.jl:
  * 248-260): y = beta*y (zero-filled when beta == 0), then y += alpha*A*x.
  * Replaces the COO branch of execute(::EmitterBackend, ::Op{:SpMV}, ...)

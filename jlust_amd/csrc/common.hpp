@@ -63,6 +63,11 @@ int exclusive_scan_i32(const int32_t *in, int32_t *out, int64_t n, jlust_stream_
 
 constexpr int NUM_XCD = 8;   // MI355X: workgroup b runs on XCD b % 8
 
+// Hands a COO plan's owned buffers to a CSR SpMV plan (spmv.hip): mem is
+// freed with the plan; perm/val_copy (or null) reorder new values on
+// update_values.
+int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, void *val_copy);
+
 // ------------------------------------------------------------ device code
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

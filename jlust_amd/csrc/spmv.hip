@@ -835,7 +835,24 @@ struct jlust_spmv_plan {
     void *val_all;
     int32_t *perm;
     void *ypart;
+    // COO plans (coo_plan.hip): the row-ordered CSR the plan runs on is owned
+    // in coo_mem; coo_perm (null when the entries were already in row order)
+    // maps its entries to the caller's, and coo_val holds the values in that
+    // order.
+    void *coo_mem = nullptr;
+    const int32_t *coo_perm = nullptr;
+    void *coo_val = nullptr;
 };
+
+namespace jlust {
+int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, void *val_copy)
+{
+    plan->coo_mem = mem;
+    plan->coo_perm = perm;
+    plan->coo_val = val_copy;
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust
 
 using namespace jlust;
 
@@ -1006,6 +1023,20 @@ extern "C" int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan, con
     if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_update_values: null plan");
     if (bad_ptr(val, plan->nnz))
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_update_values: null values");
+    if (plan->coo_perm && plan->nnz > 0) {
+        // COO entries in the caller's order -> the plan's row order.
+        const unsigned grid = (unsigned)((plan->nnz + 255) / 256);
+        JLUST_HIP_TRY(hipDeviceSynchronize());
+        if (plan->value_type == 0)
+            hipLaunchKernelGGL((gather_values_kernel<double>), dim3(grid), dim3(256), 0, 0, plan->nnz,
+                               plan->coo_perm, (const double *)val, (double *)plan->coo_val);
+        else
+            hipLaunchKernelGGL((gather_values_kernel<float>), dim3(grid), dim3(256), 0, 0, plan->nnz,
+                               plan->coo_perm, (const float *)val, (float *)plan->coo_val);
+        if (int st = check_launch("gather_values_kernel")) return st;
+        JLUST_HIP_TRY(hipDeviceSynchronize());      // visible to the next execute on any stream
+        val = plan->coo_val;
+    }
     plan->val = val;
     if (plan->sliced && plan->nnz > 0) {
         // The plan's slice-major copy of the values is refreshed in stream order
@@ -1095,6 +1126,8 @@ extern "C" int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan)
     clear_error();
     if (!plan) return JLUST_STATUS_SUCCESS;
     hipError_t e = hipFree(plan->mem);
+    hipError_t e2 = plan->coo_mem ? hipFree(plan->coo_mem) : hipSuccess;
+    if (e == hipSuccess) e = e2;
     delete plan;
     if (e != hipSuccess) return hip_fail(e, "hipFree(plan)");
     return JLUST_STATUS_SUCCESS;

@@ -328,23 +328,35 @@ class HIPSpMVHandle(AbstractKernelHandle):
     spmv.jl:518-544; the cuSPARSE handle contract, ext/CUDAExt/ops/spmv.jl:7-83)."""
 
     def __init__(self, u_A: USTensor, input_fn=None, output_fn=None):
-        if not is_csr_shaped(u_A.format):
-            raise UnsupportedFormat(u_A.format, _BE, "prepared SpMV needs CSR")
+        coo = is_coo_shaped(u_A.format)
+        if not (is_csr_shaped(u_A.format) or coo):
+            raise UnsupportedFormat(u_A.format, _BE, "prepared SpMV plans take CSR or COO")
+        if coo and output_fn is not None:
+            raise UnsupportedFormat(u_A.format, _BE,
+                                    "output_fn is unsupported for COO SpMV; convert A to CSR first")
         self.input_fn, self.output_fn = input_fn, output_fn
         suf = _value_suffix(u_A)
-        rowptr, colind = _csr_parts(u_A)
-        self.dev = _check_same_device(rowptr, colind, nonzeros(u_A))
+        if coo:
+            rows, cols = u_A.crd_buffers[0], u_A.crd_buffers[1]
+            _check_index(u_A, rows, cols)
+            if rows.numel() != nnz(u_A) or cols.numel() != nnz(u_A):
+                raise NonCanonicalStorage("COO coordinate buffers must have nnz entries")
+            first, second = rows, cols
+        else:
+            first, second = _csr_parts(u_A)
+        self.dev = _check_same_device(first, second, nonzeros(u_A))
         self.u_A = u_A                      # keeps the buffers alive (GC anchor)
         self.T = nonzeros(u_A).dtype
         self.suf = suf
         self._exec = None
         self._plan = ctypes.c_void_p(0)
         m, n = u_A.extents
+        create = "jlust_hip_coo_spmv_plan_create" if coo else "jlust_hip_csr_spmv_plan_create"
         with torch.cuda.device(self.dev):
-            st = _lib.lib().jlust_hip_csr_spmv_plan_create(
-                m, n, nnz(u_A), u_A.origin.offset, 0 if suf == "f64" else 1, _ptr(rowptr),
-                _ptr(colind), _ptr(nonzeros(u_A)), _stream(self.dev), ctypes.byref(self._plan))
-        _lib.check(st, "csr_spmv_plan_create", u_A.format, _BE, self.T)
+            st = getattr(_lib.lib(), create)(
+                m, n, nnz(u_A), u_A.origin.offset, 0 if suf == "f64" else 1, _ptr(first),
+                _ptr(second), _ptr(nonzeros(u_A)), _stream(self.dev), ctypes.byref(self._plan))
+        _lib.check(st, create[10:], u_A.format, _BE, self.T)
 
     def execute(self, *ts, alpha=1.0, beta=0.0):
         """execute(h, x, y) (the cuSPARSE handle form) or execute(h, A, x, y)
@@ -447,7 +459,7 @@ def prepare(optype, u_A: USTensor, **kw):
         bad = set(kw) - {"input_fn", "output_fn"}
         if bad:
             raise TypeError(f"prepare(SpMVOp): unexpected keywords {sorted(bad)}")
-        if is_csr_shaped(u_A.format):
+        if is_csr_shaped(u_A.format) or is_coo_shaped(u_A.format):
             return HIPSpMVHandle(u_A, kw.get("input_fn"), kw.get("output_fn"))
         return HIPOpHandle(SpMVOp, u_A, **kw)
     if optype.tag in ("SpMM", "SDDMM"):
