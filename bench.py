@@ -308,7 +308,9 @@ def build_step(cfg, use_plan=False):
         A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (m, n))
         B = dev(cfg["B"])
         C = J.dense_matrix(m, cfg["k"], dtype=A.dtype)
-        return (lambda: J.execute(J.SpMMOp, A, B, C)), "csr_spmm_kernel", "hbm", (A, B, C)
+        # One call: transpose_kernel + csr_spmm_kernel per column chunk of B.
+        return (lambda: J.execute(J.SpMMOp, A, B, C)), \
+            "transpose_kernel + csr_spmm_kernel (per column chunk)", "hbm", (A, B, C)
     if kind == "csr_sddmm":
         S = dev(cfg["mask"])
         out = torch.empty_like(S)

@@ -21,6 +21,8 @@
 //     coalesced too.
 #include "common.hpp"
 
+#include <cstdlib>
+
 namespace jlust {
 namespace {
 
@@ -74,6 +76,86 @@ __global__ __launch_bounds__(256) void transpose_kernel(int64_t n, int64_t k,
         const int64_t j = j0 + jj, c = c0 + tx;
         if (j < n && c < k) Bt[j * ldt + c] = tile[tx][jj];
     }
+}
+
+// 32-column chunks: each half-wave takes one nonzero (two per instruction),
+// its 32 lanes reading the nonzero's 32*sizeof(T)-byte row slice of Bt; the
+// halves' partial sums of a row are added at the end.
+template <typename T>
+__global__ __launch_bounds__(SPMM_BLOCK) void csr_spmm_half_kernel(
+    int64_t m, int64_t k, int32_t origin, const int32_t *__restrict__ rowptr,
+    const int32_t *__restrict__ colind, const T *__restrict__ val, const T *__restrict__ Bt,
+    int64_t ldt, T alpha, T beta, int beta_zero, T *__restrict__ C, int64_t ldc,
+    int skip_empty_rows)
+{
+    constexpr int KC = 32;
+    constexpr int NW = SPMM_BLOCK / 64;
+    __shared__ T s_c[SPMM_ROWS][KC + 1];
+    __shared__ int s_empty[SPMM_ROWS];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int half = lane >> 5;
+    const int col = lane & 31;
+    const int64_t row0 = (int64_t)blockIdx.x * SPMM_ROWS;
+    const int nrows = (int)min((int64_t)SPMM_ROWS, m - row0);
+    const bool cok = col < k;                  // k <= 32 here
+    const int64_t cl = cok ? col : 0;          // clamped, in-bounds column
+
+    for (int rr = wave; rr < nrows; rr += NW) {
+        const int64_t row = row0 + rr;
+        const int64_t lo = (int64_t)rowptr[row] - origin;
+        const int64_t hi = (int64_t)rowptr[row + 1] - origin;
+        if (lane == 0) s_empty[rr] = hi <= lo;
+        T acc = T(0);
+        for (int64_t p0 = lo; p0 < hi; p0 += 64) {
+            const int cnt = (int)min((int64_t)64, hi - p0);
+            int cidx = 0;
+            T cv = T(0);
+            if (lane < cnt) {
+                cidx = colind[p0 + lane] - origin;
+                cv = val[p0 + lane];
+            }
+            int q = 0;
+            for (; q + 2 * SPMM_UNROLL <= cnt; q += 2 * SPMM_UNROLL) {
+                T b[SPMM_UNROLL], a[SPMM_UNROLL];
+#pragma unroll
+                for (int u = 0; u < SPMM_UNROLL; ++u) {
+                    const int j0 = bcast_i(cidx, q + 2 * u), j1 = bcast_i(cidx, q + 2 * u + 1);
+                    const T a0 = bcast(cv, q + 2 * u), a1 = bcast(cv, q + 2 * u + 1);
+                    const int64_t j = half ? j1 : j0;
+                    a[u] = half ? a1 : a0;
+                    b[u] = Bt[j * ldt + cl];
+                }
+#pragma unroll
+                for (int u = 0; u < SPMM_UNROLL; ++u) acc += a[u] * b[u];
+            }
+            for (; q < cnt; q += 2) {
+                const int qa = q, qb = min(q + 1, cnt - 1);
+                const int j0 = bcast_i(cidx, qa), j1 = bcast_i(cidx, qb);
+                const T a0 = bcast(cv, qa), a1 = bcast(cv, qb);
+                const int64_t j = half ? j1 : j0;
+                const T a = half ? a1 : a0;
+                const T prod = a * Bt[j * ldt + cl];
+                acc += (half == 0 || q + 1 < cnt) ? prod : T(0);
+            }
+        }
+        acc += __shfl_xor(acc, 32, 64);
+        if (half == 0) s_c[rr][col] = acc;
+    }
+    __syncthreads();
+    const int ncols = (int)k;
+    for (int idx = tid; idx < SPMM_ROWS * ncols; idx += SPMM_BLOCK) {
+        const int rr = idx % SPMM_ROWS;
+        const int cc = idx / SPMM_ROWS;
+        if (rr >= nrows) continue;
+        if (skip_empty_rows && s_empty[rr]) continue;
+        T *dst = C + (row0 + rr) + cc * ldc;
+        const T s = alpha * s_c[rr][cc];
+        *dst = beta_zero ? s : s + beta * *dst;
+    }
+    (void)cok;
 }
 
 template <typename T, int VEC>
@@ -162,6 +244,34 @@ __global__ __launch_bounds__(SPMM_BLOCK) void csr_spmm_kernel(
     }
 }
 
+// Columns per pass: all of k while the row-major copy of B fits a budget of
+// the 256 MB MALL, else the widest multiple of 16 columns that does (at least
+// 16).  JLUST_HIP_SPMM_KCHUNK=c forces c columns per pass.
+constexpr size_t SPMM_MALL_BUDGET = (size_t)256 << 20;
+
+bool spmm_half()
+{
+    static const bool on = [] {
+        const char *e = getenv("JLUST_HIP_SPMM_HALF");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+int64_t spmm_kchunk(int64_t n, int64_t k, size_t tsz)
+{
+    static const int64_t forced = [] {
+        const char *e = getenv("JLUST_HIP_SPMM_KCHUNK");
+        return e ? (int64_t)atoll(e) : (int64_t)0;
+    }();
+    if (forced > 0) return forced < k ? forced : k;
+    const size_t row = (size_t)(n > 0 ? n : 1) * tsz;
+    if ((size_t)k * row <= SPMM_MALL_BUDGET) return k;
+    int64_t kc = (int64_t)(SPMM_MALL_BUDGET / row) / 16 * 16;
+    if (kc < 16) kc = 16;
+    return kc < k ? kc : k;
+}
+
 template <typename T>
 int csr_spmm(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
              const int32_t *rowptr, const int32_t *colind, const T *val, T alpha, const T *B,
@@ -186,29 +296,44 @@ int csr_spmm(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
     if (m == 0 || k == 0) return JLUST_STATUS_SUCCESS;
     hipStream_t s = (hipStream_t)stream;
 
-    const int vec = (sizeof(T) == 4) ? (k <= 64 ? 1 : k <= 128 ? 2 : 4) : (k <= 64 ? 1 : 2);
-    const int64_t ldt = (k + 3) / 4 * 4;       // keeps every row of Bt 16-byte aligned
+    // Column chunks: every B row a nonzero gathers is a random row of the
+    // row-major copy; when that copy is larger than the MALL budget the
+    // gathers come from HBM, so B is processed in column chunks whose copy
+    // fits (config 3: 2 chunks of 64 columns, 3.14 -> 2.56 ms).
+    const int64_t kc = spmm_kchunk(n, k, sizeof(T));
+    const int64_t ldt_max = (min(kc, k) + 3) / 4 * 4;    // keeps every row of Bt 16-byte aligned
     void *ws = nullptr;
     const int64_t nt = n > 0 ? n : 1;
-    if (int st = scratch(stream, sizeof(T) * (size_t)(nt * ldt), &ws)) return st;
+    if (int st = scratch(stream, sizeof(T) * (size_t)(nt * ldt_max), &ws)) return st;
     T *Bt = (T *)ws;
-    if (n > 0) {
-        dim3 grid((unsigned)((n + 63) / 64), (unsigned)((k + 63) / 64));
-        hipLaunchKernelGGL((transpose_kernel<T>), grid, dim3(256), 0, s, n, k, B, ldb, Bt, ldt);
-        if (int st = check_launch("transpose_kernel")) return st;
-    }
     const dim3 grid((unsigned)((m + SPMM_ROWS - 1) / SPMM_ROWS));
     const int bz = beta == T(0);
-    if (vec == 1)
-        hipLaunchKernelGGL((csr_spmm_kernel<T, 1>), grid, dim3(SPMM_BLOCK), 0, s, m, k, origin,
-                           rowptr, colind, val, Bt, ldt, alpha, beta, bz, C, ldc, skip_empty_rows);
-    else if (vec == 2)
-        hipLaunchKernelGGL((csr_spmm_kernel<T, 2>), grid, dim3(SPMM_BLOCK), 0, s, m, k, origin,
-                           rowptr, colind, val, Bt, ldt, alpha, beta, bz, C, ldc, skip_empty_rows);
-    else
-        hipLaunchKernelGGL((csr_spmm_kernel<T, 4>), grid, dim3(SPMM_BLOCK), 0, s, m, k, origin,
-                           rowptr, colind, val, Bt, ldt, alpha, beta, bz, C, ldc, skip_empty_rows);
-    return check_launch("csr_spmm_kernel");
+    for (int64_t c0 = 0; c0 < k; c0 += kc) {
+        const int64_t kk = min(kc, k - c0);
+        const int64_t ldt = (kk + 3) / 4 * 4;
+        if (n > 0) {
+            dim3 tgrid((unsigned)((n + 63) / 64), (unsigned)((kk + 63) / 64));
+            hipLaunchKernelGGL((transpose_kernel<T>), tgrid, dim3(256), 0, s, n, kk, B + c0 * ldb, ldb, Bt,
+                               ldt);
+            if (int st = check_launch("transpose_kernel")) return st;
+        }
+        const int vec = (sizeof(T) == 4) ? (kk <= 64 ? 1 : kk <= 128 ? 2 : 4) : (kk <= 64 ? 1 : 2);
+        T *Cc = C + c0 * ldc;
+        if (kk <= 32 && spmm_half())
+            hipLaunchKernelGGL((csr_spmm_half_kernel<T>), grid, dim3(SPMM_BLOCK), 0, s, m, kk, origin,
+                               rowptr, colind, val, Bt, ldt, alpha, beta, bz, Cc, ldc, skip_empty_rows);
+        else if (vec == 1)
+            hipLaunchKernelGGL((csr_spmm_kernel<T, 1>), grid, dim3(SPMM_BLOCK), 0, s, m, kk, origin,
+                               rowptr, colind, val, Bt, ldt, alpha, beta, bz, Cc, ldc, skip_empty_rows);
+        else if (vec == 2)
+            hipLaunchKernelGGL((csr_spmm_kernel<T, 2>), grid, dim3(SPMM_BLOCK), 0, s, m, kk, origin,
+                               rowptr, colind, val, Bt, ldt, alpha, beta, bz, Cc, ldc, skip_empty_rows);
+        else
+            hipLaunchKernelGGL((csr_spmm_kernel<T, 4>), grid, dim3(SPMM_BLOCK), 0, s, m, kk, origin,
+                               rowptr, colind, val, Bt, ldt, alpha, beta, bz, Cc, ldc, skip_empty_rows);
+        if (int st = check_launch("csr_spmm_kernel")) return st;
+    }
+    return JLUST_STATUS_SUCCESS;
 }
 
 }  // namespace
