@@ -205,3 +205,27 @@ def test_bsr_unaligned_leading_dims(J, O):
     rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
     absref = O.csr_spmm_absref(rp, ci, v, np.asfortranarray(Bbig[: nb * 16]))
     assert_within(host(Cd), ref, absref, np.float32, "unaligned leading dimensions")
+
+
+@pytest.mark.parametrize("case", ["scattered", "wide_band", "band_tail"])
+def test_bsr_block_patterns(J, O, case):
+    """Block patterns beside config 5's: blocks scattered over 2000 block
+    columns, a band of +-60 block columns, and a narrow band with 12 blocks
+    per block-row (more than one register chunk of 8), each for beta = 0 and
+    beta != 0."""
+    if case == "scattered":
+        mb, nb, per_row, band = 48, 2000, 4, None
+    elif case == "wide_band":
+        mb, nb, per_row, band = 64, 64, 8, 60
+    else:
+        mb, nb, per_row, band = 40, 40, 12, 10
+    k = 40
+    browptr, bcolind, val = random_bsr(mb, nb, per_row, seed=31, band=band)
+    B = np.asfortranarray(np.random.default_rng(8).standard_normal((nb * 16, k)).astype(np.float32))
+    C0 = np.asfortranarray(np.random.default_rng(9).standard_normal((mb * 16, k)).astype(np.float32))
+    for beta in (0.0, 0.5):
+        C = run_bsr(J, browptr, bcolind, val, B, mb, nb, alpha=1.5, beta=beta, C0=C0)
+        ref = O.bsr_spmm(browptr, bcolind, val, 16, B, 1.5, beta, C0)
+        rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
+        absref = O.csr_spmm_absref(rp, ci, v, B, 1.5, beta, C0)
+        assert_within(C, ref, absref, np.float32, f"{case} beta={beta}")
