@@ -55,6 +55,9 @@ def parse():
                    help="only measure random-gather bandwidth (8 B and 512 B rows) per source size")
     p.add_argument("--convert", action="store_true",
                    help="only time format conversions (convert_format) at config sizes")
+    p.add_argument("--coo", action="store_true",
+                   help="only time COO and DCSR SpMV (plain calls and prepared plans) on config 2's "
+                        "matrix, sorted and shuffled, beside the oracle's COO SpMV on this host")
     p.add_argument("--blocks", action="store_true",
                    help="only time BlockSparseMatrix / BlockBandedMatrix mul! on a synthetic "
                         "DCOPF operator of pglib case30000_goc size (T = 24)")
@@ -191,6 +194,75 @@ def blocks_bench(steps, warmup):
                     "cpu_scipy_us": round(t_cpu * 1e6, 1), "max_rel_diff_vs_scipy": err})
         log(f"{name}: {m}x{n} nnz {nz}: {t_sync*1e6:.1f} us/call synced, {t_async*1e6:.1f} queued, "
             f"first call {t_first*1e3:.1f} ms, scipy {t_cpu*1e6:.0f} us")
+    return out
+
+
+def coo_bench(steps, warmup, cpu_seconds):
+    """COO SpMV (src/interop.jl:248-260 storage; spmv.jl:407-448) on BASELINE
+    config 2's matrix: the plain entry point (atomics per row run) and the
+    prepared plan (entries row-ordered once, then the CSR plan), with the
+    entries in row order and randomly shuffled; DCSR SpMV of the same matrix
+    with every other row emptied.  Bytes: the COO compulsory bytes
+    12*nnz + 4*nnz (rows) + 8(n + m).  CPU: the oracle's COO SpMV (C,
+    sequential, oracle/jlust_cpu.c) on the box's host."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    from oracle import oracle as O
+    cfg = W.make(2)
+    m, n = cfg["m"], cfg["n"]
+    rp = cfg["rowptr"].astype(np.int64)
+    rows = np.repeat(np.arange(1, m + 1, dtype=np.int32), np.diff(rp))
+    cols, val, xh = cfg["colind"], cfg["val"], cfg["x"]
+    nz = val.size
+    perm = np.random.default_rng(0).permutation(nz)
+    byts = 16 * nz + 8 * (n + m)
+    x = dev(xh)
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    out = []
+
+    def run(name, step):
+        ms, ev = timed(step, steps, warmup)
+        out.append({"case": name, "ms_per_call": round(ms, 4), "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
+                    "event_ms": round(float(ev.mean()), 4)})
+        log(f"{name}: {ms:.3f} ms/call")
+
+    for order, (r, c, v) in (("row order", (rows, cols, val)),
+                             ("shuffled", (rows[perm], cols[perm], val[perm]))):
+        A = J.coo_tensor(dev(r), dev(c), dev(v), (m, n))
+        run(f"COO {order}, plain call", lambda: J.execute(J.SpMVOp, A, x, y))
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+        torch.cuda.synchronize()
+        t_build = time.perf_counter() - t0
+        run(f"COO {order}, prepared plan", lambda: J.execute(h, x, y))
+        out[-1]["plan_build_ms"] = round(t_build * 1e3, 2)
+        del A, h
+        torch.cuda.empty_cache()
+    # DCSR: every other row emptied.
+    keep = np.zeros(m, bool)
+    keep[::2] = True
+    lens = np.diff(rp)
+    stored = np.flatnonzero(keep & (lens > 0))
+    mask = np.repeat(keep, lens)
+    dcols, dval = cols[mask], val[mask]
+    dpos = (np.concatenate([[0], np.cumsum(lens[stored])]) + 1).astype(np.int32)
+    D = J.dcsr_tensor(dev((stored + 1).astype(np.int32)), dev(dpos), dev(dcols), dev(dval), (m, n))
+    run("DCSR (every other row stored), plain call", lambda: J.execute(J.SpMVOp, D, x, y))
+    # CPU: the oracle's COO SpMV on a bounded sample (leading entries in row order).
+    t0 = time.perf_counter()
+    probe = max(1, nz // 50)
+    O.coo_spmv(rows[:probe], cols[:probe], val[:probe], xh, m)
+    tp = max(time.perf_counter() - t0, 1e-4)
+    take = int(min(nz, probe * max(1.0, (cpu_seconds / 4) / tp)))
+    t0 = time.perf_counter()
+    O.coo_spmv(rows[:take], cols[:take], val[:take], xh, m)
+    tc = time.perf_counter() - t0
+    cpu_gbps = (16 * take + 8 * (n + m)) / tc / 1e9
+    out.append({"case": "CPU oracle COO SpMV (1 thread)", "sample_entries": take,
+                "GBps": round(cpu_gbps, 2)})
+    log(f"cpu oracle COO: {cpu_gbps:.2f} GB/s on {take} entries")
     return out
 
 
@@ -448,6 +520,10 @@ def main():
         return
     if args.convert:
         print(json.dumps({"convert": convert_bench(args.cpu_seconds)}), flush=True)
+        return
+    if args.coo:
+        print(json.dumps({"coo": coo_bench(args.steps or 50, args.warmup or 3, args.cpu_seconds)}),
+              flush=True)
         return
     if args.blocks:
         print(json.dumps({"blocks": blocks_bench(args.steps or 200, args.warmup or 10)}), flush=True)
