@@ -15,8 +15,8 @@ from .errors import (DeviceMismatch, HIPError, IncompatibleExtents, IndexOriginM
                      InvalidLevelAccess, InvalidTensorFormat, JLUSTError, NoDevice,
                      NonCanonicalStorage, UnsupportedFormat, UnsupportedIndexType,
                      UnsupportedValueType)
-from .formats import (CompressedLevel, DenseLevel, Formats, ShiftedDiagLevel, SingletonLevel,
-                      TensorFormat, dim2lvl, lvl2dim)
+from .formats import (CompressedLevel, DenseLevel, Formats, PeriodicLevel, ShiftedDiagLevel,
+                      SingletonLevel, TensorFormat, dim2lvl, lvl2dim)
 from .ops import (AbstractKernelHandle, AbstractUSTBackend, BBMSpMVOp, BlockSpMMOp, BlockSpMVOp,
                   HIPBackend, Op, OpType, SDDMMOp, SpMMOp, SpMVOp, default_backend, execute,
                   matmul, mul_, prepare, supports_backend, update_values_)
@@ -30,6 +30,6 @@ from .convert import (convert_format, convert_index_type, convert_value_type, cs
 from .tensor import (CPUDevice, HIPDevice, OneBased, USTensor, ZeroBased, bsr_tensor,
                      coo_tensor, coordinates, csr_tensor, dense_matrix, extents, format,
                      has_coordinates, has_positions, index_origin, materialize, nnz, nonzeros,
-                     positions, shifted_diag_tensor, size, ust)
+                     periodic_csr_tensor, positions, shifted_diag_tensor, size, ust)
 
 __all__ = [n for n in dir() if not n.startswith("_")]

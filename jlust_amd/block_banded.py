@@ -26,12 +26,10 @@ from __future__ import annotations
 
 from typing import List, Optional, Sequence
 
-import torch
-
 from .block_sparse import (AssembledCSR, BlockSparseMatrix, BlockStructureError, _t,
                            assemblable)
 from .errors import IncompatibleExtents, UnsupportedFormat
-from .tensor import USTensor, ust
+from .tensor import USTensor
 
 
 def diag_starts(n_diag_rows: int, n_off_rows: Sequence[int], T: int) -> List[int]:

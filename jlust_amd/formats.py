@@ -14,6 +14,8 @@ expression of the dimension coordinates (i, j):
   DensedRight(N)     N dense levels (plain column-major arrays), :219-227
   ShiftedDiag(T; shift, val)  (i : dense, j : shifted diagonal): row r holds
                      val at column r + shift, no buffers, :53-61
+  PeriodicCSR(T, br, nc)  (i÷br : periodic, i%br : dense(br), j : compressed):
+                     T copies of one br x nc CSR block on the diagonal, :77-88
 
 Only the level *types* drive operator dispatch (dense outer + compressed
 inner = CSR-shaped, compressed non-unique + singleton = COO-shaped, blocked =
@@ -59,6 +61,23 @@ class ShiftedDiagLevel:
 
     def __repr__(self):
         return f"ShiftedDiagLevel(shift={self.shift}, val={self.val})"
+
+
+@dataclass(frozen=True)
+class PeriodicLevel:
+    """src/formats.jl:87-107: the period index i ÷ block_rows of a T-fold
+    block-diagonal replica; each period shifts columns by n_cols."""
+    periods: int
+    n_cols: int
+
+    def __post_init__(self):
+        if not (isinstance(self.periods, int) and self.periods > 0 and
+                isinstance(self.n_cols, int) and self.n_cols > 0):
+            raise InvalidTensorFormat(
+                f"PeriodicLevel needs positive integers, got T={self.periods}, n_cols={self.n_cols}")
+
+    def __repr__(self):
+        return f"PeriodicLevel({self.periods}, {self.n_cols})"
 
 
 @dataclass(frozen=True, eq=False)
@@ -142,6 +161,19 @@ class Formats:
                       [DenseLevel(), ShiftedDiagLevel(int(shift), v)], "ShiftedDiag", _ident2())
 
     @staticmethod
+    def PeriodicCSR(periods: int, block_rows: int, n_cols: int) -> TensorFormat:
+        """src/named_formats.jl:77-88: (i ÷ block_rows : periodic, i % block_rows :
+        dense(block_rows), j : compressed), T copies of one CSR block along the
+        diagonal sharing its buffers."""
+        br, nc = int(block_rows), int(n_cols)
+        return TensorFormat(
+            f"PeriodicCSR(T={int(periods)},br={br},nc={nc})",
+            (PeriodicLevel(int(periods), nc), DenseLevel(br), CompressedLevel()), "PeriodicCSR", 2,
+            (lambda i, j: (i // br, i % br, j)),
+            (lambda m, n: (int(periods), br, n)),
+            (lambda t, r, j: (t * br + r, j)))
+
+    @staticmethod
     def BSRRight(blocksize) -> TensorFormat:
         b1, b2 = blocksize
         return _make2(
@@ -181,6 +213,10 @@ def is_shifted_diag(fmt: TensorFormat) -> bool:
     (ext/CUDAExt/ops/block_mul.jl:60-69)."""
     lv = fmt.levels
     return len(lv) == 2 and isinstance(lv[0], DenseLevel) and isinstance(lv[1], ShiftedDiagLevel)
+
+
+def is_periodic_csr(fmt: TensorFormat) -> bool:
+    return fmt.family == "PeriodicCSR"
 
 
 def is_bsr(fmt: TensorFormat) -> bool:

@@ -15,7 +15,8 @@ import torch
 from . import _lib
 from .errors import (DeviceMismatch, IncompatibleExtents, NonCanonicalStorage,
                      UnsupportedFormat, UnsupportedIndexType, UnsupportedValueType)
-from .formats import Formats, bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped, is_shifted_diag
+from .formats import (Formats, bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped,
+                      is_periodic_csr, is_shifted_diag)
 from .ops import AbstractKernelHandle, HIPBackend, Op, SDDMMOp, SpMMOp, SpMVOp
 from .tensor import USTensor, dense_matrix, leading_dim, nnz, nonzeros, ust
 
@@ -42,7 +43,7 @@ def supports(op: Op) -> bool:
     f = op.formats
     if op.tag == "SpMV" and len(f) == 3:
         return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_shifted_diag(f[0]) or
-                f[0] == Formats.DCSR) and \
+                f[0] == Formats.DCSR or is_periodic_csr(f[0])) and \
             _dense_fmt(f[1]) and \
             _dense_fmt(f[2]) and f[1].ndims == 1 and f[2].ndims == 1
     if op.tag == "SpMM" and len(f) == 3:
@@ -166,6 +167,9 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     L = _lib.lib()
     if u_A.format == Formats.DCSR:
         return _dcsr_product(u_A, u_x, u_y, alpha, beta)
+    if is_periodic_csr(u_A.format):
+        _periodic_spmv(u_A, x, y, alpha, beta)
+        return u_y
     if is_shifted_diag(u_A.format):
         lv = u_A.format.levels[1]
         dev = _check_same_device(x, y)
@@ -194,6 +198,22 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
             float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
     _lib.check(st, "coo_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
     return u_y
+
+
+def _periodic_spmv(u_A: USTensor, x: torch.Tensor, y: torch.Tensor, alpha, beta):
+    """PeriodicCSR SpMV (kron(I(T), block) * x, src/named_formats.jl:63-88)
+    as one CSR SpMM of the block with the T column blocks of x as the
+    columns of a column-major n_cols x T matrix and y as an m_b x T one:
+    every row of the block is read once for all T periods."""
+    lv = u_A.format.levels[0]
+    T, nc = lv.periods, lv.n_cols
+    br = u_A.format.levels[1].size
+    block = USTensor((br, nc), Formats.CSR, (None, u_A.pos_buffers[2]), (None, u_A.crd_buffers[2]),
+                     nonzeros(u_A), u_A.owner, u_A.origin)
+    X = x.view(T, nc).t()                 # column t = x[t*nc : (t+1)*nc]
+    Y = y.view(T, br).t()
+    _spmm(block, ust(X), ust(Y), alpha, beta)
+    return y
 
 
 def _dcsr_product(u_A: USTensor, u_X: USTensor, u_Y: USTensor, alpha, beta):

@@ -180,6 +180,19 @@ def shifted_diag_tensor(dtype, n_rows: int, n_cols: int, shift: int = 0, val=1.0
                     torch.empty(0, dtype=dtype, device=device), None, OneBased())
 
 
+def periodic_csr_tensor(block: USTensor, periods: int) -> USTensor:
+    """src/interop.jl:198-212: kron(I(T), block) without copying the block's
+    buffers (pos/crd at level 3, the block kept as owner)."""
+    from .errors import UnsupportedFormat
+    if block.format != Formats.CSR:
+        raise UnsupportedFormat(block.format, "HIPBackend",
+                                f"periodic_csr_tensor: block must be CSR-formatted (got {block.format})")
+    br, bc = block.extents
+    fmt = Formats.PeriodicCSR(int(periods), br, bc)
+    return USTensor((int(periods) * br, int(periods) * bc), fmt, (None, None, block.pos_buffers[1]),
+                    (None, None, block.crd_buffers[1]), block.val, block, block.origin)
+
+
 def ust(a) -> USTensor:
     """Zero-copy dense view of a vector or a column-major matrix
     (src/interop.jl:36-46)."""
