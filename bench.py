@@ -374,7 +374,7 @@ def build_step(cfg, use_plan=False):
         y = torch.empty(m, dtype=A.dtype, device="cuda")
         if use_plan:
             h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
-            return (lambda: J.execute(h, x, y)), "csr_spmv_merge_kernel", "hbm", (A, x, y, h)
+            return (lambda: J.execute(h, x, y)), f"csr_spmv_{h.kernel()}_kernel", "hbm", (A, x, y, h)
         return (lambda: J.execute(J.SpMVOp, A, x, y)), "csr_spmv_merge_kernel", "hbm", (A, x, y)
     if kind == "csr_spmm":
         A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (m, n))
@@ -546,8 +546,6 @@ def main():
                  "ms_per_step": round(p_ms, 6), "kernel": pkname,
                  "per_launch_ms": round(float(p_launch.mean()), 6)}
         del pkeep
-        kname = "csr_spmv_sliced_kernel" if cfg["n"] * np.dtype(cfg["dtype"]).itemsize > (4 << 20) \
-            else kname
     log(f"{steps} steps: wall {ms_per_step:.4f} ms/step, event mean "
         f"{per_launch_ms.mean():.4f} ms, min {per_launch_ms.min():.4f} ms")
 

@@ -135,6 +135,17 @@ int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float alpha,
                                         jlust_stream_t stream);
 int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan);
 
+/* The kernel a plan runs (no counterpart in the reference; for diagnostics
+ * and benchmarks): merge-path tiles, the vector kernel for short even rows
+ * (*lanes_per_row lanes per row), or XCD column slices. */
+enum jlust_spmv_kernel {
+    JLUST_SPMV_MERGE = 0,
+    JLUST_SPMV_VECTOR = 1,
+    JLUST_SPMV_SLICED = 2
+};
+int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *kernel,
+                                 int32_t *lanes_per_row);
+
 /*
  * Prepared COO SpMV (rows[nnz], cols[nnz] as coo_tensor stores them,
  * src/interop.jl:248-260): the entries are put in row order once (a stable

@@ -38,6 +38,7 @@ SIGNATURES = {
     "jlust_hip_csr_spmv_plan_execute_f64": (_INT, [_P, _D, _P, _D, _P, _P]),
     "jlust_hip_csr_spmv_plan_execute_f32": (_INT, [_P, _F, _P, _F, _P, _P]),
     "jlust_hip_csr_spmv_plan_destroy": (_INT, [_P]),
+    "jlust_hip_csr_spmv_plan_info": (_INT, [_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
     "jlust_hip_coo_spmv_plan_create": (_INT, [_I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
                                               ctypes.POINTER(_P)]),
     "jlust_hip_coo_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P, _P]),

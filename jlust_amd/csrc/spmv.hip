@@ -721,6 +721,80 @@ int csr_spmv(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *r
                           carry_row, carry_val, (hipStream_t)stream);
 }
 
+// Vector kernel for plans of short, even rows: LPR lanes per row, each lane
+// striding the row by LPR,
+// partial sums combined with xor-shuffles.  No LDS, no barriers, no carries:
+// every wave holds 64/LPR rows, so a small matrix still puts many waves in
+// flight (the merge kernel spends one 2048-item tile per block there).
+template <typename T, int LPR, bool BZ>
+__global__ __launch_bounds__(256) void csr_spmv_vector_kernel(int64_t m, int32_t origin,
+                                                              const int32_t *__restrict__ rowptr,
+                                                              const int32_t *__restrict__ colind,
+                                                              const T *__restrict__ val, const T *__restrict__ x,
+                                                              T *__restrict__ y, T alpha, T beta)
+{
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = t / LPR;
+    const int sub = (int)(t % LPR);
+    const int64_t r = row < m ? row : m - 1;            // clamped: loads stay in bounds
+    const int64_t lo = (int64_t)rowptr[r] - origin;
+    const int64_t hi = row < m ? (int64_t)rowptr[r + 1] - origin : lo;
+    T acc = T(0);
+    for (int64_t p = lo + sub; p < hi; p += LPR) acc += val[p] * x[colind[p] - origin];
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
+    if (sub == 0 && row < m) y[row] = BZ ? alpha * acc : alpha * acc + beta * y[row];
+}
+
+// out[0] = max row length: a grid-stride maximum per thread, reduced per
+// block in LDS, one atomicMax per block.
+__global__ __launch_bounds__(256) void row_len_max_kernel(int64_t m, const int32_t *__restrict__ rowptr,
+                                                          int32_t *__restrict__ out)
+{
+    __shared__ int32_t s_w[4];
+    int32_t len = 0;
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < m; i += (int64_t)gridDim.x * 256)
+        len = max(len, rowptr[i + 1] - rowptr[i]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) len = max(len, __shfl_xor(len, off, 64));
+    if (__lane_id() == 0) s_w[threadIdx.x >> 6] = len;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const int32_t b = max(max(s_w[0], s_w[1]), max(s_w[2], s_w[3]));
+        if (b > 0) atomicMax(out, b);
+    }
+}
+
+// Lanes per row of the vector kernel for a plan (0 = merge kernel): the
+// smallest power of two >= 2 giving a lane about 4 entries of an average row,
+// when rows average at most 64 entries and the longest needs at most 16 steps
+// per lane.  JLUST_HIP_SPMV_VECTOR=0 disables it, =L forces L lanes per row.
+// Synchronises `s`.
+int vector_lanes(int64_t m, int64_t nnz, const int32_t *rowptr, hipStream_t s, int *lpr_out)
+{
+    *lpr_out = 0;
+    const char *e = getenv("JLUST_HIP_SPMV_VECTOR");
+    if ((e && e[0] == '0') || m <= 0) return JLUST_STATUS_SUCCESS;
+    const double avg = (double)nnz / (double)m;
+    if (avg > 64.0) return JLUST_STATUS_SUCCESS;
+    int lpr = 2;                                 // about 4 entries per lane on average
+    while (lpr < 64 && 4 * lpr < avg) lpr <<= 1;
+    const int forced = e ? atoi(e) : 0;          // JLUST_HIP_SPMV_VECTOR=L: L lanes per row
+    if (forced >= 2 && forced <= 64 && (forced & (forced - 1)) == 0) lpr = forced;
+    void *ws = nullptr;
+    if (int st = scratch(s, sizeof(int32_t), &ws)) return st;
+    auto *mx = (int32_t *)ws;
+    JLUST_HIP_TRY(hipMemsetAsync(mx, 0, sizeof(int32_t), s));
+    const int64_t nblk = min((int64_t)1024, (m + 255) / 256);
+    hipLaunchKernelGGL(row_len_max_kernel, dim3((unsigned)nblk), dim3(256), 0, s, m, rowptr, mx);
+    if (int st = check_launch("row_len_max_kernel")) return st;
+    int32_t h = 0;
+    JLUST_HIP_TRY(hipMemcpyAsync(&h, mx, sizeof(h), hipMemcpyDeviceToHost, s));
+    JLUST_HIP_TRY(hipStreamSynchronize(s));
+    if (h <= 16 * lpr) *lpr_out = lpr;         // the longest row: at most 16 steps per lane
+    return JLUST_STATUS_SUCCESS;
+}
+
 // Counts the entries whose column lies within +-w of their row's diagonal
 // position r*n/m.  Each thread walks LOC_CHUNK consecutive entries from the
 // row found by binary search; one atomic per wave.
@@ -825,6 +899,7 @@ struct jlust_spmv_plan {
     int64_t *start_rows;
     int64_t *carry_row;
     void *carry_val;
+    int vec_lpr = 0;   // > 0: vector kernel with this many lanes per row
     // sliced
     bool sliced;
     int64_t slice_w;
@@ -960,6 +1035,7 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
         if (m > 0) {
             st = value_type == 0 ? spmv_grid<double>(m, nnz, p->ipt, &p->grid)
                                  : spmv_grid<float>(m, nnz, p->ipt, &p->grid);
+            if (!st) st = vector_lanes(m, nnz, rowptr, s, &p->vec_lpr);
             if (st) { delete p; return st; }
         }
         const size_t nb = (size_t)(p->grid.nblocks > 0 ? p->grid.nblocks : 1);
@@ -969,7 +1045,7 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
         p->start_rows = (int64_t *)p->mem;
         p->carry_row = (int64_t *)((char *)p->mem + sz_rows);
         p->carry_val = (char *)p->mem + 2 * sz_rows;
-        if (m > 0) {
+        if (m > 0 && p->vec_lpr == 0) {
             hipLaunchKernelGGL(merge_start_kernel, dim3((unsigned)p->grid.nblocks), dim3(64), 0, s, m,
                                nnz, origin, rowptr,
                                p->grid.tiles_per_block * (int64_t)(SPMV_BLOCK * p->ipt),
@@ -1056,6 +1132,35 @@ extern "C" int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan, con
     return JLUST_STATUS_SUCCESS;
 }
 
+namespace jlust {
+template <typename T>
+int vector_launch(const jlust_spmv_plan_t p, int lpr, T alpha, const T *x, T beta, T *y, hipStream_t s)
+{
+    const int64_t threads = p->m * lpr;
+    const dim3 grid((unsigned)((threads + 255) / 256));
+    const T *val = (const T *)p->val;
+#define V(L)                                                                                        \
+    do {                                                                                            \
+        if (beta == T(0))                                                                           \
+            hipLaunchKernelGGL((csr_spmv_vector_kernel<T, L, true>), grid, dim3(256), 0, s, p->m,    \
+                               p->origin, p->rowptr, p->colind, val, x, y, alpha, beta);           \
+        else                                                                                        \
+            hipLaunchKernelGGL((csr_spmv_vector_kernel<T, L, false>), grid, dim3(256), 0, s, p->m,   \
+                               p->origin, p->rowptr, p->colind, val, x, y, alpha, beta);           \
+    } while (0)
+    switch (lpr) {
+    case 2: V(2); break;
+    case 4: V(4); break;
+    case 8: V(8); break;
+    case 16: V(16); break;
+    case 32: V(32); break;
+    default: V(64); break;
+    }
+#undef V
+    return check_launch("csr_spmv_vector_kernel");
+}
+}  // namespace jlust
+
 template <typename T>
 static int plan_execute(jlust_spmv_plan_t plan, int want_type, T alpha, const T *x, T beta, T *y,
                         jlust_stream_t stream)
@@ -1076,6 +1181,8 @@ static int plan_execute(jlust_spmv_plan_t plan, int want_type, T alpha, const T 
                     "spmv_plan_execute: plan belongs to device %d, current device is %d",
                     plan->device, dev);
     hipStream_t s = (hipStream_t)stream;
+    if (!plan->sliced && plan->vec_lpr > 0)
+        return vector_launch<T>(plan, plan->vec_lpr, alpha, x, beta, y, s);
     if (!plan->sliced)
         return spmv_launch<T>(plan->m, plan->nnz, plan->origin, plan->rowptr, plan->colind,
                               (const T *)plan->val, alpha, x, beta, y, plan->grid, plan->ipt,
@@ -1119,6 +1226,15 @@ extern "C" int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float
                                                    jlust_stream_t stream)
 {
     return plan_execute<float>(plan, 1, alpha, x, beta, y, stream);
+}
+
+extern "C" int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *kernel, int32_t *lanes_per_row)
+{
+    clear_error();
+    if (!plan || !kernel) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_info: null argument");
+    *kernel = plan->sliced ? JLUST_SPMV_SLICED : plan->vec_lpr > 0 ? JLUST_SPMV_VECTOR : JLUST_SPMV_MERGE;
+    if (lanes_per_row) *lanes_per_row = plan->vec_lpr;
+    return JLUST_STATUS_SUCCESS;
 }
 
 extern "C" int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan)

@@ -425,6 +425,13 @@ class HIPSpMVHandle(AbstractKernelHandle):
             _lib.check(st, "csr_spmv_plan_execute", self.u_A.format, _BE, self.T)
         return y
 
+    def kernel(self) -> str:
+        """The kernel the plan runs: "merge", "vector" or "sliced"."""
+        k, lpr = ctypes.c_int32(), ctypes.c_int32()
+        st = _lib.lib().jlust_hip_csr_spmv_plan_info(self._plan, ctypes.byref(k), ctypes.byref(lpr))
+        _lib.check(st, "csr_spmv_plan_info", self.u_A.format, _BE, self.T)
+        return ("merge", "vector", "sliced")[k.value]
+
     def update_values(self, u_A: USTensor):
         if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):
             raise IncompatibleExtents("update_values!: the sparsity structure must not change")
