@@ -373,7 +373,11 @@ def build_step(cfg, use_plan=False):
         x = dev(cfg["x"])
         y = torch.empty(m, dtype=A.dtype, device="cuda")
         if use_plan:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
             h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+            torch.cuda.synchronize()
+            h.build_ms = (time.perf_counter() - t0) * 1e3
             return (lambda: J.execute(h, x, y)), f"csr_spmv_{h.kernel()}_kernel", "hbm", (A, x, y, h)
         return (lambda: J.execute(J.SpMVOp, A, x, y)), "csr_spmv_merge_kernel", "hbm", (A, x, y)
     if kind == "csr_spmm":
@@ -565,6 +569,7 @@ def main():
     roof["kernel"] = kname
     roof["per_launch_ms"] = round(k_ms, 6)
     roof["per_launch_ms_min"] = round(float(per_launch_ms.min()), 6)
+    plan_build_ms = round(keep[3].build_ms, 2) if use_plan else None
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -585,7 +590,7 @@ def main():
         "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 3),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 3),
         "algorithmic_bytes": int(nbytes), "flops": int(nflops),
-        "roofline": roof, "plain_call": plain, "cpu_baseline": cpu,
+        "roofline": roof, "plain_call": plain, "plan_build_ms": plan_build_ms, "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     del keep

@@ -504,48 +504,181 @@ __global__ void sliced_start_kernel(int64_t m, SliceInfo info, const int32_t *__
     if (__lane_id() == 0) start_rows[s * nb + lb] = r;
 }
 
-// counts[s*(m+1) + i] = entries of row i in column slice s (the i = m slot is 0).
-__global__ void slice_count_kernel(int64_t m, int32_t origin, const int32_t *__restrict__ rowptr,
-                                   const int32_t *__restrict__ colind, int64_t w,
-                                   int32_t *__restrict__ counts)
+// ---- sliced layout build: a stable partition of the entries by column slice.
+//
+// Slice s of the layout holds, in their original (row-major) order, the
+// entries whose column lies in [s*w, (s+1)*w).  So the position of entry p is
+// off[s] + (entries of slice s before p), and slice s's row pointer for row i
+// is off[s] + (entries of slice s before rowptr[i]).  Both are prefix counts
+// over the entry array, computed entry-parallel in SB_E-entry blocks, so the
+// build costs the same whatever the row lengths (a row-parallel walk waits on
+// the longest row, 100k entries in a power-law pattern).  Positions are always
+// a permutation of [0, nnz), whatever rowptr holds.
+constexpr int SB_THREADS = 256, SB_IPT = 8, SB_E = SB_THREADS * SB_IPT;
+constexpr int SB_CKPT = 32;   // prefix checkpoint every SB_CKPT entries
+
+__device__ __forceinline__ int slice_of(int64_t c, int64_t w)
+{
+    const int64_t s = c / w;          // c < 0 only on invalid input
+    return s < 0 ? 0 : (s >= NUM_XCD ? NUM_XCD - 1 : (int)s);
+}
+
+// Eight 16-bit counters packed in four words: slice s in word s/2, half s%2.
+struct Packed8 {
+    uint32_t w[4];
+};
+
+__device__ __forceinline__ uint32_t packed_get(const Packed8 &p, int s)
+{
+    const uint32_t v = (s >> 1) == 0 ? p.w[0] : (s >> 1) == 1 ? p.w[1] : (s >> 1) == 2 ? p.w[2] : p.w[3];
+    return (v >> (16 * (s & 1))) & 0xffffu;
+}
+
+__device__ __forceinline__ void packed_inc(Packed8 &p, int s)
+{
+    const uint32_t one = 1u << (16 * (s & 1));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) p.w[k] += (s >> 1) == k ? one : 0u;
+}
+
+// bcnt[s*nblk + b] = entries of slice s in entry block b.
+__global__ __launch_bounds__(SB_THREADS) void slice_block_count_kernel(int64_t nnz, int32_t origin,
+                                                                       const int32_t *__restrict__ colind,
+                                                                       int64_t w, int64_t nblk,
+                                                                       int32_t *__restrict__ bcnt)
+{
+    __shared__ uint32_t wsum[SB_THREADS / 64][4];
+    const int t = threadIdx.x;
+    const int64_t e0 = (int64_t)blockIdx.x * SB_E;
+    Packed8 c = {{0, 0, 0, 0}};
+#pragma unroll
+    for (int k = 0; k < SB_IPT; ++k) {
+        const int64_t p = e0 + k * SB_THREADS + t;
+        if (p < nnz) packed_inc(c, slice_of((int64_t)colind[p] - origin, w));
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) c.w[k] += __shfl_xor(c.w[k], off, 64);
+    if (__lane_id() == 0)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wsum[t >> 6][k] = c.w[k];
+    __syncthreads();
+    if (t < NUM_XCD) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int q = 0; q < SB_THREADS / 64; ++q) v += (wsum[q][t >> 1] >> (16 * (t & 1))) & 0xffffu;
+        bcnt[t * nblk + blockIdx.x] = (int32_t)v;
+    }
+}
+
+// With bstart = the exclusive scan of bcnt (slice-major, so bstart[s*nblk+b]
+// = off[s] + slice-s entries of blocks before b): places entry block b's
+// entries and writes the prefix checkpoints ckpt[g*8 + s] = slice s's
+// position for the entries before g*SB_CKPT.
+template <typename T>
+__global__ __launch_bounds__(SB_THREADS) void slice_place_kernel(
+    int64_t nnz, int32_t origin, const int32_t *__restrict__ colind, const T *__restrict__ val, int64_t w,
+    int64_t nblk, const int32_t *__restrict__ bstart, int32_t *__restrict__ ckpt,
+    int32_t *__restrict__ colind_all, T *__restrict__ val_all, int32_t *__restrict__ perm)
+{
+    __shared__ uint8_t sl[SB_E];
+    __shared__ int32_t qloc[SB_E];
+    __shared__ uint32_t wsum[SB_THREADS / 64][4];
+    __shared__ int32_t base[NUM_XCD];
+    const int t = threadIdx.x, lane = __lane_id(), wave = t >> 6;
+    const int64_t e0 = (int64_t)blockIdx.x * SB_E;
+    if (t < NUM_XCD) base[t] = bstart[t * nblk + blockIdx.x];
+    int32_t c[SB_IPT];
+#pragma unroll
+    for (int k = 0; k < SB_IPT; ++k) {
+        const int64_t p = e0 + k * SB_THREADS + t;
+        c[k] = p < nnz ? colind[p] - origin : 0;
+        sl[k * SB_THREADS + t] = p < nnz ? (uint8_t)slice_of(c[k], w) : (uint8_t)NUM_XCD;
+    }
+    __syncthreads();
+    // Thread t owns entries t*SB_IPT .. t*SB_IPT+7 of the block (in order).
+    uint8_t mine[SB_IPT];
+    Packed8 own = {{0, 0, 0, 0}};
+#pragma unroll
+    for (int j = 0; j < SB_IPT; ++j) {
+        mine[j] = sl[t * SB_IPT + j];
+        if (mine[j] < NUM_XCD) packed_inc(own, mine[j]);
+    }
+    Packed8 inc = own;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t v = __shfl_up(inc.w[k], off, 64);
+            if (lane >= off) inc.w[k] += v;
+        }
+    if (lane == 63)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) wsum[wave][k] = inc.w[k];
+    __syncthreads();
+    Packed8 pre;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        pre.w[k] = inc.w[k] - own.w[k];
+        for (int q = 0; q < wave; ++q) pre.w[k] += wsum[q][k];
+    }
+#pragma unroll
+    for (int j = 0; j < SB_IPT; ++j) {
+        const int jj = t * SB_IPT + j;
+        const int64_t e = e0 + jj;
+        if (jj % SB_CKPT == 0 && e < nnz) {
+            const int64_t g = e / SB_CKPT;
+#pragma unroll
+            for (int s = 0; s < NUM_XCD; ++s) ckpt[g * NUM_XCD + s] = base[s] + (int32_t)packed_get(pre, s);
+        }
+        if (mine[j] < NUM_XCD) {
+            qloc[jj] = base[mine[j]] + (int32_t)packed_get(pre, mine[j]);
+            packed_inc(pre, mine[j]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < SB_IPT; ++k) {
+        const int jj = k * SB_THREADS + t;
+        const int64_t p = e0 + jj;
+        if (p < nnz) {
+            const int32_t q = qloc[jj];
+            colind_all[q] = (int32_t)(c[k] - (int64_t)sl[jj] * w);
+            val_all[q] = val[p];
+            perm[q] = (int32_t)p;
+        }
+    }
+}
+
+// rowptr_all[s*(m+1) + i] = slice s's position for the entries before row i:
+// the checkpoint below rowptr[i] plus at most SB_CKPT-1 entries counted.
+__global__ void slice_rowptr_kernel(int64_t m, int64_t nnz, int32_t origin, const int32_t *__restrict__ rowptr,
+                                    const int32_t *__restrict__ colind, int64_t w, int64_t nblk,
+                                    const int32_t *__restrict__ bstart, const int32_t *__restrict__ ckpt,
+                                    int32_t *__restrict__ rowptr_all)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i > m) return;
-    int32_t c[NUM_XCD] = {0, 0, 0, 0, 0, 0, 0, 0};
-    if (i < m) {
-        for (int64_t p = (int64_t)rowptr[i] - origin; p < (int64_t)rowptr[i + 1] - origin; ++p) {
-            int64_t s = ((int64_t)colind[p] - origin) / w;
-            c[s < NUM_XCD ? s : NUM_XCD - 1]++;
+    int64_t e = (int64_t)rowptr[i] - origin;
+    e = e < 0 ? 0 : (e > nnz ? nnz : e);
+    int32_t v[NUM_XCD];
+    if (e == nnz) {
+        // Past the last entry: every slice's end, off[s+1].
+#pragma unroll
+        for (int s = 0; s < NUM_XCD; ++s) v[s] = s + 1 < NUM_XCD ? bstart[(s + 1) * nblk] : (int32_t)nnz;
+    } else {
+        const int64_t g = e / SB_CKPT;
+#pragma unroll
+        for (int s = 0; s < NUM_XCD; ++s) v[s] = ckpt[g * NUM_XCD + s];
+        for (int64_t k = g * SB_CKPT; k < e; ++k) {
+            const int sk = slice_of((int64_t)colind[k] - origin, w);
+#pragma unroll
+            for (int s = 0; s < NUM_XCD; ++s) v[s] += s == sk ? 1 : 0;
         }
     }
 #pragma unroll
-    for (int s = 0; s < NUM_XCD; ++s) counts[s * (m + 1) + i] = c[s];
-}
-
-template <typename T>
-__global__ void slice_scatter_kernel(int64_t m, int32_t origin, const int32_t *__restrict__ rowptr,
-                                     const int32_t *__restrict__ colind, const T *__restrict__ val,
-                                     int64_t w, const int32_t *__restrict__ rowptr_all,
-                                     int32_t *__restrict__ colind_all, T *__restrict__ val_all,
-                                     int32_t *__restrict__ perm)
-{
-    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= m) return;
-    int32_t cur[NUM_XCD];
-#pragma unroll
-    for (int s = 0; s < NUM_XCD; ++s) cur[s] = rowptr_all[s * (m + 1) + i];
-    for (int64_t p = (int64_t)rowptr[i] - origin; p < (int64_t)rowptr[i + 1] - origin; ++p) {
-        const int64_t c = (int64_t)colind[p] - origin;
-        int s = (int)(c / w);
-        if (s >= NUM_XCD) s = NUM_XCD - 1;
-        int32_t q = 0;
-#pragma unroll
-        for (int t = 0; t < NUM_XCD; ++t)
-            if (t == s) q = cur[t]++;
-        colind_all[q] = (int32_t)(c - (int64_t)s * w);
-        val_all[q] = val[p];
-        perm[q] = (int32_t)p;
-    }
+    for (int s = 0; s < NUM_XCD; ++s) rowptr_all[s * (m + 1) + i] = v[s];
 }
 
 template <typename T>
@@ -952,24 +1085,41 @@ static int plan_build_sliced(jlust_spmv_plan *p, jlust_stream_t stream)
 {
     hipStream_t s = (hipStream_t)stream;
     const int64_t m = p->m, nnz = p->nnz;
-    const int64_t lenp = NUM_XCD * (m + 1);
-    const unsigned rblocks = (unsigned)((m + 1 + 255) / 256);
-    hipLaunchKernelGGL(slice_count_kernel, dim3(rblocks), dim3(256), 0, s, m, p->origin, p->rowptr,
-                       p->colind, p->slice_w, p->rowptr_all);
-    if (int st = check_launch("slice_count_kernel")) return st;
-    if (int st = exclusive_scan_i32(p->rowptr_all, p->rowptr_all, lenp, stream)) return st;
-    if (m > 0) {
-        hipLaunchKernelGGL((slice_scatter_kernel<T>), dim3((unsigned)((m + 255) / 256)), dim3(256), 0,
-                           s, m, p->origin, p->rowptr, p->colind, (const T *)p->val, p->slice_w,
-                           p->rowptr_all, p->colind_all, (T *)p->val_all, p->perm);
-        if (int st = check_launch("slice_scatter_kernel")) return st;
+    const int64_t nblk = (nnz + SB_E - 1) / SB_E;   // nnz > 0 on the sliced path
+    const int64_t nck = (nnz + SB_CKPT - 1) / SB_CKPT;
+    // Temporary: block counts (scanned in place to block starts) and checkpoints.
+    const size_t sz_b = align_up(sizeof(int32_t) * NUM_XCD * (size_t)nblk, 256);
+    void *tmp = nullptr;
+    JLUST_HIP_TRY(hipMalloc(&tmp, sz_b + sizeof(int32_t) * NUM_XCD * (size_t)nck));
+    int32_t *bstart = (int32_t *)tmp;
+    int32_t *ckpt = (int32_t *)((char *)tmp + sz_b);
+    int st = JLUST_STATUS_SUCCESS;
+    hipLaunchKernelGGL(slice_block_count_kernel, dim3((unsigned)nblk), dim3(SB_THREADS), 0, s, nnz, p->origin,
+                       p->colind, p->slice_w, nblk, bstart);
+    st = check_launch("slice_block_count_kernel");
+    if (!st) st = exclusive_scan_i32(bstart, bstart, NUM_XCD * nblk, stream);
+    if (!st) {
+        hipLaunchKernelGGL((slice_place_kernel<T>), dim3((unsigned)nblk), dim3(SB_THREADS), 0, s, nnz, p->origin,
+                           p->colind, (const T *)p->val, p->slice_w, nblk, bstart, ckpt, p->colind_all,
+                           (T *)p->val_all, p->perm);
+        st = check_launch("slice_place_kernel");
     }
-    // Slice offsets (first entry of each slice's row pointers, plus nnz) to the host.
+    if (!st) {
+        hipLaunchKernelGGL(slice_rowptr_kernel, dim3((unsigned)((m + 1 + 255) / 256)), dim3(256), 0, s, m, nnz,
+                           p->origin, p->rowptr, p->colind, p->slice_w, nblk, bstart, ckpt, p->rowptr_all);
+        st = check_launch("slice_rowptr_kernel");
+    }
+    // Slice offsets off[s] = the first block's start in each slice.
     int32_t firsts[NUM_XCD];
-    for (int k = 0; k < NUM_XCD; ++k)
-        JLUST_HIP_TRY(hipMemcpyAsync(&firsts[k], p->rowptr_all + k * (m + 1), sizeof(int32_t),
-                                     hipMemcpyDeviceToHost, s));
-    JLUST_HIP_TRY(hipStreamSynchronize(s));
+    for (int k = 0; k < NUM_XCD && !st; ++k) {
+        const hipError_t e = hipMemcpyAsync(&firsts[k], bstart + k * nblk, sizeof(int32_t),
+                                            hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) st = hip_fail(e, "hipMemcpyAsync(slice offsets)");
+    }
+    const hipError_t es = hipStreamSynchronize(s);
+    (void)hipFree(tmp);
+    if (st) return st;
+    if (es != hipSuccess) return hip_fail(es, "hipStreamSynchronize(sliced plan build)");
     for (int k = 0; k < NUM_XCD; ++k) p->info.off[k] = firsts[k];
     p->info.off[NUM_XCD] = nnz;
     const int64_t TILE = (int64_t)SPMV_BLOCK * p->ipt;
