@@ -53,6 +53,8 @@ def parse():
                    help="only run a 1 GiB device copy (PMC byte-counter calibration)")
     p.add_argument("--gather-ceiling", action="store_true",
                    help="only measure random-gather bandwidth (8 B and 512 B rows) per source size")
+    p.add_argument("--mfma-peak", action="store_true",
+                   help="only measure the sustained fp32 MFMA rate (v_mfma_f32_16x16x4_f32 chains)")
     p.add_argument("--convert", action="store_true",
                    help="only time format conversions (convert_format) at config sizes")
     p.add_argument("--coo", action="store_true",
@@ -351,6 +353,41 @@ def gather_probe():
     return res
 
 
+def mfma_peak():
+    """Sustained fp32 matrix-core rate (jlust_amd/csrc/gather_probe.hip,
+    mfma_probe_kernel) for 1, 2 and 4 waves per SIMD, beside the published
+    dense fp32 MFMA peak."""
+    import ctypes
+    import torch
+    lib = ctypes.CDLL(os.path.join(ROOT, "jlust_amd", "libjlust_probe.so"))
+    lib.jlust_probe_mfma_f32.restype = ctypes.c_int
+    lib.jlust_probe_mfma_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    stream = torch.cuda.current_stream()
+    iters, chains = 20000, 4
+    res = []
+    for waves_per_simd in (1, 2, 4):
+        blocks = cus * waves_per_simd          # 4 waves per block = one per SIMD
+        out = torch.empty(blocks * 256, dtype=torch.float32, device="cuda")
+        call = lambda: lib.jlust_probe_mfma_f32(out.data_ptr(), blocks, iters, stream.cuda_stream)
+        assert call() == 0
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 5
+        s.record(stream)
+        for _ in range(reps):
+            call()
+        e.record(stream)
+        torch.cuda.synchronize()
+        t = s.elapsed_time(e) / reps * 1e-3
+        flops = blocks * 4 * iters * chains * 2048
+        res.append({"waves_per_simd": waves_per_simd, "blocks": blocks, "ms": round(t * 1e3, 3),
+                    "TFLOPs": round(flops / t / 1e12, 2),
+                    "frac_of_published": round(flops / t / 1e12 / MFMA_F32_PEAK_TFLOPS, 4)})
+        del out
+    return res
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -521,6 +558,9 @@ def main():
         return
     if args.gather_ceiling:
         print(json.dumps({"gather_ceiling": gather_ceiling()}), flush=True)
+        return
+    if args.mfma_peak:
+        print(json.dumps({"mfma_peak": mfma_peak()}), flush=True)
         return
     if args.convert:
         print(json.dumps({"convert": convert_bench(args.cpu_seconds)}), flush=True)

@@ -3,8 +3,9 @@
 - ``libjlust_hip.so``: the HIP kernels and the C ABI (``include/jlust_hip.h``),
   compiled by hipcc for gfx950 only.
 - ``libjlust_workloads.so``: the host-side synthetic input generator.
-- ``libjlust_probe.so``: the random-gather probe behind ``bench.py
-  --gather-ceiling`` (measurement only, not part of the C ABI).
+- ``libjlust_probe.so``: the random-gather and fp32 MFMA probes behind
+  ``bench.py --gather-ceiling`` / ``--mfma-peak`` (measurement only, not part
+  of the C ABI).
 
 Run ``python -m jlust_amd.build`` (or ``__graft_entry__.build()``).  Sources are
 compiled in parallel into ``jlust_amd/_build/`` and linked next to this file.
