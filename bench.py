@@ -508,8 +508,13 @@ def cpu_baseline(cfg, budget_s):
 
 
 def timed(step, steps, warmup):
-    """W untimed steps, then exactly K steps bracketed by synchronize();
-    returns (wall ms per step, per-step event durations in ms)."""
+    """W untimed steps, then exactly K steps bracketed by synchronize() (the
+    wall-clock pass: nothing else is queued between the steps), then K more
+    steps with a HIP event pair recorded on the launching stream around each
+    one (the per-launch pass).  Returns (wall ms per step of the first pass,
+    per-step event durations in ms of the second).  The event records are kept
+    out of the wall-clock pass: at config 1's size (an 11 us kernel) the two
+    records per step add several microseconds of queue time."""
     import torch
     for _ in range(warmup):
         step()
@@ -521,12 +526,15 @@ def timed(step, steps, warmup):
         torch.distributed.barrier()
     torch.cuda.synchronize()
     t_start = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
     for s, e in ev:
         s.record(stream)
         step()
         e.record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
     return wall * 1e3 / steps, np.array([s.elapsed_time(e) for s, e in ev])
 
 

@@ -8,6 +8,7 @@ compute path fails loudly.
 """
 from __future__ import annotations
 
+import contextlib
 import ctypes
 import os
 
@@ -78,6 +79,28 @@ STATUS = {
 }
 
 _lib = None
+
+# Per-call device plumbing, kept cheap for microsecond-scale products: torch's
+# raw current-stream handle and current-device index where this torch build
+# exposes them (the public Stream / device-guard objects cost several
+# microseconds per call), else the public API.
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_CUR_DEVICE = getattr(torch._C, "_cuda_getDevice", None)
+_NO_GUARD = contextlib.nullcontext()
+
+
+def stream_handle(dev: torch.device) -> ctypes.c_void_p:
+    """The current stream of `dev` as a hipStream_t."""
+    if _RAW_STREAM is not None and dev.index is not None:
+        return ctypes.c_void_p(_RAW_STREAM(dev.index))
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def on_device(dev: torch.device):
+    """torch.cuda.device(dev), or no guard when dev is already current."""
+    if _CUR_DEVICE is not None and dev.index is not None and _CUR_DEVICE() == dev.index:
+        return _NO_GUARD
+    return torch.cuda.device(dev)
 
 
 def lib():

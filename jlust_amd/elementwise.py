@@ -20,7 +20,6 @@ form.
 """
 from __future__ import annotations
 
-import ctypes
 from dataclasses import dataclass
 
 import torch
@@ -79,11 +78,11 @@ def apply_fn(fn, src: torch.Tensor, dst: torch.Tensor, alpha=1.0, beta=0.0) -> t
         if suf is None:
             from .errors import UnsupportedValueType
             raise UnsupportedValueType(src.dtype, "HIPBackend")
-        with torch.cuda.device(src.device):
+        with _lib.on_device(src.device):
             st = getattr(_lib.lib(), f"jlust_hip_apply_fn_{suf}")(
                 src.numel(), f.kind, f.a, f.b, src.data_ptr() if src.numel() else None,
                 float(alpha), float(beta), dst.data_ptr() if dst.numel() else None,
-                ctypes.c_void_p(torch.cuda.current_stream(src.device).cuda_stream))
+                _lib.stream_handle(src.device))
         _lib.check(st, "apply_fn")
         return dst
     v = fn(src)                                   # user callable on the device vector

@@ -28,8 +28,8 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
 
 
-def _stream(dev: torch.device):
-    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+_stream = _lib.stream_handle
+_on = _lib.on_device
 
 
 def _dense_fmt(fmt) -> bool:
@@ -127,6 +127,8 @@ def spmv_with_fns(spmv, u_A, u_x, u_y, alpha=1.0, beta=0.0, input_fn=None, outpu
     plain SpMV `spmv(u_A, u_x, u_y, alpha, beta)`: in_fn.(x) into a new
     vector, the product into a row-sum vector when output_fn is given, then
     the row write on the device (jlust_amd/elementwise.py)."""
+    if input_fn is None and output_fn is None:
+        return spmv(u_A, u_x, u_y, alpha, beta)
     from .elementwise import apply_fn, is_identity
     if is_identity(input_fn) and is_identity(output_fn):
         return spmv(u_A, u_x, u_y, alpha, beta)
@@ -173,7 +175,7 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     if is_shifted_diag(u_A.format):
         lv = u_A.format.levels[1]
         dev = _check_same_device(x, y)
-        with torch.cuda.device(dev):
+        with _on(dev):
             st = getattr(L, f"jlust_hip_shifted_diag_spmv_{suf}")(
                 m, n, lv.shift, lv.val, float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
         _lib.check(st, "shifted_diag_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
@@ -181,7 +183,7 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     if is_csr_shaped(u_A.format):
         rowptr, colind = _csr_parts(u_A)
         dev = _check_same_device(rowptr, colind, nonzeros(u_A), x, y)
-        with torch.cuda.device(dev):
+        with _on(dev):
             st = getattr(L, f"jlust_hip_csr_spmv_{suf}_i32")(
                 m, n, nnz(u_A), u_A.origin.offset, _ptr(rowptr), _ptr(colind),
                 _ptr(nonzeros(u_A)), float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
@@ -192,7 +194,7 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     if rows.numel() != nnz(u_A) or cols.numel() != nnz(u_A):
         raise NonCanonicalStorage("COO coordinate buffers must have nnz entries")
     dev = _check_same_device(rows, cols, nonzeros(u_A), x, y)
-    with torch.cuda.device(dev):
+    with _on(dev):
         st = getattr(L, f"jlust_hip_coo_spmv_{suf}_i32")(
             m, n, nnz(u_A), u_A.origin.offset, _ptr(rows), _ptr(cols), _ptr(nonzeros(u_A)),
             float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
@@ -247,7 +249,7 @@ def _dcsr_product(u_A: USTensor, u_X: USTensor, u_Y: USTensor, alpha, beta):
     L = _lib.lib()
     o = u_A.origin.offset
     if beta != 0:
-        with torch.cuda.device(dev):
+        with _on(dev):
             st = getattr(L, f"jlust_hip_gather_rows_{suf}")(nout, k, o, _ptr(rows), m, _ptr(Y), ldy,
                                                             _ptr(t), ldt, _stream(dev))
         _lib.check(st, "gather_rows", u_A.format, _BE, Y.dtype)
@@ -255,7 +257,7 @@ def _dcsr_product(u_A: USTensor, u_X: USTensor, u_Y: USTensor, alpha, beta):
         _spmv(compact, u_X, ust(t), alpha, beta)
     else:
         _spmm(compact, u_X, ust(t), alpha, beta)
-    with torch.cuda.device(dev):
+    with _on(dev):
         st = getattr(L, f"jlust_hip_scatter_rows_{suf}")(nout, k, o, _ptr(rows), m, _ptr(t), ldt,
                                                          _ptr(Y), ldy, _stream(dev))
     _lib.check(st, "scatter_rows", u_A.format, _BE, Y.dtype)
@@ -291,7 +293,7 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
         if browptr.numel() != mb + 1 or nnz(u_A) != bcolind.numel() * b1 * b2:
             raise NonCanonicalStorage("BSR: browptr must have mb+1 entries and val nnzb*b1*b2")
         dev = _check_same_device(browptr, bcolind, nonzeros(u_A), B, C)
-        with torch.cuda.device(dev):
+        with _on(dev):
             st = L.jlust_hip_bsr_spmm_f32_i32(
                 mb, nb, b1, bcolind.numel(), u_A.origin.offset, _ptr(browptr), _ptr(bcolind),
                 _ptr(nonzeros(u_A)), int(row_major), k, float(alpha), _ptr(B), leading_dim(B),
@@ -300,7 +302,7 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
         return u_C
     rowptr, colind = _csr_parts(u_A)
     dev = _check_same_device(rowptr, colind, nonzeros(u_A), B, C)
-    with torch.cuda.device(dev):
+    with _on(dev):
         st = getattr(L, f"jlust_hip_csr_spmm_{suf}_i32")(
             m, n, k, nnz(u_A), u_A.origin.offset, _ptr(rowptr), _ptr(colind),
             _ptr(nonzeros(u_A)), float(alpha), _ptr(B), leading_dim(B), float(beta), _ptr(C),
@@ -331,7 +333,7 @@ def _sddmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, mask=None):
         if mk.dtype != T or mk.numel() != nnz(u_C) or not mk.is_contiguous():
             raise IncompatibleExtents("SDDMM: mask must hold nnz(C) contiguous values of C's type")
     dev = _check_same_device(rowptr, colind, nonzeros(u_C), A, B, mk)
-    with torch.cuda.device(dev):
+    with _on(dev):
         st = getattr(_lib.lib(), f"jlust_hip_csr_sddmm_{suf}_i32")(
             m, n, K, nnz(u_C), u_C.origin.offset, _ptr(rowptr), _ptr(colind), float(alpha),
             _ptr(A), leading_dim(A), _ptr(B), leading_dim(B), float(beta), _ptr(nonzeros(u_C)),
@@ -372,17 +374,24 @@ class HIPSpMVHandle(AbstractKernelHandle):
         self._plan = ctypes.c_void_p(0)
         m, n = u_A.extents
         create = "jlust_hip_coo_spmv_plan_create" if coo else "jlust_hip_csr_spmv_plan_create"
-        with torch.cuda.device(self.dev):
+        with _on(self.dev):
             st = getattr(_lib.lib(), create)(
                 m, n, nnz(u_A), u_A.origin.offset, 0 if suf == "f64" else 1, _ptr(first),
                 _ptr(second), _ptr(nonzeros(u_A)), _stream(self.dev), ctypes.byref(self._plan))
         _lib.check(st, create[10:], u_A.format, _BE, self.T)
 
+    takes_raw = True     # execute(h, x, y) on plain device tensors: the raw-array form
+
     def execute(self, *ts, alpha=1.0, beta=0.0):
         """execute(h, x, y) (the cuSPARSE handle form) or execute(h, A, x, y)
         (EmitterSpMVHandle, spmv.jl:531-544, which takes A's buffers at each
         call: an A with other values than the plan's refreshes them first).
-        The handle's input_fn/output_fn apply."""
+        The handle's input_fn/output_fn apply.  With plain device tensors x, y
+        the call returns y, as the cuSPARSE handle's raw-array method does
+        (ext/CUDAExt/ops/spmv.jl:63-78); with USTensors it returns u_y."""
+        if len(ts) == 2 and isinstance(ts[0], torch.Tensor) and isinstance(ts[1], torch.Tensor):
+            return self.execute_tensors(ts[0], ts[1], alpha, beta)
+        ts = tuple(t if isinstance(t, USTensor) else ust(t) for t in ts)
         if len(ts) == 3:
             u_A, u_x, u_y = ts
             if u_A is not self.u_A and nonzeros(u_A).data_ptr() != nonzeros(self.u_A).data_ptr():
@@ -397,7 +406,7 @@ class HIPSpMVHandle(AbstractKernelHandle):
     def _execute_plain(self, u_A, u_x: USTensor, u_y: USTensor, alpha=1.0, beta=0.0):
         x, y = _vec_checks(self.u_A, u_x, u_y)
         _check_same_device(nonzeros(self.u_A), x, y)
-        with torch.cuda.device(self.dev):
+        with _on(self.dev):
             st = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_{self.suf}")(
                 self._plan, float(alpha), _ptr(x), float(beta), _ptr(y), _stream(self.dev))
         _lib.check(st, "csr_spmv_plan_execute", self.u_A.format, _BE, self.T)
@@ -405,22 +414,22 @@ class HIPSpMVHandle(AbstractKernelHandle):
 
     def execute_tensors(self, x: torch.Tensor, y: torch.Tensor, alpha=1.0, beta=0.0):
         """execute on plain device vectors with the checks reduced to
-        attribute compares: the per-call path of the block aggregates, whose
-        products are a few microseconds of GPU time."""
+        attribute compares (the raw-array hot path: a product here is a few
+        microseconds of GPU time).  Anything else -- another dtype or device,
+        a wrong length, strided vectors, input_fn/output_fn -- takes the
+        checked USTensor path, which raises where that path raises."""
         m, n = self.u_A.extents
-        if (x.dtype is not self.T or y.dtype is not self.T or x.device != self.dev or
-                y.device != self.dev or x.numel() != n or y.numel() != m or
+        di = self.dev.index
+        if (x.dtype is not self.T or y.dtype is not self.T or x.get_device() != di or
+                y.get_device() != di or x.numel() != n or y.numel() != m or
                 not x.is_contiguous() or not y.is_contiguous() or
                 self.input_fn is not None or self.output_fn is not None):
             self.execute(ust(x), ust(y), alpha=alpha, beta=beta)
             return y
         if self._exec is None:
             self._exec = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_{self.suf}")
-        if torch.cuda.current_device() != self.dev.index:
-            with torch.cuda.device(self.dev):
-                return self.execute_tensors(x, y, alpha, beta)
-        st = self._exec(self._plan, alpha, x.data_ptr(), beta, y.data_ptr(),
-                        torch.cuda.current_stream().cuda_stream)
+        with _on(self.dev):
+            st = self._exec(self._plan, alpha, x.data_ptr(), beta, y.data_ptr(), _stream(self.dev))
         if st:
             _lib.check(st, "csr_spmv_plan_execute", self.u_A.format, _BE, self.T)
         return y

@@ -100,10 +100,11 @@ def _wrap(a):
 def execute(optype, *args, backend=None, **kw):
     """execute(OpType, tensors...; backend, kw...)   (src/convenience.jl:15-39)
     execute(handle, tensors...; kw...)             (handle-driven call)."""
-    if isinstance(optype, AbstractKernelHandle):
-        return optype.execute(*[_wrap(a) for a in args], **kw)
-    if args and isinstance(args[0], AbstractKernelHandle):
-        return args[0].execute(*[_wrap(a) for a in args[1:]], **kw)
+    if isinstance(optype, AbstractKernelHandle) or (args and isinstance(args[0], AbstractKernelHandle)):
+        h, rest = (optype, args) if isinstance(optype, AbstractKernelHandle) else (args[0], args[1:])
+        if getattr(h, "takes_raw", False):
+            return h.execute(*rest, **kw)       # the handle wraps what it does not take raw
+        return h.execute(*[_wrap(a) for a in rest], **kw)
     if isinstance(optype, AbstractUSTBackend):          # execute(backend, op, tensors...)
         be, op, tensors = optype, args[0], [_wrap(a) for a in args[1:]]
         return _backend_execute(be, op, tensors, kw)
