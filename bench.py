@@ -553,7 +553,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
-              "multi-GPU sharding is design-only (see DESIGN.md)", file=sys.stderr)
+              "multi-GPU sharding is design-only", file=sys.stderr)
         sys.exit(2)
     import torch
     if args.calibrate_copy:

@@ -21,7 +21,7 @@
  *    T first, ext/KernelAbstractionsExt/ops/spmv.jl:377-378).  beta == 0 makes
  *    the output write-only: it is never read, so NaN/Inf in it do not
  *    propagate (the reference's Tiled/ColFirst SpMM and its SDDMM read it
- *    anyway; that difference is documented in DESIGN.md).
+ *    anyway, so a NaN there would reach the output; here it does not).
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
  *    returns without synchronising.  Entry points are reentrant.  The library
  *    keeps one scratch buffer per (device, stream) for the SpMV/SpMM partial

@@ -135,6 +135,9 @@ def _make2(name, levels, family, maps):
     return TensorFormat(name, tuple(levels), family, 2, d2l, d2ls, l2d)
 
 
+_DENSE = {}
+
+
 class Formats:
     """Named formats (src/named_formats.jl)."""
 
@@ -145,11 +148,16 @@ class Formats:
 
     @staticmethod
     def DensedRight(n: int) -> TensorFormat:
-        if n < 1:
-            raise InvalidTensorFormat("DensedRight needs at least one dimension")
-        ident = lambda *c: tuple(c)  # noqa: E731
-        return TensorFormat(f"DensedRight({n})", tuple(DenseLevel() for _ in range(n)), "Dense",
-                            n, ident, ident, ident)
+        """One shared (immutable) format object per n: every dense wrapper
+        of an operand reuses it."""
+        f = _DENSE.get(n)
+        if f is None:
+            if n < 1:
+                raise InvalidTensorFormat("DensedRight needs at least one dimension")
+            ident = lambda *c: tuple(c)  # noqa: E731
+            f = _DENSE[n] = TensorFormat(f"DensedRight({n})", tuple(DenseLevel() for _ in range(n)),
+                                         "Dense", n, ident, ident, ident)
+        return f
 
     @staticmethod
     def ShiftedDiag(dtype=None, shift: int = 0, val=1.0) -> TensorFormat:

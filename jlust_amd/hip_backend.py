@@ -38,8 +38,20 @@ def _dense_fmt(fmt) -> bool:
 
 # ---------------------------------------------------------------- capability
 
+_SUPPORTS = {}
+
+
 def supports(op: Op) -> bool:
-    """Capability table (the counterpart of KernelAbstractionsExt.jl:31-41)."""
+    """Capability table (the counterpart of KernelAbstractionsExt.jl:31-41),
+    memoised per (op, operand formats)."""
+    key = (op.tag, op.formats)
+    r = _SUPPORTS.get(key)
+    if r is None:
+        r = _SUPPORTS[key] = _supports(op)
+    return r
+
+
+def _supports(op: Op) -> bool:
     f = op.formats
     if op.tag == "SpMV" and len(f) == 3:
         return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_shifted_diag(f[0]) or

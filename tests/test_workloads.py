@@ -44,7 +44,7 @@ def test_config1_shape():
     assert (np.diff(c["rowptr"]) == 16).all() and c["rowptr"][0] == 1
     _rows_sorted_unique(c["rowptr"], c["colind"], c["n"])
     assert -1 <= c["val"].min() < -0.99 and 0.99 < c["val"].max() <= 1
-    assert W.algorithmic_bytes(c) == 21_200_004
+    assert W.algorithmic_bytes(c) == 21_200_004           # 12*nnz + 4(m+1) + 8(n+m), config 1
 
 
 def test_config2_power_law_scaled():
@@ -67,7 +67,7 @@ def test_config5_band():
 
 
 def test_baseline_byte_formulas():
-    """Compulsory bytes of configs 3-5 as BASELINE.md tabulates them."""
+    """Compulsory bytes of configs 3-5: each array counted once (the baseline's byte formulas)."""
     spmm = dict(kind="csr_spmm", rowptr=np.array([1, 32_000_001]), m=1_000_000, n=1_000_000,
                 k=128)
     assert W.algorithmic_bytes(spmm) == 1_284_000_004
