@@ -858,7 +858,14 @@ int csr_spmv(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *r
 // striding the row by LPR,
 // partial sums combined with xor-shuffles.  No LDS, no barriers, no carries:
 // every wave holds 64/LPR rows, so a small matrix still puts many waves in
-// flight (the merge kernel spends one 2048-item tile per block there).
+// flight (the merge kernel spends one 2048-item tile per block there).  All
+// waves of such a matrix are resident at once, so the time is one wave's
+// chain of dependent loads: both row pointers are loaded together, and each
+// step issues VEC_U of the lane's entries at once (indices clamped into the
+// row, products of the clamped copies dropped by a select), so a row of
+// 4*LPR entries costs one rowptr -> colind -> x chain rather than four.
+constexpr int VEC_U = 4;
+
 template <typename T, int LPR, bool BZ>
 __global__ __launch_bounds__(256) void csr_spmv_vector_kernel(int64_t m, int32_t origin,
                                                               const int32_t *__restrict__ rowptr,
@@ -870,10 +877,30 @@ __global__ __launch_bounds__(256) void csr_spmv_vector_kernel(int64_t m, int32_t
     const int64_t row = t / LPR;
     const int sub = (int)(t % LPR);
     const int64_t r = row < m ? row : m - 1;            // clamped: loads stay in bounds
-    const int64_t lo = (int64_t)rowptr[r] - origin;
-    const int64_t hi = row < m ? (int64_t)rowptr[r + 1] - origin : lo;
+    int32_t rp0 = rowptr[r], rp1 = rowptr[r + 1];
+    // Both values are needed here, so both loads are issued before the first
+    // wait (otherwise the second sinks under the row < m branch below).
+    __asm__ volatile("" : "+v"(rp0), "+v"(rp1));
+    const int64_t lo = (int64_t)rp0 - origin;
+    const int64_t hi = row < m ? (int64_t)rp1 - origin : lo;
     T acc = T(0);
-    for (int64_t p = lo + sub; p < hi; p += LPR) acc += val[p] * x[colind[p] - origin];
+    for (int64_t p0 = lo + sub; p0 < hi; p0 += VEC_U * LPR) {
+        int32_t c[VEC_U];
+        T v[VEC_U], xv[VEC_U];
+#pragma unroll
+        for (int u = 0; u < VEC_U; ++u) {
+            const int64_t p = min(p0 + u * LPR, hi - 1);
+            c[u] = colind[p];
+            v[u] = val[p];
+        }
+#pragma unroll
+        for (int u = 0; u < VEC_U; ++u) xv[u] = x[c[u] - origin];
+#pragma unroll
+        for (int u = 0; u < VEC_U; ++u) {
+            const T a = acc + v[u] * xv[u];
+            acc = p0 + u * LPR < hi ? a : acc;
+        }
+    }
 #pragma unroll
     for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, LPR);
     if (sub == 0 && row < m) y[row] = BZ ? alpha * acc : alpha * acc + beta * y[row];
