@@ -78,74 +78,75 @@ __global__ __launch_bounds__(256) void transpose_kernel(int64_t n, int64_t k,
     }
 }
 
-// 32-column chunks: each half-wave takes one nonzero (two per instruction),
-// its 32 lanes reading the nonzero's 32*sizeof(T)-byte row slice of Bt; the
-// halves' partial sums of a row are added at the end.
-template <typename T>
-__global__ __launch_bounds__(SPMM_BLOCK) void csr_spmm_half_kernel(
+// Chunks of at most 32 columns: groups of KV lanes (KV the smallest power of
+// two >= the chunk's columns), one nonzero per group per step, so a wave
+// takes 64/KV nonzeros per step (64 at k = 1, where the kernel is a
+// wave-per-row SpMV).  Each lane loads its group's col/val itself (the
+// group's lanes read one address), gathers its column of the nonzero's Bt
+// row, and keeps its group's sum in nonzero order; the groups' sums are added
+// with xor-shuffles at the row's end.  U steps are loaded at once (indices
+// clamped into the row, products of the clamped copies dropped by a select;
+// U is chosen per call from the mean row length, so a short row issues no
+// clamped copies), and the next row's pointers are loaded before the current
+// row's nonzeros, so a wave's rows do not wait on each other's pointer loads.
+template <typename T, int KV, int U>
+__global__ __launch_bounds__(SPMM_BLOCK) void csr_spmm_group_kernel(
     int64_t m, int64_t k, int32_t origin, const int32_t *__restrict__ rowptr,
     const int32_t *__restrict__ colind, const T *__restrict__ val, const T *__restrict__ Bt,
     int64_t ldt, T alpha, T beta, int beta_zero, T *__restrict__ C, int64_t ldc,
     int skip_empty_rows)
 {
-    constexpr int KC = 32;
+    constexpr int G = 64 / KV;                 // nonzeros per step
     constexpr int NW = SPMM_BLOCK / 64;
-    __shared__ T s_c[SPMM_ROWS][KC + 1];
+    __shared__ T s_c[SPMM_ROWS][KV + 1];
     __shared__ int s_empty[SPMM_ROWS];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int half = lane >> 5;
-    const int col = lane & 31;
+    const int grp = lane / KV;
+    const int col = lane % KV;
     const int64_t row0 = (int64_t)blockIdx.x * SPMM_ROWS;
     const int nrows = (int)min((int64_t)SPMM_ROWS, m - row0);
-    const bool cok = col < k;                  // k <= 32 here
-    const int64_t cl = cok ? col : 0;          // clamped, in-bounds column
+    const int64_t cl = col < k ? col : 0;      // clamped, in-bounds column
 
+    int32_t lo_n = 0, hi_n = 0;
+    if (wave < nrows) {
+        lo_n = rowptr[row0 + wave];
+        hi_n = rowptr[row0 + wave + 1];
+    }
     for (int rr = wave; rr < nrows; rr += NW) {
-        const int64_t row = row0 + rr;
-        const int64_t lo = (int64_t)rowptr[row] - origin;
-        const int64_t hi = (int64_t)rowptr[row + 1] - origin;
+        const int64_t lo = (int64_t)lo_n - origin;
+        const int64_t hi = (int64_t)hi_n - origin;
+        if (rr + NW < nrows) {                 // the wave's next row
+            lo_n = rowptr[row0 + rr + NW];
+            hi_n = rowptr[row0 + rr + NW + 1];
+        }
         if (lane == 0) s_empty[rr] = hi <= lo;
         T acc = T(0);
-        for (int64_t p0 = lo; p0 < hi; p0 += 64) {
-            const int cnt = (int)min((int64_t)64, hi - p0);
-            int cidx = 0;
-            T cv = T(0);
-            if (lane < cnt) {
-                cidx = colind[p0 + lane] - origin;
-                cv = val[p0 + lane];
-            }
-            int q = 0;
-            for (; q + 2 * SPMM_UNROLL <= cnt; q += 2 * SPMM_UNROLL) {
-                T b[SPMM_UNROLL], a[SPMM_UNROLL];
+        for (int64_t p0 = lo + grp; p0 < hi; p0 += (int64_t)G * U) {
+            int32_t c[U];
+            T a[U], b[U];
 #pragma unroll
-                for (int u = 0; u < SPMM_UNROLL; ++u) {
-                    const int j0 = bcast_i(cidx, q + 2 * u), j1 = bcast_i(cidx, q + 2 * u + 1);
-                    const T a0 = bcast(cv, q + 2 * u), a1 = bcast(cv, q + 2 * u + 1);
-                    const int64_t j = half ? j1 : j0;
-                    a[u] = half ? a1 : a0;
-                    b[u] = Bt[j * ldt + cl];
-                }
-#pragma unroll
-                for (int u = 0; u < SPMM_UNROLL; ++u) acc += a[u] * b[u];
+            for (int u = 0; u < U; ++u) {
+                const int64_t p = min(p0 + (int64_t)u * G, hi - 1);
+                c[u] = colind[p];
+                a[u] = val[p];
             }
-            for (; q < cnt; q += 2) {
-                const int qa = q, qb = min(q + 1, cnt - 1);
-                const int j0 = bcast_i(cidx, qa), j1 = bcast_i(cidx, qb);
-                const T a0 = bcast(cv, qa), a1 = bcast(cv, qb);
-                const int64_t j = half ? j1 : j0;
-                const T a = half ? a1 : a0;
-                const T prod = a * Bt[j * ldt + cl];
-                acc += (half == 0 || q + 1 < cnt) ? prod : T(0);
+#pragma unroll
+            for (int u = 0; u < U; ++u) b[u] = Bt[(int64_t)(c[u] - origin) * ldt + cl];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const T s = acc + a[u] * b[u];
+                acc = p0 + (int64_t)u * G < hi ? s : acc;
             }
         }
-        acc += __shfl_xor(acc, 32, 64);
-        if (half == 0) s_c[rr][col] = acc;
+#pragma unroll
+        for (int off = KV; off < 64; off <<= 1) acc += __shfl_xor(acc, off, 64);
+        if (lane < KV) s_c[rr][col] = acc;
     }
     __syncthreads();
-    const int ncols = (int)k;
+    const int ncols = (int)k;                  // k <= KV here
     for (int idx = tid; idx < SPMM_ROWS * ncols; idx += SPMM_BLOCK) {
         const int rr = idx % SPMM_ROWS;
         const int cc = idx / SPMM_ROWS;
@@ -155,7 +156,6 @@ __global__ __launch_bounds__(SPMM_BLOCK) void csr_spmm_half_kernel(
         const T s = alpha * s_c[rr][cc];
         *dst = beta_zero ? s : s + beta * *dst;
     }
-    (void)cok;
 }
 
 template <typename T, int VEC>
@@ -249,10 +249,10 @@ __global__ __launch_bounds__(SPMM_BLOCK) void csr_spmm_kernel(
 // 16).  JLUST_HIP_SPMM_KCHUNK=c forces c columns per pass.
 constexpr size_t SPMM_MALL_BUDGET = (size_t)256 << 20;
 
-bool spmm_half()
+bool spmm_group()
 {
     static const bool on = [] {
-        const char *e = getenv("JLUST_HIP_SPMM_HALF");
+        const char *e = getenv("JLUST_HIP_SPMM_GROUP");
         return !(e && e[0] == '0');
     }();
     return on;
@@ -310,8 +310,15 @@ int csr_spmm(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
     const int bz = beta == T(0);
     for (int64_t c0 = 0; c0 < k; c0 += kc) {
         const int64_t kk = min(kc, k - c0);
-        const int64_t ldt = (kk + 3) / 4 * 4;
-        if (n > 0) {
+        const bool group = kk <= 32 && spmm_group();
+        // One column needs no row-major copy: B's column is contiguous.  The
+        // group kernel reads single elements, so its copy is unpadded (a
+        // smaller footprint for the gathers); the wide kernel's rows are
+        // padded to 16 bytes for its vector loads.
+        const bool direct = group && kk == 1;
+        const int64_t ldt = group ? kk : (kk + 3) / 4 * 4;
+        const T *Bsrc = direct ? B + c0 * ldb : Bt;
+        if (n > 0 && !direct) {
             dim3 tgrid((unsigned)((n + 63) / 64), (unsigned)((kk + 63) / 64));
             hipLaunchKernelGGL((transpose_kernel<T>), tgrid, dim3(256), 0, s, n, kk, B + c0 * ldb, ldb, Bt,
                                ldt);
@@ -319,9 +326,27 @@ int csr_spmm(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
         }
         const int vec = (sizeof(T) == 4) ? (kk <= 64 ? 1 : kk <= 128 ? 2 : 4) : (kk <= 64 ? 1 : 2);
         T *Cc = C + c0 * ldc;
-        if (kk <= 32 && spmm_half())
-            hipLaunchKernelGGL((csr_spmm_half_kernel<T>), grid, dim3(SPMM_BLOCK), 0, s, m, kk, origin,
-                               rowptr, colind, val, Bt, ldt, alpha, beta, bz, Cc, ldc, skip_empty_rows);
+#define JLUST_GROUP_U(KV, U)                                                                           \
+    hipLaunchKernelGGL((csr_spmm_group_kernel<T, KV, U>), grid, dim3(SPMM_BLOCK), 0, s, m, kk, origin,    \
+                       rowptr, colind, val, Bsrc, ldt, alpha, beta, bz, Cc, ldc, skip_empty_rows)
+#define JLUST_GROUP(KV)                                                                                \
+    do {                                                                                               \
+        const int64_t steps = (nnz + m * (64 / KV) - 1) / (m * (64 / KV));  /* per row, rounded up */   \
+        if (steps <= 1) JLUST_GROUP_U(KV, 1);                                                          \
+        else if (steps <= 2) JLUST_GROUP_U(KV, 2);                                                     \
+        else if (steps <= 4) JLUST_GROUP_U(KV, 4);                                                     \
+        else JLUST_GROUP_U(KV, 8);                                                                     \
+    } while (0)
+        if (group) {
+            if (kk == 1) JLUST_GROUP(1);
+            else if (kk == 2) JLUST_GROUP(2);
+            else if (kk <= 4) JLUST_GROUP(4);
+            else if (kk <= 8) JLUST_GROUP(8);
+            else if (kk <= 16) JLUST_GROUP(16);
+            else JLUST_GROUP(32);
+        }
+#undef JLUST_GROUP_U
+#undef JLUST_GROUP
         else if (vec == 1)
             hipLaunchKernelGGL((csr_spmm_kernel<T, 1>), grid, dim3(SPMM_BLOCK), 0, s, m, kk, origin,
                                rowptr, colind, val, Bt, ldt, alpha, beta, bz, Cc, ldc, skip_empty_rows);

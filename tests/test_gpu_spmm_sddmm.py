@@ -53,7 +53,7 @@ def test_spmm_reference_fixture(J, dtype):
     np.testing.assert_array_equal(C, np.array(c["C"], dtype))
 
 
-@pytest.mark.parametrize("k", [1, 2, 7, 8, 33, 64, 100, 128, 200, 256, 300])
+@pytest.mark.parametrize("k", [1, 2, 3, 4, 7, 8, 16, 31, 32, 33, 64, 100, 128, 200, 256, 300])
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 def test_spmm_random(J, O, k, dtype):
     m, n = 3000, 2000
