@@ -9,11 +9,15 @@
 //
 // A block owns R consecutive rows of the pattern.  It first stages A[rows, :]
 // in LDS, row-major, reading each column segment A[i0:i0+R, kk] coalesced.
-// Its nonzeros (contiguous in colind) are then shared out to groups of
-// GROUP = 8 lanes, one nonzero per group at a time: each lane multiplies a
-// 16-byte slice of B[:, j] (one vector load; the group reads the column as
-// contiguous 128-byte lines) with the matching slice of the staged A row,
-// and the group reduces its 8 partial dots with xor-shuffles.
+// Its nonzeros (contiguous in colind) are then shared out to groups of G
+// lanes, one nonzero per group at a time: each lane multiplies a 16-byte
+// slice of B[:, j] (one vector load; the group reads the column as contiguous
+// 128-byte lines) with the matching slice of the staged A row, and the group
+// reduces its G partial dots with xor-shuffles.  G = 8 for K above 8 slices;
+// for smaller K, G is the smallest power of two whose slices cover K, and
+// each group takes U nonzeros per step with their loads issued together
+// (indices clamped into the block's nonzeros, results of the clamped copies
+// dropped), so K = 1 puts 64 nonzeros on a wave per load instead of 8.
 #include "common.hpp"
 
 namespace jlust {
@@ -28,30 +32,34 @@ template <typename T> struct V16;
 template <> struct alignas(16) V16<float> { float v[4]; static constexpr int N = 4; };
 template <> struct alignas(16) V16<double> { double v[2]; static constexpr int N = 2; };
 
-template <typename T>
+template <int G, typename T>
 __device__ __forceinline__ T group_sum(T v)
 {
 #pragma unroll
-    for (int off = SD_GROUP / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    for (int off = G / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
 }
 
-// VECB: B columns and the LDS rows allow 16-byte vector access.
-template <typename T, bool VECB>
+// VECB: B columns and the LDS rows allow 16-byte vector access.  ONE: a
+// group's G slices cover all of K (one step per nonzero), so U nonzeros per
+// group can be loaded at once; otherwise U = 1 and the lanes loop over K.
+template <typename T, bool VECB, int G, int U, bool ONE>
 __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     int64_t m, int64_t K, int32_t origin, const int32_t *__restrict__ rowptr,
     const int32_t *__restrict__ colind, T alpha, const T *__restrict__ A, int64_t lda,
     const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval,
     const T *mask, int R, int64_t lds_ld)
 {
+    static_assert(ONE || U == 1, "several nonzeros per group need one step over K");
+    constexpr int GROUPS = SD_BLOCK / G;
+    constexpr int NE = VECB ? V16<T>::N : 1;   // elements per lane load
     extern __shared__ unsigned char sd_smem[];
     T *s_a = reinterpret_cast<T *>(sd_smem);                       // R x lds_ld
     int32_t *s_rp = reinterpret_cast<int32_t *>(s_a + (int64_t)R * lds_ld);  // R + 1
 
     const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int g = tid / SD_GROUP;            // group in block
-    const int q = lane % SD_GROUP;           // lane in group
+    const int g = tid / G;                   // group in block
+    const int q = tid % G;                   // lane in group
     const int64_t i0 = (int64_t)blockIdx.x * R;
     const int nr = (int)min((int64_t)R, m - i0);
 
@@ -64,34 +72,79 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     __syncthreads();
 
     const int p_lo = s_rp[0], p_hi = s_rp[nr];
-    for (int p = p_lo + g; p < p_hi; p += SD_GROUPS) {
-        int lo = 0, hi = nr - 1;               // row rr with s_rp[rr] <= p < s_rp[rr+1]
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (s_rp[mid] <= p) lo = mid;
-            else hi = mid - 1;
-        }
-        const T *arow = s_a + lo * lds_ld;
-        const int64_t j = (int64_t)colind[p] - origin;
-        const T *bcol = B + j * ldb;
-        T dot = T(0);
-        if (VECB) {
-            constexpr int N = V16<T>::N;
-            for (int64_t kk = (int64_t)q * N; kk < K; kk += SD_GROUP * N) {
-                const V16<T> bv = *reinterpret_cast<const V16<T> *>(bcol + kk);
-                const V16<T> av = *reinterpret_cast<const V16<T> *>(arow + kk);
+    // This lane's slice of K in the one-step case, clamped into range.
+    const int64_t k1 = (int64_t)q * NE;
+    const bool k1_ok = k1 < K;
+    const int64_t k1c = k1_ok ? k1 : K - NE;
+    for (int p0 = p_lo + g; p0 < p_hi; p0 += GROUPS * U) {
+        int pc[U];
+        int64_t j[U];
+        const T *arow[U];
 #pragma unroll
-                for (int e = 0; e < N; ++e) dot += av.v[e] * bv.v[e];
+        for (int u = 0; u < U; ++u) {
+            const int p = p0 + u * GROUPS;
+            pc[u] = p < p_hi ? p : p0;
+            j[u] = (int64_t)colind[pc[u]] - origin;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            int lo = 0, hi = nr - 1;             // row rr with s_rp[rr] <= p < s_rp[rr+1]
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_rp[mid] <= pc[u]) lo = mid;
+                else hi = mid - 1;
+            }
+            arow[u] = s_a + lo * lds_ld;
+        }
+        T dot[U];
+        if (ONE) {
+            if (VECB) {
+                V16<T> bv[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) bv[u] = *reinterpret_cast<const V16<T> *>(B + j[u] * ldb + k1c);
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    const V16<T> av = *reinterpret_cast<const V16<T> *>(arow[u] + k1c);
+                    T d = T(0);
+#pragma unroll
+                    for (int e = 0; e < NE; ++e) d += av.v[e] * bv[u].v[e];
+                    dot[u] = k1_ok ? d : T(0);
+                }
+            } else {
+                T bv[U];
+#pragma unroll
+                for (int u = 0; u < U; ++u) bv[u] = B[j[u] * ldb + k1c];
+#pragma unroll
+                for (int u = 0; u < U; ++u) dot[u] = k1_ok ? arow[u][k1c] * bv[u] : T(0);
             }
         } else {
-            for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += arow[kk] * bcol[kk];
+            const T *bcol = B + j[0] * ldb;
+            T d = T(0);
+            if (VECB) {
+                for (int64_t kk = k1; kk < K; kk += G * NE) {
+                    const V16<T> bv = *reinterpret_cast<const V16<T> *>(bcol + kk);
+                    const V16<T> av = *reinterpret_cast<const V16<T> *>(arow[0] + kk);
+#pragma unroll
+                    for (int e = 0; e < NE; ++e) d += av.v[e] * bv.v[e];
+                }
+            } else {
+                for (int64_t kk = q; kk < K; kk += G) d += arow[0][kk] * bcol[kk];
+            }
+            dot[0] = d;
         }
-        dot = group_sum(dot);
+#pragma unroll
+        for (int u = 0; u < U; ++u) dot[u] = group_sum<G>(dot[u]);
         if (q == 0) {
-            T out = alpha * dot;
-            if (mask) out = mask[p] * out;
-            if (!beta_zero) out += beta * Cval[p];
-            Cval[p] = out;
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                const int p = p0 + u * GROUPS;
+                if (p < p_hi) {
+                    T out = alpha * dot[u];
+                    if (mask) out = mask[p] * out;
+                    if (!beta_zero) out += beta * Cval[p];
+                    Cval[p] = out;
+                }
+            }
         }
     }
 }
@@ -111,7 +164,7 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_direct_kernel(
         const int64_t j = (int64_t)colind[p] - origin;
         T dot = T(0);
         for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
-        dot = group_sum(dot);
+        dot = group_sum<SD_GROUP>(dot);
         if (q == 0) {
             T out = alpha * dot;
             if (mask) out = mask[p] * out;
@@ -155,13 +208,24 @@ int csr_sddmm(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin,
     const bool vecb = (K % N == 0) && (ldb % N == 0) && (((uintptr_t)B) % 16 == 0);
     const size_t smem = sizeof(T) * (size_t)R * (size_t)lds_ld + sizeof(int32_t) * (size_t)(R + 1);
     const dim3 grid((unsigned)((m + R - 1) / R));
-    if (vecb)
-        hipLaunchKernelGGL((csr_sddmm_kernel<T, true>), grid, dim3(SD_BLOCK), smem, s, m, K, origin,
-                           rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, R, lds_ld);
-    else
-        hipLaunchKernelGGL((csr_sddmm_kernel<T, false>), grid, dim3(SD_BLOCK), smem, s, m, K,
-                           origin, rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, R,
-                           lds_ld);
+    // Lane loads that cover K: G = the smallest power of two >= that, up to 8.
+    const int64_t slices = vecb ? K / N : K;
+#define JLUST_SD(V, G, U, ONE)                                                                        \
+    hipLaunchKernelGGL((csr_sddmm_kernel<T, V, G, U, ONE>), grid, dim3(SD_BLOCK), smem, s, m, K, origin, \
+                       rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, R, lds_ld)
+#define JLUST_SD_V(V)                                                                                 \
+    do {                                                                                              \
+        if (slices == 0) JLUST_SD(V, 8, 1, false);     /* K = 0: no loads of B at all */             \
+        else if (slices <= 1) JLUST_SD(V, 1, 4, true);                                                \
+        else if (slices <= 2) JLUST_SD(V, 2, 4, true);                                                \
+        else if (slices <= 4) JLUST_SD(V, 4, 2, true);                                                \
+        else if (slices <= 8) JLUST_SD(V, 8, 1, true);                                                \
+        else JLUST_SD(V, 8, 1, false);                                                                \
+    } while (0)
+    if (vecb) JLUST_SD_V(true);
+    else JLUST_SD_V(false);
+#undef JLUST_SD_V
+#undef JLUST_SD
     return check_launch("csr_sddmm_kernel");
 }
 
