@@ -1019,7 +1019,12 @@ int mostly_local(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_
 }
 
 // Slice or not: JLUST_HIP_SPMV_SLICE=0 never, =1 always, unset = when x is
-// larger than one XCD's L2 and the gathers are not mostly local.
+// larger than one XCD's L2, rows are long enough, and the gathers are not
+// mostly local.  Slices carry every row 8 times (8 merge paths of m row ends
+// plus an 8 x m partial-sum reduction, ~45-50 ps per row on MI355X) and save
+// ~9 ps per nonzero gathering from a 32 MB x, ~5 ps from an 8 MB x (random
+// columns, 4M x 4M and 4M x 1M matrices): the break-even mean row length is
+// ~5-6 and ~9 entries, so slicing needs nnz >= L * m with L by x's size.
 template <typename T>
 int want_slices(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *rowptr,
                 const int32_t *colind, hipStream_t s, bool *out)
@@ -1032,7 +1037,10 @@ int want_slices(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t
         *out = n >= NUM_XCD;
         return JLUST_STATUS_SUCCESS;
     }
-    if ((size_t)n * sizeof(T) <= SLICE_MIN_X_BYTES) return JLUST_STATUS_SUCCESS;
+    const size_t xbytes = (size_t)n * sizeof(T);
+    if (xbytes <= SLICE_MIN_X_BYTES) return JLUST_STATUS_SUCCESS;
+    const int64_t min_len = xbytes >= ((size_t)24 << 20) ? 6 : xbytes >= ((size_t)6 << 20) ? 10 : 14;
+    if (nnz < min_len * m) return JLUST_STATUS_SUCCESS;
     bool local = false;
     if (int st = mostly_local<T>(m, n, nnz, origin, rowptr, colind, s, &local)) return st;
     *out = !local;

@@ -76,8 +76,11 @@ def test_plan_matches_oracle(J, O, dtype, origin, sort):
                   dtype, "COO plan after update_values")
 
 
-def test_sliced_plan_unsorted(J, O):
-    """x of 5 MB with random columns: the CSR plan under the COO plan slices A."""
+def test_sliced_plan_unsorted(J, O, monkeypatch):
+    """x of 5 MB with random columns, slices forced: the CSR plan under the
+    COO plan slices A (its rows, 8 entries on average, are below the automatic
+    threshold)."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1")
     m, n, nnz = 50_000, 640_000, 400_000
     rows, cols, val = random_coo(m, n, nnz, 8, 1, np.float64)
     A = J.coo_tensor(dev(rows), dev(cols), dev(val), (m, n))

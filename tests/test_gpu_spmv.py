@@ -279,3 +279,24 @@ def test_plan_sliced_full_config2_deterministic(J, O, monkeypatch):
     y2 = torch.empty(cfg["m"], dtype=torch.float64, device="cuda")
     J.execute(h, dev(cfg["x"]), y2)
     np.testing.assert_array_equal(host(y2), y)
+
+
+@pytest.mark.parametrize("per_row,expect", [(2, "vector"), (8, "sliced")])
+def test_plan_slicing_threshold(J, O, per_row, expect, monkeypatch):
+    """x of 25.6 MB with random columns: slices pay from ~6 entries per row
+    (every row is carried by all 8 slices); shorter rows keep one merge path /
+    the vector kernel.  Both plans match the oracle."""
+    monkeypatch.delenv("JLUST_HIP_SPMV_SLICE", raising=False)
+    monkeypatch.delenv("JLUST_HIP_SPMV_VECTOR", raising=False)
+    m = n = 3_200_000
+    rng = np.random.default_rng(per_row)
+    colind = np.sort(rng.integers(0, n, (m, per_row)), axis=1)
+    colind = (colind.reshape(-1) + 1).astype(np.int32)
+    rowptr = (np.arange(m + 1, dtype=np.int64) * per_row + 1).astype(np.int32)
+    val = rng.uniform(-1, 1, colind.size)
+    x = rng.uniform(-1, 1, n)
+    y, h, _ = run_plan(J, rowptr, colind, val, x, m, n)
+    assert h.kernel() == expect
+    ref = O.csr_spmv(rowptr, colind, val, x)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x)
+    assert_within(y, ref, absref, np.float64, f"{per_row} per row")
