@@ -155,10 +155,12 @@ def test_sddmm_random(J, O, K, dtype):
     assert_within(out, ref, absref, dtype, f"K={K}")
 
 
-def test_sddmm_mask_in_place(J, O):
-    """The config-4 form: out = S_ij * dot, with the mask read from C.val itself."""
+@pytest.mark.parametrize("K", [128, 4, 1])
+def test_sddmm_mask_in_place(J, O, K):
+    """The config-4 form: out = S_ij * dot, with the mask read from C.val itself
+    (K = 4 and 1 run several nonzeros per lane group per step)."""
     import torch
-    m, n, K = 3000, 2500, 128
+    m, n = 3000, 2500
     rowptr, colind, _ = random_csr(m, n, lengths=np.full(m, 32), seed=11, dtype=np.float32)
     rng = np.random.default_rng(6)
     A = np.asfortranarray(rng.standard_normal((m, K)).astype(np.float32))
@@ -170,7 +172,7 @@ def test_sddmm_mask_in_place(J, O):
     torch.cuda.synchronize()
     ref = O.csr_sddmm(rowptr, colind, A, B, mask=S)
     absref = O.csr_sddmm_absref(rowptr, colind, A, B, mask=S)
-    assert_within(host(cv), ref, absref, np.float32, "mask in place")
+    assert_within(host(cv), ref, absref, np.float32, f"mask in place K={K}")
 
 
 def test_sddmm_config4_full_sampled_rows(J, O):

@@ -300,3 +300,24 @@ def test_plan_slicing_threshold(J, O, per_row, expect, monkeypatch):
     ref = O.csr_spmv(rowptr, colind, val, x)
     absref = O.csr_spmv_absref(rowptr, colind, val, x)
     assert_within(y, ref, absref, np.float64, f"{per_row} per row")
+
+
+@pytest.mark.parametrize("lanes", [2, 4])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_plan_vector_kernel_row_lengths(J, O, lanes, dtype, monkeypatch):
+    """The vector kernel forced to 2 / 4 lanes per row on rows of 0 .. 16*lanes
+    entries: a lane's entries are loaded 4 at a time, so rows end inside, at
+    and past those batches; empty rows give beta*y."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_VECTOR", str(lanes))
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "0")
+    m, n = 20_000, 30_000
+    lens = np.random.default_rng(lanes).integers(0, 16 * lanes + 1, m)
+    lens[::97] = 0
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=lanes + 40, dtype=dtype)
+    x = np.random.default_rng(3).uniform(-1, 1, n).astype(dtype)
+    y0 = np.random.default_rng(4).uniform(-1, 1, m).astype(dtype)
+    y, h, _ = run_plan(J, rowptr, colind, val, x, m, n, alpha=-1.25, beta=0.5, y0=y0)
+    assert h.kernel() == "vector"
+    ref = O.csr_spmv(rowptr, colind, val, x, -1.25, 0.5, y0)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x, -1.25, 0.5, y0)
+    assert_within(y, ref, absref, dtype, f"vector kernel, {lanes} lanes")
