@@ -175,6 +175,28 @@ def blocks_bench(steps, warmup):
             J.mul_(y, A, x)
         torch.cuda.synchronize()
         t_async = (time.perf_counter() - t0) / steps
+        # The same calls captured once in a HIP graph (G calls per graph) and
+        # replayed: the per-call launch cost without host dispatch.
+        G = 20
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            J.mul_(y, A, x)
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            for _ in range(G):
+                J.mul_(y, A, x)
+        graph.replay()
+        torch.cuda.synchronize()
+        reps = max(1, steps // G)
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            graph.replay()
+        torch.cuda.synchronize()
+        t_graph = (time.perf_counter() - t0) / (reps * G)
+        del graph
         asm = A.assembled().asm
         nz = J.nnz(asm)
         byts = 12 * nz + 4 * (m + 1) + 8 * (m + n)
@@ -191,10 +213,12 @@ def blocks_bench(steps, warmup):
                     "first_call_ms": round(t_first * 1e3, 2),
                     "us_per_call_sync": round(t_sync * 1e6, 1),
                     "us_per_call_queued": round(t_async * 1e6, 1),
+                    "us_per_call_graph": round(t_graph * 1e6, 1),
                     "effective_GBps_sync": round(byts / t_sync / 1e9, 1),
                     "effective_GBps_queued": round(byts / t_async / 1e9, 1),
                     "cpu_scipy_us": round(t_cpu * 1e6, 1), "max_rel_diff_vs_scipy": err})
         log(f"{name}: {m}x{n} nnz {nz}: {t_sync*1e6:.1f} us/call synced, {t_async*1e6:.1f} queued, "
+            f"{t_graph*1e6:.1f} in a graph, "
             f"first call {t_first*1e3:.1f} ms, scipy {t_cpu*1e6:.0f} us")
     return out
 

@@ -25,7 +25,12 @@
  *  - Work is enqueued on `stream` (a hipStream_t; NULL = the null stream) and
  *    returns without synchronising.  Entry points are reentrant.  The library
  *    keeps one scratch buffer per (device, stream) for the SpMV/SpMM partial
- *    results, so concurrent calls must use different streams.
+ *    results, so concurrent calls must use different streams.  The buffer
+ *    grows on demand and an outgrown one is kept, never freed, so work already
+ *    queued and HIP graphs that captured a call stay valid.  Capturing a call
+ *    in a graph: make one call of the same size on the capturing stream first
+ *    (no allocation may happen inside a capture); prepared plans own their
+ *    buffers and need no such warm-up.
  *  - Return value: a jlust_status code.  A message for the last failure on the
  *    calling thread is available from jlust_hip_last_error().
  *  - There is no CPU fallback: with no usable GPU every compute entry point

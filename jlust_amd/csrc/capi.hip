@@ -93,6 +93,11 @@ struct ScratchBuf {
 };
 static std::mutex g_scratch_mu;
 static std::map<std::pair<int, jlust_stream_t>, ScratchBuf> g_scratch;
+// Buffers outgrown by a later call.  They are kept until the process ends:
+// work already queued may still read them, and so may any HIP graph that
+// captured a call on that stream and is replayed later.  Growth is by at
+// least a quarter, so the kept buffers stay within a few times the largest.
+static std::vector<void *> g_scratch_retired;
 
 int scratch(jlust_stream_t stream, size_t bytes, void **out)
 {
@@ -102,15 +107,11 @@ int scratch(jlust_stream_t stream, size_t bytes, void **out)
     std::lock_guard<std::mutex> lk(g_scratch_mu);
     ScratchBuf &b = g_scratch[{dev, stream}];
     if (b.bytes < bytes) {
-        size_t want = bytes + bytes / 4 + 4096;
-        if (b.ptr) {
-            // In-flight work on this stream may still use the old buffer.
-            JLUST_HIP_TRY(hipStreamSynchronize((hipStream_t)stream));
-            JLUST_HIP_TRY(hipFree(b.ptr));
-            b.ptr = nullptr;
-            b.bytes = 0;
-        }
-        JLUST_HIP_TRY(hipMalloc(&b.ptr, want));
+        const size_t want = bytes + bytes / 4 + 4096;
+        void *p = nullptr;
+        JLUST_HIP_TRY(hipMalloc(&p, want));
+        if (b.ptr) g_scratch_retired.push_back(b.ptr);
+        b.ptr = p;
         b.bytes = want;
     }
     *out = b.ptr;

@@ -1,0 +1,88 @@
+"""HIP graph capture of the prepared and plain products: a caller may
+capture execute(h, x, y) (or the plain SpMV/SpMM calls) in a torch HIP graph
+and replay it.  Each graph is replayed several times with eager work and a
+synchronisation between replays (inputs refilled, outputs reset), and every
+replay is compared with the eager result bit for bit (the kernels are
+deterministic).  The plain calls use the library's per-stream scratch buffer,
+so they are warmed up on the capturing stream first (no allocation may happen
+inside a capture)."""
+import numpy as np
+import pytest
+
+from tests._util import dev, host, random_csr
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def J():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import jlust_amd
+    return jlust_amd
+
+
+def check_replays(run, inp, out, out0, nrep=4):
+    """Warm run() up on a side stream, capture it there, then replay nrep
+    times; before each replay inp gets new values and out its start values;
+    each replay's out must equal an eager run's."""
+    import torch
+    s = torch.cuda.Stream()                       # default priority
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            run()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run()
+    torch.cuda.synchronize()
+    for rep in range(nrep):
+        inp.uniform_(-1.0, 1.0)
+        out.copy_(out0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = host(out).copy()
+        out.copy_(out0)
+        run()                                     # eager, on the current stream
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got, host(out), err_msg=f"replay {rep}")
+
+
+@pytest.mark.parametrize("kind", ["merge", "vector", "sliced"])
+def test_graph_spmv_plan(J, kind, monkeypatch):
+    import torch
+    if kind == "vector":
+        m, n, lens = 30_000, 20_000, np.full(30_000, 12)
+    else:
+        m, n, lens = 30_000, 700_000, np.random.default_rng(1).integers(0, 90, 30_000)
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1" if kind == "sliced" else "0")
+    if kind == "merge":
+        monkeypatch.setenv("JLUST_HIP_SPMV_VECTOR", "0")
+    else:
+        monkeypatch.delenv("JLUST_HIP_SPMV_VECTOR", raising=False)
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=5)
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    assert h.kernel() == kind
+    x = torch.zeros(n, dtype=torch.float64, device="cuda")
+    y = torch.zeros(m, dtype=torch.float64, device="cuda")
+    y0 = dev(np.random.default_rng(2).uniform(-1, 1, m))
+    check_replays(lambda: J.execute(h, x, y, alpha=1.5, beta=-0.5), x, y, y0)
+
+
+def test_graph_plain_spmv_and_spmm(J):
+    import torch
+    m, n, k = 5000, 4000, 24
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(3).integers(0, 40, m),
+                                     seed=6, dtype=np.float32)
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    x = torch.zeros(n, dtype=torch.float32, device="cuda")
+    y = torch.zeros(m, dtype=torch.float32, device="cuda")
+    check_replays(lambda: J.execute(J.SpMVOp, A, x, y), x, y, torch.zeros_like(y))
+    B = J.dense_matrix(n, k, dtype=torch.float32)
+    C = J.dense_matrix(m, k, dtype=torch.float32)
+    C0 = torch.randn(k, m, device="cuda").t()
+    check_replays(lambda: J.execute(J.SpMMOp, A, B, C, alpha=2.0, beta=0.5), B, C, C0)
