@@ -53,6 +53,13 @@ def parse():
                    help="only run a 1 GiB device copy (PMC byte-counter calibration)")
     p.add_argument("--gather-ceiling", action="store_true",
                    help="only measure random-gather bandwidth (8 B and 512 B rows) per source size")
+    p.add_argument("--sweep-spmm", action="store_true",
+                   help="only time CSR SpMM on config 3's matrix for k = 1 .. 256 (and the f32 SpMV)")
+    p.add_argument("--sweep-sddmm", action="store_true",
+                   help="only time SDDMM on config 4's mask for K = 1 .. 256")
+    p.add_argument("--sweep-spmv", action="store_true",
+                   help="only time SpMV on random matrices of 1 .. 16 entries per row: plain call, "
+                        "plans forced unsliced / sliced, and the plan's own choice")
     p.add_argument("--mfma-peak", action="store_true",
                    help="only measure the sustained fp32 MFMA rate (v_mfma_f32_16x16x4_f32 chains)")
     p.add_argument("--convert", action="store_true",
@@ -377,6 +384,107 @@ def gather_probe():
     return res
 
 
+def _wall_ms(fn, reps=10, warm=3):
+    import torch
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / reps * 1e3
+
+
+def sweep_spmm():
+    """CSR SpMM C = A*B on config 3's matrix (1M x 1M, 32 per row, f32) for
+    k = 1 .. 256 (random column-major B), mean wall ms per call, with the
+    compulsory-byte rate and the gathered-byte rate (nnz*k*4); then the f32
+    SpMV of the same matrix."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    cfg = W.make(3)
+    A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (cfg["m"], cfg["n"]))
+    m, n, nnz = cfg["m"], cfg["n"], cfg["colind"].size
+    g = torch.Generator(device="cuda").manual_seed(0)
+    res = []
+    for k in (1, 2, 4, 8, 16, 32, 64, 128, 256):
+        B = torch.randn(k, n, device="cuda", generator=g).t()
+        C = J.dense_matrix(m, k, dtype=torch.float32)
+        ms = _wall_ms(lambda: J.execute(J.SpMMOp, A, B, C))
+        alg = 8 * nnz + 4 * (m + 1) + 4 * n * k + 4 * m * k
+        res.append({"k": k, "ms": round(ms, 4), "GBps": round(alg / ms / 1e6, 1),
+                    "gathered_GBps": round(nnz * k * 4 / ms / 1e6, 1)})
+        log(f"SpMM k={k}: {ms:.3f} ms")
+        del B, C
+    x = torch.randn(n, device="cuda", generator=g)
+    y = torch.empty(m, device="cuda")
+    res.append({"spmv_f32_ms": round(_wall_ms(lambda: J.execute(J.SpMVOp, A, x, y)), 4)})
+    return res
+
+
+def sweep_sddmm():
+    """SDDMM out = S .* (A B^T) at config 4's mask (500k x 500k, 32 per row,
+    f32) for K = 1 .. 256 (random column-major A, B), mean wall ms per call."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    cfg = W.make(4)
+    m, n, nnz = cfg["m"], cfg["n"], cfg["colind"].size
+    S = dev(cfg["mask"])
+    out = torch.empty_like(S)
+    Cs = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), out, (m, n))
+    g = torch.Generator(device="cuda").manual_seed(0)
+    res = []
+    for K in (1, 2, 4, 8, 16, 32, 64, 128, 256):
+        Am = torch.randn(K, m, device="cuda", generator=g).t()
+        Bm = torch.randn(n, K, device="cuda", generator=g).t()
+        ms = _wall_ms(lambda: J.execute(J.SDDMMOp, Am, Bm, Cs, mask=S))
+        alg = 4 * (m + 1) + 12 * nnz + 4 * m * K + 4 * n * K
+        res.append({"K": K, "ms": round(ms, 4), "GBps": round(alg / ms / 1e6, 1),
+                    "gathered_GBps": round(nnz * K * 4 / ms / 1e6, 1)})
+        log(f"SDDMM K={K}: {ms:.3f} ms")
+        del Am, Bm
+    return res
+
+
+def sweep_spmv():
+    """SpMV on random m x n matrices with L uniformly random columns per row
+    (f64): the plain call, plans with column slices off (vector kernel where
+    the rows allow it) and forced on, and the plan's own choice, in mean wall
+    ms per call."""
+    import torch
+    import jlust_amd as J
+    rng = np.random.default_rng(0)
+    res = []
+    for m, n in ((4_000_000, 4_000_000), (1_000_000, 4_000_000), (4_000_000, 1_000_000)):
+        for L in (1, 2, 4, 6, 8, 12, 16):
+            rp = (np.arange(m + 1, dtype=np.int64) * L + 1).astype(np.int32)
+            ci = rng.integers(0, n, (m, L))
+            ci.sort(axis=1)
+            A = J.csr_tensor(dev(rp), dev((ci.reshape(-1) + 1).astype(np.int32)),
+                             dev(rng.uniform(-1, 1, m * L)), (m, n))
+            x = dev(rng.uniform(-1, 1, n))
+            y = torch.empty(m, dtype=torch.float64, device="cuda")
+            e = {"m": m, "n": n, "per_row": L, "plain_ms": round(_wall_ms(lambda: J.execute(J.SpMVOp, A, x, y)), 4)}
+            for key, val in (("unsliced", "0"), ("sliced", "1"), ("auto", None)):
+                if val is None:
+                    os.environ.pop("JLUST_HIP_SPMV_SLICE", None)
+                else:
+                    os.environ["JLUST_HIP_SPMV_SLICE"] = val
+                h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+                e[f"{key}_ms"] = round(_wall_ms(lambda: J.execute(h, x, y)), 4)
+                e[f"{key}_kernel"] = h.kernel()
+                del h
+            os.environ.pop("JLUST_HIP_SPMV_SLICE", None)
+            res.append(e)
+            log(f"SpMV {m}x{n} L={L}: {e}")
+            del A, x, y
+            torch.cuda.empty_cache()
+    return res
+
+
 def mfma_peak():
     """Sustained fp32 matrix-core rate (jlust_amd/csrc/gather_probe.hip,
     mfma_probe_kernel) for 1, 2 and 4 waves per SIMD, beside the published
@@ -593,6 +701,15 @@ def main():
         return
     if args.mfma_peak:
         print(json.dumps({"mfma_peak": mfma_peak()}), flush=True)
+        return
+    if args.sweep_spmm:
+        print(json.dumps({"sweep_spmm": sweep_spmm()}), flush=True)
+        return
+    if args.sweep_sddmm:
+        print(json.dumps({"sweep_sddmm": sweep_sddmm()}), flush=True)
+        return
+    if args.sweep_spmv:
+        print(json.dumps({"sweep_spmv": sweep_spmv()}), flush=True)
         return
     if args.convert:
         print(json.dumps({"convert": convert_bench(args.cpu_seconds)}), flush=True)
