@@ -76,13 +76,14 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     const int64_t k1 = (int64_t)q * NE;
     const bool k1_ok = k1 < K;
     const int64_t k1c = k1_ok ? k1 : K - NE;
-    for (int p0 = p_lo + g; p0 < p_hi; p0 += GROUPS * U) {
-        int pc[U];
+    // 64-bit positions: p0 + GROUPS*U may pass INT32_MAX near the end.
+    for (int64_t p0 = (int64_t)p_lo + g; p0 < p_hi; p0 += GROUPS * U) {
+        int64_t pc[U];
         int64_t j[U];
         const T *arow[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int p = p0 + u * GROUPS;
+            const int64_t p = p0 + u * GROUPS;
             pc[u] = p < p_hi ? p : p0;
             j[u] = (int64_t)colind[pc[u]] - origin;
         }
@@ -137,7 +138,7 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
         if (q == 0) {
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                const int p = p0 + u * GROUPS;
+                const int64_t p = p0 + u * GROUPS;
                 if (p < p_hi) {
                     T out = alpha * dot[u];
                     if (mask) out = mask[p] * out;
