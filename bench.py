@@ -136,12 +136,14 @@ def blocks_bench(steps, warmup):
     sweep_cases.jl:103-166), on synthetic matrices of pglib case30000_goc
     size.  Per operator: time per call with a sync after each (the
     reference's @belapsed(mul!; sync)), time per call when calls are queued
-    back to back, the one-off assembly, effective GB/s of the assembled
+    back to back -- each with direct launches (the default) and with mul!'s
+    per-(y, x) graph cache -- the one-off assembly, effective GB/s of the assembled
     CSR's compulsory bytes, and scipy's CSR matvec of the same matrix on
     this host."""
     import torch
     import scipy.sparse as sps
     import jlust_amd as J
+    from jlust_amd import block_sparse as BS
     from jlust_amd import workloads as W
     d = W.dcopf(**W.DCOPF_CASE30000)
     nb, nl, ng, nv, nc = d["n_bus"], d["n_line"], d["n_gen"], d["n_var"], d["n_con"]
@@ -169,21 +171,27 @@ def blocks_bench(steps, warmup):
         J.mul_(y, A, x)
         torch.cuda.synchronize()
         t_first = time.perf_counter() - t0
-        for _ in range(warmup):
-            J.mul_(y, A, x)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            J.mul_(y, A, x)
+        def per_call(sync):
+            for _ in range(warmup):
+                J.mul_(y, A, x)
             torch.cuda.synchronize()
-        t_sync = (time.perf_counter() - t0) / steps
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            J.mul_(y, A, x)
-        torch.cuda.synchronize()
-        t_async = (time.perf_counter() - t0) / steps
-        # The same calls captured once in a HIP graph (G calls per graph) and
-        # replayed: the per-call launch cost without host dispatch.
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                J.mul_(y, A, x)
+                if sync:
+                    torch.cuda.synchronize()
+            torch.cuda.synchronize()
+            return (time.perf_counter() - t0) / steps
+        # mul! launching the product directly (the default), then with the
+        # reference-style cache of one captured graph per (y, x) replayed.
+        use = BS.USE_GRAPHS
+        BS.USE_GRAPHS = False
+        t_sync, t_async = per_call(True), per_call(False)
+        BS.USE_GRAPHS = True
+        t_sync_g, t_async_g = per_call(True), per_call(False)
+        BS.USE_GRAPHS = use
+        # The same calls captured by the caller in one HIP graph (G calls per
+        # graph) and replayed: the per-call launch cost without host dispatch.
         G = 20
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -220,12 +228,15 @@ def blocks_bench(steps, warmup):
                     "first_call_ms": round(t_first * 1e3, 2),
                     "us_per_call_sync": round(t_sync * 1e6, 1),
                     "us_per_call_queued": round(t_async * 1e6, 1),
+                    "us_per_call_sync_graph_cache": round(t_sync_g * 1e6, 1),
+                    "us_per_call_queued_graph_cache": round(t_async_g * 1e6, 1),
                     "us_per_call_graph": round(t_graph * 1e6, 1),
                     "effective_GBps_sync": round(byts / t_sync / 1e9, 1),
                     "effective_GBps_queued": round(byts / t_async / 1e9, 1),
                     "cpu_scipy_us": round(t_cpu * 1e6, 1), "max_rel_diff_vs_scipy": err})
-        log(f"{name}: {m}x{n} nnz {nz}: {t_sync*1e6:.1f} us/call synced, {t_async*1e6:.1f} queued, "
-            f"{t_graph*1e6:.1f} in a graph, "
+        log(f"{name}: {m}x{n} nnz {nz}: {t_sync*1e6:.1f} us/call synced, {t_async*1e6:.1f} queued "
+            f"(graph per call {t_sync_g*1e6:.1f} / {t_async_g*1e6:.1f}), "
+            f"{t_graph*1e6:.1f} in a caller's graph, "
             f"first call {t_first*1e3:.1f} ms, scipy {t_cpu*1e6:.0f} us")
     return out
 

@@ -50,6 +50,7 @@ extern "C" {
 
 typedef void *jlust_stream_t;                 /* hipStream_t */
 typedef struct jlust_spmv_plan *jlust_spmv_plan_t;
+typedef struct jlust_spmv_graph *jlust_spmv_graph_t;
 typedef struct jlust_convert *jlust_convert_t;
 
 /*
@@ -70,7 +71,8 @@ enum jlust_status {
     JLUST_STATUS_INDEX_ORIGIN = 5,
     JLUST_STATUS_HIP_ERROR = 6,
     JLUST_STATUS_NO_DEVICE = 7,
-    JLUST_STATUS_OUT_OF_MEMORY = 8
+    JLUST_STATUS_OUT_OF_MEMORY = 8,
+    JLUST_STATUS_STREAM_CAPTURING = 9   /* graph launch onto a capturing stream */
 };
 
 /* ---------------------------------------------------------------- library */
@@ -139,6 +141,31 @@ int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float alpha,
                                         const float *x, float beta, float *y,
                                         jlust_stream_t stream);
 int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan);
+
+/*
+ * A plan execution recorded once as a HIP graph and replayed on any stream of
+ * the plan's device: the reference's GPU block products capture their SpMV
+ * with CUDA.capture/instantiate and replay it with CUDA.launch, one graph per
+ * (pointer(y), pointer(x)) (ext/CUDAExt/ops/block_mul.jl:233-267, 751-786).
+ * capture records y = alpha*A*x + beta*y with these pointers and coefficients
+ * (on a private stream, thread-local capture mode; nothing runs).  A launch
+ * reads the plan's buffers as they are then: values written into the same
+ * buffers (update_values of a sliced or COO plan, or new values stored in
+ * place) are seen; update_values with another value pointer on a merge or
+ * vector plan needs a new capture.  launch onto a stream that is itself being
+ * captured returns JLUST_STATUS_STREAM_CAPTURING without launching (execute
+ * the plan instead, so the outer capture records its kernels, as the
+ * reference does under CUDA.is_capturing()).  destroy drains the device
+ * first.  The plan must outlive its graphs.
+ */
+int jlust_hip_csr_spmv_plan_capture_f64(jlust_spmv_plan_t plan, double alpha,
+                                        const double *x, double beta, double *y,
+                                        jlust_spmv_graph_t *graph_out);
+int jlust_hip_csr_spmv_plan_capture_f32(jlust_spmv_plan_t plan, float alpha,
+                                        const float *x, float beta, float *y,
+                                        jlust_spmv_graph_t *graph_out);
+int jlust_hip_spmv_graph_launch(jlust_spmv_graph_t graph, jlust_stream_t stream);
+int jlust_hip_spmv_graph_destroy(jlust_spmv_graph_t graph);
 
 /* The kernel a plan runs (no counterpart in the reference; for diagnostics
  * and benchmarks): merge-path tiles, the vector kernel for short even rows

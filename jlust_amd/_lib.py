@@ -39,6 +39,10 @@ SIGNATURES = {
     "jlust_hip_csr_spmv_plan_execute_f64": (_INT, [_P, _D, _P, _D, _P, _P]),
     "jlust_hip_csr_spmv_plan_execute_f32": (_INT, [_P, _F, _P, _F, _P, _P]),
     "jlust_hip_csr_spmv_plan_destroy": (_INT, [_P]),
+    "jlust_hip_csr_spmv_plan_capture_f64": (_INT, [_P, _D, _P, _D, _P, ctypes.POINTER(_P)]),
+    "jlust_hip_csr_spmv_plan_capture_f32": (_INT, [_P, _F, _P, _F, _P, ctypes.POINTER(_P)]),
+    "jlust_hip_spmv_graph_launch": (_INT, [_P, _P]),
+    "jlust_hip_spmv_graph_destroy": (_INT, [_P]),
     "jlust_hip_csr_spmv_plan_info": (_INT, [_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
     "jlust_hip_coo_spmv_plan_create": (_INT, [_I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
                                               ctypes.POINTER(_P)]),
@@ -75,8 +79,9 @@ SIGNATURES = {
 STATUS = {
     0: "SUCCESS", 1: "INVALID_ARGUMENT", 2: "UNSUPPORTED_VALUE_TYPE", 3: "UNSUPPORTED_FORMAT",
     4: "NONCANONICAL_STORAGE", 5: "INDEX_ORIGIN", 6: "HIP_ERROR", 7: "NO_DEVICE",
-    8: "OUT_OF_MEMORY",
+    8: "OUT_OF_MEMORY", 9: "STREAM_CAPTURING",
 }
+STREAM_CAPTURING = 9
 
 _lib = None
 

@@ -13,10 +13,28 @@ the block-by-block products of the reference's generic path.
 update_block_values_ rewrites one block's values and scatters them into the
 assembled values through the slot map kept at assembly
 (block_mul.jl:310-336), so the assembled matrix and the plan stay valid.
+
+With JLUST_HIP_BLOCK_GRAPHS=1 (or USE_GRAPHS = True), SpMV through the
+assembled CSR replays a HIP graph of the plan's launch
+(jlust_hip_csr_spmv_plan_capture_*, captured natively, outside torch's graph
+pools), one per (y, x, alpha, beta), the way the reference caches a CUDA
+graph per (pointer(y), pointer(x)) with a last-key fast path
+(block_mul.jl:233-267): the first call with a key runs the product directly
+and captures it, later calls replay the capture.  Value updates rewrite the
+buffers the capture reads, so captures stay valid across them.  A call made
+while the current stream is itself being captured launches directly (the
+outer capture records it).  Direct launch is the default because it is the
+faster one here: on MI355X with ROCm 7 one hipGraphLaunch of a single
+product costs more host time than the kernel launch it replaces (the
+DCOPF case30000 product: 25 us queued per replay against 8 us launched
+directly).  Callers with many products per step get the launch savings by
+capturing the whole step in one graph.
 """
 from __future__ import annotations
 
 import ctypes
+import os
+import warnings
 import weakref
 from typing import List, Optional
 
@@ -29,6 +47,12 @@ from .formats import Formats, is_shifted_diag
 from .tensor import USTensor, ZeroBased, csr_tensor, nnz, nonzeros, ust
 
 _VT = {torch.float64: 0, torch.float32: 1}
+
+# Replay assembled-CSR SpMV from captured HIP graphs (module switch; the
+# environment sets its initial value; off by default, see above).
+USE_GRAPHS = os.environ.get("JLUST_HIP_BLOCK_GRAPHS", "0") == "1"
+# Captures kept per assembled matrix; the oldest is dropped past this.
+GRAPH_CACHE = 16
 
 
 class BlockStructureError(JLUSTError, ValueError):
@@ -116,6 +140,10 @@ class AssembledCSR:
         _lib.check(st, "csr_assemble", Formats.CSR, "HIPBackend", dtype)
         self.asm = csr_tensor(rowptr, colind, val, (m, n), origin=ZeroBased())
         self._plan = None
+        self._graphs = {}            # (y ptr, x ptr, alpha, beta) -> SpMVGraph
+        self._last_key = None
+        self._last_graph = None
+        self.graph_error = None
 
     @property
     def nnz(self) -> int:
@@ -128,7 +156,47 @@ class AssembledCSR:
         return self._plan
 
     def spmv(self, x: torch.Tensor, y: torch.Tensor, alpha=1.0, beta=0.0):
-        return self.plan().execute_tensors(x, y, float(alpha), float(beta))
+        h = self.plan()
+        alpha, beta = float(alpha), float(beta)
+        if USE_GRAPHS and self._graphs is not None and self._plain(x, y):
+            key = (y.data_ptr(), x.data_ptr(), alpha, beta)
+            g = self._last_graph if key == self._last_key else self._graphs.get(key)
+            if g is None:
+                h.execute_tensors(x, y, alpha, beta)      # this call's product
+                self._capture(h, x, y, alpha, beta, key)  # replayed from the next call on
+                return y
+            self._last_key, self._last_graph = key, g
+            if g.launch():
+                return y
+        return h.execute_tensors(x, y, alpha, beta)
+
+    def _plain(self, x, y) -> bool:
+        """x and y are what the plan's direct path takes without conversion."""
+        di = self.device.index
+        return (x.dtype is self.dtype and y.dtype is self.dtype and x.get_device() == di and
+                y.get_device() == di and x.numel() == self.n and y.numel() == self.m and
+                x.is_contiguous() and y.is_contiguous() and self.m > 0)
+
+    def _capture(self, h, x, y, alpha, beta, key):
+        """Record the product for later calls with this key
+        (_bsm_mul_slowpath!, block_mul.jl:247-267); not while the current
+        stream is itself being captured (that capture records the direct
+        launch instead)."""
+        if torch.cuda.is_current_stream_capturing():
+            return
+        try:
+            g = h.capture(x, y, alpha, beta)
+        except JLUSTError as e:
+            # This matrix runs its products directly from now on; the reason
+            # is kept in graph_error.
+            self._graphs = None
+            self.graph_error = str(e)
+            warnings.warn(f"BlockSparse SpMV graph capture failed, launching directly: {e}")
+            return
+        if len(self._graphs) >= GRAPH_CACHE:
+            self._graphs.pop(next(iter(self._graphs)))
+        self._graphs[key] = g
+        self._last_key, self._last_graph = key, g
 
     def spmm(self, X: torch.Tensor, Y: torch.Tensor, alpha=1.0, beta=0.0):
         from .hip_backend import _spmm

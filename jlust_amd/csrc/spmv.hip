@@ -33,6 +33,7 @@
 // gathers from x[s*w : (s+1)*w] and keeps it in its own L2.  Slice s writes a
 // partial y_s; a last pass forms y = alpha*(y_0 + ... + y_7) + beta*y in that
 // fixed order.
+#include <new>
 #include <cstdlib>
 #include <cstring>
 
@@ -1422,6 +1423,107 @@ extern "C" int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float
                                                    jlust_stream_t stream)
 {
     return plan_execute<float>(plan, 1, alpha, x, beta, y, stream);
+}
+
+// A plan execution recorded once as a HIP graph and replayed: the capture
+// runs on a private stream in thread-local mode (other threads' work is not
+// affected), and the executable graph is launched on the caller's stream.
+struct jlust_spmv_graph {
+    hipGraphExec_t exec;
+    int device;
+};
+
+template <typename T>
+static int plan_capture(jlust_spmv_plan_t plan, int want_type, T alpha, const T *x, T beta, T *y,
+                        jlust_spmv_graph_t *out)
+{
+    clear_error();
+    if (!out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_capture: null output");
+    *out = nullptr;
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_capture: null plan");
+    if (plan->m == 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_capture: a plan with no rows launches nothing");
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    if (dev != plan->device)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "spmv_plan_capture: plan belongs to device %d, current device is %d", plan->device, dev);
+    hipStream_t cs = nullptr;
+    JLUST_HIP_TRY(hipStreamCreateWithFlags(&cs, hipStreamNonBlocking));
+    hipError_t e = hipStreamBeginCapture(cs, hipStreamCaptureModeThreadLocal);
+    if (e != hipSuccess) {
+        (void)hipStreamDestroy(cs);
+        return hip_fail(e, "hipStreamBeginCapture");
+    }
+    const int st = plan_execute<T>(plan, want_type, alpha, x, beta, y, cs);
+    hipGraph_t g = nullptr;
+    e = hipStreamEndCapture(cs, &g);
+    (void)hipStreamDestroy(cs);
+    if (st != JLUST_STATUS_SUCCESS || e != hipSuccess) {
+        if (g) (void)hipGraphDestroy(g);
+        return st != JLUST_STATUS_SUCCESS ? st : hip_fail(e, "hipStreamEndCapture");
+    }
+    hipGraphExec_t ex = nullptr;
+    e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate");
+    auto *h = new (std::nothrow) jlust_spmv_graph{ex, dev};
+    if (!h) {
+        (void)hipGraphExecDestroy(ex);
+        return fail(JLUST_STATUS_OUT_OF_MEMORY, "spmv_plan_capture: host allocation failed");
+    }
+    *out = h;
+    return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_csr_spmv_plan_capture_f64(jlust_spmv_plan_t plan, double alpha, const double *x,
+                                                   double beta, double *y, jlust_spmv_graph_t *graph_out)
+{
+    return plan_capture<double>(plan, 0, alpha, x, beta, y, graph_out);
+}
+
+extern "C" int jlust_hip_csr_spmv_plan_capture_f32(jlust_spmv_plan_t plan, float alpha, const float *x,
+                                                   float beta, float *y, jlust_spmv_graph_t *graph_out)
+{
+    return plan_capture<float>(plan, 1, alpha, x, beta, y, graph_out);
+}
+
+extern "C" int jlust_hip_spmv_graph_launch(jlust_spmv_graph_t graph, jlust_stream_t stream)
+{
+    clear_error();
+    if (!graph) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_graph_launch: null graph");
+    hipStream_t s = (hipStream_t)stream;
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    JLUST_HIP_TRY(hipStreamIsCapturing(s, &cap));
+    if (cap != hipStreamCaptureStatusNone)
+        return fail(JLUST_STATUS_STREAM_CAPTURING,
+                    "spmv_graph_launch: the stream is being captured; execute the plan so that the "
+                    "capture records its kernels");
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    if (dev != graph->device)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "spmv_graph_launch: graph belongs to device %d, current device is %d", graph->device, dev);
+    JLUST_HIP_TRY(hipGraphLaunch(graph->exec, s));
+    return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_spmv_graph_destroy(jlust_spmv_graph_t graph)
+{
+    clear_error();
+    if (!graph) return JLUST_STATUS_SUCCESS;
+    // Launches already queued finish first: the device is drained before the
+    // executable graph goes away.
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != graph->device) e = hipSetDevice(graph->device);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    const hipError_t d = hipGraphExecDestroy(graph->exec);
+    if (cur != graph->device) (void)hipSetDevice(cur);
+    delete graph;
+    if (e != hipSuccess) return hip_fail(e, "spmv_graph_destroy: hipDeviceSynchronize");
+    if (d != hipSuccess) return hip_fail(d, "hipGraphExecDestroy");
+    return JLUST_STATUS_SUCCESS;
 }
 
 extern "C" int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *kernel, int32_t *lanes_per_row)

@@ -446,6 +446,29 @@ class HIPSpMVHandle(AbstractKernelHandle):
             _lib.check(st, "csr_spmv_plan_execute", self.u_A.format, _BE, self.T)
         return y
 
+    def capture(self, x: torch.Tensor, y: torch.Tensor, alpha=1.0, beta=0.0) -> "SpMVGraph":
+        """Record execute(h, x, y, alpha, beta) once as a HIP graph
+        (jlust_hip_csr_spmv_plan_capture_*; the reference's CUDA.capture of
+        its SpMV, ext/CUDAExt/ops/block_mul.jl:258-263).  Nothing runs until
+        the graph is launched; x and y are plain contiguous vectors of the
+        plan's type on its device, and the handle has no input_fn/output_fn."""
+        m, n = self.u_A.extents
+        di = self.dev.index
+        if (x.dtype is not self.T or y.dtype is not self.T or x.get_device() != di or
+                y.get_device() != di):
+            raise UnsupportedValueType(x.dtype, _BE, f"capture takes {self.T} vectors on {self.dev}")
+        if x.numel() != n or y.numel() != m or not x.is_contiguous() or not y.is_contiguous():
+            raise IncompatibleExtents(f"capture: A is {m}x{n}, x has {tuple(x.shape)}, "
+                                      f"y has {tuple(y.shape)} (contiguous vectors)")
+        if self.input_fn is not None or self.output_fn is not None:
+            raise UnsupportedFormat(self.u_A.format, _BE, "capture takes handles without input_fn/output_fn")
+        g = ctypes.c_void_p()
+        with _on(self.dev):
+            st = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_capture_{self.suf}")(
+                self._plan, alpha, x.data_ptr(), beta, y.data_ptr(), ctypes.byref(g))
+        _lib.check(st, "csr_spmv_plan_capture", self.u_A.format, _BE, self.T)
+        return SpMVGraph(g, self)
+
     def kernel(self) -> str:
         """The kernel the plan runs: "merge", "vector" or "sliced"."""
         k, lpr = ctypes.c_int32(), ctypes.c_int32()
@@ -468,6 +491,38 @@ class HIPSpMVHandle(AbstractKernelHandle):
         if plan is not None and plan.value:
             try:
                 _lib.lib().jlust_hip_csr_spmv_plan_destroy(plan)
+            except Exception:
+                pass
+
+
+class SpMVGraph:
+    """A captured plan execution (HIPSpMVHandle.capture).  launch() replays
+    it on the current stream of the plan's device and returns True, or
+    returns False without launching when that stream is itself being
+    captured (the caller then executes the plan, so the outer capture records
+    the kernels).  Holds its handle, so the plan outlives the graph."""
+
+    __slots__ = ("_g", "_h", "dev", "_launch")
+
+    def __init__(self, g: ctypes.c_void_p, h: "HIPSpMVHandle"):
+        self._g, self._h, self.dev = g, h, h.dev
+        self._launch = _lib.lib().jlust_hip_spmv_graph_launch
+
+    def launch(self) -> bool:
+        with _on(self.dev):
+            st = self._launch(self._g, _stream(self.dev))
+        if st == 0:
+            return True
+        if st == _lib.STREAM_CAPTURING:
+            return False
+        _lib.check(st, "spmv_graph_launch", self._h.u_A.format, _BE, self._h.T)
+        return False
+
+    def __del__(self):
+        g, self._g = getattr(self, "_g", None), None
+        if g is not None and g.value:
+            try:
+                _lib.lib().jlust_hip_spmv_graph_destroy(g)
             except Exception:
                 pass
 

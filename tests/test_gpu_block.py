@@ -365,6 +365,112 @@ def test_bbm_bw2_time_varying(J, BO):
     assert host(J.coordinates(MM.assembled().asm, 2)).tolist() == colind.tolist()
 
 
+def test_bsm_graph_replay(J, BO, monkeypatch):
+    """Repeated products with the same (y, x, alpha, beta) replay a captured
+    graph (block_mul.jl:233-267).  Every call -- after new x values, with
+    beta != 0 reading y, after update_block_values! -- equals the direct
+    launch bit for bit; new buffers or coefficients get their own capture, the
+    oldest is dropped past the cache size, and a call made inside an outer
+    capture launches directly so that the outer graph records it."""
+    import torch
+    from jlust_amd import block_sparse as bs
+    monkeypatch.setattr(bs, "USE_GRAPHS", True)
+    grid = mixed_grid(9)
+    BM = device_bsm(J, grid)
+    m, n = BM.shape
+    rng = np.random.default_rng(12)
+    y0 = dev(rng.uniform(-1, 1, m))
+    x1, x2 = torch.empty(n, dtype=torch.float64, device="cuda"), \
+        torch.empty(n, dtype=torch.float64, device="cuda")
+    y1, yr = torch.empty(m, dtype=torch.float64, device="cuda"), \
+        torch.empty(m, dtype=torch.float64, device="cuda")
+
+    def direct(x, alpha, beta):
+        monkeypatch.setattr(bs, "USE_GRAPHS", False)
+        yr.copy_(y0)
+        J.mul_(yr, BM, x, alpha, beta)
+        monkeypatch.setattr(bs, "USE_GRAPHS", True)
+        return host(yr).copy()
+
+    def check(x, alpha, beta, what):
+        x.uniform_(-1.0, 1.0)
+        y1.copy_(y0)
+        J.mul_(y1, BM, x, alpha, beta)
+        got = host(y1).copy()
+        np.testing.assert_array_equal(got, direct(x, alpha, beta), err_msg=what)
+
+    for call in range(4):
+        check(x1, 1.5, -0.5, f"call {call}")
+    asm = BM.assembled()
+    assert len(asm._graphs) == 1 and asm._last_graph is not None
+    A = BO.BSM(grid)
+    xs = host(x1).copy()
+    y1.copy_(y0)
+    J.mul_(y1, BM, x1, 1.5, -0.5)
+    assert_within(host(y1), 1.5 * A.matvec(xs) - 0.5 * host(y0),
+                  1.5 * abs_bound(A.dense(), xs) + 0.5 * np.abs(host(y0)), np.float64, "replayed")
+    for (i, j) in ((1, 1), (3, 4)):
+        b = grid[i - 1][j - 1]
+        b["val"] = rng.uniform(-1, 1, b["val"].size)
+        J.update_block_values_(BM, i, j, dev(b["val"]))
+        check(x1, 1.5, -0.5, f"after update of ({i},{j})")
+    assert len(asm._graphs) == 1
+    check(x2, 1.5, -0.5, "second x buffer")
+    check(x2, 1.5, -0.5, "second x buffer, replay")
+    check(x1, 1.0, 0.0, "other coefficients")
+    check(x1, 1.0, 0.0, "other coefficients, replay")
+    check(x1, 1.5, -0.5, "first key again")
+    assert len(asm._graphs) == 3
+
+    monkeypatch.setattr(bs, "GRAPH_CACHE", 3)
+    for a in (2.0, 3.0, 2.0, 4.0, 4.0):
+        check(x1, a, 0.25, f"alpha {a}")
+        assert len(asm._graphs) <= 3
+
+    # Inside an outer capture the product is recorded, not replayed.
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        J.mul_(y1, BM, x1, 1.5, -0.5)
+    for rep in range(3):
+        x1.uniform_(-1.0, 1.0)
+        y1.copy_(y0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(y1), direct(x1, 1.5, -0.5), err_msg=f"outer {rep}")
+
+
+def test_bbm_graph_replay(J, BO, monkeypatch):
+    """A block-banded product replays its capture too, and follows value
+    updates of its diagonal block matrix."""
+    import torch
+    from jlust_amd import block_sparse as bs
+    monkeypatch.setattr(bs, "USE_GRAPHS", True)
+    T = 5
+    grid = [[random_block(10, 6, 0.4, 21), random_block(10, 4, 0.4, 22, 1)]]
+    negR, R = random_block(3, 10, 0.3, 23), random_block(3, 10, 0.3, 24)
+    BM = device_bsm(J, grid)
+    MM = J.BlockBandedMatrix(BM, to_ust(J, negR), to_ust(J, R), T, 10, 3, 10)
+    x = torch.empty(T * 10, dtype=torch.float64, device="cuda")
+    y = torch.empty(MM.size(1), dtype=torch.float64, device="cuda")
+    rng = np.random.default_rng(25)
+    for call in range(4):
+        if call == 2:
+            grid[0][0]["val"] = rng.uniform(-1, 1, grid[0][0]["val"].size)
+            J.update_block_values_(BM, 1, 1, dev(grid[0][0]["val"]))
+        x.uniform_(-1.0, 1.0)
+        J.mul_(y, MM, x)
+        xs = host(x).copy()
+        M = BO.BBM(BO.BSM(grid), [(negR, R)], T, 10, [3], 10)
+        rowptr, colind, val = BO.assemble(*M.shape, list(M.placements()))
+        D = sp.csr_matrix((val, colind, rowptr), shape=M.shape)
+        assert_within(host(y), M.matvec(xs), abs(D) @ np.abs(xs), np.float64, f"BBM call {call}")
+    assert len(MM.assembled()._graphs) == 1
+
+
 def test_bbm_follows_bsm_updates(J, BO):
     import torch
     T = 3

@@ -86,3 +86,53 @@ def test_graph_plain_spmv_and_spmm(J):
     C = J.dense_matrix(m, k, dtype=torch.float32)
     C0 = torch.randn(k, m, device="cuda").t()
     check_replays(lambda: J.execute(J.SpMMOp, A, B, C, alpha=2.0, beta=0.5), B, C, C0)
+
+
+@pytest.mark.parametrize("kind", ["merge", "vector", "sliced"])
+def test_plan_capture_launch(J, kind, monkeypatch):
+    """jlust_hip_csr_spmv_plan_capture_* / spmv_graph_launch: each launch
+    equals execute(h, x, y) bit for bit with the inputs as they are at launch
+    (new x, y read through beta, new values stored in place); a launch onto a
+    stream that is itself being captured launches nothing and reports it."""
+    import torch
+    if kind == "vector":
+        m, n, lens = 20_000, 15_000, np.full(20_000, 10)
+    else:
+        m, n, lens = 20_000, 700_000, np.random.default_rng(7).integers(0, 80, 20_000)
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1" if kind == "sliced" else "0")
+    if kind == "merge":
+        monkeypatch.setenv("JLUST_HIP_SPMV_VECTOR", "0")
+    else:
+        monkeypatch.delenv("JLUST_HIP_SPMV_VECTOR", raising=False)
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=8)
+    v = dev(val)
+    A = J.csr_tensor(dev(rowptr), dev(colind), v, (m, n))
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    assert h.kernel() == kind
+    x = torch.empty(n, dtype=torch.float64, device="cuda")
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    ye = torch.empty(m, dtype=torch.float64, device="cuda")
+    y0 = dev(np.random.default_rng(9).uniform(-1, 1, m))
+    g = h.capture(x, y, alpha=-2.0, beta=0.75)
+    for rep in range(4):
+        x.uniform_(-1.0, 1.0)
+        if rep == 2:                        # new values in the same buffer
+            v.copy_(dev(np.random.default_rng(10).uniform(-1, 1, v.numel())))
+            J.update_values_(h, A)
+        y.copy_(y0)
+        assert g.launch()
+        ye.copy_(y0)
+        J.execute(h, x, ye, alpha=-2.0, beta=0.75)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(y), host(ye), err_msg=f"launch {rep}")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    outer = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(outer, stream=s):
+        launched = g.launch()
+    assert launched is False
+    with pytest.raises(J.IncompatibleExtents):
+        h.capture(x[:-1], y)
+    del g
+    torch.cuda.synchronize()
