@@ -137,12 +137,15 @@ def blocks_bench(steps, warmup):
     size.  Per operator: time per call with a sync after each (the
     reference's @belapsed(mul!; sync)), time per call when calls are queued
     back to back -- each with direct launches (the default) and with mul!'s
-    per-(y, x) graph cache -- the one-off assembly, effective GB/s of the assembled
+    per-(y, x) graph cache; the BlockBandedMatrix with its periodic kernel
+    (the default) and through the T-fold assembled CSR -- the one-off
+    assembly, effective GB/s of the assembled
     CSR's compulsory bytes, and scipy's CSR matvec of the same matrix on
     this host."""
     import torch
     import scipy.sparse as sps
     import jlust_amd as J
+    from jlust_amd import block_banded as BB
     from jlust_amd import block_sparse as BS
     from jlust_amd import workloads as W
     d = W.dcopf(**W.DCOPF_CASE30000)
@@ -190,6 +193,19 @@ def blocks_bench(steps, warmup):
         BS.USE_GRAPHS = True
         t_sync_g, t_async_g = per_call(True), per_call(False)
         BS.USE_GRAPHS = use
+        extra = {}
+        if A is MS:
+            # The block-banded product through the T-fold assembled CSR
+            # instead of the periodic kernel.
+            per = BB.USE_PERIODIC
+            BB.USE_PERIODIC = False
+            ts, ta = per_call(True), per_call(False)
+            BB.USE_PERIODIC = per
+            extra = {"periodic_kernel": per and A.periodic() is not None,
+                     "us_per_call_sync_assembled": round(ts * 1e6, 1),
+                     "us_per_call_queued_assembled": round(ta * 1e6, 1)}
+            log(f"{name}: assembled CSR instead of the periodic kernel: {ts*1e6:.1f} us/call synced, "
+                f"{ta*1e6:.1f} queued")
         # The same calls captured by the caller in one HIP graph (G calls per
         # graph) and replayed: the per-call launch cost without host dispatch.
         G = 20
@@ -233,7 +249,7 @@ def blocks_bench(steps, warmup):
                     "us_per_call_graph": round(t_graph * 1e6, 1),
                     "effective_GBps_sync": round(byts / t_sync / 1e9, 1),
                     "effective_GBps_queued": round(byts / t_async / 1e9, 1),
-                    "cpu_scipy_us": round(t_cpu * 1e6, 1), "max_rel_diff_vs_scipy": err})
+                    "cpu_scipy_us": round(t_cpu * 1e6, 1), "max_rel_diff_vs_scipy": err, **extra})
         log(f"{name}: {m}x{n} nnz {nz}: {t_sync*1e6:.1f} us/call synced, {t_async*1e6:.1f} queued "
             f"(graph per call {t_sync_g*1e6:.1f} / {t_async_g*1e6:.1f}), "
             f"{t_graph*1e6:.1f} in a caller's graph, "

@@ -454,6 +454,37 @@ int jlust_hip_csr_assemble(int64_t m, int64_t n, int32_t nplacements,
                            int64_t nnz, jlust_stream_t stream);
 
 /*
+ * y = alpha*M*x + beta*y for a T-period block-banded matrix M of bandwidth 1
+ * whose diagonal block D (n_diag_rows x n_cols) is shared by every period and
+ * whose coupling pair (neg, pos) (n_off_rows x n_cols each) is shared by
+ * every transition, without the T-fold matrix: the reference's periodic view
+ * and fused kernel (ext/CUDAExt/ops/block_mul.jl:584-676,
+ * ext/KernelAbstractionsExt/ops/block_periodic.jl:108-236).  Rows of period
+ * t: D's rows against x[t*n_cols ...], then (t < T-1) the coupling rows,
+ * neg's against x[t*n_cols ...] plus pos's against x[(t+1)*n_cols ...]
+ * (block_banded.jl:5-14); M is (T*n_diag_rows + (T-1)*n_off_rows) x
+ * T*n_cols.  Each block is a placement's CSR block (any origin) or its
+ * shifted diagonal (block == NULL; diag_m x diag_n, entries
+ * (i, i + diag_shift) = diag_val); row_off, col_off and slots are ignored.
+ * Other block formats return UNSUPPORTED_FORMAT.  neg and pos are read only
+ * when T > 1 and n_off_rows > 0.  Rows must fit in 32 bits.
+ */
+int jlust_hip_bbm_periodic_spmv_f64(int64_t T, int64_t n_diag_rows,
+                                    int64_t n_off_rows, int64_t n_cols,
+                                    const jlust_placement *diag,
+                                    const jlust_placement *neg,
+                                    const jlust_placement *pos, double alpha,
+                                    const double *x, double beta, double *y,
+                                    jlust_stream_t stream);
+int jlust_hip_bbm_periodic_spmv_f32(int64_t T, int64_t n_diag_rows,
+                                    int64_t n_off_rows, int64_t n_cols,
+                                    const jlust_placement *diag,
+                                    const jlust_placement *neg,
+                                    const jlust_placement *pos, float alpha,
+                                    const float *x, float beta, float *y,
+                                    jlust_stream_t stream);
+
+/*
  * dst[slots[k]] = src[k] for k < len (slots outside [0, dst_len) are
  * skipped): new values of one block into an assembled matrix, the compiled
  * view update of update_block_values! (ext/CUDAExt/ops/block_mul.jl:310-336).

@@ -66,6 +66,8 @@ SIGNATURES = {
     "jlust_hip_shift_index": (_INT, [_P, _P, _I64, _I32, _P]),
     "jlust_hip_csr_assemble": (_INT, [_I64, _I64, _I32, _P, _INT, _P, _P, _P, _I64, _P]),
     "jlust_hip_scatter_values": (_INT, [_P, _I64, _P, _P, _I64, _INT, _P]),
+    "jlust_hip_bbm_periodic_spmv_f64": (_INT, [_I64, _I64, _I64, _I64, _P, _P, _P, _D, _P, _D, _P, _P]),
+    "jlust_hip_bbm_periodic_spmv_f32": (_INT, [_I64, _I64, _I64, _I64, _P, _P, _P, _F, _P, _F, _P, _P]),
     "jlust_hip_shifted_diag_spmv_f64": (_INT, [_I64, _I64, _I64, _D, _D, _P, _D, _P, _P]),
     "jlust_hip_shifted_diag_spmv_f32": (_INT, [_I64, _I64, _I64, _F, _F, _P, _F, _P, _P]),
     "jlust_hip_apply_fn_f64": (_INT, [_I64, _I32, _D, _D, _P, _D, _D, _P, _P]),

@@ -13,23 +13,94 @@ block_banded.jl:129-137): the band-k coupling rows of period t exist only
 while t + k <= T, so the period stride shrinks over the last bw periods.
 Column block t of x holds period t's n_cols variables.
 
-The product runs as one SpMV over a CSR assembled once on the device from
-every placed block (the reference's _compile_bbm, ext/CUDAExt/ops/
-block_mul.jl:453-556, row for row the same arrays).  A diagonal that is a
-BlockSparseMatrix is placed block by block; its update_block_values_ is
-propagated into this matrix's assembled values through the slot maps.
-Blocks the assembly does not take fall back to the per-period products of
-the reference's generic execute(BBMSpMVOp) (block_banded.jl:79-122), with
-every period placed at d_starts.
+With bandwidth 1, one BlockSparseMatrix diagonal shared by every period and
+one (neg, pos) pair shared by every transition, each CSR or ShiftedDiag,
+the product is one launch of the periodic kernel
+(jlust_hip_bbm_periodic_spmv_*; the reference's periodic view,
+ext/CUDAExt/ops/block_mul.jl:584-676, block_periodic.jl:108-236): it walks
+the diagonal's own assembled CSR and the coupling blocks' buffers in place
+for every period, so the T-fold matrix is never built and a product moves
+little more than x and y.  It launches directly (the graph cache of the
+assembled path, block_sparse.USE_GRAPHS, does not apply).
+JLUST_HIP_BBM_PERIODIC=0 turns it off.
+
+Otherwise the product runs as one SpMV over a CSR assembled once on the
+device from every placed block (the reference's _compile_bbm,
+ext/CUDAExt/ops/block_mul.jl:453-556, row for row the same arrays).  A
+diagonal that is a BlockSparseMatrix is placed block by block; its
+update_block_values_ is propagated into this matrix's assembled values
+through the slot maps.  Blocks the assembly does not take fall back to the
+per-period products of the reference's generic execute(BBMSpMVOp)
+(block_banded.jl:79-122), with every period placed at d_starts.
 """
 from __future__ import annotations
 
+import ctypes
+import os
 from typing import List, Optional, Sequence
 
-from .block_sparse import (AssembledCSR, BlockSparseMatrix, BlockStructureError, _t,
-                           assemblable)
-from .errors import IncompatibleExtents, UnsupportedFormat
+import torch
+
+from . import _lib
+from .block_sparse import (AssembledCSR, BlockSparseMatrix, BlockStructureError, Placement, _t,
+                           _check_block_buffers, assemblable)
+from .convert import _descriptor
+from .errors import IncompatibleExtents, JLUSTError, UnsupportedFormat
+from .formats import is_shifted_diag
 from .tensor import USTensor
+
+# Periodic kernel for the shared-block bandwidth-1 case (module switch; the
+# environment sets its initial value).
+USE_PERIODIC = os.environ.get("JLUST_HIP_BBM_PERIODIC", "1") != "0"
+
+
+def _periodic_block(u: USTensor):
+    """The placement the periodic kernel reads for a coupling or diagonal
+    block: its CSR buffers in place, or its shifted diagonal."""
+    p = Placement()
+    if is_shifted_diag(u.format):
+        lv = u.format.levels[1]
+        p.diag_m, p.diag_n = u.extents
+        p.diag_shift, p.diag_val = lv.shift, lv.val
+        return p
+    _check_block_buffers(u)
+    d = _descriptor(u)
+    if d.format != 0:
+        raise UnsupportedFormat(u.format, "HIPBackend", "periodic blocks are CSR or ShiftedDiag")
+    p.block = ctypes.pointer(d)
+    return p
+
+
+class _PeriodicView:
+    """Arguments of jlust_hip_bbm_periodic_spmv_*: the diagonal matrix's own
+    assembled CSR (refreshed in place by its update_block_values_) and the
+    coupling pair as stored."""
+
+    def __init__(self, M: "BlockBandedMatrix"):
+        self.asm = M.diags.assembled()
+        neg, pos = M.off_diags[0]
+        self.blocks = (self.asm, neg, pos)              # keeps the buffers alive
+        self.pl = (_periodic_block(self.asm.asm), _periodic_block(neg), _periodic_block(pos))
+        self.refs = tuple(ctypes.byref(p) for p in self.pl)
+        self.args = (M.T, M.n_diag_rows, M.n_off_rows[0], M.n_cols)
+        self.m, self.n = M.shape
+        self.T, self.dev = M._T, self.asm.device
+        self.fn = getattr(_lib.lib(), "jlust_hip_bbm_periodic_spmv_" +
+                          ("f64" if self.T == torch.float64 else "f32"))
+
+    def plain(self, x, y) -> bool:
+        di = self.dev.index
+        return (x.dtype is self.T and y.dtype is self.T and x.get_device() == di and
+                y.get_device() == di and x.numel() == self.n and y.numel() == self.m and
+                x.is_contiguous() and y.is_contiguous())
+
+    def spmv(self, x, y, alpha, beta):
+        with _lib.on_device(self.dev):
+            st = self.fn(*self.args, *self.refs, alpha, x.data_ptr(), beta, y.data_ptr(),
+                         _lib.stream_handle(self.dev))
+        if st:
+            _lib.check(st, "bbm_periodic_spmv", "BlockBandedMatrix", "HIPBackend", self.T)
+        return y
 
 
 def diag_starts(n_diag_rows: int, n_off_rows: Sequence[int], T: int) -> List[int]:
@@ -97,6 +168,7 @@ class BlockBandedMatrix:
         self.n_diag_rows, self.n_off_rows, self.n_cols = n_diag_rows, n_off_rows, n_cols
         self._check()
         self._asm: Optional[AssembledCSR] = None
+        self._pv = None                                 # periodic view, False when not eligible
         self._assemblable = all(assemblable(b) for obj in self._matrices() for b in _all_blocks(obj))
         for obj in self._matrices():
             if isinstance(obj, BlockSparseMatrix):
@@ -232,6 +304,22 @@ class BlockBandedMatrix:
             self._asm = AssembledCSR(m, n, list(self.placements()), self._T, self._device())
         return self._asm
 
+    def periodic(self) -> Optional[_PeriodicView]:
+        """The periodic view when this matrix has one (bandwidth 1, one
+        BlockSparseMatrix diagonal, one shared (neg, pos) pair of CSR or
+        ShiftedDiag tensors; _bbm_supports_periodic, block_mul.jl:600-606)."""
+        if self._pv is None:
+            self._pv = False
+            od = self.off_diags[0] if self.bw == 1 else None
+            if (isinstance(self.diags, BlockSparseMatrix) and isinstance(od, tuple) and
+                    all(isinstance(b, USTensor) for b in od) and self.diags.assemblable()):
+                try:
+                    self._device()
+                    self._pv = _PeriodicView(self)
+                except JLUSTError:
+                    self._pv = False
+        return self._pv or None
+
     def _block_values_changed(self, bsm, ij, vals):
         if self._asm is not None:
             self._asm.update((id(bsm), ij), vals)
@@ -246,6 +334,10 @@ class BlockBandedMatrix:
         if x.dim() != 1 or y.dim() != 1 or x.numel() != n or y.numel() != m:
             raise IncompatibleExtents(
                 f"BBMSpMV: M is {m}x{n}, x has {tuple(x.shape)}, y has {tuple(y.shape)}")
+        if USE_PERIODIC:
+            pv = self.periodic()
+            if pv is not None and pv.plain(x, y):
+                return pv.spmv(x, y, float(alpha), float(beta))
         if self.assemblable():
             return self.assembled().spmv(x, y, alpha, beta)
         from .ops import mul_

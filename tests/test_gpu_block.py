@@ -343,6 +343,73 @@ def test_bbm_dcopf_bw1(J, BO, dtype):
     assert np.array_equal(host(J.nonzeros(asm)), val)
 
 
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("T", [1, 2, 7])
+def test_bbm_periodic(J, BO, monkeypatch, dtype, T):
+    """The periodic kernel (block_periodic.jl:108-236, periodic view
+    block_mul.jl:584-676): one BlockSparseMatrix diagonal (CSR of both
+    origins, DCSR, ShiftedDiag blocks) shared by every period, coupling pairs
+    of CSR (both origins) and ShiftedDiag blocks (shifts 0, 3, -2), against
+    the oracle's BBM product and the assembled-CSR path, with alpha and beta,
+    and after update_block_values! of the diagonal."""
+    import torch
+    from jlust_amd import block_banded as bb
+    monkeypatch.setattr(bb, "USE_PERIODIC", True)
+    grid = mixed_grid(4, dtype)
+    nd, nc, no = 72, 104, 5
+    sd = lambda shift, val: dict(format="ShiftedDiag", m=no, n=nc, shift=shift, val=val, dtype=dtype)
+    cases = [(random_block(no, nc, 0.2, 31, 0, dtype), random_block(no, nc, 0.2, 32, 1, dtype)),
+             (sd(3, -1.0), random_block(no, nc, 0.3, 33, 1, dtype, shuffle=True)),
+             (sd(0, -1.0), sd(-2, 2.5))]
+    rng = np.random.default_rng(34)
+    for ci, (neg, pos) in enumerate(cases):
+        BM = device_bsm(J, grid)
+        MM = J.BlockBandedMatrix(BM, to_ust(J, neg), to_ust(J, pos), T, nd, no, nc)
+        assert MM.periodic() is not None
+        for step in range(2):
+            if step == 1:
+                b = grid[0][0]
+                b["val"] = rng.uniform(-1, 1, b["val"].size).astype(dtype)
+                J.update_block_values_(BM, 1, 1, dev(b["val"]))
+            M = BO.BBM(BO.BSM(grid), [(neg, pos)], T, nd, [no], nc)
+            assert MM.size() == M.shape
+            rowptr, colind, val = BO.assemble(*M.shape, list(M.placements()))
+            D = abs(sp.csr_matrix((val.astype(np.float64), colind, rowptr), shape=M.shape))
+            xs = rng.uniform(-1, 1, M.shape[1]).astype(dtype)
+            y0 = rng.uniform(-1, 1, M.shape[0]).astype(dtype)
+            x64, y64 = xs.astype(np.float64), y0.astype(np.float64)
+            y = dev(y0)
+            J.mul_(y, MM, dev(xs), 1.5, -0.5)
+            what = f"case {ci} step {step}"
+            assert_within(host(y), 1.5 * M.matvec(x64) - 0.5 * y64,
+                          1.5 * (D @ np.abs(x64)) + 0.5 * np.abs(y64), dtype, what)
+            y = torch.empty(M.shape[0], dtype=MM.dtype, device="cuda")
+            J.mul_(y, MM, dev(xs))
+            got = host(y).copy()
+            assert_within(got, M.matvec(x64), D @ np.abs(x64), dtype, what + " beta 0")
+            monkeypatch.setattr(bb, "USE_PERIODIC", False)
+            J.mul_(y, MM, dev(xs))
+            monkeypatch.setattr(bb, "USE_PERIODIC", True)
+            assert_within(got, host(y).astype(np.float64), D @ np.abs(x64), dtype, what + " vs assembled")
+
+
+def test_bbm_periodic_eligibility(J):
+    """The periodic view exists only for bandwidth 1 with a BlockSparseMatrix
+    diagonal and one shared (neg, pos) pair of CSR or ShiftedDiag tensors
+    (_bbm_supports_periodic, block_mul.jl:600-606)."""
+    T, nd, no, nc = 3, 10, 3, 10
+    grid = [[random_block(nd, 6, 0.4, 41), random_block(nd, 4, 0.4, 42, 1)]]
+    neg, pos = random_block(no, nc, 0.3, 43), random_block(no, nc, 0.3, 44)
+    BM = device_bsm(J, grid)
+    assert J.BlockBandedMatrix(BM, to_ust(J, neg), to_ust(J, pos), T, nd, no, nc).periodic() is not None
+    D = to_ust(J, random_block(nd, nc, 0.3, 45))
+    assert J.BlockBandedMatrix(D, to_ust(J, neg), to_ust(J, pos), T, nd, no, nc).periodic() is None
+    coo = to_ust(J, random_block(no, nc, 0.3, 46, fmt="COO"))
+    assert J.BlockBandedMatrix(BM, coo, to_ust(J, pos), T, nd, no, nc).periodic() is None
+    pairs = [(to_ust(J, neg), to_ust(J, pos))] * (T - 1)
+    assert J.BlockBandedMatrix(BM, [pairs], T, 1, nd, [no], nc).periodic() is None
+
+
 def test_bbm_bw2_time_varying(J, BO):
     import torch
     T, nd, n1, n2, nc = 5, 12, 4, 3, 10
@@ -444,11 +511,14 @@ def test_bsm_graph_replay(J, BO, monkeypatch):
 
 
 def test_bbm_graph_replay(J, BO, monkeypatch):
-    """A block-banded product replays its capture too, and follows value
-    updates of its diagonal block matrix."""
+    """A block-banded product through the assembled CSR replays its capture
+    too, and follows value updates of its diagonal block matrix (the periodic
+    kernel, this matrix's default, launches directly)."""
     import torch
+    from jlust_amd import block_banded as bb
     from jlust_amd import block_sparse as bs
     monkeypatch.setattr(bs, "USE_GRAPHS", True)
+    monkeypatch.setattr(bb, "USE_PERIODIC", False)
     T = 5
     grid = [[random_block(10, 6, 0.4, 21), random_block(10, 4, 0.4, 22, 1)]]
     negR, R = random_block(3, 10, 0.3, 23), random_block(3, 10, 0.3, 24)
