@@ -80,3 +80,39 @@ def test_status_mapping_to_reference_exceptions():
         with pytest.raises(exc):
             _lib.check(code, "test")
     _lib.check(0, "ok")
+
+
+def test_bbm_periodic_argument_checks():
+    """jlust_hip_bbm_periodic_spmv_*: sizes, block extents and block formats
+    are checked on the host before anything reaches the device (the host
+    addresses below stand in for device buffers and are never read)."""
+    from jlust_amd import _lib
+    from jlust_amd.block_sparse import Placement
+    from jlust_amd.convert import Sparse
+    L = _lib.lib()
+    buf = np.zeros(64, np.int64)
+    p = buf.ctypes.data
+
+    def csr(m, n, fmt=0):
+        s = Sparse(format=fmt, origin=0, m=m, n=n, nnz=4, pos1=p, crd1=p, pos2=p, crd2=p, val=p)
+        return Placement(block=ctypes.pointer(s))
+
+    def sd(m, n):
+        return Placement(diag_m=m, diag_n=n, diag_shift=0, diag_val=1.0)
+
+    def call(T, nd, no, nc, d, neg, pos):
+        return L.jlust_hip_bbm_periodic_spmv_f64(T, nd, no, nc, ctypes.byref(d), ctypes.byref(neg),
+                                                 ctypes.byref(pos), 1.0, p, 0.0, p, None)
+
+    assert call(0, 4, 2, 5, csr(4, 5), sd(2, 5), sd(2, 5)) == 1            # T < 1
+    assert call(3, 2 ** 31, 2, 5, csr(4, 5), sd(2, 5), sd(2, 5)) == 1      # rows beyond 32 bits
+    assert "32-bit" in _lib.last_error()
+    assert call(3, 4, 2, 5, csr(4, 6), sd(2, 5), sd(2, 5)) == 1            # diagonal extents
+    assert "diagonal block is 4 x 6" in _lib.last_error()
+    assert call(3, 4, 2, 5, csr(4, 5), sd(3, 5), sd(2, 5)) == 1            # neg extents
+    assert call(3, 4, 2, 5, csr(4, 5), sd(2, 5), csr(2, 4)) == 1           # pos extents
+    assert call(3, 4, 2, 5, csr(4, 5, fmt=2), sd(2, 5), sd(2, 5)) == 3     # COO diagonal
+    assert call(3, 4, 2, 5, csr(4, 5), csr(2, 5, fmt=3), sd(2, 5)) == 3    # DCSR coupling
+    assert "CSR or a shifted diagonal" in _lib.last_error()
+    with pytest.raises(TypeError):
+        L.jlust_hip_bbm_periodic_spmv_f64(3, 4, 2, 5)                      # arity from the header
