@@ -108,3 +108,41 @@ def test_empty_and_errors(J):
         J.prepare(J.HIPBackend(), J.SpMVOp, bad)
     with pytest.raises(J.UnsupportedFormat, match="output_fn"):
         J.prepare(J.HIPBackend(), J.SpMVOp, A, output_fn=J.abs_fn)
+
+
+@pytest.mark.parametrize("sliced", [False, True])
+def test_coo_plan_capture(J, O, monkeypatch, sliced):
+    """A COO plan recorded as a HIP graph (jlust_hip_csr_spmv_plan_capture_*)
+    and launched: each launch equals execute(h, x, y) bit for bit, also after
+    update_values! (new values in caller order, scattered into the plan's own
+    row-ordered copy, which the graph reads), and matches the oracle."""
+    import torch
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1" if sliced else "0")
+    m, n, nnz = 20_000, (640_000 if sliced else 30_000), 160_000
+    rows, cols, val = random_coo(m, n, nnz, 12, 1, np.float64)
+    A = J.coo_tensor(dev(rows), dev(cols), dev(val), (m, n))
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    assert (h.kernel() == "sliced") == sliced
+    x = torch.empty(n, dtype=torch.float64, device="cuda")
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    ye = torch.empty(m, dtype=torch.float64, device="cuda")
+    y0 = np.random.default_rng(13).uniform(-1, 1, m)
+    g = h.capture(x, y, alpha=1.25, beta=-1.0)
+    for rep in range(3):
+        if rep == 2:
+            val = -0.5 * val
+            J.update_values_(h, J.coo_tensor(dev(rows), dev(cols), dev(val), (m, n)))
+        xs = np.random.default_rng(20 + rep).uniform(-1, 1, n)
+        x.copy_(torch.from_numpy(xs))
+        y.copy_(torch.from_numpy(y0))
+        assert g.launch()
+        ye.copy_(torch.from_numpy(y0))
+        J.execute(h, x, ye, alpha=1.25, beta=-1.0)
+        torch.cuda.synchronize()
+        got = host(y).copy()
+        np.testing.assert_array_equal(got, host(ye), err_msg=f"launch {rep}")
+        ref = 1.25 * O.coo_spmv(rows, cols, val, xs, m) - y0
+        assert_within(got, ref, absref(rows, cols, val, xs, m, 1.25, -1.0, y0, 1), np.float64,
+                      f"captured COO plan, launch {rep}")
+    del g
+    torch.cuda.synchronize()
