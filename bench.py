@@ -574,7 +574,9 @@ def build_step(cfg, use_plan=False):
             h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
             torch.cuda.synchronize()
             h.build_ms = (time.perf_counter() - t0) * 1e3
-            return (lambda: J.execute(h, x, y)), f"csr_spmv_{h.kernel()}_kernel", "hbm", (A, x, y, h)
+            kname = ("binned_slice_kernel + binned_bin_kernel" if h.kernel() == "binned"
+                     else f"csr_spmv_{h.kernel()}_kernel")
+            return (lambda: J.execute(h, x, y)), kname, "hbm", (A, x, y, h)
         return (lambda: J.execute(J.SpMVOp, A, x, y)), "csr_spmv_merge_kernel", "hbm", (A, x, y)
     if kind == "csr_spmm":
         A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (m, n))

@@ -169,11 +169,13 @@ int jlust_hip_spmv_graph_destroy(jlust_spmv_graph_t graph);
 
 /* The kernel a plan runs (no counterpart in the reference; for diagnostics
  * and benchmarks): merge-path tiles, the vector kernel for short even rows
- * (*lanes_per_row lanes per row), or XCD column slices. */
+ * (*lanes_per_row lanes per row), XCD column slices, or the LDS-binned
+ * two-pass layout (x slices and y bins held in LDS). */
 enum jlust_spmv_kernel {
     JLUST_SPMV_MERGE = 0,
     JLUST_SPMV_VECTOR = 1,
-    JLUST_SPMV_SLICED = 2
+    JLUST_SPMV_SLICED = 2,
+    JLUST_SPMV_BINNED = 3
 };
 int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *kernel,
                                  int32_t *lanes_per_row);

@@ -28,7 +28,7 @@ PROBE_LIB = os.path.join(HERE, "libjlust_probe.so")
 
 HIP_SOURCES = ["capi.hip", "scan.hip", "spmv.hip", "coo_spmv.hip", "spmm.hip", "sddmm.hip",
                "bsr_spmm.hip", "convert.hip", "assemble.hip", "fn.hip", "dcsr.hip", "coo_plan.hip",
-               "periodic.hip"]
+               "periodic.hip", "spmv_binned.hip"]
 
 ARCH = os.environ.get("JLUST_HIP_ARCH", "gfx950")
 

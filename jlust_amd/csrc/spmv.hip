@@ -38,6 +38,8 @@
 #include <cstring>
 
 #include "common.hpp"
+#include "spmv_binned.hpp"
+#include "wave.hpp"
 
 namespace jlust {
 namespace {
@@ -87,50 +89,6 @@ __device__ int64_t wave_merge_search(const int32_t *__restrict__ rowptr, int64_t
         hi = new_hi;
     }
     return lo;
-}
-
-// ---- wave64 DPP (GFX9 controls): row_shr:n = 0x110+n, row_bcast:15 = 0x142,
-// row_bcast:31 = 0x143, wave_shr:1 = 0x138.  Lanes without a source keep `old`.
-template <int CTRL, int ROW_MASK>
-__device__ __forceinline__ int32_t dpp_i32(int32_t old, int32_t v)
-{
-    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
-}
-
-template <int CTRL, int ROW_MASK, typename T>
-__device__ __forceinline__ T dpp_val(T old, T v)
-{
-    if constexpr (sizeof(T) == 4) {
-        return __builtin_bit_cast(T, dpp_i32<CTRL, ROW_MASK>(__builtin_bit_cast(int32_t, old),
-                                                             __builtin_bit_cast(int32_t, v)));
-    } else {
-        const uint64_t o = __builtin_bit_cast(uint64_t, old), x = __builtin_bit_cast(uint64_t, v);
-        const uint32_t lo = (uint32_t)dpp_i32<CTRL, ROW_MASK>((int32_t)o, (int32_t)x);
-        const uint32_t hi = (uint32_t)dpp_i32<CTRL, ROW_MASK>((int32_t)(o >> 32), (int32_t)(x >> 32));
-        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
-    }
-}
-
-template <int CTRL, int ROW_MASK, typename T>
-__device__ __forceinline__ void seg_scan_step(int32_t key, T &v)
-{
-    const int32_t k2 = dpp_i32<CTRL, ROW_MASK>(-1, key);
-    const T v2 = dpp_val<CTRL, ROW_MASK>(T(0), v);
-    if (k2 == key) v += v2;
-}
-
-// Inclusive scan of v over the wave in lane order, segmented by key (keys are
-// non-decreasing with the lane and never -1).
-template <typename T>
-__device__ __forceinline__ T wave_seg_scan(int32_t key, T v)
-{
-    seg_scan_step<0x111, 0xf>(key, v);
-    seg_scan_step<0x112, 0xf>(key, v);
-    seg_scan_step<0x114, 0xf>(key, v);
-    seg_scan_step<0x118, 0xf>(key, v);
-    seg_scan_step<0x142, 0xa>(key, v);
-    seg_scan_step<0x143, 0xc>(key, v);
-    return v;
 }
 
 // One block's share [dbeg, dend) of the merge path of a CSR matrix whose row
@@ -1059,6 +1017,14 @@ int want_slices(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t
     return JLUST_STATUS_SUCCESS;
 }
 
+// The LDS-binned layout: JLUST_HIP_SPMV_SLICE=2 asks for it where it fits.
+bool want_binned(int value_type, int64_t m, int64_t n, int64_t nnz)
+{
+    const char *e = getenv("JLUST_HIP_SPMV_SLICE");
+    if (!(e && e[0] == '2')) return false;
+    return binned_fits(value_type, m, n, nnz);
+}
+
 }  // namespace
 }  // namespace jlust
 
@@ -1097,6 +1063,8 @@ struct jlust_spmv_plan {
     void *coo_mem = nullptr;
     const int32_t *coo_perm = nullptr;
     void *coo_val = nullptr;
+    // LDS-binned layout (spmv_binned.hip), or null.
+    jlust::BinnedLayout *binned = nullptr;
 };
 
 namespace jlust {
@@ -1228,6 +1196,16 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
         delete p;
         return st;
     }
+    if (want_binned(value_type, m, n, nnz)) {
+        p->sliced = false;
+        st = binned_build(&p->binned, value_type, m, n, nnz, origin, rowptr, colind, val, s);
+        if (st) {
+            delete p;
+            return st;
+        }
+        *plan_out = p;
+        return JLUST_STATUS_SUCCESS;
+    }
     if (!p->sliced) {
         if (m > 0) {
             st = value_type == 0 ? spmv_grid<double>(m, nnz, p->ipt, &p->grid)
@@ -1311,6 +1289,12 @@ extern "C" int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan, con
         val = plan->coo_val;
     }
     plan->val = val;
+    if (plan->binned) {
+        // Same protocol as the sliced copy below.
+        JLUST_HIP_TRY(hipDeviceSynchronize());
+        if (int st = binned_update(plan->binned, val, 0)) return st;
+        JLUST_HIP_TRY(hipDeviceSynchronize());
+    }
     if (plan->sliced && plan->nnz > 0) {
         // The plan's slice-major copy of the values is refreshed in stream order
         // on the null stream, then waited for, so the caller's next execute on
@@ -1378,6 +1362,12 @@ static int plan_execute(jlust_spmv_plan_t plan, int want_type, T alpha, const T 
                     "spmv_plan_execute: plan belongs to device %d, current device is %d",
                     plan->device, dev);
     hipStream_t s = (hipStream_t)stream;
+    if (plan->binned) {
+        if constexpr (sizeof(T) == 8)
+            return binned_execute_f64(plan->binned, alpha, x, beta, y, s);
+        else
+            return binned_execute_f32(plan->binned, alpha, x, beta, y, s);
+    }
     if (!plan->sliced && plan->vec_lpr > 0)
         return vector_launch<T>(plan, plan->vec_lpr, alpha, x, beta, y, s);
     if (!plan->sliced)
@@ -1530,7 +1520,9 @@ extern "C" int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *ker
 {
     clear_error();
     if (!plan || !kernel) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_info: null argument");
-    *kernel = plan->sliced ? JLUST_SPMV_SLICED : plan->vec_lpr > 0 ? JLUST_SPMV_VECTOR : JLUST_SPMV_MERGE;
+    *kernel = plan->binned ? JLUST_SPMV_BINNED
+              : plan->sliced ? JLUST_SPMV_SLICED
+              : plan->vec_lpr > 0 ? JLUST_SPMV_VECTOR : JLUST_SPMV_MERGE;
     if (lanes_per_row) *lanes_per_row = plan->vec_lpr;
     return JLUST_STATUS_SUCCESS;
 }
@@ -1539,8 +1531,9 @@ extern "C" int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan)
 {
     clear_error();
     if (!plan) return JLUST_STATUS_SUCCESS;
-    hipError_t e = hipFree(plan->mem);
+    hipError_t e = plan->mem ? hipFree(plan->mem) : hipSuccess;
     hipError_t e2 = plan->coo_mem ? hipFree(plan->coo_mem) : hipSuccess;
+    binned_destroy(plan->binned);
     if (e == hipSuccess) e = e2;
     delete plan;
     if (e != hipSuccess) return hip_fail(e, "hipFree(plan)");

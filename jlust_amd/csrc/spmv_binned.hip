@@ -1,0 +1,558 @@
+// spmv_binned.hip -- CSR SpMV through an LDS-binned layout, for prepared plans
+// whose x is far larger than an XCD's L2 and whose columns are scattered.
+//
+// The per-row arithmetic is that of the reference's CSR SpMV,
+// y[i] = alpha * sum_k val[k] * x[col[k]] (+ beta * y[i])
+// (ext/KernelAbstractionsExt/ops/spmv.jl:154-169, _walker.jl:123-132); only the
+// association of the row sum differs: it is summed per column slice, and the
+// slice sums are added in slice order (deterministic run to run).
+//
+// Why: a random 8-byte gather of x from HBM or the MALL costs a whole line and
+// queues on the L1/L2 miss capacity; even x cut into eight 4 MB slices, one per
+// XCD L2, gathers at only ~190 G/s.  Here no gather ever leaves a CU's LDS:
+//
+//   slice pass (one workgroup per column slice c of W columns, W*sizeof(T) =
+//   128 KB of LDS): x[cW, (c+1)W) is copied into LDS; the slice's entries,
+//   stored slice-major and inside a slice in (row bin, row, k) order, are
+//   streamed once (value + 16-bit local column), multiplied by their x from LDS
+//   and summed per row with a wave64 segmented scan.  Each (row, slice) pair
+//   with entries yields one partial sum, written contiguously.
+//
+//   bin pass (one workgroup per bin b of H rows, H*sizeof(T) = 128 KB of
+//   LDS): the partials of bin b come in S runs, one per slice, each run sorted
+//   by row with every row at most once.  Runs are added into an LDS copy of
+//   y[bH, (b+1)H) in slice order, a workgroup barrier between runs (so no two
+//   adds to one row ever race), and y is written once.
+//
+// HBM bytes per entry: value + 2-byte column, then a partial (written, read)
+// and its 2-byte row: about 28 B for fp64 against 12 B + a 128-byte line per
+// missed gather for the plain layout.  The partial of a (row, slice) pair with
+// several entries covers all of them, so long rows cost less.
+//
+// Layout build (once per plan, on the device): row of each entry by a prefix
+// count of row starts, key = slice * B + bin, a stable radix sort of the keys
+// (entry order inside a run stays the CSR order), the "last entry of a partial"
+// flags, their prefix count (= partial indices), run and chunk boundaries.
+#include <algorithm>
+
+#include <rocprim/device/device_radix_sort.hpp>
+
+#include "spmv_binned.hpp"
+#include "wave.hpp"
+
+namespace jlust {
+namespace {
+
+constexpr int BN_THREADS = 1024;
+constexpr int BN_WAVES = BN_THREADS / 64;
+constexpr int BN_LDS = 128 * 1024;       // x slice / y bin in LDS
+constexpr int BN_SMAX = 1024;            // slices (the bin pass keeps two run bounds per slice in LDS)
+constexpr int64_t BN_MAX_RUNS = (int64_t)1 << 22;
+constexpr uint32_t BN_END = 0x8000u;     // scol flag: last entry of its partial
+constexpr uint32_t BN_COL = 0x7fffu;
+
+int64_t round_up(int64_t v, int64_t a) { return (v + a - 1) / a * a; }
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Slice width / bin height: about one slice and one bin per CU, at most
+// BN_LDS bytes of x or y each.
+bool geometry(int value_type, int64_t m, int64_t n, int64_t nnz, int cu, int32_t *W, int32_t *S,
+              int32_t *G, int32_t *H, int32_t *B)
+{
+    if (m <= 0 || n <= 0 || nnz <= 0 || nnz > (int64_t)INT32_MAX - 4096) return false;
+    if (cu < 1) cu = 1;
+    const int64_t tsz = value_type == 0 ? 8 : 4;
+    const int64_t wmax = BN_LDS / tsz;    // <= 32768: the column fits 15 bits
+    const int64_t w = std::min(wmax, round_up((n + cu - 1) / cu, 64));
+    const int64_t s = (n + w - 1) / w;
+    const int64_t h = std::min(wmax, round_up((m + cu - 1) / cu, 64));
+    const int64_t b = (m + h - 1) / h;
+    if (s > BN_SMAX || s * b > BN_MAX_RUNS) return false;
+    *W = (int32_t)w;
+    *S = (int32_t)s;
+    *G = (int32_t)std::max<int64_t>(1, cu / s);
+    *H = (int32_t)h;
+    *B = (int32_t)b;
+    return true;
+}
+
+template <typename T>
+__device__ __forceinline__ T readlane63(T v)
+{
+    if constexpr (sizeof(T) == 4) {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(int32_t, v), 63));
+    } else {
+        const uint64_t u = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int32_t)u, 63);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int32_t)(u >> 32), 63);
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    }
+}
+
+// ---- slice pass.  Workgroup g of slice c = blockIdx / G; wave w streams chunk
+// c*nch + g*BN_WAVES + w, a run of whole partials [cst[q], cst[q+1]) whose
+// first partial is cpi[q].
+template <typename T>
+__global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
+    int64_t n, int32_t W, int32_t G, int32_t nch, const T *__restrict__ sval,
+    const uint16_t *__restrict__ scol, const int32_t *__restrict__ cst,
+    const int32_t *__restrict__ cpi, const T *__restrict__ x, T *__restrict__ pval)
+{
+    constexpr int XMAX = BN_LDS / sizeof(T);
+    constexpr int XPT = XMAX / BN_THREADS;
+    __shared__ T xs[XMAX];
+    const int c = blockIdx.x / G;
+    const int g = blockIdx.x % G;
+    const int64_t c0 = (int64_t)c * W;
+    const int wn = (int)min((int64_t)W, n - c0);     // >= 1: slice c starts inside x
+    {
+        T t[XPT];
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) t[u] = x[c0 + min((int)threadIdx.x + u * BN_THREADS, wn - 1)];
+#pragma unroll
+        for (int u = 0; u < XPT; ++u) {
+            const int j = threadIdx.x + u * BN_THREADS;
+            if (j < wn) xs[j] = t[u];
+        }
+    }
+    __syncthreads();
+
+    const int lane = threadIdx.x & 63;
+    // Wave-uniform (scalar) chunk bounds: the stream loop is then scalar
+    // control flow and the two load buffers stay apart.
+    const int q = __builtin_amdgcn_readfirstlane(c * nch + g * BN_WAVES + (int)(threadIdx.x >> 6));
+    const int32_t ea = cst[q], eb = cst[q + 1];
+    if (ea >= eb) return;
+    int32_t pk = cpi[q];
+    T carry = T(0);
+
+    constexpr int U = 4;            // steps of 64 entries per load group
+    constexpr int GS = U * 64;
+    T va[U], vb[U];
+    uint32_t ka[U], kb[U];
+    // Loads are clamped into the chunk, never predicated: a load under an
+    // exec-masked branch makes the compiler wait for every outstanding one.
+    auto load = [&](T(&v)[U], uint32_t(&k)[U], int32_t e) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t p = (uint32_t)min(e + u * 64 + lane, eb - 1);
+            v[u] = sval[p];
+            k[u] = scol[p];
+        }
+    };
+    auto process = [&](const T(&v)[U], const uint32_t(&k)[U], int32_t e) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int32_t eu = e + u * 64;
+            if (eu >= eb) break;
+            const bool ok = eu + lane < eb;
+            const uint32_t kk = k[u];
+            T p = v[u] * xs[kk & BN_COL];
+            p = ok ? p : T(0);
+            const bool endf = ok && (kk & BN_END);
+            const uint64_t mask = __ballot(endf);
+            // Partials ended by earlier lanes of this step: this lane's segment.
+            const int32_t seg = (int32_t)__builtin_amdgcn_mbcnt_hi(
+                (uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
+            T sum = wave_seg_scan<T>(seg, p);
+            if (seg == 0) sum += carry;
+            if (endf) pval[pk + seg] = sum;
+            const T last = readlane63(sum);
+            carry = (mask >> 63) ? T(0) : last;
+            pk += (int32_t)__popcll(mask);
+        }
+    };
+    int32_t e = ea;
+    load(va, ka, e);
+    for (;;) {
+        load(vb, kb, e + GS);
+        process(va, ka, e);
+        e += GS;
+        if (e >= eb) break;
+        load(va, ka, e + GS);
+        process(vb, kb, e);
+        e += GS;
+        if (e >= eb) break;
+    }
+}
+
+// ---- bin pass.  Workgroup b adds the runs of bin b, slice by slice, into
+// ys = y[bH, bH + hn) and writes y.  Each thread takes K slots of a run; the
+// slots of the next D runs are loaded ahead in registers.
+template <typename T, bool BZ>
+__global__ __launch_bounds__(BN_THREADS) void binned_bin_kernel(
+    int64_t m, int32_t S, int32_t B, int32_t H, const int32_t *__restrict__ pr,
+    const uint16_t *__restrict__ prow, const T *__restrict__ pval, T alpha, T beta,
+    T *__restrict__ y)
+{
+    constexpr int YMAX = BN_LDS / sizeof(T);
+    constexpr int D = 8, K = 2;
+    __shared__ T ys[YMAX];
+    __shared__ int32_t rs[2 * BN_SMAX];
+    const int b = blockIdx.x;
+    const int t = threadIdx.x;
+    const int64_t r0 = (int64_t)b * H;
+    const int hn = (int)min((int64_t)H, m - r0);
+    for (int j = t; j < hn; j += BN_THREADS) ys[j] = T(0);
+    for (int c = t; c < S; c += BN_THREADS) {
+        rs[2 * c] = pr[(int64_t)c * B + b];
+        rs[2 * c + 1] = pr[(int64_t)c * B + b + 1];
+    }
+    __syncthreads();
+
+    // Ring of the next D runs' slots: slot d holds run c with c % D == d.  A
+    // slot is consumed before it is reloaded, and loaded values are not touched
+    // before their use (flags apart), so waits only ever reach the oldest run.
+    T pv[D][K];
+    uint32_t pw[D][K];
+    bool pok[D][K];
+    auto load = [&](int c, int d) {
+        const int cc = c < S ? c : S - 1;
+        const int32_t lo = rs[2 * cc];
+        const int32_t hi = c < S ? rs[2 * cc + 1] : lo;
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int32_t a = lo + t + k * BN_THREADS;
+            pok[d][k] = a < hi;
+            // pval/prow hold P + 1 elements, so a run start is always readable.
+            const uint32_t p = (uint32_t)(a < hi ? a : lo);
+            pv[d][k] = pval[p];
+            pw[d][k] = prow[p];
+        }
+    };
+    auto consume = [&](int c, int d) {
+#pragma unroll
+        for (int k = 0; k < K; ++k)
+            if (pok[d][k]) ys[pw[d][k]] += pv[d][k];
+        // Runs longer than K * BN_THREADS (rows of the bin with entries in this
+        // slice): the rest, unpipelined.
+        const int32_t hi = rs[2 * c + 1];
+        for (int32_t a = rs[2 * c] + t + K * BN_THREADS; a < hi; a += BN_THREADS)
+            ys[prow[a]] += pval[a];
+    };
+#pragma unroll
+    for (int d = 0; d < D; ++d) load(d, d);
+    int c0 = 0;
+    for (; c0 + D <= S; c0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+            consume(c0 + d, d);
+            load(c0 + d + D, d);
+            __syncthreads();
+        }
+    }
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+        if (c0 + d < S) {
+            consume(c0 + d, d);
+            __syncthreads();
+        }
+    }
+    for (int j = t; j < hn; j += BN_THREADS) {
+        const T r = alpha * ys[j];
+        y[r0 + j] = BZ ? r : r + beta * y[r0 + j];
+    }
+}
+
+// ---- layout build
+
+// cnt[rowptr[i] - origin] += 1 for i in [1, m): after an exclusive scan over
+// nnz + 1 counts, cnt[k + 1] is the row of entry k (rows are counted, so a
+// malformed rowptr still gives rows in [0, m) in non-decreasing order).
+__global__ void bn_rowmark_kernel(int64_t m, int64_t nnz, int32_t origin,
+                                  const int32_t *__restrict__ rowptr, int32_t *__restrict__ cnt)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x + 1;
+    if (i >= m) return;
+    int64_t v = (int64_t)rowptr[i] - origin;
+    v = v < 0 ? 0 : (v > nnz ? nnz : v);
+    atomicAdd(&cnt[v], 1);
+}
+
+__device__ __forceinline__ int32_t bn_row(const int32_t *erow, int64_t k, int64_t m)
+{
+    const int32_t r = erow[k];
+    return r < 0 ? 0 : (r >= m ? (int32_t)(m - 1) : r);
+}
+
+__global__ void bn_key_kernel(int64_t nnz, int64_t m, int32_t origin, const int32_t *__restrict__ colind,
+                              const int32_t *__restrict__ erow, int32_t W, int32_t S, int32_t H,
+                              int32_t B, uint32_t *__restrict__ key, int32_t *__restrict__ iota)
+{
+    const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (k >= nnz) return;
+    int64_t c = ((int64_t)colind[k] - origin) / W;
+    c = c < 0 ? 0 : (c >= S ? S - 1 : c);
+    const int32_t b = bn_row(erow, k, m) / H;
+    key[k] = (uint32_t)(c * B + b);
+    iota[k] = (int32_t)k;
+}
+
+// Per sorted entry e: value, local column, and whether it ends its partial
+// (the next entry is in another run or another row).  flag[nnz] = 0.
+template <typename T>
+__global__ void bn_fill_kernel(int64_t nnz, int64_t m, int32_t origin, const int32_t *__restrict__ colind,
+                               const T *__restrict__ val, const int32_t *__restrict__ erow, int32_t W,
+                               int32_t B, const uint32_t *__restrict__ skey,
+                               const int32_t *__restrict__ perm, T *__restrict__ sval,
+                               uint16_t *__restrict__ scol, int32_t *__restrict__ flag)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e > nnz) return;
+    if (e == nnz) {
+        flag[e] = 0;
+        return;
+    }
+    const int32_t k = perm[e];
+    const uint32_t key = skey[e];
+    bool last = e == nnz - 1;
+    if (!last) last = skey[e + 1] != key || bn_row(erow, perm[e + 1], m) != bn_row(erow, k, m);
+    const int64_t c = key / (uint32_t)B;
+    int64_t lc = (int64_t)colind[k] - origin - c * W;
+    lc = lc < 0 ? 0 : (lc >= W ? W - 1 : lc);
+    scol[e] = (uint16_t)(lc | (last ? BN_END : 0u));
+    sval[e] = val[k];
+    flag[e] = last ? 1 : 0;
+}
+
+// prow[partial] = bin-local row, for the entry that ends each partial.
+__global__ void bn_prow_kernel(int64_t nnz, int64_t m, const int32_t *__restrict__ erow, int32_t H,
+                               int32_t B, const uint32_t *__restrict__ skey,
+                               const int32_t *__restrict__ perm, const uint16_t *__restrict__ scol,
+                               const int32_t *__restrict__ fpre, uint16_t *__restrict__ prow)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nnz || !(scol[e] & BN_END)) return;
+    const int32_t b = (int32_t)(skey[e] % (uint32_t)B);
+    prow[fpre[e]] = (uint16_t)(bn_row(erow, perm[e], m) - b * H);
+}
+
+// Run bounds from the sorted keys: est[r] = first entry with key >= r and
+// pr[r] = its partial index, for r in [0, R]; every r is written once.
+__global__ void bn_runs_kernel(int64_t nnz, int64_t R, const uint32_t *__restrict__ skey,
+                               const int32_t *__restrict__ fpre, int32_t *__restrict__ est,
+                               int32_t *__restrict__ pr)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e > nnz) return;
+    const int64_t prev = e == 0 ? -1 : (int64_t)skey[e - 1];
+    const int64_t cur = e == nnz ? R : (int64_t)skey[e];
+    for (int64_t r = prev + 1; r <= cur; ++r) {
+        est[r] = (int32_t)e;
+        pr[r] = fpre[e];
+    }
+}
+
+// Chunk q = c*nch + w of slice c starts at the first partial start at or after
+// the slice's entries split evenly nch ways.
+__global__ void bn_chunk_kernel(int64_t nnz, int32_t S, int32_t B, int32_t nch,
+                                const int32_t *__restrict__ est, const int32_t *__restrict__ fpre,
+                                int32_t *__restrict__ cst, int32_t *__restrict__ cpi)
+{
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q == (int64_t)S * nch) cst[q] = (int32_t)nnz;
+    if (q >= (int64_t)S * nch) return;
+    const int64_t c = q / nch, w = q % nch;
+    const int64_t s0 = est[c * B], s1 = est[(c + 1) * B];
+    int64_t e = s0 + (s1 - s0) * w / nch;
+    while (e > s0 && e < s1 && fpre[e] == fpre[e - 1]) ++e;
+    cst[q] = (int32_t)e;
+    cpi[q] = fpre[e];
+}
+
+template <typename T>
+__global__ void bn_gather_kernel(int64_t nnz, const int32_t *__restrict__ perm, const T *__restrict__ src,
+                                 T *__restrict__ dst)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < nnz) dst[e] = src[perm[e]];
+}
+
+unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+template <typename T>
+int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t *colind, const T *val,
+          hipStream_t s)
+{
+    const int64_t m = L->m, nnz = L->nnz;
+    const int64_t R = (int64_t)L->S * L->B;
+    const int64_t nchunks = (int64_t)L->S * L->nch;
+    // Persistent arrays.
+    const size_t sz_v = align_up(sizeof(T) * (size_t)nnz, 256);
+    const size_t sz_c = align_up(sizeof(uint16_t) * (size_t)nnz, 256);
+    const size_t sz_p = align_up(sizeof(int32_t) * (size_t)nnz, 256);
+    const size_t sz_ch = align_up(sizeof(int32_t) * (size_t)(nchunks + 1), 256);
+    const size_t sz_pr = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
+    const size_t sz_rw = align_up(sizeof(uint16_t) * (size_t)(nnz + 1), 256);
+    const size_t sz_pv = align_up(sizeof(T) * (size_t)(nnz + 1), 256);
+    JLUST_HIP_TRY(hipMalloc(&L->mem, sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_rw + sz_pv));
+    char *p = (char *)L->mem;
+    L->sval = p;                 p += sz_v;
+    L->scol = (uint16_t *)p;     p += sz_c;
+    L->perm = (int32_t *)p;      p += sz_p;
+    L->cst = (int32_t *)p;       p += sz_ch;
+    L->cpi = (int32_t *)p;       p += sz_ch;
+    L->pr = (int32_t *)p;        p += sz_pr;
+    L->prow = (uint16_t *)p;     p += sz_rw;
+    L->pval = p;
+
+    // Temporaries: row counts / rows (nnz + 1), keys, sorted keys, iota,
+    // flags / partial indices (nnz + 1), run starts, sort storage.
+    uint32_t *nk = nullptr;
+    size_t sort_bytes = 0;
+    int bits = 1;
+    while (((int64_t)1 << bits) < R) ++bits;
+    JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, sort_bytes, nk, nk, (int32_t *)nullptr,
+                                            (int32_t *)nullptr, (size_t)nnz, 0, bits, s));
+    const size_t sz_i = align_up(sizeof(int32_t) * (size_t)(nnz + 1), 256);
+    const size_t sz_r = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
+    void *tmp = nullptr;
+    JLUST_HIP_TRY(hipMalloc(&tmp, 5 * sz_i + sz_r + align_up(sort_bytes, 256)));
+    char *q = (char *)tmp;
+    int32_t *cnt = (int32_t *)q;    q += sz_i;
+    uint32_t *key = (uint32_t *)q;  q += sz_i;
+    uint32_t *skey = (uint32_t *)q; q += sz_i;
+    int32_t *iota = (int32_t *)q;   q += sz_i;
+    int32_t *fpre = (int32_t *)q;   q += sz_i;
+    int32_t *est = (int32_t *)q;    q += sz_r;
+    void *sort_tmp = q;
+    const int32_t *erow = cnt + 1;
+
+    int st = JLUST_STATUS_SUCCESS;
+    hipError_t e = hipMemsetAsync(cnt, 0, sizeof(int32_t) * (size_t)(nnz + 1), s);
+    if (e != hipSuccess) st = hip_fail(e, "hipMemsetAsync(binned row counts)");
+    if (!st && m > 1) {
+        hipLaunchKernelGGL(bn_rowmark_kernel, dim3(blocks256(m - 1)), dim3(256), 0, s, m, nnz, origin,
+                           rowptr, cnt);
+        st = check_launch("bn_rowmark_kernel");
+    }
+    if (!st) st = exclusive_scan_i32(cnt, cnt, nnz + 1, (jlust_stream_t)s);
+    if (!st) {
+        hipLaunchKernelGGL(bn_key_kernel, dim3(blocks256(nnz)), dim3(256), 0, s, nnz, m, origin, colind,
+                           erow, L->W, L->S, L->H, L->B, key, iota);
+        st = check_launch("bn_key_kernel");
+    }
+    if (!st) {
+        e = rocprim::radix_sort_pairs(sort_tmp, sort_bytes, key, skey, iota, L->perm, (size_t)nnz, 0, bits,
+                                      s);
+        if (e != hipSuccess) st = hip_fail(e, "rocprim::radix_sort_pairs(binned keys)");
+    }
+    if (!st) {
+        hipLaunchKernelGGL((bn_fill_kernel<T>), dim3(blocks256(nnz + 1)), dim3(256), 0, s, nnz, m, origin,
+                           colind, val, erow, L->W, L->B, skey, L->perm, (T *)L->sval, L->scol, fpre);
+        st = check_launch("bn_fill_kernel");
+    }
+    if (!st) st = exclusive_scan_i32(fpre, fpre, nnz + 1, (jlust_stream_t)s);
+    if (!st) {
+        hipLaunchKernelGGL(bn_prow_kernel, dim3(blocks256(nnz)), dim3(256), 0, s, nnz, m, erow, L->H, L->B,
+                           skey, L->perm, L->scol, fpre, L->prow);
+        st = check_launch("bn_prow_kernel");
+    }
+    if (!st) {
+        hipLaunchKernelGGL(bn_runs_kernel, dim3(blocks256(nnz + 1)), dim3(256), 0, s, nnz, R, skey, fpre,
+                           est, L->pr);
+        st = check_launch("bn_runs_kernel");
+    }
+    if (!st) {
+        hipLaunchKernelGGL(bn_chunk_kernel, dim3(blocks256(nchunks + 1)), dim3(256), 0, s, nnz, L->S, L->B,
+                           L->nch, est, fpre, L->cst, L->cpi);
+        st = check_launch("bn_chunk_kernel");
+    }
+    int32_t P = 0;
+    if (!st) {
+        e = hipMemcpyAsync(&P, fpre + nnz, sizeof(int32_t), hipMemcpyDeviceToHost, s);
+        if (e != hipSuccess) st = hip_fail(e, "hipMemcpyAsync(binned partial count)");
+    }
+    const hipError_t es = hipStreamSynchronize(s);
+    (void)hipFree(tmp);
+    if (st) return st;
+    if (es != hipSuccess) return hip_fail(es, "hipStreamSynchronize(binned layout build)");
+    L->P = P;
+    return JLUST_STATUS_SUCCESS;
+}
+
+template <typename T>
+int execute(const BinnedLayout *L, T alpha, const T *x, T beta, T *y, hipStream_t s)
+{
+    hipLaunchKernelGGL((binned_slice_kernel<T>), dim3((unsigned)(L->S * L->G)), dim3(BN_THREADS), 0, s,
+                       L->n, L->W, L->G, L->nch, (const T *)L->sval, L->scol, L->cst, L->cpi, x,
+                       (T *)L->pval);
+    if (int st = check_launch("binned_slice_kernel")) return st;
+    if (beta == T(0))
+        hipLaunchKernelGGL((binned_bin_kernel<T, true>), dim3((unsigned)L->B), dim3(BN_THREADS), 0, s, L->m,
+                           L->S, L->B, L->H, L->pr, L->prow, (const T *)L->pval, alpha, beta, y);
+    else
+        hipLaunchKernelGGL((binned_bin_kernel<T, false>), dim3((unsigned)L->B), dim3(BN_THREADS), 0, s,
+                           L->m, L->S, L->B, L->H, L->pr, L->prow, (const T *)L->pval, alpha, beta, y);
+    return check_launch("binned_bin_kernel");
+}
+
+}  // namespace
+
+bool binned_fits(int value_type, int64_t m, int64_t n, int64_t nnz)
+{
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return false;
+    int32_t W, S, G, H, B;
+    return geometry(value_type, m, n, nnz, device_info(dev).cu_count, &W, &S, &G, &H, &B);
+}
+
+int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64_t nnz, int32_t origin,
+                 const int32_t *rowptr, const int32_t *colind, const void *val, hipStream_t s)
+{
+    *out = nullptr;
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    auto *L = new BinnedLayout();
+    L->m = m;
+    L->n = n;
+    L->nnz = nnz;
+    L->value_type = value_type;
+    if (!geometry(value_type, m, n, nnz, device_info(dev).cu_count, &L->W, &L->S, &L->G, &L->H, &L->B)) {
+        delete L;
+        return fail(JLUST_STATUS_UNSUPPORTED_FORMAT,
+                    "binned spmv layout: %lld x %lld with %lld entries does not fit its index widths",
+                    (long long)m, (long long)n, (long long)nnz);
+    }
+    L->nch = L->G * BN_WAVES;
+    const int st = value_type == 0 ? build<double>(L, origin, rowptr, colind, (const double *)val, s)
+                                   : build<float>(L, origin, rowptr, colind, (const float *)val, s);
+    if (st) {
+        binned_destroy(L);
+        return st;
+    }
+    *out = L;
+    return JLUST_STATUS_SUCCESS;
+}
+
+int binned_update(BinnedLayout *L, const void *val, hipStream_t s)
+{
+    if (L->value_type == 0)
+        hipLaunchKernelGGL((bn_gather_kernel<double>), dim3(blocks256(L->nnz)), dim3(256), 0, s, L->nnz,
+                           L->perm, (const double *)val, (double *)L->sval);
+    else
+        hipLaunchKernelGGL((bn_gather_kernel<float>), dim3(blocks256(L->nnz)), dim3(256), 0, s, L->nnz,
+                           L->perm, (const float *)val, (float *)L->sval);
+    return check_launch("bn_gather_kernel");
+}
+
+int binned_execute_f64(const BinnedLayout *L, double alpha, const double *x, double beta, double *y,
+                       hipStream_t s)
+{
+    return execute<double>(L, alpha, x, beta, y, s);
+}
+
+int binned_execute_f32(const BinnedLayout *L, float alpha, const float *x, float beta, float *y,
+                       hipStream_t s)
+{
+    return execute<float>(L, alpha, x, beta, y, s);
+}
+
+void binned_destroy(BinnedLayout *L)
+{
+    if (!L) return;
+    if (L->mem) (void)hipFree(L->mem);
+    delete L;
+}
+
+}  // namespace jlust

@@ -470,11 +470,11 @@ class HIPSpMVHandle(AbstractKernelHandle):
         return SpMVGraph(g, self)
 
     def kernel(self) -> str:
-        """The kernel the plan runs: "merge", "vector" or "sliced"."""
+        """The kernel the plan runs: "merge", "vector", "sliced" or "binned"."""
         k, lpr = ctypes.c_int32(), ctypes.c_int32()
         st = _lib.lib().jlust_hip_csr_spmv_plan_info(self._plan, ctypes.byref(k), ctypes.byref(lpr))
         _lib.check(st, "csr_spmv_plan_info", self.u_A.format, _BE, self.T)
-        return ("merge", "vector", "sliced")[k.value]
+        return ("merge", "vector", "sliced", "binned")[k.value]
 
     def update_values(self, u_A: USTensor):
         if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):

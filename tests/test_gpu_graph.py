@@ -51,14 +51,14 @@ def check_replays(run, inp, out, out0, nrep=4):
         np.testing.assert_array_equal(got, host(out), err_msg=f"replay {rep}")
 
 
-@pytest.mark.parametrize("kind", ["merge", "vector", "sliced"])
+@pytest.mark.parametrize("kind", ["merge", "vector", "sliced", "binned"])
 def test_graph_spmv_plan(J, kind, monkeypatch):
     import torch
     if kind == "vector":
         m, n, lens = 30_000, 20_000, np.full(30_000, 12)
     else:
         m, n, lens = 30_000, 700_000, np.random.default_rng(1).integers(0, 90, 30_000)
-    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1" if kind == "sliced" else "0")
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", {"sliced": "1", "binned": "2"}.get(kind, "0"))
     if kind == "merge":
         monkeypatch.setenv("JLUST_HIP_SPMV_VECTOR", "0")
     else:
@@ -88,7 +88,7 @@ def test_graph_plain_spmv_and_spmm(J):
     check_replays(lambda: J.execute(J.SpMMOp, A, B, C, alpha=2.0, beta=0.5), B, C, C0)
 
 
-@pytest.mark.parametrize("kind", ["merge", "vector", "sliced"])
+@pytest.mark.parametrize("kind", ["merge", "vector", "sliced", "binned"])
 def test_plan_capture_launch(J, kind, monkeypatch):
     """jlust_hip_csr_spmv_plan_capture_* / spmv_graph_launch: each launch
     equals execute(h, x, y) bit for bit with the inputs as they are at launch
@@ -99,7 +99,7 @@ def test_plan_capture_launch(J, kind, monkeypatch):
         m, n, lens = 20_000, 15_000, np.full(20_000, 10)
     else:
         m, n, lens = 20_000, 700_000, np.random.default_rng(7).integers(0, 80, 20_000)
-    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1" if kind == "sliced" else "0")
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", {"sliced": "1", "binned": "2"}.get(kind, "0"))
     if kind == "merge":
         monkeypatch.setenv("JLUST_HIP_SPMV_VECTOR", "0")
     else:

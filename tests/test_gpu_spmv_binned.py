@@ -1,0 +1,148 @@
+"""GPU parity of the LDS-binned SpMV plan (x in column slices held in LDS by
+a slice pass, partial sums added per row bin in LDS by a bin pass) against
+the CPU oracle.
+
+JLUST_HIP_SPMV_SLICE=2 asks a plan for the binned layout wherever it fits
+(nnz >= 1, at most 1024 slices).  Bar: |y - y_ref| <= 1e-12 (fp64) / 1e-5
+(fp32) x (|alpha||A||x| + |beta||y0|) elementwise; the binned sums associate
+per slice, so they are not bit-identical to the sequential oracle, but they
+are deterministic run to run (checked bit for bit).
+"""
+import zlib
+
+import numpy as np
+import pytest
+
+from tests._util import assert_within, dev, host, random_csr
+from tests.test_gpu_spmv import SHAPES
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def J():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import jlust_amd
+    return jlust_amd
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+def run_binned(J, rowptr, colind, val, x, m, n, origin=1, alpha=1.0, beta=0.0, y0=None):
+    import torch
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n),
+                     origin=J.OneBased() if origin == 1 else J.ZeroBased())
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    y = dev(y0) if y0 is not None else torch.full((m,), float("nan"), dtype=A.dtype,
+                                                   device="cuda")
+    J.execute(h, dev(x), y, alpha=alpha, beta=beta)
+    return host(y), h, A
+
+
+def check(J, O, rowptr, colind, val, x, m, n, dtype, what, origin=1, alpha=1.0, beta=0.0,
+          y0=None):
+    y, h, A = run_binned(J, rowptr, colind, val, x, m, n, origin, alpha, beta, y0)
+    if colind.size:
+        assert h.kernel() == "binned", what
+    ref = O.csr_spmv(rowptr, colind, val, x, alpha, beta, y0, origin=origin)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x, alpha, beta, y0, origin=origin)
+    assert_within(y, ref, absref, dtype, what)
+    return y, h, A
+
+
+@pytest.mark.parametrize("name,kw", SHAPES, ids=[s[0] for s in SHAPES])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("origin", [1, 0])
+def test_binned_shapes(J, O, name, kw, dtype, origin, monkeypatch):
+    """Tiny, empty-row, one 250k-entry row (one partial per slice spans a whole
+    chunk), long rows among short ones, no entries (another plan kind), dense
+    rows, uniform rows."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m, n = kw["m"], kw["n"]
+    rowptr, colind, val = random_csr(m, n, density=kw.get("density"), lengths=kw.get("lengths"),
+                                     seed=zlib.crc32(name.encode()) % 1000 + 11, origin=origin,
+                                     dtype=dtype)
+    x = np.random.default_rng(5).uniform(-1, 1, n).astype(dtype)
+    y0 = np.random.default_rng(6).uniform(-1, 1, m).astype(dtype)
+    check(J, O, rowptr, colind, val, x, m, n, dtype, f"binned {name}", origin=origin,
+          alpha=-0.75, beta=1.25, y0=y0)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_binned_long_runs(J, O, dtype, monkeypatch):
+    """One slice (n = 64) and 600k rows: every bin's single run holds more
+    partials than the bin pass's pipelined slots (2 x 1024), so the rest of the
+    run goes through its unpipelined loop; every 7th row is empty."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m, n = 600_000, 64
+    rng = np.random.default_rng(21)
+    lens = np.ones(m, np.int64)
+    lens[::7] = 0
+    lens[::13] = 5
+    # Five distinct sorted columns per long row: the first five of a random
+    # permutation of the 64 columns.
+    five = np.sort(np.argsort(rng.random((m, n)), axis=1)[:, :5], axis=1)
+    one = rng.integers(0, n, (m, 1))
+    cols = [five[i] if lens[i] == 5 else one[i, :lens[i]] for i in range(m)]
+    colind = (np.concatenate(cols) + 1).astype(np.int32)
+    rowptr = (np.r_[0, np.cumsum(lens)] + 1).astype(np.int32)
+    val = rng.uniform(-1, 1, colind.size).astype(dtype)
+    x = np.random.default_rng(7).uniform(-1, 1, n).astype(dtype)
+    check(J, O, rowptr, colind, val, x, m, n, dtype, "binned long runs")
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_binned_many_slices_few_rows(J, O, dtype, monkeypatch):
+    """300 rows over 4M columns: 256 slices (several workgroups per slice when
+    slices are fewer than CUs is covered by the shapes above), one bin."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m, n = 300, 4_000_000
+    lens = np.random.default_rng(8).integers(0, 3000, m)
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=22, dtype=dtype)
+    x = np.random.default_rng(9).uniform(-1, 1, n).astype(dtype)
+    check(J, O, rowptr, colind, val, x, m, n, dtype, "binned many slices")
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_binned_powerlaw_update_deterministic(J, O, dtype, monkeypatch):
+    """Config 2's power-law rows at 1M x 1M: alpha/beta, bit-identical repeat,
+    update_values with new values in the caller's order."""
+    import torch
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    from jlust_amd import workloads as W
+    cfg = W.make(2, scale=4)
+    m, n = cfg["m"], cfg["n"]
+    val = cfg["val"].astype(dtype)
+    x = cfg["x"].astype(dtype)
+    y0 = np.random.default_rng(3).uniform(-1, 1, m).astype(dtype)
+    y, h, A = check(J, O, cfg["rowptr"], cfg["colind"], val, x, m, n, dtype, "binned power law",
+                    alpha=1.5, beta=-0.5, y0=y0)
+    y2 = dev(y0)
+    J.execute(h, dev(x), y2, alpha=1.5, beta=-0.5)
+    np.testing.assert_array_equal(host(y2), y)
+    val2 = (val * -3.0).astype(dtype)
+    J.update_values_(h, J.csr_tensor(A.pos_buffers[1], A.crd_buffers[1], dev(val2), (m, n)))
+    yt = torch.empty(m, dtype=A.dtype, device="cuda")
+    J.execute(h, dev(x), yt)
+    ref2 = O.csr_spmv(cfg["rowptr"], cfg["colind"], val2, x)
+    absref2 = O.csr_spmv_absref(cfg["rowptr"], cfg["colind"], val2, x)
+    assert_within(host(yt), ref2, absref2, dtype, "binned after update_values!")
+
+
+def test_binned_full_config2(J, O, monkeypatch):
+    """BASELINE config 2 (4M x 4M, 64M entries, Pareto rows) through the binned
+    plan, against the oracle, and bit-identical on a second execute."""
+    import torch
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    from jlust_amd import workloads as W
+    cfg = W.make(2)
+    y, h, _ = check(J, O, cfg["rowptr"], cfg["colind"], cfg["val"], cfg["x"], cfg["m"], cfg["n"],
+                    np.float64, "binned full config 2")
+    y2 = torch.empty(cfg["m"], dtype=torch.float64, device="cuda")
+    J.execute(h, dev(cfg["x"]), y2)
+    np.testing.assert_array_equal(host(y2), y)
