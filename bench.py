@@ -479,13 +479,14 @@ def sweep_sddmm():
 def sweep_spmv():
     """SpMV on random m x n matrices with L uniformly random columns per row
     (f64): the plain call, plans with column slices off (vector kernel where
-    the rows allow it) and forced on, and the plan's own choice, in mean wall
-    ms per call."""
+    the rows allow it), forced XCD slices, forced LDS bins, and the plan's own
+    choice, in mean wall ms per call."""
     import torch
     import jlust_amd as J
     rng = np.random.default_rng(0)
     res = []
-    for m, n in ((4_000_000, 4_000_000), (1_000_000, 4_000_000), (4_000_000, 1_000_000)):
+    for m, n in ((4_000_000, 4_000_000), (1_000_000, 4_000_000), (4_000_000, 1_000_000),
+                 (4_000_000, 500_000)):
         for L in (1, 2, 4, 6, 8, 12, 16):
             rp = (np.arange(m + 1, dtype=np.int64) * L + 1).astype(np.int32)
             ci = rng.integers(0, n, (m, L))
@@ -495,7 +496,7 @@ def sweep_spmv():
             x = dev(rng.uniform(-1, 1, n))
             y = torch.empty(m, dtype=torch.float64, device="cuda")
             e = {"m": m, "n": n, "per_row": L, "plain_ms": round(_wall_ms(lambda: J.execute(J.SpMVOp, A, x, y)), 4)}
-            for key, val in (("unsliced", "0"), ("sliced", "1"), ("auto", None)):
+            for key, val in (("unsliced", "0"), ("sliced", "1"), ("binned", "2"), ("auto", None)):
                 if val is None:
                     os.environ.pop("JLUST_HIP_SPMV_SLICE", None)
                 else:

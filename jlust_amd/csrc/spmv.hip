@@ -995,34 +995,51 @@ int mostly_local(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_
 // ~9 ps per nonzero gathering from a 32 MB x, ~5 ps from an 8 MB x (random
 // columns, 4M x 4M and 4M x 1M matrices): the break-even mean row length is
 // ~5-6 and ~9 entries, so slicing needs nnz >= L * m with L by x's size.
+enum Layout { LAYOUT_ROWS = 0, LAYOUT_SLICED = 1, LAYOUT_BINNED = 2 };
+
+// The LDS-binned layout costs a fixed ~85 us (its bin pass is a chain of one
+// step per column slice) plus ~4-5 ns per 1000 entries; scattered gathers of
+// an x beyond the L2 cost the row-order kernels ~16 ns per 1000 entries at
+// 32 MB and ~7 ns at 4 MB.  Measured crossovers (f64, random columns): 7M
+// entries for x >= 24 MB, 12M for x >= 6 MB, 20M above 2 MB.
+constexpr size_t BINNED_MIN_X_BYTES = (size_t)2 << 20;
+
+int64_t binned_min_nnz(size_t xbytes)
+{
+    return xbytes >= ((size_t)24 << 20) ? 7000000 : xbytes >= ((size_t)6 << 20) ? 12000000 : 20000000;
+}
+
+// The layout of a prepared plan.  JLUST_HIP_SPMV_SLICE: 0 = row order, 1 =
+// XCD column slices (n >= 8), 2 = LDS bins where they fit.  Default: row
+// order while x fits the L2 or the columns are mostly local; otherwise LDS
+// bins above binned_min_nnz entries (where they fit), else XCD slices from
+// min_len entries per row once x exceeds one XCD's L2.
 template <typename T>
-int want_slices(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *rowptr,
-                const int32_t *colind, hipStream_t s, bool *out)
+int choose_layout(int value_type, int64_t m, int64_t n, int64_t nnz, int32_t origin,
+                  const int32_t *rowptr, const int32_t *colind, hipStream_t s, int *out)
 {
     const char *e = getenv("JLUST_HIP_SPMV_SLICE");
-    *out = false;
+    *out = LAYOUT_ROWS;
     if (m <= 0 || nnz <= 0) return JLUST_STATUS_SUCCESS;   // the sliced kernel needs a nonzero
     if (e && e[0] == '0') return JLUST_STATUS_SUCCESS;
     if (e && e[0] == '1') {
-        *out = n >= NUM_XCD;
+        if (n >= NUM_XCD) *out = LAYOUT_SLICED;
+        return JLUST_STATUS_SUCCESS;
+    }
+    if (e && e[0] == '2') {
+        if (binned_fits(value_type, m, n, nnz)) *out = LAYOUT_BINNED;
         return JLUST_STATUS_SUCCESS;
     }
     const size_t xbytes = (size_t)n * sizeof(T);
-    if (xbytes <= SLICE_MIN_X_BYTES) return JLUST_STATUS_SUCCESS;
+    if (xbytes <= BINNED_MIN_X_BYTES) return JLUST_STATUS_SUCCESS;
+    const bool bins = nnz >= binned_min_nnz(xbytes) && binned_fits(value_type, m, n, nnz);
     const int64_t min_len = xbytes >= ((size_t)24 << 20) ? 6 : xbytes >= ((size_t)6 << 20) ? 10 : 14;
-    if (nnz < min_len * m) return JLUST_STATUS_SUCCESS;
+    const bool slices = xbytes > SLICE_MIN_X_BYTES && nnz >= min_len * m;
+    if (!bins && !slices) return JLUST_STATUS_SUCCESS;
     bool local = false;
     if (int st = mostly_local<T>(m, n, nnz, origin, rowptr, colind, s, &local)) return st;
-    *out = !local;
+    if (!local) *out = bins ? LAYOUT_BINNED : LAYOUT_SLICED;
     return JLUST_STATUS_SUCCESS;
-}
-
-// The LDS-binned layout: JLUST_HIP_SPMV_SLICE=2 asks for it where it fits.
-bool want_binned(int value_type, int64_t m, int64_t n, int64_t nnz)
-{
-    const char *e = getenv("JLUST_HIP_SPMV_SLICE");
-    if (!(e && e[0] == '2')) return false;
-    return binned_fits(value_type, m, n, nnz);
 }
 
 }  // namespace
@@ -1190,14 +1207,16 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
     p->ipt = spmv_ipt();
     hipStream_t s = (hipStream_t)stream;
     // (The sliced kernel's clamped prefetch needs at least one nonzero.)
-    int st = value_type == 0 ? want_slices<double>(m, n, nnz, origin, rowptr, colind, s, &p->sliced)
-                             : want_slices<float>(m, n, nnz, origin, rowptr, colind, s, &p->sliced);
+    int layout = LAYOUT_ROWS;
+    int st = value_type == 0
+                 ? choose_layout<double>(value_type, m, n, nnz, origin, rowptr, colind, s, &layout)
+                 : choose_layout<float>(value_type, m, n, nnz, origin, rowptr, colind, s, &layout);
     if (st) {
         delete p;
         return st;
     }
-    if (want_binned(value_type, m, n, nnz)) {
-        p->sliced = false;
+    p->sliced = layout == LAYOUT_SLICED;
+    if (layout == LAYOUT_BINNED) {
         st = binned_build(&p->binned, value_type, m, n, nnz, origin, rowptr, colind, val, s);
         if (st) {
             delete p;

@@ -126,7 +126,7 @@ __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
     int32_t pk = cpi[q];
     T carry = T(0);
 
-    constexpr int U = 4;            // steps of 64 entries per load group
+    constexpr int U = 8;            // steps of 64 entries per load group
     constexpr int GS = U * 64;
     T va[U], vb[U];
     uint32_t ka[U], kb[U];
@@ -178,15 +178,17 @@ __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
 
 // ---- bin pass.  Workgroup b adds the runs of bin b, slice by slice, into
 // ys = y[bH, bH + hn) and writes y.  Each thread takes K slots of a run; the
-// slots of the next D runs are loaded ahead in registers.
-template <typename T, bool BZ>
+// slots of the next D runs are loaded ahead in registers.  The S runs are a
+// chain of S steps, each waiting on loads issued D steps earlier, so a step
+// costs about the memory latency / D: the plan picks the deepest ring whose K
+// slots per thread hold its longest run (D*K = 24).
+template <typename T, bool BZ, int D, int K>
 __global__ __launch_bounds__(BN_THREADS) void binned_bin_kernel(
     int64_t m, int32_t S, int32_t B, int32_t H, const int32_t *__restrict__ pr,
     const uint16_t *__restrict__ prow, const T *__restrict__ pval, T alpha, T beta,
     T *__restrict__ y)
 {
     constexpr int YMAX = BN_LDS / sizeof(T);
-    constexpr int D = 8, K = 2;
     __shared__ T ys[YMAX];
     __shared__ int32_t rs[2 * BN_SMAX];
     const int b = blockIdx.x;
@@ -343,6 +345,13 @@ __global__ void bn_runs_kernel(int64_t nnz, int64_t R, const uint32_t *__restric
     }
 }
 
+// Longest run, in partials.
+__global__ void bn_maxrun_kernel(int64_t R, const int32_t *__restrict__ pr, int32_t *__restrict__ out)
+{
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < R) atomicMax(out, pr[r + 1] - pr[r]);
+}
+
 // Chunk q = c*nch + w of slice c starts at the first partial start at or after
 // the slice's entries split evenly nch ways.
 __global__ void bn_chunk_kernel(int64_t nnz, int32_t S, int32_t B, int32_t nch,
@@ -458,9 +467,19 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
                            L->nch, est, fpre, L->cst, L->cpi);
         st = check_launch("bn_chunk_kernel");
     }
-    int32_t P = 0;
+    // cnt is free again: cnt[0] receives the longest run.
+    if (!st) {
+        e = hipMemsetAsync(cnt, 0, sizeof(int32_t), s);
+        if (e != hipSuccess) st = hip_fail(e, "hipMemsetAsync(binned longest run)");
+    }
+    if (!st) {
+        hipLaunchKernelGGL(bn_maxrun_kernel, dim3(blocks256(R)), dim3(256), 0, s, R, L->pr, cnt);
+        st = check_launch("bn_maxrun_kernel");
+    }
+    int32_t P = 0, maxrun = 0;
     if (!st) {
         e = hipMemcpyAsync(&P, fpre + nnz, sizeof(int32_t), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipMemcpyAsync(&maxrun, cnt, sizeof(int32_t), hipMemcpyDeviceToHost, s);
         if (e != hipSuccess) st = hip_fail(e, "hipMemcpyAsync(binned partial count)");
     }
     const hipError_t es = hipStreamSynchronize(s);
@@ -468,6 +487,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     if (st) return st;
     if (es != hipSuccess) return hip_fail(es, "hipStreamSynchronize(binned layout build)");
     L->P = P;
+    L->maxrun = maxrun;
     return JLUST_STATUS_SUCCESS;
 }
 
@@ -478,12 +498,15 @@ int execute(const BinnedLayout *L, T alpha, const T *x, T beta, T *y, hipStream_
                        L->n, L->W, L->G, L->nch, (const T *)L->sval, L->scol, L->cst, L->cpi, x,
                        (T *)L->pval);
     if (int st = check_launch("binned_slice_kernel")) return st;
-    if (beta == T(0))
-        hipLaunchKernelGGL((binned_bin_kernel<T, true>), dim3((unsigned)L->B), dim3(BN_THREADS), 0, s, L->m,
-                           L->S, L->B, L->H, L->pr, L->prow, (const T *)L->pval, alpha, beta, y);
-    else
-        hipLaunchKernelGGL((binned_bin_kernel<T, false>), dim3((unsigned)L->B), dim3(BN_THREADS), 0, s,
-                           L->m, L->S, L->B, L->H, L->pr, L->prow, (const T *)L->pval, alpha, beta, y);
+#define BIN(Z, D, K)                                                                                \
+    hipLaunchKernelGGL((binned_bin_kernel<T, Z, D, K>), dim3((unsigned)L->B), dim3(BN_THREADS), 0, s,  \
+                       L->m, L->S, L->B, L->H, L->pr, L->prow, (const T *)L->pval, alpha, beta, y)
+#define BINZ(D, K) do { if (beta == T(0)) BIN(true, D, K); else BIN(false, D, K); } while (0)
+    if (L->maxrun <= BN_THREADS) BINZ(24, 1);
+    else if (L->maxrun <= 2 * BN_THREADS) BINZ(12, 2);
+    else BINZ(6, 4);
+#undef BINZ
+#undef BIN
     return check_launch("binned_bin_kernel");
 }
 

@@ -14,6 +14,7 @@ struct BinnedLayout {
     int32_t G = 1;           // workgroups per slice in the slice pass
     int32_t nch = 0;         // chunks per slice (G * waves per workgroup)
     int64_t P = 0;           // partial sums (one per (row, slice) pair with entries)
+    int32_t maxrun = 0;      // longest run (partials of one slice in one bin)
     void *mem = nullptr;     // one allocation holds everything below
     void *sval = nullptr;    // values in slice-major (slice, bin, row, k) order
     uint16_t *scol = nullptr;  // slice-local column | (last entry of a partial) << 15

@@ -244,7 +244,7 @@ def test_plan_sliced_random_shapes(J, O, name, kw, dtype, monkeypatch):
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 def test_plan_sliced_auto_alpha_beta_update(J, O, dtype, monkeypatch):
     """Scaled config 2 with n = 1M: x is 8 MB (f64) / 4 MB (f32); the plan
-    slices when x exceeds 4 MB."""
+    re-lays A out (LDS bins) when x exceeds 4 MB."""
     monkeypatch.delenv("JLUST_HIP_SPMV_SLICE", raising=False)
     from jlust_amd import workloads as W
     cfg = W.make(2, scale=4)
@@ -281,11 +281,11 @@ def test_plan_sliced_full_config2_deterministic(J, O, monkeypatch):
     np.testing.assert_array_equal(host(y2), y)
 
 
-@pytest.mark.parametrize("per_row,expect", [(2, "vector"), (8, "sliced")])
+@pytest.mark.parametrize("per_row,expect", [(2, "vector"), (8, "binned")])
 def test_plan_slicing_threshold(J, O, per_row, expect, monkeypatch):
-    """x of 25.6 MB with random columns: slices pay from ~6 entries per row
-    (every row is carried by all 8 slices); shorter rows keep one merge path /
-    the vector kernel.  Both plans match the oracle."""
+    """x of 25.6 MB with random columns: the LDS-binned layout pays from ~4
+    entries per row; shorter rows keep the vector kernel.  Both plans match
+    the oracle."""
     monkeypatch.delenv("JLUST_HIP_SPMV_SLICE", raising=False)
     monkeypatch.delenv("JLUST_HIP_SPMV_VECTOR", raising=False)
     m = n = 3_200_000
