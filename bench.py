@@ -62,6 +62,8 @@ def parse():
                         "plans forced unsliced / sliced, and the plan's own choice")
     p.add_argument("--mfma-peak", action="store_true",
                    help="only measure the sustained fp32 MFMA rate (v_mfma_f32_16x16x4_f32 chains)")
+    p.add_argument("--stream-ceiling", action="store_true",
+                   help="only measure the attainable HBM copy / read / fill rates (2 GiB f64)")
     p.add_argument("--convert", action="store_true",
                    help="only time format conversions (convert_format) at config sizes")
     p.add_argument("--coo", action="store_true",
@@ -513,6 +515,23 @@ def sweep_spmv():
     return res
 
 
+def stream_ceiling():
+    """Attainable HBM streaming rates on this box for a 2 GiB f64 tensor: a
+    device copy (read + write), a read-only reduction and a fill, in TB/s of
+    bytes moved."""
+    import torch
+    a = torch.empty(1 << 28, dtype=torch.float64, device="cuda").uniform_()
+    b = torch.empty_like(a)
+    nbytes = a.numel() * 8
+    out = {"bytes": nbytes}
+    for key, fn, mult in (("copy_TBps", lambda: b.copy_(a), 2), ("read_sum_TBps", lambda: a.sum(), 1),
+                          ("write_fill_TBps", lambda: b.fill_(1.0), 1)):
+        ms = _wall_ms(fn, reps=20)
+        out[key] = round(mult * nbytes / (ms * 1e-3) / 1e12, 3)
+    del a, b
+    return out
+
+
 def mfma_peak():
     """Sustained fp32 matrix-core rate (jlust_amd/csrc/gather_probe.hip,
     mfma_probe_kernel) for 1, 2 and 4 waves per SIMD, beside the published
@@ -731,6 +750,9 @@ def main():
         return
     if args.mfma_peak:
         print(json.dumps({"mfma_peak": mfma_peak()}), flush=True)
+        return
+    if args.stream_ceiling:
+        print(json.dumps({"stream_ceiling": stream_ceiling()}), flush=True)
         return
     if args.sweep_spmm:
         print(json.dumps({"sweep_spmm": sweep_spmm()}), flush=True)

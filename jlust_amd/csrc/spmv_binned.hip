@@ -34,6 +34,7 @@
 // (entry order inside a run stays the CSR order), the "last entry of a partial"
 // flags, their prefix count (= partial indices), run and chunk boundaries.
 #include <algorithm>
+#include <cstdlib>
 
 #include <rocprim/device/device_radix_sort.hpp>
 
@@ -92,7 +93,7 @@ __device__ __forceinline__ T readlane63(T v)
 // ---- slice pass.  Workgroup g of slice c = blockIdx / G; wave w streams chunk
 // c*nch + g*BN_WAVES + w, a run of whole partials [cst[q], cst[q+1]) whose
 // first partial is cpi[q].
-template <typename T>
+template <typename T, bool NT>
 __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
     int64_t n, int32_t W, int32_t G, int32_t nch, const T *__restrict__ sval,
     const uint16_t *__restrict__ scol, const int32_t *__restrict__ cst,
@@ -136,8 +137,8 @@ __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const uint32_t p = (uint32_t)min(e + u * 64 + lane, eb - 1);
-            v[u] = sval[p];
-            k[u] = scol[p];
+            v[u] = NT ? __builtin_nontemporal_load(sval + p) : sval[p];
+            k[u] = NT ? __builtin_nontemporal_load(scol + p) : scol[p];
         }
     };
     auto process = [&](const T(&v)[U], const uint32_t(&k)[U], int32_t e) {
@@ -182,7 +183,7 @@ __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
 // chain of S steps, each waiting on loads issued D steps earlier, so a step
 // costs about the memory latency / D: the plan picks the deepest ring whose K
 // slots per thread hold its longest run (D*K = 24).
-template <typename T, bool BZ, int D, int K>
+template <typename T, bool BZ, int D, int K, bool NT>
 __global__ __launch_bounds__(BN_THREADS) void binned_bin_kernel(
     int64_t m, int32_t S, int32_t B, int32_t H, const int32_t *__restrict__ pr,
     const uint16_t *__restrict__ prow, const T *__restrict__ pval, T alpha, T beta,
@@ -218,8 +219,8 @@ __global__ __launch_bounds__(BN_THREADS) void binned_bin_kernel(
             pok[d][k] = a < hi;
             // pval/prow hold P + 1 elements, so a run start is always readable.
             const uint32_t p = (uint32_t)(a < hi ? a : lo);
-            pv[d][k] = pval[p];
-            pw[d][k] = prow[p];
+            pv[d][k] = NT ? __builtin_nontemporal_load(pval + p) : pval[p];
+            pw[d][k] = NT ? __builtin_nontemporal_load(prow + p) : prow[p];
         }
     };
     auto consume = [&](int c, int d) {
@@ -491,21 +492,42 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     return JLUST_STATUS_SUCCESS;
 }
 
+// Streams read once are loaded nontemporal: bit 0 = the entries in the slice
+// pass, bit 1 = the partials and their rows in the bin pass.  Both (the
+// default, JLUST_HIP_BINNED_NT=3) measured 0.326 ms per config-2 step against
+// 0.368 ms with neither and 0.342 ms with the bin pass's alone: the entries then
+// stop evicting the partials the bin pass is about to read.
+int binned_nt()
+{
+    static const int v = [] {
+        const char *e = getenv("JLUST_HIP_BINNED_NT");
+        return e ? atoi(e) & 3 : 3;
+    }();
+    return v;
+}
+
 template <typename T>
 int execute(const BinnedLayout *L, T alpha, const T *x, T beta, T *y, hipStream_t s)
 {
-    hipLaunchKernelGGL((binned_slice_kernel<T>), dim3((unsigned)(L->S * L->G)), dim3(BN_THREADS), 0, s,
-                       L->n, L->W, L->G, L->nch, (const T *)L->sval, L->scol, L->cst, L->cpi, x,
-                       (T *)L->pval);
+    const int nt = binned_nt();
+#define SL(N)                                                                                        \
+    hipLaunchKernelGGL((binned_slice_kernel<T, N>), dim3((unsigned)(L->S * L->G)), dim3(BN_THREADS), 0, \
+                       s, L->n, L->W, L->G, L->nch, (const T *)L->sval, L->scol, L->cst, L->cpi, x,    \
+                       (T *)L->pval)
+    if (nt & 1) SL(true);
+    else SL(false);
+#undef SL
     if (int st = check_launch("binned_slice_kernel")) return st;
-#define BIN(Z, D, K)                                                                                \
-    hipLaunchKernelGGL((binned_bin_kernel<T, Z, D, K>), dim3((unsigned)L->B), dim3(BN_THREADS), 0, s,  \
+#define BIN(Z, D, K, N)                                                                                \
+    hipLaunchKernelGGL((binned_bin_kernel<T, Z, D, K, N>), dim3((unsigned)L->B), dim3(BN_THREADS), 0, s, \
                        L->m, L->S, L->B, L->H, L->pr, L->prow, (const T *)L->pval, alpha, beta, y)
-#define BINZ(D, K) do { if (beta == T(0)) BIN(true, D, K); else BIN(false, D, K); } while (0)
+#define BINN(Z, D, K) do { if (nt & 2) BIN(Z, D, K, true); else BIN(Z, D, K, false); } while (0)
+#define BINZ(D, K) do { if (beta == T(0)) BINN(true, D, K); else BINN(false, D, K); } while (0)
     if (L->maxrun <= BN_THREADS) BINZ(24, 1);
     else if (L->maxrun <= 2 * BN_THREADS) BINZ(12, 2);
     else BINZ(6, 4);
 #undef BINZ
+#undef BINN
 #undef BIN
     return check_launch("binned_bin_kernel");
 }
