@@ -825,23 +825,33 @@ int csr_spmv(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *r
 // 4*LPR entries costs one rowptr -> colind -> x chain rather than four.
 constexpr int VEC_U = 4;
 
-template <typename T, int LPR, bool BZ>
+// UNI: every row holds exactly ulen entries (rowptr[i] = origin + i*ulen, checked
+// when the plan was made), so the row bounds are computed instead of loaded and
+// the column/value loads are the first memory access.
+template <typename T, int LPR, bool BZ, bool UNI>
 __global__ __launch_bounds__(256) void csr_spmv_vector_kernel(int64_t m, int32_t origin,
                                                               const int32_t *__restrict__ rowptr,
                                                               const int32_t *__restrict__ colind,
                                                               const T *__restrict__ val, const T *__restrict__ x,
-                                                              T *__restrict__ y, T alpha, T beta)
+                                                              T *__restrict__ y, T alpha, T beta,
+                                                              int32_t ulen)
 {
     const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t row = t / LPR;
     const int sub = (int)(t % LPR);
     const int64_t r = row < m ? row : m - 1;            // clamped: loads stay in bounds
-    int32_t rp0 = rowptr[r], rp1 = rowptr[r + 1];
-    // Both values are needed here, so both loads are issued before the first
-    // wait (otherwise the second sinks under the row < m branch below).
-    __asm__ volatile("" : "+v"(rp0), "+v"(rp1));
-    const int64_t lo = (int64_t)rp0 - origin;
-    const int64_t hi = row < m ? (int64_t)rp1 - origin : lo;
+    int64_t lo, hi;
+    if constexpr (UNI) {
+        lo = r * ulen;
+        hi = row < m ? lo + ulen : lo;
+    } else {
+        int32_t rp0 = rowptr[r], rp1 = rowptr[r + 1];
+        // Both values are needed here, so both loads are issued before the first
+        // wait (otherwise the second sinks under the row < m branch below).
+        __asm__ volatile("" : "+v"(rp0), "+v"(rp1));
+        lo = (int64_t)rp0 - origin;
+        hi = row < m ? (int64_t)rp1 - origin : lo;
+    }
     T acc = T(0);
     for (int64_t p0 = lo + sub; p0 < hi; p0 += VEC_U * LPR) {
         int32_t c[VEC_U];
@@ -889,9 +899,22 @@ __global__ __launch_bounds__(256) void row_len_max_kernel(int64_t m, const int32
 // when rows average at most 64 entries and the longest needs at most 16 steps
 // per lane.  JLUST_HIP_SPMV_VECTOR=0 disables it, =L forces L lanes per row.
 // Synchronises `s`.
-int vector_lanes(int64_t m, int64_t nnz, const int32_t *rowptr, hipStream_t s, int *lpr_out)
+// flag[0] = 1 if some row pointer differs from origin + i*len.
+__global__ __launch_bounds__(256) void row_uniform_kernel(int64_t m, int32_t origin, int32_t len,
+                                                          const int32_t *__restrict__ rowptr,
+                                                          int32_t *__restrict__ flag)
+{
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i <= m; i += (int64_t)gridDim.x * 256)
+        if ((int64_t)rowptr[i] != origin + i * len) flag[0] = 1;
+}
+
+// Lanes per row of the vector kernel (0: rows too long for it) and, in
+// *ulen_out, the common row length when every row has the same one (else 0).
+int vector_lanes(int64_t m, int64_t nnz, int32_t origin, const int32_t *rowptr, hipStream_t s,
+                 int *lpr_out, int32_t *ulen_out)
 {
     *lpr_out = 0;
+    *ulen_out = 0;
     const char *e = getenv("JLUST_HIP_SPMV_VECTOR");
     if ((e && e[0] == '0') || m <= 0) return JLUST_STATUS_SUCCESS;
     const double avg = (double)nnz / (double)m;
@@ -901,16 +924,25 @@ int vector_lanes(int64_t m, int64_t nnz, const int32_t *rowptr, hipStream_t s, i
     const int forced = e ? atoi(e) : 0;          // JLUST_HIP_SPMV_VECTOR=L: L lanes per row
     if (forced >= 2 && forced <= 64 && (forced & (forced - 1)) == 0) lpr = forced;
     void *ws = nullptr;
-    if (int st = scratch(s, sizeof(int32_t), &ws)) return st;
-    auto *mx = (int32_t *)ws;
-    JLUST_HIP_TRY(hipMemsetAsync(mx, 0, sizeof(int32_t), s));
+    if (int st = scratch(s, 2 * sizeof(int32_t), &ws)) return st;
+    auto *mx = (int32_t *)ws;                    // [0] longest row, [1] non-uniform flag
+    JLUST_HIP_TRY(hipMemsetAsync(mx, 0, 2 * sizeof(int32_t), s));
     const int64_t nblk = min((int64_t)1024, (m + 255) / 256);
     hipLaunchKernelGGL(row_len_max_kernel, dim3((unsigned)nblk), dim3(256), 0, s, m, rowptr, mx);
     if (int st = check_launch("row_len_max_kernel")) return st;
-    int32_t h = 0;
-    JLUST_HIP_TRY(hipMemcpyAsync(&h, mx, sizeof(h), hipMemcpyDeviceToHost, s));
+    const bool may_be_uniform = nnz % m == 0 && nnz / m <= INT32_MAX;
+    if (may_be_uniform) {
+        hipLaunchKernelGGL(row_uniform_kernel, dim3((unsigned)nblk), dim3(256), 0, s, m, origin,
+                           (int32_t)(nnz / m), rowptr, mx + 1);
+        if (int st = check_launch("row_uniform_kernel")) return st;
+    }
+    int32_t h[2] = {0, 1};
+    JLUST_HIP_TRY(hipMemcpyAsync(h, mx, sizeof(h), hipMemcpyDeviceToHost, s));
     JLUST_HIP_TRY(hipStreamSynchronize(s));
-    if (h <= 16 * lpr) *lpr_out = lpr;         // the longest row: at most 16 steps per lane
+    if (h[0] <= 16 * lpr) {                      // the longest row: at most 16 steps per lane
+        *lpr_out = lpr;
+        if (may_be_uniform && h[1] == 0) *ulen_out = (int32_t)(nnz / m);
+    }
     return JLUST_STATUS_SUCCESS;
 }
 
@@ -1063,6 +1095,7 @@ struct jlust_spmv_plan {
     int64_t *carry_row;
     void *carry_val;
     int vec_lpr = 0;   // > 0: vector kernel with this many lanes per row
+    int32_t vec_ulen = 0;  // > 0: every row holds this many entries (bounds computed)
     // sliced
     bool sliced;
     int64_t slice_w;
@@ -1229,7 +1262,7 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
         if (m > 0) {
             st = value_type == 0 ? spmv_grid<double>(m, nnz, p->ipt, &p->grid)
                                  : spmv_grid<float>(m, nnz, p->ipt, &p->grid);
-            if (!st) st = vector_lanes(m, nnz, rowptr, s, &p->vec_lpr);
+            if (!st) st = vector_lanes(m, nnz, origin, rowptr, s, &p->vec_lpr, &p->vec_ulen);
             if (st) { delete p; return st; }
         }
         const size_t nb = (size_t)(p->grid.nblocks > 0 ? p->grid.nblocks : 1);
@@ -1339,15 +1372,11 @@ int vector_launch(const jlust_spmv_plan_t p, int lpr, T alpha, const T *x, T bet
     const int64_t threads = p->m * lpr;
     const dim3 grid((unsigned)((threads + 255) / 256));
     const T *val = (const T *)p->val;
-#define V(L)                                                                                        \
-    do {                                                                                            \
-        if (beta == T(0))                                                                           \
-            hipLaunchKernelGGL((csr_spmv_vector_kernel<T, L, true>), grid, dim3(256), 0, s, p->m,    \
-                               p->origin, p->rowptr, p->colind, val, x, y, alpha, beta);           \
-        else                                                                                        \
-            hipLaunchKernelGGL((csr_spmv_vector_kernel<T, L, false>), grid, dim3(256), 0, s, p->m,   \
-                               p->origin, p->rowptr, p->colind, val, x, y, alpha, beta);           \
-    } while (0)
+#define VK(L, Z, U)                                                                                 \
+    hipLaunchKernelGGL((csr_spmv_vector_kernel<T, L, Z, U>), grid, dim3(256), 0, s, p->m, p->origin,   \
+                       p->rowptr, p->colind, val, x, y, alpha, beta, p->vec_ulen)
+#define VZ(L, U) do { if (beta == T(0)) VK(L, true, U); else VK(L, false, U); } while (0)
+#define V(L) do { if (p->vec_ulen > 0) VZ(L, true); else VZ(L, false); } while (0)
     switch (lpr) {
     case 2: V(2); break;
     case 4: V(4); break;
@@ -1357,6 +1386,8 @@ int vector_launch(const jlust_spmv_plan_t p, int lpr, T alpha, const T *x, T bet
     default: V(64); break;
     }
 #undef V
+#undef VZ
+#undef VK
     return check_launch("csr_spmv_vector_kernel");
 }
 }  // namespace jlust

@@ -76,11 +76,12 @@ def test_plan_matches_oracle(J, O, dtype, origin, sort):
                   dtype, "COO plan after update_values")
 
 
-def test_sliced_plan_unsorted(J, O, monkeypatch):
-    """x of 5 MB with random columns, slices forced: the CSR plan under the
-    COO plan slices A (its rows, 8 entries on average, are below the automatic
-    threshold)."""
-    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1")
+@pytest.mark.parametrize("layout", ["1", "2"], ids=["sliced", "binned"])
+def test_sliced_plan_unsorted(J, O, monkeypatch, layout):
+    """x of 5 MB with random columns, slices (1) or LDS bins (2) forced: the
+    CSR plan under the COO plan re-lays A out (its 400k entries are below the
+    automatic thresholds)."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", layout)
     m, n, nnz = 50_000, 640_000, 400_000
     rows, cols, val = random_coo(m, n, nnz, 8, 1, np.float64)
     A = J.coo_tensor(dev(rows), dev(cols), dev(val), (m, n))
@@ -110,19 +111,23 @@ def test_empty_and_errors(J):
         J.prepare(J.HIPBackend(), J.SpMVOp, A, output_fn=J.abs_fn)
 
 
-@pytest.mark.parametrize("sliced", [False, True])
-def test_coo_plan_capture(J, O, monkeypatch, sliced):
+@pytest.mark.parametrize("kind", ["rows", "sliced", "binned"])
+def test_coo_plan_capture(J, O, monkeypatch, kind):
     """A COO plan recorded as a HIP graph (jlust_hip_csr_spmv_plan_capture_*)
     and launched: each launch equals execute(h, x, y) bit for bit, also after
     update_values! (new values in caller order, scattered into the plan's own
-    row-ordered copy, which the graph reads), and matches the oracle."""
+    row-ordered copy, which the graph reads, and from there into the sliced or
+    binned layout), and matches the oracle."""
     import torch
-    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "1" if sliced else "0")
-    m, n, nnz = 20_000, (640_000 if sliced else 30_000), 160_000
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", {"rows": "0", "sliced": "1", "binned": "2"}[kind])
+    m, n, nnz = 20_000, (30_000 if kind == "rows" else 640_000), 160_000
     rows, cols, val = random_coo(m, n, nnz, 12, 1, np.float64)
     A = J.coo_tensor(dev(rows), dev(cols), dev(val), (m, n))
     h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
-    assert (h.kernel() == "sliced") == sliced
+    if kind == "rows":
+        assert h.kernel() in ("merge", "vector")
+    else:
+        assert h.kernel() == kind
     x = torch.empty(n, dtype=torch.float64, device="cuda")
     y = torch.empty(m, dtype=torch.float64, device="cuda")
     ye = torch.empty(m, dtype=torch.float64, device="cuda")

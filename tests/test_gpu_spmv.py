@@ -321,3 +321,27 @@ def test_plan_vector_kernel_row_lengths(J, O, lanes, dtype, monkeypatch):
     ref = O.csr_spmv(rowptr, colind, val, x, -1.25, 0.5, y0)
     absref = O.csr_spmv_absref(rowptr, colind, val, x, -1.25, 0.5, y0)
     assert_within(y, ref, absref, dtype, f"vector kernel, {lanes} lanes")
+
+
+@pytest.mark.parametrize("L", [1, 3, 16, 40])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_plan_vector_uniform_rows(J, O, L, dtype, monkeypatch):
+    """Rows of exactly L entries: the vector kernel computes the row bounds
+    (i*L) instead of loading rowptr, so it is also checked on a pattern whose
+    entry count is a multiple of m but whose rows alternate L-1 and L+1 entries
+    (the plan must see it is not uniform), and with origin 0."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "0")
+    monkeypatch.delenv("JLUST_HIP_SPMV_VECTOR", raising=False)
+    m, n = 30_000, 50_000
+    for lens, origin in ((np.full(m, L), 1), (np.full(m, L), 0),
+                         (np.where(np.arange(m) % 2 == 0, L + 1, max(L - 1, 0)), 1)):
+        if lens.sum() % m:
+            continue
+        rowptr, colind, val = random_csr(m, n, lengths=lens, seed=L + 60, origin=origin, dtype=dtype)
+        x = np.random.default_rng(L).uniform(-1, 1, n).astype(dtype)
+        y0 = np.random.default_rng(L + 1).uniform(-1, 1, m).astype(dtype)
+        y, h, _ = run_plan(J, rowptr, colind, val, x, m, n, origin=origin, alpha=0.5, beta=2.0, y0=y0)
+        assert h.kernel() == "vector"
+        ref = O.csr_spmv(rowptr, colind, val, x, 0.5, 2.0, y0, origin=origin)
+        absref = O.csr_spmv_absref(rowptr, colind, val, x, 0.5, 2.0, y0, origin=origin)
+        assert_within(y, ref, absref, dtype, f"uniform rows L={L} origin={origin}")
