@@ -33,6 +33,11 @@
 // gathers from x[s*w : (s+1)*w] and keeps it in its own L2.  Slice s writes a
 // partial y_s; a last pass forms y = alpha*(y_0 + ... + y_7) + beta*y in that
 // fixed order.
+//
+// LDS-binned plans (spmv_binned.hip) go further for a large x with scattered
+// columns: x is cut into one LDS-sized slice per CU and y into LDS-sized row
+// bins, so no gather leaves a CU.  choose_layout() below picks row order,
+// column slices or bins when a plan is made.
 #include <new>
 #include <cstdlib>
 #include <cstring>
