@@ -146,3 +146,24 @@ def test_binned_full_config2(J, O, monkeypatch):
     y2 = torch.empty(cfg["m"], dtype=torch.float64, device="cuda")
     J.execute(h, dev(cfg["x"]), y2)
     np.testing.assert_array_equal(host(y2), y)
+
+
+@pytest.mark.parametrize("dtype,n,fits", [(np.float64, 16_000_000, True),
+                                          (np.float32, 33_000_000, True),
+                                          (np.float64, 17_000_000, False)],
+                         ids=["f64-977-slices", "f32-1008-slices", "f64-past-1024-slices"])
+def test_binned_slice_count_limit(J, O, dtype, n, fits, monkeypatch):
+    """Slices of at most 128 KB of x and at most 1024 of them (the bin pass
+    keeps two run bounds per slice in LDS): n = 16M f64 / 33M f32 run binned
+    with close to 1024 slices; n = 17M f64 needs more, and the forced request
+    falls back to another layout with the same results."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m = 2000
+    lens = np.random.default_rng(31).integers(0, 300, m)
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=32, dtype=dtype)
+    x = np.random.default_rng(33).uniform(-1, 1, n).astype(dtype)
+    y, h, _ = run_binned(J, rowptr, colind, val, x, m, n)
+    assert (h.kernel() == "binned") == fits, h.kernel()
+    ref = O.csr_spmv(rowptr, colind, val, x)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x)
+    assert_within(y, ref, absref, dtype, f"slice limit n={n}")
