@@ -106,6 +106,32 @@ __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
     const int g = blockIdx.x % G;
     const int64_t c0 = (int64_t)c * W;
     const int wn = (int)min((int64_t)W, n - c0);     // >= 1: slice c starts inside x
+    const int lane = threadIdx.x & 63;
+    // Wave-uniform (scalar) chunk bounds: the stream loop is then scalar
+    // control flow and the two load buffers stay apart.
+    const int q = __builtin_amdgcn_readfirstlane(c * nch + g * BN_WAVES + (int)(threadIdx.x >> 6));
+    const int32_t ea = cst[q], eb = cst[q + 1];
+    int32_t pk = cpi[q];
+    T carry = T(0);
+
+    constexpr int U = 8;            // steps of 64 entries per load group
+    constexpr int GS = U * 64;
+    T va[U], vb[U];
+    uint32_t ka[U], kb[U];
+    // Loads are clamped into the chunk, never predicated: a load under an
+    // exec-masked branch makes the compiler wait for every outstanding one.
+    // An empty chunk (ea == eb) clamps to its start, a valid entry or, for the
+    // last chunk, entry nnz - 1 (the layout has nnz >= 1 entries).
+    auto load = [&](T(&v)[U], uint32_t(&k)[U], int32_t e) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t p = (uint32_t)min(e + u * 64 + lane, max(eb - 1, 0));
+            v[u] = NT ? __builtin_nontemporal_load(sval + p) : sval[p];
+            k[u] = NT ? __builtin_nontemporal_load(scol + p) : scol[p];
+        }
+    };
+    // The first group of entries is in flight while x's slice is copied to LDS.
+    load(va, ka, ea);
     {
         T t[XPT];
 #pragma unroll
@@ -117,30 +143,8 @@ __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
         }
     }
     __syncthreads();
-
-    const int lane = threadIdx.x & 63;
-    // Wave-uniform (scalar) chunk bounds: the stream loop is then scalar
-    // control flow and the two load buffers stay apart.
-    const int q = __builtin_amdgcn_readfirstlane(c * nch + g * BN_WAVES + (int)(threadIdx.x >> 6));
-    const int32_t ea = cst[q], eb = cst[q + 1];
     if (ea >= eb) return;
-    int32_t pk = cpi[q];
-    T carry = T(0);
 
-    constexpr int U = 8;            // steps of 64 entries per load group
-    constexpr int GS = U * 64;
-    T va[U], vb[U];
-    uint32_t ka[U], kb[U];
-    // Loads are clamped into the chunk, never predicated: a load under an
-    // exec-masked branch makes the compiler wait for every outstanding one.
-    auto load = [&](T(&v)[U], uint32_t(&k)[U], int32_t e) {
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const uint32_t p = (uint32_t)min(e + u * 64 + lane, eb - 1);
-            v[u] = NT ? __builtin_nontemporal_load(sval + p) : sval[p];
-            k[u] = NT ? __builtin_nontemporal_load(scol + p) : scol[p];
-        }
-    };
     auto process = [&](const T(&v)[U], const uint32_t(&k)[U], int32_t e) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
@@ -164,7 +168,6 @@ __global__ __launch_bounds__(BN_THREADS) void binned_slice_kernel(
         }
     };
     int32_t e = ea;
-    load(va, ka, e);
     for (;;) {
         load(vb, kb, e + GS);
         process(va, ka, e);
