@@ -143,16 +143,47 @@ int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float alpha,
 int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan);
 
 /*
+ * Which values a plan reads.  Merge and vector plans read the value buffer
+ * they were given (plan_create or the last update_values), so values stored
+ * into it in place are seen by the next execute.  The sliced and binned
+ * layouts, and COO plans whose entries were reordered, run on a permuted copy
+ * of the values: execute then uses the values as of plan_create or the last
+ * update_values / execute_values, the cuSPARSE handle contract where values
+ * change through update_values! (ext/CUDAExt/ops/spmv.jl:40-43,63-78).
+ *
+ * execute_values is the form that takes A at every call,
+ * execute(h::EmitterSpMVHandle, A, x, y) (ext/KernelAbstractionsExt/ops/
+ * spmv.jl:531-544): it reads `val` (nnz values, the plan's pattern) as they
+ * are when the call's work runs on `stream`, whatever the plan kind: a copy
+ * is refreshed on `stream` before the product (one gather of the values
+ * through the stored permutation), and `val` becomes the plan's values for
+ * later executes.  update_values does the same refresh but orders it against
+ * every stream of the device (it synchronises the device twice).
+ * Executes of one plan on different streams must be ordered by the caller:
+ * they share the plan's partial sums and value copy.
+ */
+int jlust_hip_csr_spmv_plan_execute_values_f64(jlust_spmv_plan_t plan,
+                                               const double *val, double alpha,
+                                               const double *x, double beta,
+                                               double *y, jlust_stream_t stream);
+int jlust_hip_csr_spmv_plan_execute_values_f32(jlust_spmv_plan_t plan,
+                                               const float *val, float alpha,
+                                               const float *x, float beta,
+                                               float *y, jlust_stream_t stream);
+
+/*
  * A plan execution recorded once as a HIP graph and replayed on any stream of
  * the plan's device: the reference's GPU block products capture their SpMV
  * with CUDA.capture/instantiate and replay it with CUDA.launch, one graph per
  * (pointer(y), pointer(x)) (ext/CUDAExt/ops/block_mul.jl:233-267, 751-786).
  * capture records y = alpha*A*x + beta*y with these pointers and coefficients
  * (on a private stream, thread-local capture mode; nothing runs).  A launch
- * reads the plan's buffers as they are then: values written into the same
- * buffers (update_values of a sliced or COO plan, or new values stored in
- * place) are seen; update_values with another value pointer on a merge or
- * vector plan needs a new capture.  launch onto a stream that is itself being
+ * reads the buffers the captured kernels were given as they are then: a merge
+ * or vector plan's value buffer (values stored into it in place are seen), or
+ * the value copy of a sliced, binned or reordered-COO plan (refreshed in place
+ * by update_values / execute_values, which are then seen).  update_values or
+ * execute_values with another value pointer on a merge or vector plan needs a
+ * new capture.  launch onto a stream that is itself being
  * captured returns JLUST_STATUS_STREAM_CAPTURING without launching (execute
  * the plan instead, so the outer capture records its kernels, as the
  * reference does under CUDA.is_capturing()).  destroy drains the device

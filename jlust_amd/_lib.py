@@ -39,6 +39,8 @@ SIGNATURES = {
     "jlust_hip_csr_spmv_plan_execute_f64": (_INT, [_P, _D, _P, _D, _P, _P]),
     "jlust_hip_csr_spmv_plan_execute_f32": (_INT, [_P, _F, _P, _F, _P, _P]),
     "jlust_hip_csr_spmv_plan_destroy": (_INT, [_P]),
+    "jlust_hip_csr_spmv_plan_execute_values_f64": (_INT, [_P, _P, _D, _P, _D, _P, _P]),
+    "jlust_hip_csr_spmv_plan_execute_values_f32": (_INT, [_P, _P, _F, _P, _F, _P, _P]),
     "jlust_hip_csr_spmv_plan_capture_f64": (_INT, [_P, _D, _P, _D, _P, ctypes.POINTER(_P)]),
     "jlust_hip_csr_spmv_plan_capture_f32": (_INT, [_P, _F, _P, _F, _P, ctypes.POINTER(_P)]),
     "jlust_hip_spmv_graph_launch": (_INT, [_P, _P]),

@@ -38,9 +38,9 @@
 // columns: x is cut into one LDS-sized slice per CU and y into LDS-sized row
 // bins, so no gather leaves a CU.  choose_layout() below picks row order,
 // column slices or bins when a plan is made.
-#include <new>
 #include <cstdlib>
 #include <cstring>
+#include <new>
 
 #include "common.hpp"
 #include "spmv_binned.hpp"
@@ -1325,48 +1325,57 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
     return JLUST_STATUS_SUCCESS;
 }
 
+namespace jlust {
+// Makes the plan read the values `val` (same pattern as the plan's), in stream
+// order on s: merge and vector plans only take the pointer; a COO plan whose
+// entries were reordered gathers them into its row-ordered copy first; the
+// sliced and binned layouts gather them into their own slice-major copy.  A
+// later execute on s (or anything ordered after s) sees them.
+int plan_refresh(jlust_spmv_plan_t plan, const void *val, hipStream_t s)
+{
+    if (plan->coo_perm && plan->nnz > 0) {
+        // COO entries in the caller's order -> the plan's row order.
+        const unsigned grid = (unsigned)((plan->nnz + 255) / 256);
+        if (plan->value_type == 0)
+            hipLaunchKernelGGL((gather_values_kernel<double>), dim3(grid), dim3(256), 0, s, plan->nnz,
+                               plan->coo_perm, (const double *)val, (double *)plan->coo_val);
+        else
+            hipLaunchKernelGGL((gather_values_kernel<float>), dim3(grid), dim3(256), 0, s, plan->nnz,
+                               plan->coo_perm, (const float *)val, (float *)plan->coo_val);
+        if (int st = check_launch("gather_values_kernel")) return st;
+        val = plan->coo_val;
+    }
+    plan->val = val;
+    if (plan->binned)
+        if (int st = binned_update(plan->binned, val, s)) return st;
+    if (plan->sliced && plan->nnz > 0) {
+        const unsigned grid = (unsigned)((plan->nnz + 255) / 256);
+        if (plan->value_type == 0)
+            hipLaunchKernelGGL((gather_values_kernel<double>), dim3(grid), dim3(256), 0, s, plan->nnz,
+                               plan->perm, (const double *)val, (double *)plan->val_all);
+        else
+            hipLaunchKernelGGL((gather_values_kernel<float>), dim3(grid), dim3(256), 0, s, plan->nnz,
+                               plan->perm, (const float *)val, (float *)plan->val_all);
+        if (int st = check_launch("gather_values_kernel")) return st;
+    }
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust
+
 extern "C" int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan, const void *val)
 {
     clear_error();
     if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_update_values: null plan");
     if (bad_ptr(val, plan->nnz))
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_update_values: null values");
-    if (plan->coo_perm && plan->nnz > 0) {
-        // COO entries in the caller's order -> the plan's row order.
-        const unsigned grid = (unsigned)((plan->nnz + 255) / 256);
-        JLUST_HIP_TRY(hipDeviceSynchronize());
-        if (plan->value_type == 0)
-            hipLaunchKernelGGL((gather_values_kernel<double>), dim3(grid), dim3(256), 0, 0, plan->nnz,
-                               plan->coo_perm, (const double *)val, (double *)plan->coo_val);
-        else
-            hipLaunchKernelGGL((gather_values_kernel<float>), dim3(grid), dim3(256), 0, 0, plan->nnz,
-                               plan->coo_perm, (const float *)val, (float *)plan->coo_val);
-        if (int st = check_launch("gather_values_kernel")) return st;
-        JLUST_HIP_TRY(hipDeviceSynchronize());      // visible to the next execute on any stream
-        val = plan->coo_val;
-    }
-    plan->val = val;
-    if (plan->binned) {
-        // Same protocol as the sliced copy below.
-        JLUST_HIP_TRY(hipDeviceSynchronize());
-        if (int st = binned_update(plan->binned, val, 0)) return st;
-        JLUST_HIP_TRY(hipDeviceSynchronize());
-    }
-    if (plan->sliced && plan->nnz > 0) {
-        // The plan's slice-major copy of the values is refreshed in stream order
-        // on the null stream, then waited for, so the caller's next execute on
-        // any stream sees it.
-        const unsigned grid = (unsigned)((plan->nnz + 255) / 256);
-        JLUST_HIP_TRY(hipDeviceSynchronize());      // the new values are complete
-        if (plan->value_type == 0)
-            hipLaunchKernelGGL((gather_values_kernel<double>), dim3(grid), dim3(256), 0, 0, plan->nnz,
-                               plan->perm, (const double *)val, (double *)plan->val_all);
-        else
-            hipLaunchKernelGGL((gather_values_kernel<float>), dim3(grid), dim3(256), 0, 0, plan->nnz,
-                               plan->perm, (const float *)val, (float *)plan->val_all);
-        if (int st = check_launch("gather_values_kernel")) return st;
-        JLUST_HIP_TRY(hipDeviceSynchronize());
-    }
+    // Not tied to a stream: the new values are complete once every queued
+    // kernel on the device has finished, the plan's copies are refreshed on
+    // the null stream, and that is waited for, so the caller's next execute
+    // on any stream sees them.
+    const bool copies = plan->coo_perm || plan->binned || plan->sliced;
+    if (copies) JLUST_HIP_TRY(hipDeviceSynchronize());
+    if (int st = plan_refresh(plan, val, 0)) return st;
+    if (copies) JLUST_HIP_TRY(hipDeviceSynchronize());
     return JLUST_STATUS_SUCCESS;
 }
 
@@ -1468,6 +1477,42 @@ extern "C" int jlust_hip_csr_spmv_plan_execute_f32(jlust_spmv_plan_t plan, float
                                                    jlust_stream_t stream)
 {
     return plan_execute<float>(plan, 1, alpha, x, beta, y, stream);
+}
+
+template <typename T>
+static int plan_execute_values(jlust_spmv_plan_t plan, int want_type, const T *val, T alpha, const T *x,
+                               T beta, T *y, jlust_stream_t stream)
+{
+    clear_error();
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_execute_values: null plan");
+    if (plan->value_type != want_type)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE,
+                    "spmv_plan_execute_values: plan was created for %s values",
+                    plan->value_type == 0 ? "Float64" : "Float32");
+    if (bad_ptr(val, plan->nnz))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_execute_values: null values");
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    if (dev != plan->device)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "spmv_plan_execute_values: plan belongs to device %d, current device is %d",
+                    plan->device, dev);
+    if (int st = plan_refresh(plan, val, (hipStream_t)stream)) return st;
+    return plan_execute<T>(plan, want_type, alpha, x, beta, y, stream);
+}
+
+extern "C" int jlust_hip_csr_spmv_plan_execute_values_f64(jlust_spmv_plan_t plan, const double *val,
+                                                          double alpha, const double *x, double beta,
+                                                          double *y, jlust_stream_t stream)
+{
+    return plan_execute_values<double>(plan, 0, val, alpha, x, beta, y, stream);
+}
+
+extern "C" int jlust_hip_csr_spmv_plan_execute_values_f32(jlust_spmv_plan_t plan, const float *val,
+                                                          float alpha, const float *x, float beta,
+                                                          float *y, jlust_stream_t stream)
+{
+    return plan_execute_values<float>(plan, 1, val, alpha, x, beta, y, stream);
 }
 
 // A plan execution recorded once as a HIP graph and replayed: the capture

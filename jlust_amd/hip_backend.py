@@ -391,23 +391,38 @@ class HIPSpMVHandle(AbstractKernelHandle):
                 m, n, nnz(u_A), u_A.origin.offset, 0 if suf == "f64" else 1, _ptr(first),
                 _ptr(second), _ptr(nonzeros(u_A)), _stream(self.dev), ctypes.byref(self._plan))
         _lib.check(st, create[10:], u_A.format, _BE, self.T)
+        # The values the plan reads and torch's in-place version of them when
+        # it last read them.  Sliced and binned layouts (and COO plans, whose
+        # entries may have been reordered) run on a permuted copy of the
+        # values, so an in-place write into them has to be gathered again;
+        # merge and vector plans read the buffer itself.
+        self._vals = nonzeros(u_A)
+        self._ver = self._vals._version
+        self._copies = coo or self.kernel() in ("sliced", "binned")
+        self._exec_values = None
 
     takes_raw = True     # execute(h, x, y) on plain device tensors: the raw-array form
 
     def execute(self, *ts, alpha=1.0, beta=0.0):
         """execute(h, x, y) (the cuSPARSE handle form) or execute(h, A, x, y)
-        (EmitterSpMVHandle, spmv.jl:531-544, which takes A's buffers at each
-        call: an A with other values than the plan's refreshes them first).
-        The handle's input_fn/output_fn apply.  With plain device tensors x, y
-        the call returns y, as the cuSPARSE handle's raw-array method does
-        (ext/CUDAExt/ops/spmv.jl:63-78); with USTensors it returns u_y."""
+        (EmitterSpMVHandle, spmv.jl:531-544, which reads A's buffers at each
+        call).  Both see A's values as they are at the call: values written
+        in place through torch since the plan last read them (torch's version
+        counter of the value tensor moved) are gathered again into the
+        plan's copy, in stream order, before the product; an A whose value
+        tensor is another one than the plan's becomes the plan's values
+        (update_values! semantics).  Writes that bypass torch (raw device
+        pointers) need update_values_.  The handle's input_fn/output_fn
+        apply.  With plain device tensors x, y the call returns y, as the
+        cuSPARSE handle's raw-array method does (ext/CUDAExt/ops/spmv.jl:
+        63-78); with USTensors it returns u_y."""
         if len(ts) == 2 and isinstance(ts[0], torch.Tensor) and isinstance(ts[1], torch.Tensor):
             return self.execute_tensors(ts[0], ts[1], alpha, beta)
         ts = tuple(t if isinstance(t, USTensor) else ust(t) for t in ts)
         if len(ts) == 3:
             u_A, u_x, u_y = ts
-            if u_A is not self.u_A and nonzeros(u_A).data_ptr() != nonzeros(self.u_A).data_ptr():
-                self.update_values(u_A)
+            if nonzeros(u_A) is not self._vals:
+                self._rebind(u_A)
         elif len(ts) == 2:
             u_x, u_y = ts
         else:
@@ -415,12 +430,45 @@ class HIPSpMVHandle(AbstractKernelHandle):
         return spmv_with_fns(self._execute_plain, self.u_A, u_x, u_y, alpha, beta,
                              self.input_fn, self.output_fn)
 
+    def _rebind(self, u_A: USTensor):
+        """Take u_A's value tensor as the plan's values; the next product
+        reads them (a stale version forces the stream-ordered gather)."""
+        if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):
+            raise IncompatibleExtents("execute(h, A, x, y): A's sparsity structure is not the plan's")
+        _check_values(u_A, self.T)
+        _check_same_device(nonzeros(u_A), self._vals)
+        self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
+                            self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+        self._vals = nonzeros(u_A)
+        self._ver = -1        # never a tensor's version: the next product reads the values
+
+    def _stale(self) -> bool:
+        """Whether the plan must read its value tensor again before a product:
+        a new tensor (_rebind), or one a copying plan holds written in place."""
+        return self._ver < 0 or (self._copies and self._vals._version != self._ver)
+
+    def _launch(self, alpha, x_ptr, beta, y_ptr, stream):
+        """One plan execute on raw pointers; through execute_values when the
+        plan's values are stale (refresh on the same stream, then product)."""
+        if self._stale():
+            if self._exec_values is None:
+                self._exec_values = getattr(_lib.lib(),
+                                            f"jlust_hip_csr_spmv_plan_execute_values_{self.suf}")
+            v = self._vals
+            st = self._exec_values(self._plan, v.data_ptr() if v.numel() else None, alpha, x_ptr,
+                                   beta, y_ptr, stream)
+            if st == 0:
+                self._ver = v._version
+            return st
+        if self._exec is None:
+            self._exec = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_{self.suf}")
+        return self._exec(self._plan, alpha, x_ptr, beta, y_ptr, stream)
+
     def _execute_plain(self, u_A, u_x: USTensor, u_y: USTensor, alpha=1.0, beta=0.0):
         x, y = _vec_checks(self.u_A, u_x, u_y)
         _check_same_device(nonzeros(self.u_A), x, y)
         with _on(self.dev):
-            st = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_{self.suf}")(
-                self._plan, float(alpha), _ptr(x), float(beta), _ptr(y), _stream(self.dev))
+            st = self._launch(float(alpha), _ptr(x), float(beta), _ptr(y), _stream(self.dev))
         _lib.check(st, "csr_spmv_plan_execute", self.u_A.format, _BE, self.T)
         return u_y
 
@@ -438,10 +486,8 @@ class HIPSpMVHandle(AbstractKernelHandle):
                 self.input_fn is not None or self.output_fn is not None):
             self.execute(ust(x), ust(y), alpha=alpha, beta=beta)
             return y
-        if self._exec is None:
-            self._exec = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_{self.suf}")
         with _on(self.dev):
-            st = self._exec(self._plan, alpha, x.data_ptr(), beta, y.data_ptr(), _stream(self.dev))
+            st = self._launch(alpha, x.data_ptr(), beta, y.data_ptr(), _stream(self.dev))
         if st:
             _lib.check(st, "csr_spmv_plan_execute", self.u_A.format, _BE, self.T)
         return y
@@ -462,12 +508,17 @@ class HIPSpMVHandle(AbstractKernelHandle):
                                       f"y has {tuple(y.shape)} (contiguous vectors)")
         if self.input_fn is not None or self.output_fn is not None:
             raise UnsupportedFormat(self.u_A.format, _BE, "capture takes handles without input_fn/output_fn")
+        return SpMVGraph(self, x.data_ptr(), y.data_ptr(), alpha, beta)
+
+    def _capture_raw(self, x_ptr: int, y_ptr: int, alpha, beta) -> ctypes.c_void_p:
+        if self._stale():
+            self.update_values(self.u_A)
         g = ctypes.c_void_p()
         with _on(self.dev):
             st = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_capture_{self.suf}")(
-                self._plan, alpha, x.data_ptr(), beta, y.data_ptr(), ctypes.byref(g))
+                self._plan, alpha, x_ptr, beta, y_ptr, ctypes.byref(g))
         _lib.check(st, "csr_spmv_plan_capture", self.u_A.format, _BE, self.T)
-        return SpMVGraph(g, self)
+        return g
 
     def kernel(self) -> str:
         """The kernel the plan runs: "merge", "vector", "sliced" or "binned"."""
@@ -480,10 +531,14 @@ class HIPSpMVHandle(AbstractKernelHandle):
         if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):
             raise IncompatibleExtents("update_values!: the sparsity structure must not change")
         _check_values(u_A, self.T)
-        st = _lib.lib().jlust_hip_csr_spmv_plan_update_values(self._plan, _ptr(nonzeros(u_A)))
+        v = nonzeros(u_A)
+        ver = v._version
+        with _on(self.dev):
+            st = _lib.lib().jlust_hip_csr_spmv_plan_update_values(self._plan, _ptr(v))
         _lib.check(st, "csr_spmv_plan_update_values", u_A.format, _BE, self.T)
         self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
-                            self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+                            self.u_A.crd_buffers, v, self.u_A.owner, self.u_A.origin)
+        self._vals, self._ver = v, ver
         return self
 
     def __del__(self):
@@ -500,31 +555,54 @@ class SpMVGraph:
     it on the current stream of the plan's device and returns True, or
     returns False without launching when that stream is itself being
     captured (the caller then executes the plan, so the outer capture records
-    the kernels).  Holds its handle, so the plan outlives the graph."""
+    the kernels).  Like the reference's graphs (keyed by pointer(y),
+    pointer(x)) it replays on the device addresses of x and y given at
+    capture, which the caller keeps valid.  It holds its handle and the value
+    tensor the captured kernels read, so neither is freed under it.  A launch sees
+    the handle's values as they are then: a merge or vector plan whose value
+    tensor was replaced (update_values_ or execute(h, A, ...) with another
+    tensor) is captured again, and values a copying plan holds that were
+    written in place through torch are gathered again first."""
 
-    __slots__ = ("_g", "_h", "dev", "_launch")
+    __slots__ = ("_g", "_h", "dev", "_launch", "_x", "_y", "_alpha", "_beta", "_vals")
 
-    def __init__(self, g: ctypes.c_void_p, h: "HIPSpMVHandle"):
-        self._g, self._h, self.dev = g, h, h.dev
+    def __init__(self, h: "HIPSpMVHandle", x: int, y: int, alpha, beta):
+        self._h, self.dev = h, h.dev
+        self._x, self._y, self._alpha, self._beta = x, y, alpha, beta
+        self._g = None
         self._launch = _lib.lib().jlust_hip_spmv_graph_launch
+        self._g = h._capture_raw(x, y, alpha, beta)
+        self._vals = h._vals
 
     def launch(self) -> bool:
+        h = self._h
+        if h._vals is not self._vals and not h._copies:
+            # The graph's kernels hold the old value pointer: capture again.
+            g = h._capture_raw(self._x, self._y, self._alpha, self._beta)
+            self._destroy()
+            self._g, self._vals = g, h._vals
+        elif h._stale():
+            h.update_values(h.u_A)
+            self._vals = h._vals
         with _on(self.dev):
             st = self._launch(self._g, _stream(self.dev))
         if st == 0:
             return True
         if st == _lib.STREAM_CAPTURING:
             return False
-        _lib.check(st, "spmv_graph_launch", self._h.u_A.format, _BE, self._h.T)
+        _lib.check(st, "spmv_graph_launch", h.u_A.format, _BE, h.T)
         return False
 
-    def __del__(self):
+    def _destroy(self):
         g, self._g = getattr(self, "_g", None), None
         if g is not None and g.value:
             try:
                 _lib.lib().jlust_hip_spmv_graph_destroy(g)
             except Exception:
                 pass
+
+    def __del__(self):
+        self._destroy()
 
 
 class HIPOpHandle(AbstractKernelHandle):
