@@ -118,6 +118,27 @@ int jlust_hip_csr_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz,
                                float *y, jlust_stream_t stream);
 
 /*
+ * jlust_hip_csr_spmv_f64_i32 without any allocation.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results (bit for bit) as the plain call; the
+ * merge path's carry slots live in a static device array of the library
+ * (64 KiB per device, 4096 slots, held until the process ends) instead of the
+ * per-stream scratch buffer, so the call never calls hipMalloc, hipFree or an
+ * allocating library routine.  Any matrix size is accepted: the grid needs
+ * at most one slot per resident workgroup (2048 on MI355X); a device whose
+ * grid would need more than 4096 slots gets INVALID_ARGUMENT.  Every call on
+ * one device shares that array, so calls that overlap in time on one device
+ * (two streams, two host threads) race; order them.
+ */
+int jlust_hip_csr_spmv_f64_i32_noalloc(int64_t m, int64_t n, int64_t nnz,
+                                       int32_t origin, const int32_t *rowptr,
+                                       const int32_t *colind, const double *val,
+                                       double alpha, const double *x,
+                                       double beta, double *y,
+                                       jlust_stream_t stream);
+
+/*
  * Prepared SpMV: analysis once (the merge-path partition of the pattern),
  * execute many times, refresh the value pointer without re-analysis.
  * Replaces prepare(::EmitterBackend, SpMVOp, u_A) / execute(h, ...)

@@ -33,6 +33,8 @@ SIGNATURES = {
     "jlust_hip_check_csr": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _INT]),
     "jlust_hip_csr_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P, _P]),
     "jlust_hip_csr_spmv_f32_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _F, _P, _P]),
+    "jlust_hip_csr_spmv_f64_i32_noalloc": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P,
+                                                  _P]),
     "jlust_hip_csr_spmv_plan_create": (_INT, [_I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
                                               ctypes.POINTER(_P)]),
     "jlust_hip_csr_spmv_plan_update_values": (_INT, [_P, _P]),

@@ -40,6 +40,7 @@
 // column slices or bins when a plan is made.
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <new>
 
 #include "common.hpp"
@@ -1148,6 +1149,69 @@ extern "C" int jlust_hip_csr_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz, int
                                           float beta, float *y, jlust_stream_t stream)
 {
     return csr_spmv<float>(m, n, nnz, origin, rowptr, colind, val, alpha, x, beta, y, stream);
+}
+
+// ------------------------------------------------- allocation-free SpMV call
+
+// Carry slots of jlust_hip_csr_spmv_f64_i32_noalloc: carry rows (int64) in
+// the first half, carry values (double) in the second.  The plain merge grid
+// has one block per resident slot (occupancy x CUs: at most 2048 blocks of
+// 256 threads on 256 CUs), so 4096 slots cover it with room to spare.  Every
+// block of a launch writes its own slot before the fix-up kernel reads it,
+// so nothing needs clearing between calls.  The array is never named in
+// host code below except to take its device address.
+constexpr int64_t NOALLOC_MAX_BLOCKS = 4096;
+constexpr size_t NOALLOC_SCRATCH_BYTES = (size_t)NOALLOC_MAX_BLOCKS * (sizeof(int64_t) + sizeof(double));
+static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[NOALLOC_MAX_DEVICES];   // device address of `scratch` on each device
+
+// The device address of this device's copy of `scratch`, looked up once per
+// device (with that device current) by hipGetSymbolAddress.
+int noalloc_scratch(int dev, void **out)
+{
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_spmv_noalloc: device %d beyond the %d supported",
+                    dev, NOALLOC_MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (!g_noalloc_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(::scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(JLUST_STATUS_HIP_ERROR, "hipGetSymbolAddress(scratch) returned null");
+        g_noalloc_ptr[dev] = p;
+    }
+    *out = g_noalloc_ptr[dev];
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace
+
+extern "C" int jlust_hip_csr_spmv_f64_i32_noalloc(int64_t m, int64_t n, int64_t nnz, int32_t origin,
+                                                  const int32_t *rowptr, const int32_t *colind,
+                                                  const double *val, double alpha, const double *x,
+                                                  double beta, double *y, jlust_stream_t stream)
+{
+    clear_error();
+    if (int st = check_spmv_args(m, n, nnz, origin, rowptr, colind, val, x, y)) return st;
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    void *base = nullptr;
+    if (int st = noalloc_scratch(dev, &base)) return st;
+    if (m == 0) return JLUST_STATUS_SUCCESS;
+    SpmvGrid g;
+    const int ipt = spmv_ipt();
+    if (int st = spmv_grid<double>(m, nnz, ipt, &g)) return st;
+    if (g.nblocks > NOALLOC_MAX_BLOCKS)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "csr_spmv_noalloc: the launch needs %lld carry slots, the static scratch holds %lld",
+                    (long long)g.nblocks, (long long)NOALLOC_MAX_BLOCKS);
+    int64_t *carry_row = (int64_t *)base;
+    double *carry_val = (double *)((char *)base + sizeof(int64_t) * NOALLOC_MAX_BLOCKS);
+    return spmv_launch<double>(m, nnz, origin, rowptr, colind, val, alpha, x, beta, y, g, ipt, nullptr,
+                               carry_row, carry_val, (hipStream_t)stream);
 }
 
 template <typename T>
