@@ -52,6 +52,8 @@ typedef void *jlust_stream_t;                 /* hipStream_t */
 typedef struct jlust_spmv_plan *jlust_spmv_plan_t;
 typedef struct jlust_spmv_graph *jlust_spmv_graph_t;
 typedef struct jlust_convert *jlust_convert_t;
+typedef struct jlust_spmm_plan *jlust_spmm_plan_t;
+typedef struct jlust_sddmm_plan *jlust_sddmm_plan_t;
 
 /*
  * Status codes.  The Julia side maps them onto the reference's exception
@@ -272,6 +274,26 @@ int jlust_hip_coo_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz,
                                float *y, jlust_stream_t stream);
 
 /*
+ * CSC SpMV (colptr[n+1], rowind[nnz], val[nnz], Formats.CSC): y = beta*y
+ * (zero-filled when beta == 0), then y[row] += (alpha*val)*x[col] for every
+ * stored entry, with atomics, in the reference's scatter mode for column-outer
+ * formats (execute(::EmitterBackend, ::Op{:SpMV}), ext/KernelAbstractionsExt/
+ * ops/spmv.jl:391-408).  The atomic order varies, so results vary in their
+ * last bits run to run.  input_fn composes (apply it to x first); output_fn
+ * does not, as in the reference (spmv.jl:396-399).
+ */
+int jlust_hip_csc_spmv_f64_i32(int64_t m, int64_t n, int64_t nnz,
+                               int32_t origin, const int32_t *colptr,
+                               const int32_t *rowind, const double *val,
+                               double alpha, const double *x, double beta,
+                               double *y, jlust_stream_t stream);
+int jlust_hip_csc_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz,
+                               int32_t origin, const int32_t *colptr,
+                               const int32_t *rowind, const float *val,
+                               float alpha, const float *x, float beta,
+                               float *y, jlust_stream_t stream);
+
+/*
  * Elementwise transforms for SpMV's input_fn / output_fn
  * (execute(::EmitterBackend, ::Op{:SpMV}; input_fn, output_fn),
  * ext/KernelAbstractionsExt/ops/spmv.jl:371-374): f(v) of one kind.
@@ -350,6 +372,47 @@ int jlust_hip_csr_spmm_f32_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
                                float beta, float *C, int64_t ldc,
                                int skip_empty_rows, jlust_stream_t stream);
 
+/*
+ * Prepared CSR SpMM for B and C of k columns: prepare(backend, SpMMOp, A;
+ * n_cols = k) -> execute(h, B, C) -> update_values!(h, A), the cuSPARSE SpMM
+ * handle contract (ext/CUDAExt/ops/spmm.jl:8-70, src/ops.jl:170-188).
+ * Analysis once: the column chunk per pass for this k, and the rows longer
+ * than 1024 entries, which are cut into segments of 256 entries computed in
+ * parallel into partial rows and added back in segment order (one wave would
+ * otherwise walk each such row alone).  Workspace owned by the plan: the
+ * row-major copy of one column chunk of B and the partial rows, so an execute
+ * allocates nothing.  Results equal jlust_hip_csr_spmm_* bit for bit on rows
+ * that are not split, and are deterministic run to run.  The plan records
+ * rowptr, colind and val (read in place at each execute: values stored into
+ * val are seen); update_values points it at another value buffer.
+ * value_type: 0 = f64, 1 = f32.  Synchronises `stream` (the row analysis
+ * reads rowptr on the host).  Executes of one plan must not overlap in time.
+ */
+int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k,
+                                   int64_t nnz, int32_t origin, int value_type,
+                                   const int32_t *rowptr,
+                                   const int32_t *colind, const void *val,
+                                   jlust_stream_t stream,
+                                   jlust_spmm_plan_t *plan_out);
+int jlust_hip_csr_spmm_plan_update_values(jlust_spmm_plan_t plan,
+                                          const void *val);
+int jlust_hip_csr_spmm_plan_execute_f64(jlust_spmm_plan_t plan, double alpha,
+                                        const double *B, int64_t ldb,
+                                        double beta, double *C, int64_t ldc,
+                                        int skip_empty_rows,
+                                        jlust_stream_t stream);
+int jlust_hip_csr_spmm_plan_execute_f32(jlust_spmm_plan_t plan, float alpha,
+                                        const float *B, int64_t ldb,
+                                        float beta, float *C, int64_t ldc,
+                                        int skip_empty_rows,
+                                        jlust_stream_t stream);
+/* What the analysis found (no counterpart in the reference; diagnostics):
+ * rows split into segments, segments, columns per pass. */
+int jlust_hip_csr_spmm_plan_info(jlust_spmm_plan_t plan, int64_t *split_rows,
+                                 int64_t *segments, int64_t *cols_per_pass);
+/* Drains the device, then frees the plan's workspace. */
+int jlust_hip_csr_spmm_plan_destroy(jlust_spmm_plan_t plan);
+
 /* ---------------------------------------------------------------- SDDMM */
 
 /*
@@ -372,6 +435,67 @@ int jlust_hip_csr_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
                                 const float *A, int64_t lda, const float *B,
                                 int64_t ldb, float beta, float *Cval,
                                 const float *mask, jlust_stream_t stream);
+
+/*
+ * SDDMM with a COO mask (rows[nnz], cols[nnz] as coo_tensor stores them;
+ * rows in any order): the same operator, outputs and mask values in the
+ * mask's storage order.  Replaces the COO case of execute(::EmitterBackend,
+ * ::Op{:SDDMM}) (ext/KernelAbstractionsExt/ops/sddmm.jl:49-65; reference
+ * answer test/test_emitter.jl:289-307).  No analysis: a group of lanes per
+ * entry reads A's row with stride lda; a prepared plan (below) puts the
+ * entries in row order once and runs the CSR kernel instead.
+ */
+int jlust_hip_coo_sddmm_f64_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                int32_t origin, const int32_t *rows,
+                                const int32_t *cols, double alpha,
+                                const double *A, int64_t lda, const double *B,
+                                int64_t ldb, double beta, double *Cval,
+                                const double *mask, jlust_stream_t stream);
+int jlust_hip_coo_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                int32_t origin, const int32_t *rows,
+                                const int32_t *cols, float alpha,
+                                const float *A, int64_t lda, const float *B,
+                                int64_t ldb, float beta, float *Cval,
+                                const float *mask, jlust_stream_t stream);
+
+/*
+ * Prepared SDDMM for a mask pattern C (m x n) and inner dimension K:
+ * prepare(backend, SDDMMOp, A, B, C) -> execute(h, A, B, C) ->
+ * update_values!(h, C), the cuSPARSE SDDMM handle contract (ext/CUDAExt/ops/
+ * sddmm.jl:10-76).  mask_format is JLUST_FORMAT_CSR (idx1 = rowptr[m+1],
+ * idx2 = colind[nnz]) or JLUST_FORMAT_COO (idx1 = rows[nnz], idx2 =
+ * cols[nnz]).  Analysis once: a COO mask is put in row order (rowptr, the
+ * columns and the permutation back to storage order, owned by the plan; a
+ * row outside [origin, m + origin) is NONCANONICAL_STORAGE); the row blocks
+ * that hold entries become work items of at most 4096 entries, so blocks
+ * without entries cost nothing and a block holding a long row is shared by
+ * several workgroups.  execute writes Cval (and reads mask) in the mask's
+ * storage order, with the semantics of jlust_hip_csr_sddmm_*; the values of
+ * C are not part of the plan, so update_values! needs no call here.  The
+ * plan keeps the caller's rowptr/colind (CSR) or cols (COO whose rows were
+ * already in order): they must outlive it.  Synchronises `stream`.
+ */
+int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64_t n,
+                                int64_t K, int64_t nnz, int32_t origin,
+                                int value_type, const int32_t *idx1,
+                                const int32_t *idx2, jlust_stream_t stream,
+                                jlust_sddmm_plan_t *plan_out);
+int jlust_hip_sddmm_plan_execute_f64(jlust_sddmm_plan_t plan, double alpha,
+                                     const double *A, int64_t lda,
+                                     const double *B, int64_t ldb, double beta,
+                                     double *Cval, const double *mask,
+                                     jlust_stream_t stream);
+int jlust_hip_sddmm_plan_execute_f32(jlust_sddmm_plan_t plan, float alpha,
+                                     const float *A, int64_t lda,
+                                     const float *B, int64_t ldb, float beta,
+                                     float *Cval, const float *mask,
+                                     jlust_stream_t stream);
+/* Work items of the plan and whether a COO mask was reordered (diagnostics;
+ * no counterpart in the reference). */
+int jlust_hip_sddmm_plan_info(jlust_sddmm_plan_t plan, int64_t *work_items,
+                              int32_t *reordered);
+/* Drains the device, then frees the plan's tables. */
+int jlust_hip_sddmm_plan_destroy(jlust_sddmm_plan_t plan);
 
 /* ------------------------------------------------------------------ BSR */
 

@@ -60,6 +60,26 @@ SIGNATURES = {
                                            _I64, _D, _P, _P, _P]),
     "jlust_hip_csr_sddmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _F, _P, _I64, _P,
                                            _I64, _F, _P, _P, _P]),
+    "jlust_hip_csr_spmm_plan_create": (_INT, [_I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
+                                              ctypes.POINTER(_P)]),
+    "jlust_hip_csr_spmm_plan_update_values": (_INT, [_P, _P]),
+    "jlust_hip_csr_spmm_plan_execute_f64": (_INT, [_P, _D, _P, _I64, _D, _P, _I64, _INT, _P]),
+    "jlust_hip_csr_spmm_plan_execute_f32": (_INT, [_P, _F, _P, _I64, _F, _P, _I64, _INT, _P]),
+    "jlust_hip_csr_spmm_plan_info": (_INT, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I64),
+                                            ctypes.POINTER(_I64)]),
+    "jlust_hip_csr_spmm_plan_destroy": (_INT, [_P]),
+    "jlust_hip_coo_sddmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _D, _P, _I64, _P,
+                                           _I64, _D, _P, _P, _P]),
+    "jlust_hip_coo_sddmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _F, _P, _I64, _P,
+                                           _I64, _F, _P, _P, _P]),
+    "jlust_hip_sddmm_plan_create": (_INT, [_I32, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P,
+                                           ctypes.POINTER(_P)]),
+    "jlust_hip_sddmm_plan_execute_f64": (_INT, [_P, _D, _P, _I64, _P, _I64, _D, _P, _P, _P]),
+    "jlust_hip_sddmm_plan_execute_f32": (_INT, [_P, _F, _P, _I64, _P, _I64, _F, _P, _P, _P]),
+    "jlust_hip_sddmm_plan_info": (_INT, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I32)]),
+    "jlust_hip_sddmm_plan_destroy": (_INT, [_P]),
+    "jlust_hip_csc_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P, _P]),
+    "jlust_hip_csc_spmv_f32_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _F, _P, _P]),
     "jlust_hip_bsr_spmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _INT, _I64, _F,
                                           _P, _I64, _F, _P, _I64, _P]),
     "jlust_hip_convert_analyze": (_INT, [_P, _I32, _I32, _I32, _I32, _INT, _P, ctypes.POINTER(_P),

@@ -68,6 +68,15 @@ constexpr int NUM_XCD = 8;   // MI355X: workgroup b runs on XCD b % 8
 // update_values.
 int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, void *val_copy);
 
+// Row order of m x n COO entries (coo_plan.hip): rowptr[m+1] (origin-based)
+// of the entries in row order and, unless the rows were already
+// non-decreasing (*sorted set, perm and cols_out untouched), perm[q] = the
+// caller's position of row-ordered entry q (a stable sort) and cols_out[q] =
+// its column.  Buffers are the caller's (perm and cols_out nnz entries); a
+// row outside [origin, m + origin) is NONCANONICAL_STORAGE.  Synchronises s.
+int coo_row_order(int64_t m, int64_t nnz, int32_t origin, const int32_t *rows, const int32_t *cols,
+                  int32_t *rowptr, int32_t *perm, int32_t *cols_out, bool *sorted, hipStream_t s);
+
 // ------------------------------------------------------------ device code
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

@@ -57,15 +57,21 @@ __global__ void coo_rowptr_kernel(int64_t nnz, const uint32_t *__restrict__ keys
     rowptr[i] = (int32_t)(lo + origin);
 }
 
-template <typename T>
-__global__ void coo_gather_kernel(int64_t nnz, const int32_t *__restrict__ perm, const int32_t *__restrict__ cols,
-                                  const T *__restrict__ val, int32_t *__restrict__ cols_out, T *__restrict__ val_out)
+__global__ void coo_gather_cols_kernel(int64_t nnz, const int32_t *__restrict__ perm,
+                                       const int32_t *__restrict__ cols, int32_t *__restrict__ cols_out)
 {
     const int64_t i = (int64_t)blockIdx.x * CP_BLOCK + threadIdx.x;
     if (i >= nnz) return;
-    const int32_t p = perm[i];
-    cols_out[i] = cols[p];
-    val_out[i] = val[p];
+    cols_out[i] = cols[perm[i]];
+}
+
+template <typename T>
+__global__ void coo_gather_kernel(int64_t nnz, const int32_t *__restrict__ perm, const T *__restrict__ val,
+                                  T *__restrict__ val_out)
+{
+    const int64_t i = (int64_t)blockIdx.x * CP_BLOCK + threadIdx.x;
+    if (i >= nnz) return;
+    val_out[i] = val[perm[i]];
 }
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
@@ -83,6 +89,54 @@ struct Mem {
 };
 
 }  // namespace
+}  // namespace jlust
+
+namespace jlust {
+
+int coo_row_order(int64_t m, int64_t nnz, int32_t origin, const int32_t *rows, const int32_t *cols,
+                  int32_t *rowptr, int32_t *perm, int32_t *cols_out, bool *sorted, hipStream_t s)
+{
+    const size_t nz = (size_t)(nnz > 0 ? nnz : 1);
+    const size_t sz_i = align256(4 * nz);
+    // Scratch: keys x2, iota, flags, sort temporary.
+    size_t sort_bytes = 0;
+    JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, sort_bytes, (uint32_t *)nullptr, (uint32_t *)nullptr,
+                                            (int32_t *)nullptr, (int32_t *)nullptr, nz, 0, bits_for(m), s));
+    Mem work;
+    JLUST_HIP_TRY(hipMalloc(&work.p, 3 * sz_i + 256 + align256(sort_bytes)));
+    char *w = (char *)work.p;
+    uint32_t *keys = (uint32_t *)w;
+    uint32_t *keys_s = (uint32_t *)(w + sz_i);
+    int32_t *iota = (int32_t *)(w + 2 * sz_i);
+    int32_t *flags = (int32_t *)(w + 3 * sz_i);
+    void *sort_tmp = w + 3 * sz_i + 256;
+    JLUST_HIP_TRY(hipMemsetAsync(flags, 0, 4, s));
+    if (nnz > 0) {
+        hipLaunchKernelGGL(coo_rows_check_kernel, dim3(cp_grid(nnz)), dim3(CP_BLOCK), 0, s, nnz, rows, origin, m,
+                           keys, iota, flags);
+        if (int st = check_launch("coo_rows_check_kernel")) return st;
+    }
+    int32_t fh = 0;
+    JLUST_HIP_TRY(hipMemcpyAsync(&fh, flags, 4, hipMemcpyDeviceToHost, s));
+    JLUST_HIP_TRY(hipStreamSynchronize(s));
+    if (fh & 1) return fail(JLUST_STATUS_NONCANONICAL_STORAGE, "COO analysis: a row index is out of range");
+    *sorted = !(fh & 2);
+    const uint32_t *sorted_keys = keys;
+    if (!*sorted) {
+        JLUST_HIP_TRY(rocprim::radix_sort_pairs(sort_tmp, sort_bytes, keys, keys_s, iota, perm, (size_t)nnz, 0,
+                                                bits_for(m), s));
+        hipLaunchKernelGGL(coo_gather_cols_kernel, dim3(cp_grid(nnz)), dim3(CP_BLOCK), 0, s, nnz, perm, cols,
+                           cols_out);
+        if (int st = check_launch("coo_gather_cols_kernel")) return st;
+        sorted_keys = keys_s;
+    }
+    hipLaunchKernelGGL(coo_rowptr_kernel, dim3(cp_grid(m + 1)), dim3(CP_BLOCK), 0, s, nnz, sorted_keys, m, origin,
+                       rowptr);
+    if (int st = check_launch("coo_rowptr_kernel")) return st;
+    JLUST_HIP_TRY(hipStreamSynchronize(s));       // the scratch is freed on return
+    return JLUST_STATUS_SUCCESS;
+}
+
 }  // namespace jlust
 
 using namespace jlust;
@@ -111,60 +165,33 @@ extern "C" int jlust_hip_coo_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
     const size_t sz_rp = align256(4 * (size_t)(m + 1));
     const size_t sz_i = align256(4 * nz);
     const size_t sz_v = align256(tsz * nz);
-    Mem own, work;
+    Mem own;
     JLUST_HIP_TRY(hipMalloc(&own.p, sz_rp + 2 * sz_i + sz_v));
     char *b = (char *)own.p;
     int32_t *rowptr = (int32_t *)b;
     int32_t *perm = (int32_t *)(b + sz_rp);
     int32_t *cols_s = (int32_t *)(b + sz_rp + sz_i);
     void *val_s = b + sz_rp + 2 * sz_i;
-    // Scratch: keys x2, iota, flags, sort temporary.
-    size_t sort_bytes = 0;
-    JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, sort_bytes, (uint32_t *)nullptr, (uint32_t *)nullptr,
-                                            (int32_t *)nullptr, (int32_t *)nullptr, nz, 0, bits_for(m), s));
-    JLUST_HIP_TRY(hipMalloc(&work.p, 3 * sz_i + 256 + align256(sort_bytes)));
-    char *w = (char *)work.p;
-    uint32_t *keys = (uint32_t *)w;
-    uint32_t *keys_s = (uint32_t *)(w + sz_i);
-    int32_t *iota = (int32_t *)(w + 2 * sz_i);
-    int32_t *flags = (int32_t *)(w + 3 * sz_i);
-    void *sort_tmp = w + 3 * sz_i + 256;
-    JLUST_HIP_TRY(hipMemsetAsync(flags, 0, 4, s));
-    if (nnz > 0) {
-        hipLaunchKernelGGL(coo_rows_check_kernel, dim3(cp_grid(nnz)), dim3(CP_BLOCK), 0, s, nnz, rows, origin, m,
-                           keys, iota, flags);
-        if (int st = check_launch("coo_rows_check_kernel")) return st;
-    }
-    int32_t fh = 0;
-    JLUST_HIP_TRY(hipMemcpyAsync(&fh, flags, 4, hipMemcpyDeviceToHost, s));
-    JLUST_HIP_TRY(hipStreamSynchronize(s));
-    if (fh & 1) return fail(JLUST_STATUS_NONCANONICAL_STORAGE, "coo_spmv_plan_create: a row index is out of range");
-    const bool sorted = !(fh & 2);
+    bool sorted = true;
+    if (int st = coo_row_order(m, nnz, origin, rows, cols, rowptr, perm, cols_s, &sorted, s)) return st;
     const int32_t *csr_cols = cols;
     const void *csr_val = val;
-    const uint32_t *sorted_keys = keys;
     if (!sorted) {
-        JLUST_HIP_TRY(rocprim::radix_sort_pairs(sort_tmp, sort_bytes, keys, keys_s, iota, perm, (size_t)nnz, 0,
-                                                bits_for(m), s));
         if (value_type == 0)
-            hipLaunchKernelGGL(coo_gather_kernel<double>, dim3(cp_grid(nnz)), dim3(CP_BLOCK), 0, s, nnz, perm, cols,
-                               (const double *)val, cols_s, (double *)val_s);
+            hipLaunchKernelGGL(coo_gather_kernel<double>, dim3(cp_grid(nnz)), dim3(CP_BLOCK), 0, s, nnz, perm,
+                               (const double *)val, (double *)val_s);
         else
-            hipLaunchKernelGGL(coo_gather_kernel<float>, dim3(cp_grid(nnz)), dim3(CP_BLOCK), 0, s, nnz, perm, cols,
-                               (const float *)val, cols_s, (float *)val_s);
+            hipLaunchKernelGGL(coo_gather_kernel<float>, dim3(cp_grid(nnz)), dim3(CP_BLOCK), 0, s, nnz, perm,
+                               (const float *)val, (float *)val_s);
         if (int st = check_launch("coo_gather_kernel")) return st;
         csr_cols = cols_s;
         csr_val = val_s;
-        sorted_keys = keys_s;
     }
-    hipLaunchKernelGGL(coo_rowptr_kernel, dim3(cp_grid(m + 1)), dim3(CP_BLOCK), 0, s, nnz, sorted_keys, m, origin,
-                       rowptr);
-    if (int st = check_launch("coo_rowptr_kernel")) return st;
     jlust_spmv_plan_t plan = nullptr;
     if (int st = jlust_hip_csr_spmv_plan_create(m, n, nnz, origin, value_type, rowptr, csr_cols, csr_val, stream,
                                                 &plan))
         return st;
-    JLUST_HIP_TRY(hipStreamSynchronize(s));       // the sort's scratch is freed on return
+    JLUST_HIP_TRY(hipStreamSynchronize(s));
     spmv_plan_adopt_coo(plan, own.p, sorted ? nullptr : perm, sorted ? nullptr : val_s);
     own.p = nullptr;
     *plan_out = plan;

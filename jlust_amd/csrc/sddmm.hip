@@ -18,10 +18,15 @@
 // each group takes U nonzeros per step with their loads issued together
 // (indices clamped into the block's nonzeros, results of the clamped copies
 // dropped), so K = 1 puts 64 nonzeros on a wave per load instead of 8.
+#include <memory>
+#include <vector>
+
 #include "common.hpp"
 
 namespace jlust {
 namespace {
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 constexpr int SD_BLOCK = 256;
 constexpr int SD_GROUP = 8;
@@ -48,7 +53,8 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     int64_t m, int64_t K, int32_t origin, const int32_t *__restrict__ rowptr,
     const int32_t *__restrict__ colind, T alpha, const T *__restrict__ A, int64_t lda,
     const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval,
-    const T *mask, int R, int64_t lds_ld)
+    const T *mask, int R, int64_t lds_ld, const int32_t *__restrict__ items, int64_t chunk,
+    const int32_t *__restrict__ perm)
 {
     static_assert(ONE || U == 1, "several nonzeros per group need one step over K");
     constexpr int GROUPS = SD_BLOCK / G;
@@ -60,7 +66,11 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     const int tid = threadIdx.x;
     const int g = tid / G;                   // group in block
     const int q = tid % G;                   // lane in group
-    const int64_t i0 = (int64_t)blockIdx.x * R;
+    // A plan's work item: (row block, part) -- the part-th run of `chunk`
+    // nonzeros of that block; without items, block b is row block b whole.
+    const int64_t rb = items ? items[2 * (int64_t)blockIdx.x] : (int64_t)blockIdx.x;
+    const int64_t part = items ? items[2 * (int64_t)blockIdx.x + 1] : 0;
+    const int64_t i0 = rb * R;
     const int nr = (int)min((int64_t)R, m - i0);
 
     for (int r = tid; r <= nr; r += SD_BLOCK) s_rp[r] = rowptr[i0 + r] - origin;
@@ -71,7 +81,11 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     }
     __syncthreads();
 
-    const int p_lo = s_rp[0], p_hi = s_rp[nr];
+    int64_t p_lo = s_rp[0], p_hi = s_rp[nr];
+    if (items) {
+        p_lo += part * chunk;
+        p_hi = min(p_hi, p_lo + chunk);
+    }
     // This lane's slice of K in the one-step case, clamped into range.
     const int64_t k1 = (int64_t)q * NE;
     const bool k1_ok = k1 < K;
@@ -140,10 +154,11 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
             for (int u = 0; u < U; ++u) {
                 const int64_t p = p0 + u * GROUPS;
                 if (p < p_hi) {
+                    const int64_t o = perm ? (int64_t)perm[p] : p;   // output position
                     T out = alpha * dot[u];
-                    if (mask) out = mask[p] * out;
-                    if (!beta_zero) out += beta * Cval[p];
-                    Cval[p] = out;
+                    if (mask) out = mask[o] * out;
+                    if (!beta_zero) out += beta * Cval[o];
+                    Cval[o] = out;
                 }
             }
         }
@@ -155,7 +170,8 @@ template <typename T>
 __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_direct_kernel(
     int64_t m, int64_t K, int32_t origin, const int32_t *__restrict__ rowptr,
     const int32_t *__restrict__ colind, T alpha, const T *__restrict__ A, int64_t lda,
-    const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval, const T *mask)
+    const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval, const T *mask,
+    const int32_t *__restrict__ perm)
 {
     const int64_t i = blockIdx.x;
     if (i >= m) return;
@@ -167,53 +183,75 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_direct_kernel(
         for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
         dot = group_sum<SD_GROUP>(dot);
         if (q == 0) {
+            const int64_t o = perm ? (int64_t)perm[p] : p;
             T out = alpha * dot;
-            if (mask) out = mask[p] * out;
-            if (!beta_zero) out += beta * Cval[p];
-            Cval[p] = out;
+            if (mask) out = mask[o] * out;
+            if (!beta_zero) out += beta * Cval[o];
+            Cval[o] = out;
         }
     }
 }
 
+// COO mask, no analysis (the plain COO SDDMM call): a group of SD_GROUP
+// lanes per stored entry in storage order, A's row read with stride lda.
 template <typename T>
-int csr_sddmm(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin,
-              const int32_t *rowptr, const int32_t *colind, T alpha, const T *A, int64_t lda,
-              const T *B, int64_t ldb, T beta, T *Cval, const T *mask, jlust_stream_t stream)
+__global__ __launch_bounds__(SD_BLOCK) void coo_sddmm_kernel(
+    int64_t nnz, int64_t K, int32_t origin, const int32_t *__restrict__ rows,
+    const int32_t *__restrict__ cols, T alpha, const T *__restrict__ A, int64_t lda,
+    const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval, const T *mask)
 {
-    clear_error();
-    if (m < 0 || n < 0 || K < 0 || nnz < 0)
-        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_sddmm: negative extent");
-    if (m > INT32_MAX || n > INT32_MAX || nnz > INT32_MAX)
-        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_sddmm: extents exceed the Int32 index range");
-    if (int st = check_origin(origin)) return st;
-    if (lda < (m > 0 ? m : 1) || ldb < (K > 0 ? K : 1))
-        return fail(JLUST_STATUS_INVALID_ARGUMENT,
-                    "csr_sddmm: leading dimensions too small (lda=%lld < m=%lld or ldb=%lld < K=%lld)",
-                    (long long)lda, (long long)m, (long long)ldb, (long long)K);
-    if ((m > 0 && !rowptr) || bad_ptr(colind, nnz) || bad_ptr(Cval, nnz) ||
-        bad_ptr(A, (nnz > 0 && K > 0) ? m : 0) || bad_ptr(B, (nnz > 0 && K > 0) ? n : 0))
-        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_sddmm: null device pointer");
-    if (int st = require_device(nullptr)) return st;
-    if (m == 0 || nnz == 0) return JLUST_STATUS_SUCCESS;
-    hipStream_t s = (hipStream_t)stream;
+    const int g = threadIdx.x / SD_GROUP, q = threadIdx.x % SD_GROUP;
+    const int64_t p = (int64_t)blockIdx.x * SD_GROUPS + g;
+    if (p >= nnz) return;
+    const int64_t i = (int64_t)rows[p] - origin, j = (int64_t)cols[p] - origin;
+    T dot = T(0);
+    for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
+    dot = group_sum<SD_GROUP>(dot);
+    if (q == 0) {
+        T out = alpha * dot;
+        if (mask) out = mask[p] * out;
+        if (!beta_zero) out += beta * Cval[p];
+        Cval[p] = out;
+    }
+}
+
+// Rows per block for A's staging: as many (up to 32) as fit the LDS budget
+// with rows padded to 16 bytes; 0 = K too large, the direct kernel runs.
+template <typename T>
+int sddmm_rows(int64_t K, int64_t *lds_ld)
+{
+    constexpr int N = V16<T>::N;
+    *lds_ld = (K + N - 1) / N * N + N;       // padded, keeps rows 16-byte aligned
+    int64_t R = (int64_t)((SD_LDS_BUDGET - 64 * sizeof(int32_t)) / (sizeof(T) * (size_t)*lds_ld));
+    return (int)(R > 32 ? 32 : R);
+}
+
+// The SDDMM launch over the CSR pattern (rowptr, colind), plain or from a
+// plan: items/chunk cut row blocks into runs of nonzeros (null: one block per
+// row block), perm maps CSR positions to the output's (null: identity).
+template <typename T>
+int sddmm_launch(int64_t m, int64_t K, int32_t origin, const int32_t *rowptr, const int32_t *colind, T alpha,
+                 const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *Cval, const T *mask,
+                 const int32_t *items, int64_t nitems, int64_t chunk, const int32_t *perm, hipStream_t s)
+{
     const int bz = beta == T(0);
     constexpr int N = V16<T>::N;
-    const int64_t lds_ld = (K + N - 1) / N * N + N;       // padded, keeps rows 16-byte aligned
-    int R = (int)((SD_LDS_BUDGET - 64 * sizeof(int32_t)) / (sizeof(T) * (size_t)lds_ld));
-    if (R > 32) R = 32;
+    int64_t lds_ld = 0;
+    const int R = sddmm_rows<T>(K, &lds_ld);
     if (R < 1) {
         hipLaunchKernelGGL((csr_sddmm_direct_kernel<T>), dim3((unsigned)m), dim3(SD_BLOCK), 0, s, m,
-                           K, origin, rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask);
+                           K, origin, rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, perm);
         return check_launch("csr_sddmm_direct_kernel");
     }
     const bool vecb = (K % N == 0) && (ldb % N == 0) && (((uintptr_t)B) % 16 == 0);
     const size_t smem = sizeof(T) * (size_t)R * (size_t)lds_ld + sizeof(int32_t) * (size_t)(R + 1);
-    const dim3 grid((unsigned)((m + R - 1) / R));
+    const dim3 grid((unsigned)(items ? nitems : (m + R - 1) / R));
     // Lane loads that cover K: G = the smallest power of two >= that, up to 8.
     const int64_t slices = vecb ? K / N : K;
 #define JLUST_SD(V, G, U, ONE)                                                                        \
     hipLaunchKernelGGL((csr_sddmm_kernel<T, V, G, U, ONE>), grid, dim3(SD_BLOCK), smem, s, m, K, origin, \
-                       rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, R, lds_ld)
+                       rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, R, lds_ld, items,  \
+                       chunk, perm)
 #define JLUST_SD_V(V)                                                                                 \
     do {                                                                                              \
         if (slices == 0) JLUST_SD(V, 8, 1, false);     /* K = 0: no loads of B at all */             \
@@ -228,6 +266,63 @@ int csr_sddmm(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin,
 #undef JLUST_SD_V
 #undef JLUST_SD
     return check_launch("csr_sddmm_kernel");
+}
+
+int check_sddmm_dense(const char *who, int64_t m, int64_t n, int64_t K, int64_t nnz, const void *A, int64_t lda,
+                      const void *B, int64_t ldb, const void *Cval)
+{
+    if (lda < (m > 0 ? m : 1) || ldb < (K > 0 ? K : 1))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "%s: leading dimensions too small (lda=%lld < m=%lld or ldb=%lld < K=%lld)", who,
+                    (long long)lda, (long long)m, (long long)ldb, (long long)K);
+    if (bad_ptr(Cval, nnz) || bad_ptr(A, (nnz > 0 && K > 0) ? m : 0) || bad_ptr(B, (nnz > 0 && K > 0) ? n : 0))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "%s: null device pointer", who);
+    return JLUST_STATUS_SUCCESS;
+}
+
+int check_sddmm_extents(const char *who, int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin)
+{
+    if (m < 0 || n < 0 || K < 0 || nnz < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "%s: negative extent", who);
+    if (m > INT32_MAX - 1 || n > INT32_MAX || nnz > INT32_MAX - 1)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "%s: extents exceed the Int32 index range", who);
+    return check_origin(origin);
+}
+
+template <typename T>
+int csr_sddmm(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin,
+              const int32_t *rowptr, const int32_t *colind, T alpha, const T *A, int64_t lda,
+              const T *B, int64_t ldb, T beta, T *Cval, const T *mask, jlust_stream_t stream)
+{
+    clear_error();
+    if (int st = check_sddmm_extents("csr_sddmm", m, n, K, nnz, origin)) return st;
+    if (int st = check_sddmm_dense("csr_sddmm", m, n, K, nnz, A, lda, B, ldb, Cval)) return st;
+    if ((m > 0 && !rowptr) || bad_ptr(colind, nnz))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "csr_sddmm: null device pointer");
+    if (int st = require_device(nullptr)) return st;
+    if (m == 0 || nnz == 0) return JLUST_STATUS_SUCCESS;
+    return sddmm_launch<T>(m, K, origin, rowptr, colind, alpha, A, lda, B, ldb, beta, Cval, mask, nullptr, 0, 0,
+                           nullptr, (hipStream_t)stream);
+}
+
+template <typename T>
+int coo_sddmm(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin, const int32_t *rows,
+              const int32_t *cols, T alpha, const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *Cval,
+              const T *mask, jlust_stream_t stream)
+{
+    clear_error();
+    if (int st = check_sddmm_extents("coo_sddmm", m, n, K, nnz, origin)) return st;
+    if (int st = check_sddmm_dense("coo_sddmm", m, n, K, nnz, A, lda, B, ldb, Cval)) return st;
+    if (bad_ptr(rows, nnz) || bad_ptr(cols, nnz))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "coo_sddmm: null device pointer");
+    if (nnz > 0 && (m == 0 || n == 0))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "coo_sddmm: entries in an empty matrix");
+    if (int st = require_device(nullptr)) return st;
+    if (nnz == 0) return JLUST_STATUS_SUCCESS;
+    hipLaunchKernelGGL((coo_sddmm_kernel<T>), dim3((unsigned)((nnz + SD_GROUPS - 1) / SD_GROUPS)), dim3(SD_BLOCK),
+                       0, (hipStream_t)stream, nnz, K, origin, rows, cols, alpha, A, lda, B, ldb, beta,
+                       (int)(beta == T(0)), Cval, mask);
+    return check_launch("coo_sddmm_kernel");
 }
 
 }  // namespace
@@ -253,4 +348,202 @@ extern "C" int jlust_hip_csr_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int6
 {
     return csr_sddmm<float>(m, n, K, nnz, origin, rowptr, colind, alpha, A, lda, B, ldb, beta,
                             Cval, mask, stream);
+}
+
+extern "C" int jlust_hip_coo_sddmm_f64_i32(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin,
+                                           const int32_t *rows, const int32_t *cols, double alpha,
+                                           const double *A, int64_t lda, const double *B, int64_t ldb,
+                                           double beta, double *Cval, const double *mask, jlust_stream_t stream)
+{
+    return coo_sddmm<double>(m, n, K, nnz, origin, rows, cols, alpha, A, lda, B, ldb, beta, Cval, mask, stream);
+}
+
+extern "C" int jlust_hip_coo_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin,
+                                           const int32_t *rows, const int32_t *cols, float alpha,
+                                           const float *A, int64_t lda, const float *B, int64_t ldb,
+                                           float beta, float *Cval, const float *mask, jlust_stream_t stream)
+{
+    return coo_sddmm<float>(m, n, K, nnz, origin, rows, cols, alpha, A, lda, B, ldb, beta, Cval, mask, stream);
+}
+
+// ------------------------------------------------------------------- plans
+
+// A prepared SDDMM (the cuSPARSE SDDMM handle contract, ext/CUDAExt/ops/
+// sddmm.jl:10-76).  Analysis: the mask in CSR order (a COO mask is put in row
+// order once: rowptr, columns and the permutation back to its storage order,
+// so outputs and mask values stay in the caller's order), then the work
+// items: every row block of R rows holding nonzeros, cut into runs of at
+// most SD_CHUNK nonzeros.  Row blocks without nonzeros get no item (their A
+// rows are never read), and a block holding a very long row is shared by
+// several workgroups instead of one.
+constexpr int64_t SD_CHUNK = 4096;
+
+struct jlust_sddmm_plan {
+    int64_t m = 0, n = 0, K = 0, nnz = 0;
+    int32_t origin = 0;
+    int value_type = 0;
+    int device = 0;
+    const int32_t *rowptr = nullptr;   // CSR order: the caller's, or owned (COO)
+    const int32_t *colind = nullptr;
+    const int32_t *perm = nullptr;     // output position of CSR position q (null: q)
+    int32_t *items = nullptr;          // [2 * nitems] (row block, part)
+    int64_t nitems = 0;
+    void *mem = nullptr;
+};
+
+extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                           int32_t origin, int value_type, const int32_t *idx1,
+                                           const int32_t *idx2, jlust_stream_t stream,
+                                           jlust_sddmm_plan_t *plan_out)
+{
+    clear_error();
+    if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: null plan_out");
+    *plan_out = nullptr;
+    if (value_type != 0 && value_type != 1)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE,
+                    "sddmm_plan_create: value_type %d (0 = Float64, 1 = Float32)", value_type);
+    if (mask_format != JLUST_FORMAT_CSR && mask_format != JLUST_FORMAT_COO)
+        return fail(JLUST_STATUS_UNSUPPORTED_FORMAT, "sddmm_plan_create: the mask must be CSR or COO");
+    if (int st = check_sddmm_extents("sddmm_plan_create", m, n, K, nnz, origin)) return st;
+    const bool coo = mask_format == JLUST_FORMAT_COO;
+    if ((!coo && m > 0 && !idx1) || (coo && bad_ptr(idx1, nnz)) || bad_ptr(idx2, nnz))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: null device pointer");
+    if (nnz > 0 && (m == 0 || n == 0))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: entries in an empty matrix");
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    hipStream_t s = (hipStream_t)stream;
+    std::unique_ptr<jlust_sddmm_plan> p(new jlust_sddmm_plan());
+    p->m = m;
+    p->n = n;
+    p->K = K;
+    p->nnz = nnz;
+    p->origin = origin;
+    p->value_type = value_type;
+    p->device = dev;
+    p->rowptr = idx1;
+    p->colind = idx2;
+    int64_t lds_ld = 0;
+    const int R = value_type == 0 ? sddmm_rows<double>(K, &lds_ld) : sddmm_rows<float>(K, &lds_ld);
+    const int64_t nblk = R >= 1 ? (m + R - 1) / R : 0;
+    const size_t nz = (size_t)(nnz > 0 ? nnz : 1);
+    // Owned: [rowptr, perm, columns (COO)], items (at most 2 per block plus
+    // one per SD_CHUNK nonzeros).
+    const size_t sz_rp = coo ? align_up(4 * (size_t)(m + 1), 256) : 0;
+    const size_t sz_i = coo ? align_up(4 * nz, 256) : 0;
+    const int64_t max_items = nblk + nnz / SD_CHUNK + 1;
+    const size_t sz_items = align_up(8 * (size_t)max_items, 256);
+    JLUST_HIP_TRY(hipMalloc(&p->mem, sz_rp + 2 * sz_i + sz_items));
+    char *b = (char *)p->mem;
+    int st = JLUST_STATUS_SUCCESS;
+    if (coo) {
+        int32_t *rowptr = (int32_t *)b;
+        int32_t *perm = (int32_t *)(b + sz_rp);
+        int32_t *cols_s = (int32_t *)(b + sz_rp + sz_i);
+        bool sorted = true;
+        st = coo_row_order(m, nnz, origin, idx1, idx2, rowptr, perm, cols_s, &sorted, s);
+        p->rowptr = rowptr;
+        if (!sorted) {
+            p->perm = perm;
+            p->colind = cols_s;
+        }
+    }
+    p->items = (int32_t *)(b + sz_rp + 2 * sz_i);
+    // Work items from the row pointers of each row block (host analysis).
+    if (!st && R >= 1 && m > 0) {
+        std::vector<int32_t> rp((size_t)(m + 1));
+        hipError_t e = hipMemcpyAsync(rp.data(), p->rowptr, sizeof(int32_t) * (size_t)(m + 1),
+                                      hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) st = hip_fail(e, "sddmm_plan_create: rowptr copy");
+        if (!st && ((int64_t)rp[0] != origin || (int64_t)rp[m] - origin != nnz))
+            st = fail(JLUST_STATUS_NONCANONICAL_STORAGE,
+                      "sddmm_plan_create: rowptr runs from %d to %d, expected %d to %lld", rp[0], rp[m], origin,
+                      (long long)(nnz + origin));
+        std::vector<int32_t> items;
+        for (int64_t rb = 0; !st && rb < nblk; ++rb) {
+            const int64_t r1 = min((rb + 1) * (int64_t)R, m);
+            const int64_t cnt = (int64_t)rp[r1] - rp[rb * R];
+            if (cnt < 0) {
+                st = fail(JLUST_STATUS_NONCANONICAL_STORAGE, "sddmm_plan_create: rowptr decreases near row %lld",
+                          (long long)(rb * R));
+                break;
+            }
+            for (int64_t part = 0; part * SD_CHUNK < cnt; ++part) {
+                items.push_back((int32_t)rb);
+                items.push_back((int32_t)part);
+            }
+        }
+        p->nitems = (int64_t)items.size() / 2;
+        if (!st && p->nitems > max_items) st = fail(JLUST_STATUS_HIP_ERROR, "sddmm_plan_create: item overflow");
+        if (!st && p->nitems > 0) {
+            e = hipMemcpyAsync(p->items, items.data(), sizeof(int32_t) * items.size(), hipMemcpyHostToDevice, s);
+            if (e == hipSuccess) e = hipStreamSynchronize(s);
+            if (e != hipSuccess) st = hip_fail(e, "sddmm_plan_create: item upload");
+        }
+    }
+    if (st) {
+        (void)hipStreamSynchronize(s);
+        (void)hipFree(p->mem);
+        return st;
+    }
+    *plan_out = p.release();
+    return JLUST_STATUS_SUCCESS;
+}
+
+template <typename T>
+static int sddmm_plan_execute(jlust_sddmm_plan_t p, int want_type, T alpha, const T *A, int64_t lda, const T *B,
+                              int64_t ldb, T beta, T *Cval, const T *mask, jlust_stream_t stream)
+{
+    clear_error();
+    if (!p) return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_execute: null plan");
+    if (p->value_type != want_type)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE, "sddmm_plan_execute: plan was created for %s values",
+                    p->value_type == 0 ? "Float64" : "Float32");
+    if (int st = check_sddmm_dense("sddmm_plan_execute", p->m, p->n, p->K, p->nnz, A, lda, B, ldb, Cval)) return st;
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    if (dev != p->device)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "sddmm_plan_execute: plan belongs to device %d, current device is %d", p->device, dev);
+    if (p->m == 0 || p->nnz == 0) return JLUST_STATUS_SUCCESS;
+    return sddmm_launch<T>(p->m, p->K, p->origin, p->rowptr, p->colind, alpha, A, lda, B, ldb, beta, Cval, mask,
+                           p->nitems > 0 ? p->items : nullptr, p->nitems, SD_CHUNK, p->perm, (hipStream_t)stream);
+}
+
+extern "C" int jlust_hip_sddmm_plan_execute_f64(jlust_sddmm_plan_t plan, double alpha, const double *A,
+                                                int64_t lda, const double *B, int64_t ldb, double beta,
+                                                double *Cval, const double *mask, jlust_stream_t stream)
+{
+    return sddmm_plan_execute<double>(plan, 0, alpha, A, lda, B, ldb, beta, Cval, mask, stream);
+}
+
+extern "C" int jlust_hip_sddmm_plan_execute_f32(jlust_sddmm_plan_t plan, float alpha, const float *A,
+                                                int64_t lda, const float *B, int64_t ldb, float beta,
+                                                float *Cval, const float *mask, jlust_stream_t stream)
+{
+    return sddmm_plan_execute<float>(plan, 1, alpha, A, lda, B, ldb, beta, Cval, mask, stream);
+}
+
+extern "C" int jlust_hip_sddmm_plan_info(jlust_sddmm_plan_t plan, int64_t *work_items, int32_t *reordered)
+{
+    clear_error();
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_info: null plan");
+    if (work_items) *work_items = plan->nitems;
+    if (reordered) *reordered = plan->perm != nullptr;
+    return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_sddmm_plan_destroy(jlust_sddmm_plan_t plan)
+{
+    clear_error();
+    if (!plan) return JLUST_STATUS_SUCCESS;
+    hipError_t e = hipDeviceSynchronize();          // queued executes may still read the tables
+    if (plan->mem) {
+        const hipError_t e2 = hipFree(plan->mem);
+        if (e == hipSuccess) e = e2;
+    }
+    delete plan;
+    if (e != hipSuccess) return hip_fail(e, "sddmm_plan_destroy");
+    return JLUST_STATUS_SUCCESS;
 }

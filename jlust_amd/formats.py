@@ -209,6 +209,14 @@ def is_csr_shaped(fmt: TensorFormat) -> bool:
         isinstance(lv[1], CompressedLevel) and lv[1].unique
 
 
+def is_csc_shaped(fmt: TensorFormat) -> bool:
+    """Dense outer over columns + unique compressed inner over rows: the
+    column-outer shape the reference walks in scatter mode (spmv.jl:104-112)."""
+    lv = fmt.levels
+    return fmt.family == "CSC" and len(lv) == 2 and isinstance(lv[0], DenseLevel) and \
+        isinstance(lv[1], CompressedLevel) and lv[1].unique
+
+
 def is_coo_shaped(fmt: TensorFormat) -> bool:
     """Non-unique compressed outer + singleton inner (spmv.jl:382-384)."""
     lv = fmt.levels

@@ -15,7 +15,7 @@ import torch
 from . import _lib
 from .errors import (DeviceMismatch, IncompatibleExtents, NonCanonicalStorage,
                      UnsupportedFormat, UnsupportedIndexType, UnsupportedValueType)
-from .formats import (Formats, bsr_blocksize, is_bsr, is_coo_shaped, is_csr_shaped,
+from .formats import (Formats, bsr_blocksize, is_bsr, is_coo_shaped, is_csc_shaped, is_csr_shaped,
                       is_periodic_csr, is_shifted_diag)
 from .ops import AbstractKernelHandle, HIPBackend, Op, SDDMMOp, SpMMOp, SpMVOp
 from .tensor import USTensor, dense_matrix, leading_dim, nnz, nonzeros, ust
@@ -54,8 +54,8 @@ def supports(op: Op) -> bool:
 def _supports(op: Op) -> bool:
     f = op.formats
     if op.tag == "SpMV" and len(f) == 3:
-        return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_shifted_diag(f[0]) or
-                f[0] == Formats.DCSR or is_periodic_csr(f[0])) and \
+        return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_csc_shaped(f[0]) or
+                is_shifted_diag(f[0]) or f[0] == Formats.DCSR or is_periodic_csr(f[0])) and \
             _dense_fmt(f[1]) and \
             _dense_fmt(f[2]) and f[1].ndims == 1 and f[2].ndims == 1
     if op.tag == "SpMM" and len(f) == 3:
@@ -64,7 +64,7 @@ def _supports(op: Op) -> bool:
         return a_ok and _dense_fmt(f[1]) and _dense_fmt(f[2]) and f[1].ndims == 2 and \
             f[2].ndims == 2
     if op.tag == "SDDMM" and len(f) == 3:
-        return _dense_fmt(f[0]) and _dense_fmt(f[1]) and is_csr_shaped(f[2])
+        return _dense_fmt(f[0]) and _dense_fmt(f[1]) and (is_csr_shaped(f[2]) or is_coo_shaped(f[2]))
     return False
 
 
@@ -145,11 +145,12 @@ def spmv_with_fns(spmv, u_A, u_x, u_y, alpha=1.0, beta=0.0, input_fn=None, outpu
     if is_identity(input_fn) and is_identity(output_fn):
         return spmv(u_A, u_x, u_y, alpha, beta)
     x, y = _vec_checks(u_A, u_x, u_y)
-    if not is_identity(output_fn) and is_coo_shaped(u_A.format):
+    if not is_identity(output_fn) and (is_coo_shaped(u_A.format) or is_csc_shaped(u_A.format)):
         # The reference rejects output_fn where rows are accumulated by atomics
-        # (spmv.jl:394-399); COO's row sums are such atomics here.
+        # (scatter mode, spmv.jl:394-399); COO's and CSC's row sums are such
+        # atomics here.
         raise UnsupportedFormat(u_A.format, _BE,
-                                "output_fn is unsupported for COO SpMV; convert A to CSR first")
+                                f"output_fn is unsupported for {u_A.format.name} SpMV; convert A to CSR first")
     if not is_identity(input_fn):
         x2 = torch.empty_like(x)
         apply_fn(input_fn, x, x2)
@@ -201,10 +202,22 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
                 _ptr(nonzeros(u_A)), float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
         _lib.check(st, "csr_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
         return u_y
-    rows, cols = u_A.crd_buffers[0], u_A.crd_buffers[1]
-    _check_index(u_A, rows, cols)
-    if rows.numel() != nnz(u_A) or cols.numel() != nnz(u_A):
-        raise NonCanonicalStorage("COO coordinate buffers must have nnz entries")
+    if is_csc_shaped(u_A.format):
+        colptr, rowind = u_A.pos_buffers[1], u_A.crd_buffers[1]
+        if colptr is None or rowind is None:
+            raise NonCanonicalStorage("CSC: missing level-2 pos/crd buffer")
+        _check_index(u_A, colptr, rowind)
+        if colptr.numel() != n + 1 or rowind.numel() != nnz(u_A):
+            raise NonCanonicalStorage(f"CSC: colptr needs n+1 = {n + 1} entries (got {colptr.numel()}) "
+                                      f"and rowind nnz = {nnz(u_A)} (got {rowind.numel()})")
+        dev = _check_same_device(colptr, rowind, nonzeros(u_A), x, y)
+        with _on(dev):
+            st = getattr(L, f"jlust_hip_csc_spmv_{suf}_i32")(
+                m, n, nnz(u_A), u_A.origin.offset, _ptr(colptr), _ptr(rowind), _ptr(nonzeros(u_A)),
+                float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
+        _lib.check(st, "csc_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
+        return u_y
+    rows, cols = _coo_parts(u_A)
     dev = _check_same_device(rows, cols, nonzeros(u_A), x, y)
     with _on(dev):
         st = getattr(L, f"jlust_hip_coo_spmv_{suf}_i32")(
@@ -212,6 +225,16 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
             float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
     _lib.check(st, "coo_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
     return u_y
+
+
+def _coo_parts(u: USTensor):
+    rows, cols = u.crd_buffers[0], u.crd_buffers[1]
+    if rows is None or cols is None:
+        raise NonCanonicalStorage("COO: missing coordinate buffers")
+    _check_index(u, rows, cols)
+    if rows.numel() != nnz(u) or cols.numel() != nnz(u):
+        raise NonCanonicalStorage("COO coordinate buffers must have nnz entries")
+    return rows, cols
 
 
 def _periodic_spmv(u_A: USTensor, x: torch.Tensor, y: torch.Tensor, alpha, beta):
@@ -326,6 +349,36 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
 def _sddmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, mask=None):
     suf = _value_suffix(u_C)
     T = nonzeros(u_C).dtype
+    A, B = _sddmm_dense_checks(u_A, u_B, u_C)
+    m, n = u_C.extents
+    K = A.shape[1]
+    coo = is_coo_shaped(u_C.format)
+    idx1, idx2 = _coo_parts(u_C) if coo else _csr_parts(u_C)
+    mk = _sddmm_mask(mask, u_C, T)
+    dev = _check_same_device(idx1, idx2, nonzeros(u_C), A, B, mk)
+    entry = f"jlust_hip_{'coo' if coo else 'csr'}_sddmm_{suf}_i32"
+    with _on(dev):
+        st = getattr(_lib.lib(), entry)(
+            m, n, K, nnz(u_C), u_C.origin.offset, _ptr(idx1), _ptr(idx2), float(alpha),
+            _ptr(A), leading_dim(A), _ptr(B), leading_dim(B), float(beta), _ptr(nonzeros(u_C)),
+            _ptr(mk), _stream(dev))
+    _lib.check(st, entry[10:], u_C.format, _BE, T)
+    return u_C
+
+
+def _sddmm_mask(mask, u_C: USTensor, T):
+    """The optional S_ij factor: nnz(C) contiguous values of C's type, in
+    C's storage order (a USTensor's values or a plain tensor)."""
+    if mask is None:
+        return None
+    mk = nonzeros(mask) if isinstance(mask, USTensor) else mask
+    if mk.dtype != T or mk.numel() != nnz(u_C) or not mk.is_contiguous():
+        raise IncompatibleExtents("SDDMM: mask must hold nnz(C) contiguous values of C's type")
+    return mk
+
+
+def _sddmm_dense_checks(u_A: USTensor, u_B: USTensor, u_C: USTensor):
+    T = nonzeros(u_C).dtype
     A, B = nonzeros(u_A), nonzeros(u_B)
     if A.dtype != T or B.dtype != T:
         raise UnsupportedValueType(A.dtype if A.dtype != T else B.dtype, _BE)
@@ -337,21 +390,7 @@ def _sddmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, mask=None):
     for t, nm in ((A, "A"), (B, "B")):
         if t.shape[0] > 1 and t.shape[1] > 0 and t.stride(0) != 1:
             raise NonCanonicalStorage(f"SDDMM: {nm} must be column-major (stride(0) == 1)")
-    K = A.shape[1]
-    rowptr, colind = _csr_parts(u_C)
-    mk = None
-    if mask is not None:
-        mk = nonzeros(mask) if isinstance(mask, USTensor) else mask
-        if mk.dtype != T or mk.numel() != nnz(u_C) or not mk.is_contiguous():
-            raise IncompatibleExtents("SDDMM: mask must hold nnz(C) contiguous values of C's type")
-    dev = _check_same_device(rowptr, colind, nonzeros(u_C), A, B, mk)
-    with _on(dev):
-        st = getattr(_lib.lib(), f"jlust_hip_csr_sddmm_{suf}_i32")(
-            m, n, K, nnz(u_C), u_C.origin.offset, _ptr(rowptr), _ptr(colind), float(alpha),
-            _ptr(A), leading_dim(A), _ptr(B), leading_dim(B), float(beta), _ptr(nonzeros(u_C)),
-            _ptr(mk), _stream(dev))
-    _lib.check(st, "csr_sddmm", u_C.format, _BE, T)
-    return u_C
+    return A, B
 
 
 # -------------------------------------------------------------------- handles
@@ -606,23 +645,21 @@ class SpMVGraph:
 
 
 class HIPOpHandle(AbstractKernelHandle):
-    """Prepared SpMM / SDDMM: holds A (or the mask pattern C) and dispatches to
-    the plain entry points, the contract of the cuSPARSE SpMM/SDDMM handles
-    (ext/CUDAExt/ops/spmm.jl:8-70, sddmm.jl:10-76)."""
+    """Prepared SpMV / SpMM of the formats without a plan of their own (DCSR,
+    ShiftedDiag, PeriodicCSR, BSR): holds A and dispatches to the plain entry
+    points, the contract of the cuSPARSE handles (ext/CUDAExt/ops/
+    spmm.jl:8-70)."""
 
     def __init__(self, optype, u_A: USTensor, **kw):
         self.optype, self.u_A, self.kw = optype, u_A, kw
         _value_suffix(u_A)
 
     def execute(self, *ts, **kw):
-        """execute(h, x, y) / execute(h, A, x, y) for SpMV and SpMM (A given
-        at the call wins, as EmitterSpMVHandle takes it per call), and
-        execute(h, A, B[, C]) for SDDMM; keywords given at prepare apply."""
+        """execute(h, x, y) / execute(h, A, x, y): A given at the call wins,
+        as EmitterSpMVHandle takes it per call; keywords given at prepare
+        apply."""
         from .ops import execute as _execute
         kw = {**self.kw, **kw}
-        if self.optype.tag == "SDDMM":
-            a, b, c = ts if len(ts) == 3 else (*ts, self.u_A)
-            return _execute(self.optype, a, b, c, backend=_BE, **kw)
         if len(ts) == 3:
             return _execute(self.optype, *ts, backend=_BE, **kw)
         return _execute(self.optype, self.u_A, *ts, backend=_BE, **kw)
@@ -635,14 +672,230 @@ class HIPOpHandle(AbstractKernelHandle):
         return self
 
 
-def prepare(optype, u_A: USTensor, **kw):
-    if optype is SpMVOp or getattr(optype, "tag", None) == "SpMV":
+class HIPSpMMHandle(AbstractKernelHandle):
+    """Prepared CSR SpMM (jlust_hip_csr_spmm_plan_*): prepare(HIPBackend(),
+    SpMMOp, A; n_cols=k) -> execute(h, B, C) -> update_values!(h, A), the
+    cuSPARSE SpMM handle contract (ext/CUDAExt/ops/spmm.jl:8-70).  The plan
+    analyses A once (column chunk per pass for k, long rows split into
+    segments) and owns the workspace.  It reads A's values in place, so
+    values written into them are seen; update_values_ or execute(h, A, B, C)
+    with another value tensor points the plan at it.  B with another number
+    of columns than the plan's rebuilds the plan."""
+
+    def __init__(self, u_A: USTensor, n_cols=None, skip_empty_rows=False):
+        if not is_csr_shaped(u_A.format):
+            raise UnsupportedFormat(u_A.format, _BE, "prepared SpMM plans take CSR")
+        self.suf = _value_suffix(u_A)
+        self.T = nonzeros(u_A).dtype
+        rowptr, colind = _csr_parts(u_A)
+        self.dev = _check_same_device(rowptr, colind, nonzeros(u_A))
+        self.u_A = u_A
+        self.skip_empty_rows = bool(skip_empty_rows)
+        self._plan = ctypes.c_void_p(0)
+        self.k = None
+        if n_cols is not None:
+            self._make(int(n_cols))
+
+    def _make(self, k: int):
+        self._destroy()
+        m, n = self.u_A.extents
+        rowptr, colind = _csr_parts(self.u_A)
+        plan = ctypes.c_void_p(0)
+        with _on(self.dev):
+            st = _lib.lib().jlust_hip_csr_spmm_plan_create(
+                m, n, k, nnz(self.u_A), self.u_A.origin.offset, 0 if self.suf == "f64" else 1,
+                _ptr(rowptr), _ptr(colind), _ptr(nonzeros(self.u_A)), _stream(self.dev),
+                ctypes.byref(plan))
+        _lib.check(st, "csr_spmm_plan_create", self.u_A.format, _BE, self.T)
+        self._plan, self.k = plan, k
+
+    def execute(self, *ts, alpha=1.0, beta=0.0, skip_empty_rows=None):
+        """execute(h, B, C) or execute(h, A, B, C); returns C (a USTensor)."""
+        ts = tuple(t if isinstance(t, USTensor) else ust(t) for t in ts)
+        if len(ts) == 3:
+            u_A, u_B, u_C = ts
+            if nonzeros(u_A) is not nonzeros(self.u_A):
+                self.update_values(u_A)
+        elif len(ts) == 2:
+            u_B, u_C = ts
+        else:
+            raise TypeError("execute(handle, [A,] B, C)")
+        B, C = nonzeros(u_B), nonzeros(u_C)
+        m, n = self.u_A.extents
+        if B.dtype != self.T or C.dtype != self.T:
+            raise UnsupportedValueType(B.dtype if B.dtype != self.T else C.dtype, _BE)
+        if B.dim() != 2 or C.dim() != 2 or B.shape[0] != n or C.shape[0] != m or \
+                B.shape[1] != C.shape[1]:
+            raise IncompatibleExtents(
+                f"SpMM: A is {m}x{n}, B is {tuple(B.shape)}, C is {tuple(C.shape)}")
+        for t, nm in ((B, "B"), (C, "C")):
+            if t.shape[0] > 1 and t.shape[1] > 0 and t.stride(0) != 1:
+                raise NonCanonicalStorage(f"SpMM: {nm} must be column-major (stride(0) == 1)")
+        _check_same_device(nonzeros(self.u_A), B, C)
+        k = B.shape[1]
+        if self.k != k:
+            self._make(k)
+        skip = self.skip_empty_rows if skip_empty_rows is None else bool(skip_empty_rows)
+        with _on(self.dev):
+            st = getattr(_lib.lib(), f"jlust_hip_csr_spmm_plan_execute_{self.suf}")(
+                self._plan, float(alpha), _ptr(B), leading_dim(B), float(beta), _ptr(C),
+                leading_dim(C), int(skip), _stream(self.dev))
+        _lib.check(st, "csr_spmm_plan_execute", self.u_A.format, _BE, self.T)
+        return u_C
+
+    def update_values(self, u_A: USTensor):
+        if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):
+            raise IncompatibleExtents("update_values!: the sparsity structure must not change")
+        _check_values(u_A, self.T)
+        _check_same_device(nonzeros(u_A), nonzeros(self.u_A))
+        if self._plan.value:
+            st = _lib.lib().jlust_hip_csr_spmm_plan_update_values(self._plan, _ptr(nonzeros(u_A)))
+            _lib.check(st, "csr_spmm_plan_update_values", u_A.format, _BE, self.T)
+        self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
+                            self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+        return self
+
+    def info(self) -> dict:
+        """What the plan's analysis found: split rows, their segments, columns per pass."""
+        if not self._plan.value:
+            return {}
+        a, b, c = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        st = _lib.lib().jlust_hip_csr_spmm_plan_info(self._plan, ctypes.byref(a), ctypes.byref(b),
+                                                     ctypes.byref(c))
+        _lib.check(st, "csr_spmm_plan_info", self.u_A.format, _BE, self.T)
+        return {"split_rows": a.value, "segments": b.value, "cols_per_pass": c.value}
+
+    def _destroy(self):
+        plan, self._plan = getattr(self, "_plan", None), ctypes.c_void_p(0)
+        if plan is not None and plan.value:
+            try:
+                _lib.lib().jlust_hip_csr_spmm_plan_destroy(plan)
+            except Exception:
+                pass
+
+    def __del__(self):
+        self._destroy()
+
+
+class HIPSDDMMHandle(AbstractKernelHandle):
+    """Prepared SDDMM (jlust_hip_sddmm_plan_*): prepare(HIPBackend(), SDDMMOp,
+    A, B, C) -> execute(h, A, B, C) -> update_values!(h, C), the cuSPARSE
+    SDDMM handle contract (ext/CUDAExt/ops/sddmm.jl:10-76); prepare(...,
+    SDDMMOp, C) also works, the inner dimension taken from the first A.  C
+    (CSR or COO) is the mask pattern; the plan holds its row order and work
+    items.  execute(h, A, B) writes into the handle's C; update_values_(h,
+    C2) makes C2 (same pattern) the handle's output."""
+
+    def __init__(self, u_C: USTensor, n_inner=None):
+        self.coo = is_coo_shaped(u_C.format)
+        if not (is_csr_shaped(u_C.format) or self.coo):
+            raise UnsupportedFormat(u_C.format, _BE, "prepared SDDMM plans take a CSR or COO mask")
+        self.suf = _value_suffix(u_C)
+        self.T = nonzeros(u_C).dtype
+        idx = _coo_parts(u_C) if self.coo else _csr_parts(u_C)
+        self.dev = _check_same_device(*idx, nonzeros(u_C))
+        self.u_C = u_C
+        self._plan = ctypes.c_void_p(0)
+        self.K = None
+        if n_inner is not None:
+            self._make(int(n_inner))
+
+    def _make(self, K: int):
+        self._destroy()
+        m, n = self.u_C.extents
+        idx1, idx2 = _coo_parts(self.u_C) if self.coo else _csr_parts(self.u_C)
+        plan = ctypes.c_void_p(0)
+        with _on(self.dev):
+            st = _lib.lib().jlust_hip_sddmm_plan_create(
+                2 if self.coo else 0, m, n, K, nnz(self.u_C), self.u_C.origin.offset,
+                0 if self.suf == "f64" else 1, _ptr(idx1), _ptr(idx2), _stream(self.dev),
+                ctypes.byref(plan))
+        _lib.check(st, "sddmm_plan_create", self.u_C.format, _BE, self.T)
+        self._plan, self.K = plan, K
+
+    def execute(self, *ts, alpha=1.0, beta=0.0, mask=None):
+        """execute(h, A, B, C) or execute(h, A, B) (into the handle's C);
+        returns C."""
+        ts = tuple(t if isinstance(t, USTensor) else ust(t) for t in ts)
+        if len(ts) == 3:
+            u_A, u_B, u_C = ts
+            if nonzeros(u_C) is not nonzeros(self.u_C):
+                self.update_values(u_C)
+        elif len(ts) == 2:
+            u_A, u_B = ts
+        else:
+            raise TypeError("execute(handle, A, B[, C])")
+        u_C = self.u_C
+        A, B = _sddmm_dense_checks(u_A, u_B, u_C)
+        mk = _sddmm_mask(mask, u_C, self.T)
+        _check_same_device(nonzeros(u_C), A, B, mk)
+        if self.K != A.shape[1]:
+            self._make(A.shape[1])
+        with _on(self.dev):
+            st = getattr(_lib.lib(), f"jlust_hip_sddmm_plan_execute_{self.suf}")(
+                self._plan, float(alpha), _ptr(A), leading_dim(A), _ptr(B), leading_dim(B),
+                float(beta), _ptr(nonzeros(u_C)), _ptr(mk), _stream(self.dev))
+        _lib.check(st, "sddmm_plan_execute", u_C.format, _BE, self.T)
+        return u_C
+
+    def update_values(self, u_C: USTensor):
+        if u_C.extents != self.u_C.extents or nnz(u_C) != nnz(self.u_C):
+            raise IncompatibleExtents("update_values!: the sparsity structure must not change")
+        _check_values(u_C, self.T)
+        _check_same_device(nonzeros(u_C), nonzeros(self.u_C))
+        self.u_C = USTensor(self.u_C.extents, self.u_C.format, self.u_C.pos_buffers,
+                            self.u_C.crd_buffers, nonzeros(u_C), self.u_C.owner, self.u_C.origin)
+        return self
+
+    def info(self) -> dict:
+        """Work items of the plan and whether a COO mask was reordered."""
+        if not self._plan.value:
+            return {}
+        a, b = ctypes.c_int64(), ctypes.c_int32()
+        st = _lib.lib().jlust_hip_sddmm_plan_info(self._plan, ctypes.byref(a), ctypes.byref(b))
+        _lib.check(st, "sddmm_plan_info", self.u_C.format, _BE, self.T)
+        return {"work_items": a.value, "reordered": bool(b.value)}
+
+    def _destroy(self):
+        plan, self._plan = getattr(self, "_plan", None), ctypes.c_void_p(0)
+        if plan is not None and plan.value:
+            try:
+                _lib.lib().jlust_hip_sddmm_plan_destroy(plan)
+            except Exception:
+                pass
+
+    def __del__(self):
+        self._destroy()
+
+
+def prepare(optype, u_A: USTensor, *more, **kw):
+    """prepare(HIPBackend(), OpType, A; kw...) (src/ops.jl:163-177).  SpMV:
+    input_fn/output_fn; SpMM: n_cols, skip_empty_rows; SDDMM: (A, B, C) as
+    the cuSPARSE handle takes them, or the mask C alone (n_inner = K)."""
+    tag = getattr(optype, "tag", None)
+    if tag == "SpMV":
         bad = set(kw) - {"input_fn", "output_fn"}
-        if bad:
-            raise TypeError(f"prepare(SpMVOp): unexpected keywords {sorted(bad)}")
+        if bad or more:
+            raise TypeError(f"prepare(SpMVOp): unexpected keywords {sorted(bad)} or tensors ({len(more)})")
         if is_csr_shaped(u_A.format) or is_coo_shaped(u_A.format):
             return HIPSpMVHandle(u_A, kw.get("input_fn"), kw.get("output_fn"))
         return HIPOpHandle(SpMVOp, u_A, **kw)
-    if optype.tag in ("SpMM", "SDDMM"):
-        return HIPOpHandle(SpMMOp if optype.tag == "SpMM" else SDDMMOp, u_A, **kw)
+    if tag == "SpMM":
+        bad = set(kw) - {"n_cols", "skip_empty_rows"}
+        if bad or more:
+            raise TypeError(f"prepare(SpMMOp): unexpected keywords {sorted(bad)} or tensors ({len(more)})")
+        if is_csr_shaped(u_A.format):
+            return HIPSpMMHandle(u_A, kw.get("n_cols"), kw.get("skip_empty_rows", False))
+        kw.pop("n_cols", None)
+        return HIPOpHandle(SpMMOp, u_A, **kw)
+    if tag == "SDDMM":
+        bad = set(kw) - {"n_inner"}
+        if bad:
+            raise TypeError(f"prepare(SDDMMOp): unexpected keywords {sorted(bad)}")
+        if len(more) == 2:                     # (A, B, C)
+            A = nonzeros(u_A)
+            return HIPSDDMMHandle(more[1], A.shape[1] if A.dim() == 2 else None)
+        if more:
+            raise TypeError("prepare(SDDMMOp, A, B, C) or prepare(SDDMMOp, C)")
+        return HIPSDDMMHandle(u_A, kw.get("n_inner"))
     raise UnsupportedFormat(u_A.format, _BE, f"prepare: {optype} is not supported")

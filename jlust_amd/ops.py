@@ -142,12 +142,15 @@ def _backend_execute(be, op: Op, tensors, kw):
     raise UnsupportedFormat(op.formats, be, "no such backend in jlust_amd")
 
 
-def prepare(backend, optype: OpType, u_A: USTensor, **kw):
-    """prepare(backend, OpType, A; kw...) -> handle (src/ops.jl:179)."""
+def prepare(backend, optype: OpType, u_A, *more, **kw):
+    """prepare(backend, OpType, A; kw...) -> handle (src/ops.jl:179);
+    prepare(backend, SDDMMOp, A, B, C) as the cuSPARSE SDDMM handle takes it
+    (ext/CUDAExt/ops/sddmm.jl:24-26)."""
+    u_A = _wrap(u_A)
     if not isinstance(backend, HIPBackend):
         raise UnsupportedFormat(u_A.format, backend, "prepare is implemented for HIPBackend")
     from . import hip_backend
-    return hip_backend.prepare(optype, u_A, **kw)
+    return hip_backend.prepare(optype, u_A, *[_wrap(t) for t in more], **kw)
 
 
 def update_values_(handle, u_A: USTensor):

@@ -151,6 +151,36 @@ DEF_COO_SPMV(f64, double)
 DEF_COO_SPMV(f32, float)
 
 /* ------------------------------------------------------------------------- */
+/* CSC SpMV (scatter mode)                                                   */
+/* ------------------------------------------------------------------------- */
+/*
+ * y = beta*y (filled with zero when beta == 0), then for every column j in
+ * order and every stored entry p of it in storage order:
+ *   y[rowind[p]] += (alpha * val[p]) * x[j].
+ * Follows the scatter branch of execute(::EmitterBackend, ::Op{:SpMV})
+ * (ext/KernelAbstractionsExt/ops/spmv.jl:391-408: the pre-scale at :401 and
+ * the launch with the dense outer level walking columns) and the scatter leaf
+ * `@atomic _y[_y_idx] += _alpha * _nzval[_nnz_pos] * input_fn(_x[_x_idx])`
+ * (spmv.jl:140-141; Julia evaluates alpha*val first).  The atomics' order is
+ * not fixed in the reference; this restatement applies them sequentially in
+ * storage order, one of its admissible orders.
+ */
+#define DEF_CSC_SPMV(SUF, T)                                                   \
+void oracle_csc_spmv_##SUF(int32_t m, int32_t n, int32_t origin,               \
+                           const int32_t *colptr, const int32_t *rowind,       \
+                           const T *val, T alpha, const T *x, T beta, T *y)    \
+{                                                                              \
+    if (beta == (T)0) { for (int64_t i = 0; i < m; ++i) y[i] = (T)0; }         \
+    else              { for (int64_t i = 0; i < m; ++i) y[i] *= beta; }        \
+    for (int64_t j = 0; j < n; ++j)                                            \
+        for (int64_t p = (int64_t)colptr[j] - origin;                          \
+             p < (int64_t)colptr[j + 1] - origin; ++p)                         \
+            y[rowind[p] - origin] += (alpha * val[p]) * x[j];                  \
+}
+DEF_CSC_SPMV(f64, double)
+DEF_CSC_SPMV(f32, float)
+
+/* ------------------------------------------------------------------------- */
 /* CSR SpMM                                                                  */
 /* ------------------------------------------------------------------------- */
 /*
@@ -296,6 +326,32 @@ void oracle_csr_sddmm_##SUF(int32_t m, int32_t origin, const int32_t *rowptr,  \
 }
 DEF_SDDMM(f64, double)
 DEF_SDDMM(f32, float)
+
+/*
+ * SDDMM with a COO mask (coo_tensor storage, src/interop.jl:248-260): the
+ * same per-entry arithmetic as above for every stored (rows[p], cols[p]) in
+ * storage order -- the walker visits each stored entry once whatever its outer
+ * level (sddmm.jl:23-30 is format-generic; reference answer
+ * test/test_emitter.jl:289-307).
+ */
+#define DEF_COO_SDDMM(SUF, T)                                                  \
+void oracle_coo_sddmm_##SUF(int64_t nnz, int32_t origin, const int32_t *rows,  \
+                            const int32_t *cols, int64_t K, T alpha,           \
+                            const T *A, int64_t lda, const T *B, int64_t ldb,  \
+                            T beta, T *Cval, const T *mask)                    \
+{                                                                              \
+    for (int64_t p = 0; p < nnz; ++p) {                                        \
+        int64_t i = (int64_t)rows[p] - origin, j = (int64_t)cols[p] - origin;  \
+        T dot = (T)0;                                                          \
+        for (int64_t kk = 0; kk < K; ++kk)                                     \
+            dot += A[i + kk * lda] * B[kk + j * ldb];                          \
+        T term = alpha * dot;                                                  \
+        if (mask) term = mask[p] * term;                                       \
+        Cval[p] = term + beta * Cval[p];                                       \
+    }                                                                          \
+}
+DEF_COO_SDDMM(f64, double)
+DEF_COO_SDDMM(f32, float)
 
 /* |alpha| * |mask| * sum|A||B| + |beta| |C0| per stored entry, in double. */
 #define DEF_SDDMM_ABSREF(SUF, T)                                               \

@@ -52,6 +52,10 @@ def lib():
                 _I32, _I32, _P, _P, _P, _D, _P, _D, _P, _P, _INT]
             getattr(L, f"oracle_coo_spmv_{suf}").argtypes = [
                 _I64, _I32, _I32, _P, _P, _P, S, _P, S, _P]
+            getattr(L, f"oracle_csc_spmv_{suf}").argtypes = [
+                _I32, _I32, _I32, _P, _P, _P, S, _P, S, _P]
+            getattr(L, f"oracle_coo_sddmm_{suf}").argtypes = [
+                _I64, _I32, _P, _P, _I64, S, _P, _I64, _P, _I64, S, _P, _P]
             f = getattr(L, f"oracle_csr_spmm_{suf}")
             f.argtypes = [_I32, _I32, _P, _P, _P, _I64, S, _P, _I64, S, _P,
                           _I64, _INT, _INT]
@@ -183,6 +187,42 @@ def coo_spmv(rows, cols, val, x, m, alpha=1.0, beta=0.0, y0=None, origin=1):
         val.size, m, origin, _ptr(rows), _ptr(cols), _ptr(val), alpha,
         _ptr(x), beta, _ptr(y))
     return y
+
+
+def csc_spmv(colptr, rowind, val, x, m, alpha=1.0, beta=0.0, y0=None, origin=1):
+    """Scatter-mode CSC SpMV: y = beta*y, then y[row] += (alpha*val)*x[col]
+    column by column in storage order (oracle_csc_spmv_*)."""
+    L = lib()
+    dt = np.asarray(val).dtype
+    suf = _suf(dt)
+    colptr = _c(colptr, np.int32)
+    rowind = _c(rowind, np.int32)
+    val = _c(val, dt)
+    x = _c(x, dt)
+    y = np.zeros(m, dt) if y0 is None else _c(y0, dt).copy()
+    getattr(L, f"oracle_csc_spmv_{suf}")(
+        m, colptr.size - 1, origin, _ptr(colptr), _ptr(rowind), _ptr(val), alpha, _ptr(x), beta,
+        _ptr(y))
+    return y
+
+
+def coo_sddmm(rows, cols, A, B, alpha=1.0, beta=0.0, C0=None, mask=None, origin=1):
+    """SDDMM over a COO mask, outputs in the mask's storage order
+    (oracle_coo_sddmm_*)."""
+    L = lib()
+    dt = np.asarray(A).dtype
+    suf = _suf(dt)
+    rows = _c(rows, np.int32)
+    cols = _c(cols, np.int32)
+    A = _f(A, dt)
+    B = _f(B, dt)
+    nnz = rows.size
+    C = np.zeros(nnz, dt) if C0 is None else _c(C0, dt).copy()
+    mk = None if mask is None else _c(mask, dt)
+    getattr(L, f"oracle_coo_sddmm_{suf}")(
+        nnz, origin, _ptr(rows), _ptr(cols), A.shape[1], alpha, _ptr(A), max(A.shape[0], 1),
+        _ptr(B), max(B.shape[0], 1), beta, _ptr(C), _ptr(mk))
+    return C
 
 
 def spmm_strategy(m, k, nnz, skip_empty_rows=False) -> str:

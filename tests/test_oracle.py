@@ -349,3 +349,93 @@ def test_dcsr_fixtures_and_untouched_rows(dtype):
                     s["m"], beta=1.0, C0=C0, origin=s["origin"])
     assert C[1].tolist() == [7.0, 7.0]
     np.testing.assert_allclose(C[[0, 2]], np.array(s["C"], dtype)[[0, 2]] + 7.0, rtol=1e-6)
+
+
+# ------------------------------------------------------- CSC SpMV (scatter)
+
+def _csc_of(rowptr, colind, val, n, origin=1):
+    """CSC arrays of a CSR matrix through the oracle's conversion (pinned by
+    the test_convert.jl fixtures in test_convert_fixtures)."""
+    return O.csr_to_csc(rowptr, colind, val, n, origin)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_csc_spmv_reference_answer(dtype):
+    """A = [1 0 2; 0 3 0; 4 0 5] stored column-major, x = [1, 2, 3] ->
+    [7, 6, 19] (the matrix of test_emitter.jl:85-102 in Formats.CSC)."""
+    c = GOLDEN["spmv"][0]
+    cp, ri, cv = _csc_of(np.array(c["rowptr"]), np.array(c["colind"]), np.array(c["val"], dtype), 3)
+    assert cp.tolist() == [1, 3, 4, 6] and ri.tolist() == [1, 3, 2, 1, 3]
+    y = O.csc_spmv(cp, ri, cv, np.array(c["x"], dtype), 3)
+    np.testing.assert_array_equal(y, np.array(c["y"], dtype))
+
+
+@pytest.mark.parametrize("origin", [1, 0])
+def test_csc_spmv_bitexact_scipy(origin):
+    """scipy's csc_matvec adds val*x[col] into y[row] column by column in
+    storage order from zero: with alpha = 1 the scatter is the same sum."""
+    m, n = 700, 900
+    rowptr, colind, val = random_csr(m, n, density=0.03, seed=41, origin=origin)
+    cp, ri, cv = _csc_of(rowptr, colind, val, n, origin)
+    x = np.random.default_rng(42).uniform(-1, 1, n)
+    y = O.csc_spmv(cp, ri, cv, x, m, origin=origin)
+    S = sp.csc_matrix((cv, ri - origin, cp - origin), shape=(m, n))
+    np.testing.assert_array_equal(y, S @ x)
+    # alpha = 2, beta = 0.5 scale every term by powers of two: exact.
+    y0 = np.random.default_rng(43).uniform(-1, 1, m)
+    y2 = O.csc_spmv(cp, ri, cv, x, m, alpha=2.0, beta=0.5, y0=y0, origin=origin)
+    want = 0.5 * y0
+    for j in range(n):
+        for p in range(cp[j] - origin, cp[j + 1] - origin):
+            want[ri[p] - origin] += (2.0 * cv[p]) * x[j]
+    np.testing.assert_array_equal(y2, want)
+    # planted mistakes: x reversed, and (square) the CSC arrays read as CSR,
+    # i.e. A^T x, both fail the scipy check.
+    assert not np.array_equal(O.csc_spmv(cp, ri, cv, x[::-1].copy(), m, origin=origin), y)
+    rs, cs, vs = random_csr(400, 400, density=0.03, seed=46, origin=origin)
+    cps, ris, cvs = _csc_of(rs, cs, vs, 400, origin)
+    xs = np.random.default_rng(47).uniform(-1, 1, 400)
+    want_s = sp.csc_matrix((cvs, ris - origin, cps - origin), shape=(400, 400)) @ xs
+    np.testing.assert_array_equal(O.csc_spmv(cps, ris, cvs, xs, 400, origin=origin), want_s)
+    assert not np.array_equal(O.csr_spmv(cps, ris, cvs, xs, origin=origin), want_s)
+
+
+# ------------------------------------------------------------- COO SDDMM
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_coo_sddmm_reference_fixture(dtype):
+    c = next(c for c in GOLDEN["sddmm"] if c["format"] == "COO")
+    A = np.asfortranarray(np.array(c["A"], dtype))
+    B = np.asfortranarray(np.array(c["B"], dtype))
+    out = O.coo_sddmm(c["rows"], c["cols"], A, B, beta=c["beta"], C0=np.array(c["c0"], dtype),
+                      origin=c["origin"])
+    np.testing.assert_array_equal(out, np.array(c["cval"], dtype))
+
+
+def test_coo_sddmm_equals_csr_and_permutes():
+    """Row-ordered COO = the CSR result bit for bit (the same sequential dot
+    per stored entry); shuffled entries give the shuffled outputs."""
+    m, n, K = 400, 300, 24
+    rowptr, colind, _ = random_csr(m, n, density=0.04, seed=44)
+    rng = np.random.default_rng(45)
+    A = np.asfortranarray(rng.standard_normal((m, K)))
+    B = np.asfortranarray(rng.standard_normal((K, n)))
+    mask = rng.uniform(0.5, 1.5, colind.size)
+    C0 = rng.standard_normal(colind.size)
+    rows = np.repeat(np.arange(1, m + 1, dtype=np.int32), np.diff(rowptr))
+    csr = O.csr_sddmm(rowptr, colind, A, B, 1.5, -0.5, C0, mask)
+    coo = O.coo_sddmm(rows, colind, A, B, 1.5, -0.5, C0, mask)
+    np.testing.assert_array_equal(coo, csr)
+    perm = rng.permutation(colind.size)
+    shuf = O.coo_sddmm(rows[perm], colind[perm], A, B, 1.5, -0.5, C0[perm], mask[perm])
+    np.testing.assert_array_equal(shuf, csr[perm])
+    # planted mistakes: rows and columns swapped (a transposed mask read on a
+    # square problem), and a wrong sign of beta, both differ.
+    assert not np.array_equal(O.coo_sddmm(rows, colind, A, B, 1.5, 0.5, C0, mask), csr)
+    rs, cs, _ = random_csr(200, 200, density=0.05, seed=48)
+    rr = np.repeat(np.arange(1, 201, dtype=np.int32), np.diff(rs))
+    As = np.asfortranarray(rng.standard_normal((200, K)))
+    Bs = np.asfortranarray(rng.standard_normal((K, 200)))
+    good = O.coo_sddmm(rr, cs, As, Bs)
+    np.testing.assert_array_equal(good, O.csr_sddmm(rs, cs, As, Bs))
+    assert not np.array_equal(O.coo_sddmm(cs, rr, As, Bs), good)
