@@ -46,6 +46,11 @@ def parse():
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="CPU work budget of the cpu_baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", action="store_true",
+                   help="time only --config (default: the headline --config, then every other "
+                        "BASELINE configuration, reported in all_configs)")
+    p.add_argument("--other-cpu-seconds", type=float, default=6.0,
+                   help="CPU work budget of the cpu_baseline sample of the non-headline configs")
     p.add_argument("--no-plan", action="store_true",
                    help="SpMV: time only the plain per-call entry point (default: a prepared plan, "
                         "as JLUST's prepare/execute handle API, with the plain call timed beside it)")
@@ -286,7 +291,7 @@ def coo_bench(steps, warmup, cpu_seconds):
     def run(name, step):
         ms, ev = timed(step, steps, warmup)
         out.append({"case": name, "ms_per_call": round(ms, 4), "GBps": round(byts / (ms * 1e-3) / 1e9, 1),
-                    "event_ms": round(float(ev.mean()), 4)})
+                    "event_ms": round(float(ev), 4)})
         log(f"{name}: {ms:.3f} ms/call")
 
     for order, (r, c, v) in (("row order", (rows, cols, val)),
@@ -690,19 +695,17 @@ def cpu_baseline(cfg, budget_s):
 
 def timed(step, steps, warmup):
     """W untimed steps, then exactly K steps bracketed by synchronize() (the
-    wall-clock pass: nothing else is queued between the steps), then K more
-    steps with a HIP event pair recorded on the launching stream around each
-    one (the per-launch pass).  Returns (wall ms per step of the first pass,
-    per-step event durations in ms of the second).  The event records are kept
-    out of the wall-clock pass: at config 1's size (an 11 us kernel) the two
-    records per step add several microseconds of queue time."""
+    wall-clock pass), then K more steps between one pair of HIP events
+    recorded on the launching stream (the kernel pass: the queue runs the K
+    steps back to back, so elapsed / K is the step's kernel time without the
+    host).  Returns (wall ms per step, kernel ms per step).  One event pair
+    over the whole region rather than one per step: at config 1's size (a
+    9 us kernel) each extra record adds about 2 us of queue time."""
     import torch
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
     if torch.distributed.is_available() and torch.distributed.is_initialized():
         torch.distributed.barrier()
     torch.cuda.synchronize()
@@ -711,12 +714,13 @@ def timed(step, steps, warmup):
         step()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
-    for s, e in ev:
-        s.record(stream)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
         step()
-        e.record(stream)
+    e1.record(stream)
     torch.cuda.synchronize()
-    return wall * 1e3 / steps, np.array([s.elapsed_time(e) for s, e in ev])
+    return wall * 1e3 / steps, e0.elapsed_time(e1) / steps
 
 
 def traffic_for(workload):
@@ -728,6 +732,102 @@ def traffic_for(workload):
         return None if e is None else int(e["traffic_bytes"])
     except (OSError, ValueError, KeyError):
         return None
+
+
+def host_info():
+    """CPU model, sockets and logical CPUs of this host (from /proc/cpuinfo)."""
+    model, sockets, logical = None, set(), 0
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    sockets.add(v)
+                elif k == "processor":
+                    logical += 1
+    except OSError:
+        pass
+    return {"cpu_model": model, "sockets": len(sockets) or None, "logical_cpus": logical or None,
+            "nproc": os.cpu_count()}
+
+
+def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False):
+    """One configuration: W untimed + K timed steps (wall clock) and K steps
+    under HIP events, the plain SpMV call beside a plan, the CPU baseline.
+    Returns the result object (the headline keys of the JSON line)."""
+    import torch
+    from jlust_amd import workloads as W
+
+    t0 = time.perf_counter()
+    cfg = W.make(config)
+    log(f"generated {cfg['name']} in {time.perf_counter() - t0:.1f}s")
+    use_plan = cfg["kind"] == "csr_spmv" and not no_plan
+    step, kname, bound, keep = build_step(cfg, use_plan=use_plan)
+    ms_per_step, per_launch_ms = timed(step, steps, warmup)
+    plain = None
+    if use_plan:
+        pstep, pkname, _, pkeep = build_step(cfg, use_plan=False)
+        p_ms, p_launch = timed(pstep, steps, warmup)
+        plain = {"value": round(W.algorithmic_bytes(cfg) / (p_ms * 1e-3) / 1e9, 3),
+                 "ms_per_step": round(p_ms, 6), "kernel": pkname,
+                 "per_launch_ms": round(p_launch, 6)}
+        del pkeep
+    log(f"config {config}: {steps} steps: wall {ms_per_step:.4f} ms/step, events "
+        f"{per_launch_ms:.4f} ms/step")
+
+    nbytes = W.algorithmic_bytes(cfg)
+    nflops = W.flops(cfg)
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    k_ms = float(per_launch_ms)
+    if bound == "hbm":
+        achieved = nbytes / (k_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5)}
+    else:
+        achieved = nflops / (k_ms * 1e-3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 5)}
+    roof["traffic"] = traffic_for(cfg["name"] + (":plan" if use_plan else ""))
+    roof["traffic_counts"] = ("L2-miss bytes (FETCH_SIZE x 2.0 + WRITE_SIZE, rocprofv3 --pmc): "
+                              "requests leaving the L2s, served by the MALL or by HBM")
+    roof["kernel"] = kname
+    roof["per_launch_ms"] = round(k_ms, 6)
+    plan_build_ms = round(keep[3].build_ms, 2) if use_plan else None
+
+    cpu = None
+    if not no_cpu:
+        log(f"config {config}: timing the CPU baseline (oracle) ...")
+        cpu = cpu_baseline(cfg, cpu_seconds)
+        cpu.update(host_info())
+
+    nnz_key = "nnzb" if cfg["kind"] == "bsr_spmm" else "nnz"
+    nnz_val = int((cfg["browptr"] if cfg["kind"] == "bsr_spmm" else cfg["rowptr"])[-1]) - 1
+    out = {
+        "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 6),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f64" if np.dtype(cfg["dtype"]) == np.float64 else "f32",
+        "data": "synthetic (seeded generator, jlust_amd/csrc/workloads.c)",
+        "config": {"workload": cfg["name"], "baseline_config": cfg["config"], "m": cfg["m"],
+                   "n": cfg["n"], nnz_key: nnz_val, "seed": cfg["seed"],
+                   "index": "Int32, 1-based", "plan": bool(use_plan)},
+        "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 3),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 3),
+        "algorithmic_bytes": int(nbytes), "flops": int(nflops),
+        "roofline": roof, "plain_call": plain, "plan_build_ms": plan_build_ms, "cpu_baseline": cpu,
+    }
+    del keep, step, cfg
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
+# Steps per configuration when bench.py runs them all (the driver's default
+# run): enough events for a stable mean while the five fit in a few minutes.
+ALL_STEPS = {1: 200, 2: 200, 3: 30, 4: 30, 5: 30}
 
 
 def main():
@@ -773,68 +873,25 @@ def main():
     if args.blocks:
         print(json.dumps({"blocks": blocks_bench(args.steps or 200, args.warmup or 10)}), flush=True)
         return
-    from jlust_amd import workloads as W
-
-    steps = args.steps if args.steps is not None else (200 if args.config in (1, 2) else 30)
+    steps = args.steps if args.steps is not None else ALL_STEPS[args.config]
     warmup = args.warmup if args.warmup is not None else 5
-    t0 = time.perf_counter()
-    cfg = W.make(args.config)
-    log(f"generated {cfg['name']} in {time.perf_counter() - t0:.1f}s")
-    use_plan = cfg["kind"] == "csr_spmv" and not args.no_plan
-    step, kname, bound, keep = build_step(cfg, use_plan=use_plan)
-    ms_per_step, per_launch_ms = timed(step, steps, warmup)
-    plain = None
-    if use_plan:
-        pstep, pkname, _, pkeep = build_step(cfg, use_plan=False)
-        p_ms, p_launch = timed(pstep, steps, warmup)
-        plain = {"value": round(W.algorithmic_bytes(cfg) / (p_ms * 1e-3) / 1e9, 3),
-                 "ms_per_step": round(p_ms, 6), "kernel": pkname,
-                 "per_launch_ms": round(float(p_launch.mean()), 6)}
-        del pkeep
-    log(f"{steps} steps: wall {ms_per_step:.4f} ms/step, event mean "
-        f"{per_launch_ms.mean():.4f} ms, min {per_launch_ms.min():.4f} ms")
-
-    nbytes = W.algorithmic_bytes(cfg)
-    nflops = W.flops(cfg)
-    value = nbytes / (ms_per_step * 1e-3) / 1e9
-    k_ms = float(per_launch_ms.mean())
-    if bound == "hbm":
-        achieved = nbytes / (k_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 3), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 5)}
-    else:
-        achieved = nflops / (k_ms * 1e-3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 5)}
-    roof["traffic"] = traffic_for(cfg["name"] + (":plan" if use_plan else ""))
-    roof["kernel"] = kname
-    roof["per_launch_ms"] = round(k_ms, 6)
-    roof["per_launch_ms_min"] = round(float(per_launch_ms.min()), 6)
-    plan_build_ms = round(keep[3].build_ms, 2) if use_plan else None
-
-    cpu = None
-    if not args.no_cpu_baseline:
-        log("timing the CPU baseline (oracle) ...")
-        cpu = cpu_baseline(cfg, args.cpu_seconds)
-
-    nnz_key = "nnzb" if cfg["kind"] == "bsr_spmm" else "nnz"
-    nnz_val = int((cfg["browptr"] if cfg["kind"] == "bsr_spmm" else cfg["rowptr"])[-1]) - 1
-    out = {
-        "metric": METRIC, "value": round(value, 3), "unit": "GB/s", "n_gpus": 1,
-        "steps": steps, "warmup": warmup, "ms_per_step": round(ms_per_step, 6),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f64" if np.dtype(cfg["dtype"]) == np.float64 else "f32",
-        "data": "synthetic (seeded generator, jlust_amd/csrc/workloads.c)",
-        "config": {"workload": cfg["name"], "baseline_config": cfg["config"], "m": cfg["m"],
-                   "n": cfg["n"], nnz_key: nnz_val, "seed": cfg["seed"],
-                   "index": "Int32, 1-based", "plan": bool(use_plan)},
-        "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 3),
-        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 3),
-        "algorithmic_bytes": int(nbytes), "flops": int(nflops),
-        "roofline": roof, "plain_call": plain, "plan_build_ms": plan_build_ms, "cpu_baseline": cpu,
-    }
+    out = bench_config(args.config, steps, warmup, args.cpu_seconds, args.no_plan,
+                       args.no_cpu_baseline)
+    if not args.only:
+        # Every BASELINE configuration in the same run, the headline first.
+        rows = []
+        for c in sorted(ALL_STEPS):
+            if c == args.config:
+                e = out
+            else:
+                e = bench_config(c, ALL_STEPS[c], warmup, args.other_cpu_seconds,
+                                 no_cpu=args.no_cpu_baseline)
+            rows.append({k: e[k] for k in ("config", "value", "unit", "ms_per_step", "gflops",
+                                           "pct_hbm_peak", "dtype", "algorithmic_bytes", "flops",
+                                           "roofline", "plain_call", "plan_build_ms",
+                                           "cpu_baseline")})
+        out["all_configs"] = rows
     print(json.dumps(out), flush=True)
-    del keep
 
 
 if __name__ == "__main__":
