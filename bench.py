@@ -74,6 +74,13 @@ def parse():
     p.add_argument("--coo", action="store_true",
                    help="only time COO and DCSR SpMV (plain calls and prepared plans) on config 2's "
                         "matrix, sorted and shuffled, beside the oracle's COO SpMV on this host")
+    p.add_argument("--gather-floor", action="store_true",
+                   help="only time the random-row gathers of configs 3 and 4 alone (their floor)")
+    p.add_argument("--mall-probe", action="store_true",
+                   help="only measure whether a just-written buffer reads back faster than a cold one")
+    p.add_argument("--cold", action="store_true",
+                   help="time each step after a 1 GiB read that flushes the L2s and the MALL "
+                        "(reported as cold_ms_per_step beside the warm figures)")
     p.add_argument("--blocks", action="store_true",
                    help="only time BlockSparseMatrix / BlockBandedMatrix mul! on a synthetic "
                         "DCOPF operator of pglib case30000_goc size (T = 24)")
@@ -373,13 +380,141 @@ def gather_ceiling():
     return res
 
 
+PROBE_SRC = os.path.join(ROOT, "bench_probes.hip")
+PROBE_LIB = os.path.join(ROOT, "bench_probes.so")
+
+
+def build_probes() -> str:
+    """hipcc bench_probes.hip -> bench_probes.so (measurement kernels of this
+    script; not part of libjlust_hip.so)."""
+    import subprocess
+    tmp = PROBE_LIB + ".tmp"
+    subprocess.run(["/opt/rocm/bin/hipcc", "-O3", "-std=c++17", "-fPIC", "-shared", "--offload-arch=gfx950",
+                    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", PROBE_SRC, "-o", tmp],
+                   check=True)
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
+def probe_lib():
+    """bench_probes.so, built first when it is missing or older than its source."""
+    import ctypes
+    if not os.path.exists(PROBE_LIB) or os.path.getmtime(PROBE_LIB) < os.path.getmtime(PROBE_SRC):
+        build_probes()
+    return ctypes.CDLL(PROBE_LIB)
+
+
+def gather_floor():
+    """The gathers of configs 3 and 4 alone (bench_probes.hip,
+    rows_probe_kernel): config 3's SpMM gathers, per 64-column chunk, one
+    256-byte row of the 256 MB row-major copy of B for each of its 32M
+    nonzeros; config 4's SDDMM gathers one 512-byte column of B (256 MB) for
+    each of its 16M nonzeros.  Uniform random rows, 8 in flight per wave,
+    a wave per 32 (or 64) consecutive indices; the time bounds any kernel
+    making those gathers."""
+    import ctypes
+    import torch
+    lib = probe_lib()
+    lib.jlust_probe_rows_f32.restype = ctypes.c_int
+    lib.jlust_probe_rows_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(3)
+    res = []
+    for name, nrows, row, count in (("config 3 SpMM chunk: 256 B rows of a 256 MB B copy", 1_000_000, 64,
+                                     32_000_000),
+                                    ("config 4 SDDMM: 512 B columns of a 256 MB B", 500_000, 128,
+                                     16_000_000)):
+        src = torch.randn(nrows * row, dtype=torch.float32, device="cuda")
+        idx = torch.randint(0, nrows, (count,), generator=g, device="cuda", dtype=torch.int64).to(torch.int32)
+        for per_wave in (32, 64):
+            waves = (count + per_wave - 1) // per_wave
+            out = torch.empty(waves * 64, dtype=torch.float32, device="cuda")
+            call = lambda: lib.jlust_probe_rows_f32(src.data_ptr(), nrows, row, idx.data_ptr(), count,  # noqa: E731
+                                                    per_wave, out.data_ptr(), stream.cuda_stream)
+            for _ in range(3):
+                assert call() == 0
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 10
+            s.record(stream)
+            for _ in range(reps):
+                call()
+            e.record(stream)
+            torch.cuda.synchronize()
+            t = s.elapsed_time(e) / reps * 1e-3
+            res.append({"case": name, "rows_per_wave": per_wave, "gathers": count, "row_bytes": row * 4,
+                        "ms": round(t * 1e3, 4), "gathered_TBps": round(count * row * 4 / t / 1e12, 3)})
+            log(f"{name}, {per_wave} per wave: {t * 1e3:.3f} ms")
+            del out
+        del src, idx
+        torch.cuda.empty_cache()
+    return res
+
+
+def mall_probe():
+    """Does a buffer written by one kernel come back faster in the next than a
+    cold one (from the 256 MB MALL rather than HBM)?  For sizes 16-512 MB:
+    the write, a read right after it, a read after 160 MB of other reads in
+    between, and a read after a 1 GiB flush; 16-byte nontemporal loads,
+    2048 workgroups, best of 5 (bench_probes.hip)."""
+    import ctypes
+    import torch
+    lib = probe_lib()
+    lib.jlust_probe_stream.restype = ctypes.c_int
+    lib.jlust_probe_stream.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int64,
+                                       ctypes.c_void_p, ctypes.c_void_p]
+    MB = 1 << 20
+    grid = 2048
+    P = torch.empty(512 * MB, dtype=torch.uint8, device="cuda")
+    E = torch.empty(160 * MB, dtype=torch.uint8, device="cuda")
+    F = torch.empty(1024 * MB, dtype=torch.uint8, device="cuda")
+    out = torch.empty(grid * 256, dtype=torch.float64, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def run(buf, nbytes, write):
+        assert lib.jlust_probe_stream(buf.data_ptr(), nbytes, int(write), grid, out.data_ptr(),
+                                      stream.cuda_stream) == 0
+
+    for b in (P, E, F):
+        run(b, b.numel(), True)
+    res = []
+    for mb in (16, 32, 64, 128, 256, 384, 512):
+        nb = mb * MB
+        best = {}
+        for _ in range(5):
+            for case in ("write", "read_after_write", "read_after_160MB", "read_cold"):
+                run(F, F.numel(), False)
+                if case != "write":
+                    run(P, nb, True)
+                if case == "read_after_160MB":
+                    run(E, E.numel(), False)
+                if case == "read_cold":
+                    run(F, F.numel(), False)
+                s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.record(stream)
+                run(P, nb, case == "write")
+                e.record(stream)
+                torch.cuda.synchronize()
+                t = s.elapsed_time(e)
+                best[case] = min(best.get(case, 1e9), t)
+        row = {"MB": mb}
+        for case, t in best.items():
+            row[case + "_us"] = round(t * 1e3, 1)
+            row[case + "_TBps"] = round(nb / (t * 1e-3) / 1e12, 2)
+        res.append(row)
+        log(f"mall probe {mb} MB: {row}")
+    del P, E, F, out
+    return res
+
+
 def gather_probe():
-    """8-byte random gathers by jlust_amd/csrc/gather_probe.hip (8 per thread),
+    """8-byte random gathers by bench_probes.hip (8 per thread),
     from the whole source or, XCD-sliced, from source/8 per XCD (the access
     pattern of the column-sliced SpMV plan)."""
     import ctypes
     import torch
-    lib = ctypes.CDLL(os.path.join(ROOT, "jlust_amd", "libjlust_probe.so"))
+    lib = probe_lib()
     lib.jlust_probe_gather_f64.restype = ctypes.c_int
     lib.jlust_probe_gather_f64.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
                                            ctypes.c_void_p, ctypes.c_int64, ctypes.c_int,
@@ -538,12 +673,12 @@ def stream_ceiling():
 
 
 def mfma_peak():
-    """Sustained fp32 matrix-core rate (jlust_amd/csrc/gather_probe.hip,
+    """Sustained fp32 matrix-core rate (bench_probes.hip,
     mfma_probe_kernel) for 1, 2 and 4 waves per SIMD, beside the published
     dense fp32 MFMA peak."""
     import ctypes
     import torch
-    lib = ctypes.CDLL(os.path.join(ROOT, "jlust_amd", "libjlust_probe.so"))
+    lib = probe_lib()
     lib.jlust_probe_mfma_f32.restype = ctypes.c_int
     lib.jlust_probe_mfma_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p]
     cus = torch.cuda.get_device_properties(0).multi_processor_count
@@ -621,7 +756,7 @@ def build_step(cfg, use_plan=False):
         A = J.bsr_tensor(dev(cfg["browptr"]), dev(cfg["bcolind"]), dev(cfg["val"]), (m, n))
         B = dev(cfg["B"])
         C = J.dense_matrix(m, cfg["k"], dtype=torch.float32)
-        return (lambda: J.execute(J.SpMMOp, A, B, C)), "bsr16_spmm_rowwave_kernel", "mfma", (A, B, C)
+        return (lambda: J.execute(J.SpMMOp, A, B, C)), "bsr16_spmm_strip_kernel", "mfma", (A, B, C)
     raise ValueError(kind)
 
 
@@ -723,6 +858,27 @@ def timed(step, steps, warmup):
     return wall * 1e3 / steps, e0.elapsed_time(e1) / steps
 
 
+def timed_cold(step, steps):
+    """Each of K steps timed alone (an event pair around it) right after a
+    1 GiB read that evicts the operands from the L2s and the 256 MB MALL.
+    Returns the mean and minimum step time in ms (the two event records add
+    about 2 us to each)."""
+    import torch
+    flush = torch.empty(1 << 28, dtype=torch.float32, device="cuda").fill_(1.0)
+    stream = torch.cuda.current_stream()
+    times = []
+    for _ in range(steps):
+        flush.sum()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    del flush
+    return float(np.mean(times)), float(np.min(times))
+
+
 def traffic_for(workload):
     path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     try:
@@ -754,7 +910,7 @@ def host_info():
             "nproc": os.cpu_count()}
 
 
-def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False):
+def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False, cold=False):
     """One configuration: W untimed + K timed steps (wall clock) and K steps
     under HIP events, the plain SpMV call beside a plan, the CPU baseline.
     Returns the result object (the headline keys of the JSON line)."""
@@ -777,6 +933,13 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
         del pkeep
     log(f"config {config}: {steps} steps: wall {ms_per_step:.4f} ms/step, events "
         f"{per_launch_ms:.4f} ms/step")
+    cold_res = None
+    if cold:
+        c_mean, c_min = timed_cold(step, steps)
+        cold_res = {"cold_ms_per_step": round(c_mean, 6), "cold_ms_min": round(c_min, 6),
+                    "flush": "1 GiB read before each step (L2s and MALL evicted); one event pair "
+                             "around each step"}
+        log(f"config {config}: cold {c_mean:.4f} ms/step (min {c_min:.4f})")
 
     nbytes = W.algorithmic_bytes(cfg)
     nflops = W.flops(cfg)
@@ -819,6 +982,8 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
         "algorithmic_bytes": int(nbytes), "flops": int(nflops),
         "roofline": roof, "plain_call": plain, "plan_build_ms": plan_build_ms, "cpu_baseline": cpu,
     }
+    if cold_res is not None:
+        out["cold"] = cold_res
     del keep, step, cfg
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
@@ -844,6 +1009,12 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         print(json.dumps({"calibrate_copy_bytes": a.numel() * 4}), flush=True)
+        return
+    if args.gather_floor:
+        print(json.dumps({"gather_floor": gather_floor()}), flush=True)
+        return
+    if args.mall_probe:
+        print(json.dumps({"mall_probe": mall_probe()}), flush=True)
         return
     if args.gather_ceiling:
         print(json.dumps({"gather_ceiling": gather_ceiling()}), flush=True)
@@ -876,7 +1047,7 @@ def main():
     steps = args.steps if args.steps is not None else ALL_STEPS[args.config]
     warmup = args.warmup if args.warmup is not None else 5
     out = bench_config(args.config, steps, warmup, args.cpu_seconds, args.no_plan,
-                       args.no_cpu_baseline)
+                       args.no_cpu_baseline, args.cold)
     if not args.only:
         # Every BASELINE configuration in the same run, the headline first.
         rows = []

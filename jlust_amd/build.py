@@ -3,9 +3,6 @@
 - ``libjlust_hip.so``: the HIP kernels and the C ABI (``include/jlust_hip.h``),
   compiled by hipcc for gfx950 only.
 - ``libjlust_workloads.so``: the host-side synthetic input generator.
-- ``libjlust_probe.so``: the random-gather and fp32 MFMA probes behind
-  ``bench.py --gather-ceiling`` / ``--mfma-peak`` (measurement only, not part
-  of the C ABI).
 
 Run ``python -m jlust_amd.build`` (or ``__graft_entry__.build()``).  Sources are
 compiled in parallel into ``jlust_amd/_build/`` and linked next to this file.
@@ -24,7 +21,6 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 HIP_LIB = os.path.join(HERE, "libjlust_hip.so")
 WL_LIB = os.path.join(HERE, "libjlust_workloads.so")
-PROBE_LIB = os.path.join(HERE, "libjlust_probe.so")
 
 HIP_SOURCES = ["capi.hip", "scan.hip", "spmv.hip", "coo_spmv.hip", "spmm.hip", "sddmm.hip",
                "bsr_spmm.hip", "convert.hip", "assemble.hip", "fn.hip", "dcsr.hip", "coo_plan.hip",
@@ -77,13 +73,6 @@ def build_hip(jobs: int = 8, verbose: bool = False) -> str:
     return HIP_LIB
 
 
-def build_probe() -> str:
-    tmp = PROBE_LIB + ".tmp"
-    _run([_hipcc(), *HIPCC_FLAGS, "-shared", os.path.join(CSRC, "gather_probe.hip"), "-o", tmp])
-    os.replace(tmp, PROBE_LIB)
-    return PROBE_LIB
-
-
 def build_workloads() -> str:
     tmp = WL_LIB + ".tmp"
     _run(["gcc", "-O3", "-fPIC", "-fopenmp", "-shared", "-std=gnu11", "-Wall",
@@ -93,11 +82,10 @@ def build_workloads() -> str:
 
 
 def build(jobs: int = 8, verbose: bool = False):
-    with cf.ThreadPoolExecutor(max_workers=3) as ex:
+    with cf.ThreadPoolExecutor(max_workers=2) as ex:
         f1 = ex.submit(build_hip, jobs, verbose)
         f2 = ex.submit(build_workloads)
-        f3 = ex.submit(build_probe)
-        return f1.result(), f2.result(), f3.result()
+        return f1.result(), f2.result()
 
 
 if __name__ == "__main__":

@@ -24,6 +24,8 @@
 // XCD's L2.
 #include "common.hpp"
 
+#include <cstdlib>
+
 namespace jlust {
 namespace {
 
@@ -124,11 +126,14 @@ __global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_mfma_kernel(
 // memory page, so loading B in the MFMA operand layout (16 columns per
 // instruction) costs 16 address translations per load.  Here each 16-column
 // tile of B is loaded down the columns instead -- lane l covers block
-// sq = l/8 of the chunk, rows 4*((l/2)%4) .. +3, column 2t + l%2 of load t --
-// so one load touches 2 columns, and is transposed into the MFMA layout
-// through a per-wave LDS area.  Load t lands at t*BSR_LSTRIDE + 16*l bytes;
-// the 32-byte pad per load puts column i of an MFMA operand read at bank
-// 4*i (mod 64), so its 16 lanes hit distinct banks.  The chunk's A operands (up to BSR_QCHUNK blocks) stay in
+// sq = l/8 of the chunk, rows 4*(l%4) .. +3, column 2t + (l/4)%2 of load t,
+// so each quad of lanes reads one whole 64-byte column segment (the address
+// unit handles a quad per step when its 64 bytes are contiguous) and one
+// load touches 2 columns -- and is transposed into the MFMA layout through a
+// per-wave LDS area.  Load t lands at t*BSR_LSTRIDE + 16*slot bytes, slot =
+// 8*block + 2*(row group) + column; the 32-byte pad per load puts column i of
+// an MFMA operand read at bank 4*i (mod 64), so its 16 lanes hit distinct
+// banks.  The chunk's A operands (up to BSR_QCHUNK blocks) stay in
 // registers for all of k; the next tile's B is loaded while the current
 // tile's MFMAs run.
 constexpr int BSR_QCHUNK = 8;
@@ -155,8 +160,12 @@ __global__ __launch_bounds__(256) void bsr16_spmm_rowwave_kernel(
     const int i = lane & 15;               // MFMA: A row / B, C column in the tile
     const int g = lane >> 4;               // MFMA: contraction group / C row group
     const int sq = lane >> 3;              // staging: block of the chunk
-    const int srow = 4 * ((lane >> 1) & 3);
-    const int sj = lane & 1;
+    const int srow = 4 * (lane & 3);       // a quad of lanes reads one 64-byte column segment
+    const int sj = (lane >> 2) & 1;
+    // LDS slot of this lane's 16 bytes in a load's area: block sq, row group
+    // srow/4, column sj at (8*sq + 2*(srow/4) + sj) * 16, so that the MFMA
+    // operand reads below (16 lanes, 16 columns) hit distinct banks.
+    const int wslot = (8 * sq + 2 * (lane & 3) + sj) * 16;
     const int64_t crow = R * BSR_BS + 4 * g;
     const int64_t q0 = (int64_t)browptr[R] - origin;
     const int64_t q1 = (int64_t)browptr[R + 1] - origin;
@@ -195,7 +204,7 @@ __global__ __launch_bounds__(256) void bsr16_spmm_rowwave_kernel(
         for (int64_t c0 = 0; c0 < k; c0 += 16) {
 #pragma unroll
             for (int t = 0; t < 8; ++t)
-                *reinterpret_cast<floatx4 *>(ws + t * BSR_LSTRIDE + lane * 16) = st[t];
+                *reinterpret_cast<floatx4 *>(ws + t * BSR_LSTRIDE + wslot) = st[t];
             if (c0 + 16 < k) load_tile(c0 + 16);
             floatx4 acc = zero;
             const char *rd = ws + (i >> 1) * BSR_LSTRIDE + (g * 2 + (i & 1)) * 16;
@@ -218,6 +227,171 @@ __global__ __launch_bounds__(256) void bsr16_spmm_rowwave_kernel(
             }
         }
     }
+}
+
+// Strip kernel (row-major blocks, B and C float4-aligned).  A workgroup owns
+// BSR_SR consecutive block-rows, one wave each, with the row's blocks (up to
+// BSR_QCHUNK) held as MFMA A operands in registers for all of k.  For each
+// 16-column tile the strip's window of B -- block-rows [J_min, J_max] of all
+// its blocks, each of the 16 columns one contiguous run of (J_max - J_min +
+// 1) * 64 bytes -- is copied into LDS with direct global-to-LDS loads
+// (global_load_lds_dwordx4: 64 lanes x 16 bytes of one column per
+// instruction, whole 128-byte lines, no registers), then every wave runs its
+// row's MFMAs from it.  A block used by several rows of the strip is fetched
+// from L2 once instead of once per row, in whole lines instead of 64-byte
+// column pieces: at the banded config the L1-to-L2 read requests fall from
+// 124.7M to 54.8M per call and the address unit's busy time from 86 % to
+// about a third.  The window buffer is single (78 KB), so two workgroups
+// share a CU and each computes while the other waits for its copies (a
+// double-buffered 156 KB window leaves one workgroup per CU with its copy
+// latency exposed: 1.32 ms against 1.15 ms).  Columns sit BSR_CS bytes apart
+// (a 16-byte pad per column), so the 16 lanes of an operand read (16
+// columns, one row group) hit distinct banks.  A strip whose rows hold more
+// than BSR_QCHUNK blocks or whose window exceeds BSR_WMAX block-rows computes
+// its rows with direct operand loads instead (same arithmetic).
+constexpr int BSR_SR = 12;                        // block-rows (waves) per workgroup
+constexpr int BSR_WMAX = BSR_SR + 64;             // window block-rows (a +-32 band)
+constexpr int BSR_CS = BSR_WMAX * 64 + 16;        // LDS bytes per column of a window
+constexpr int BSR_BUF = 16 * BSR_CS;              // the window buffer
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+template <bool BZ>
+__global__ __launch_bounds__(64 * BSR_SR) void bsr16_spmm_strip_kernel(
+    int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
+    const int32_t *__restrict__ bcolind, const float *__restrict__ val, int64_t k, float alpha,
+    const float *__restrict__ B, int64_t ldb, float beta, float *__restrict__ C, int64_t ldc)
+{
+    __shared__ __align__(16) char win[BSR_BUF];
+    __shared__ int32_t s_jmin[BSR_SR], s_jmax[BSR_SR], s_len[BSR_SR];
+    // XCD-major remap of the strip index (grid padded to a multiple of 8).
+    const int64_t per_xcd = (int64_t)gridDim.x / NUM_XCD;
+    const int64_t strip = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+    const int64_t R0 = strip * BSR_SR;
+    if (R0 >= mb) return;                  // whole workgroup
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 15;               // MFMA: A row / B, C column in the tile
+    const int g = lane >> 4;               // MFMA: contraction group / C row group
+    const int64_t R = R0 + wave;
+    const bool live = R < mb;
+    const int64_t q0 = live ? (int64_t)browptr[R] - origin : 0;
+    const int64_t q1 = live ? (int64_t)browptr[R + 1] - origin : 0;
+    const int nq = (int)(q1 - q0);
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+
+    // The strip's window: smallest and largest block column of its blocks.
+    {
+        int32_t jmin = INT32_MAX, jmax = INT32_MIN;
+        for (int64_t q = q0 + lane; q < q1; q += 64) {
+            const int32_t j = bcolind[q] - origin;
+            jmin = min(jmin, j);
+            jmax = max(jmax, j);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            jmin = min(jmin, __shfl_xor(jmin, off, 64));
+            jmax = max(jmax, __shfl_xor(jmax, off, 64));
+        }
+        if (lane == 0) {
+            s_jmin[wave] = jmin;
+            s_jmax[wave] = jmax;
+            s_len[wave] = nq;
+        }
+    }
+    __syncthreads();
+    int32_t jw0 = INT32_MAX, jw1 = INT32_MIN, lmax = 0;
+#pragma unroll
+    for (int w = 0; w < BSR_SR; ++w) {
+        jw0 = min(jw0, s_jmin[w]);
+        jw1 = max(jw1, s_jmax[w]);
+        lmax = max(lmax, s_len[w]);
+    }
+    const int32_t nwin = jw1 >= jw0 ? jw1 - jw0 + 1 : 0;
+    const int64_t crow = R * BSR_BS + 4 * g;
+
+    if (lmax > BSR_QCHUNK || nwin > BSR_WMAX) {
+        // Direct operand loads (any row length, any window).
+        if (!live) return;
+        for (int64_t c0 = 0; c0 < k; c0 += 16) {
+            const int64_t col = c0 + i;
+            const int64_t colc = col < k ? col : k - 1;
+            floatx4 acc = zero;
+            for (int64_t q = q0; q < q1; ++q) {
+                const floatx4 a = *reinterpret_cast<const floatx4 *>(val + q * 256 + i * 16 + 4 * g);
+                const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
+                const floatx4 b = *reinterpret_cast<const floatx4 *>(B + brow + colc * ldb);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+            }
+            if (col < k) {
+                floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + col * ldc);
+                floatx4 out = alpha * acc;
+                if (!BZ) out += beta * *dst;
+                *dst = out;
+            }
+        }
+        return;
+    }
+
+    // A operands and window-relative block rows of this wave's row.
+    floatx4 a[BSR_QCHUNK];
+    int32_t jrel[BSR_QCHUNK];
+#pragma unroll
+    for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+        a[qq] = qq < nq ? *reinterpret_cast<const floatx4 *>(val + (q0 + qq) * 256 + i * 16 + 4 * g) : zero;
+        jrel[qq] = qq < nq ? bcolind[q0 + qq] - origin - jw0 : 0;
+    }
+    // Window copy of one tile: instruction ii = (column j, part p) moves the
+    // column's floats [256 p, 256 p + 256) of the window; lanes past the
+    // window's end, and columns past k, are masked off.
+    const int npc = (nwin * 16 + 255) / 256;     // instructions per column
+    const int ninst = 16 * npc;
+    const int64_t wfloats = (int64_t)nwin * 16;
+    const float *bwin = B + (int64_t)jw0 * BSR_BS;
+    const char *col_i = win + i * BSR_CS + 16 * g;
+    for (int64_t c0 = 0; c0 < k; c0 += 16) {
+        for (int ii = wave; ii < ninst; ii += BSR_SR) {
+            const int j = ii / npc, p = ii % npc;
+            const int64_t f = (int64_t)p * 256 + 4 * lane;
+            if (f < wfloats && c0 + j < k) {
+                __builtin_amdgcn_global_load_lds((const void *)(bwin + f + (c0 + j) * ldb),
+                                                 (lds_void *)(win + j * BSR_CS + p * 1024), 16, 0, 0);
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0);     // this wave's copies are in LDS
+        __syncthreads();                   // ... and every wave's
+        if (live) {
+            floatx4 acc = zero;
+#pragma unroll
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+                if (qq < nq) {
+                    const floatx4 b = *reinterpret_cast<const floatx4 *>(col_i + jrel[qq] * 64);
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[qq][u], b[u], acc, 0, 0, 0);
+                }
+            }
+            const int64_t col = c0 + i;
+            if (col < k) {
+                floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + col * ldc);
+                floatx4 out = alpha * acc;
+                if (!BZ) out += beta * *dst;
+                *dst = out;
+            }
+        }
+        __syncthreads();                   // every wave is done reading before the next copies
+    }
+}
+
+// JLUST_HIP_BSR_STRIP=0 keeps the row-wave kernel.
+bool bsr_strip()
+{
+    static const bool on = [] {
+        const char *e = getenv("JLUST_HIP_BSR_STRIP");
+        return !(e && e[0] == '0');
+    }();
+    return on;
 }
 
 int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
@@ -258,6 +432,17 @@ int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
     const bool rm = row_major_blocks && vals_aligned;
     if (row_major_blocks && !vals_aligned)
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: block values must be 16-byte aligned");
+    if (rm && vec && bsr_strip()) {
+        const int64_t strips = (mb + BSR_SR - 1) / BSR_SR;
+        const int64_t grids = (strips + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+        if (beta == 0.f)
+            hipLaunchKernelGGL((bsr16_spmm_strip_kernel<true>), dim3((unsigned)grids), dim3(64 * BSR_SR), 0, s,
+                               mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
+        else
+            hipLaunchKernelGGL((bsr16_spmm_strip_kernel<false>), dim3((unsigned)grids), dim3(64 * BSR_SR), 0, s,
+                               mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
+        return check_launch("bsr16_spmm_strip_kernel");
+    }
     if (rm && vec) {
         const int64_t wgs = (mb + 3) / 4;
         const int64_t grid4 = (wgs + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
