@@ -506,7 +506,8 @@ int jlust_hip_sddmm_plan_destroy(jlust_sddmm_plan_t plan);
  * column-major = BSRLeft; src/named_formats.jl:106-128, storage as in
  * ext/CUDAExt/CUDAExt.jl:144-156).  B (nb*bs) x k (ldb), C (mb*bs) x k (ldc),
  * column-major.  bs == 16 runs on fp32 MFMA; other block sizes return
- * JLUST_STATUS_UNSUPPORTED_FORMAT.  The reference routes BSR SpMM through the
+ * JLUST_STATUS_UNSUPPORTED_FORMAT (jlust_hip_bsr_expand_csr_i32 + the CSR
+ * SpMM serve them).  The reference routes BSR SpMM through the
  * generic execute(::EmitterBackend, ::Op{:SpMM}) (KernelAbstractionsExt.jl:
  * 35-37), which does not compute it correctly; this entry point implements
  * the operator's definition.
@@ -518,6 +519,29 @@ int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs,
                                int64_t k, float alpha, const float *B,
                                int64_t ldb, float beta, float *C, int64_t ldc,
                                jlust_stream_t stream);
+
+/*
+ * BSR of any b1 x b2 block shape and value type, expanded to CSR for the CSR
+ * kernels: the route of BSR SpMV, and of BSR SpMM where the MFMA path above does
+ * not apply (blocks other than 16 x 16, or Float64).  The reference's
+ * EmitterBackend claims SpMV and SpMM for every sparse format
+ * (KernelAbstractionsExt.jl:31-37); its BSR layout is Formats.BSRRight /
+ * BSRLeft((b1, b2)) (src/named_formats.jl:106-128).  Scalar row b1*R + r lists, for
+ * each stored block q of block-row R in storage order, columns b2*bcol[q] + s,
+ * s = 0..b2-1.  Every stored entry is kept, explicit zeros included, so the
+ * product is the block definition's.  Outputs (caller's buffers, the input's
+ * origin): rowptr[mb*b1 + 1], colind[nnzb*b1*b2], val_out[nnzb*b1*b2].
+ * value_type: 0 = Float64, 1 = Float32.  A browptr that does not run from
+ * origin to origin + nnzb is NONCANONICAL_STORAGE.  Reads two entries of browptr
+ * back, so it synchronises `stream` (not capturable).
+ */
+int jlust_hip_bsr_expand_csr_i32(int64_t mb, int64_t b1, int64_t b2,
+                                 int64_t nnzb, int32_t origin,
+                                 const int32_t *browptr,
+                                 const int32_t *bcolind, const void *val,
+                                 int value_type, int row_major_blocks,
+                                 int32_t *rowptr, int32_t *colind,
+                                 void *val_out, jlust_stream_t stream);
 
 /* ----------------------------------------------------------- conversions */
 

@@ -394,6 +394,102 @@ bool bsr_strip()
     return on;
 }
 
+// ------------------------------------------------- expansion to CSR
+
+// rowptr of the expansion: scalar row b1*R + r starts after the entries of
+// block-rows 0..R-1 (b1*b2 per block) and r rows of block-row R (its block
+// count times b2 each).  One thread per scalar row, plus the final entry.
+__global__ void bsr_expand_rowptr_kernel(int64_t mb, int64_t b1, int64_t b2, int32_t origin,
+                                         const int32_t *__restrict__ browptr, int32_t *__restrict__ rowptr)
+{
+    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row > mb * b1) return;
+    const int64_t R = row / b1, r = row % b1;
+    int64_t v;
+    if (R == mb) {
+        v = ((int64_t)browptr[mb] - origin) * b1 * b2;
+    } else {
+        const int64_t q0 = (int64_t)browptr[R] - origin, q1 = (int64_t)browptr[R + 1] - origin;
+        v = q0 * b1 * b2 + r * (q1 - q0) * b2;
+    }
+    rowptr[row] = (int32_t)(v + origin);
+}
+
+// Columns and values: one thread per stored block entry (q, r, s).  The
+// block-row of block q is found by binary search of browptr; an entry whose
+// target position falls outside [0, total) -- possible only for a browptr
+// that is not non-decreasing -- is not written.
+template <typename T>
+__global__ void bsr_expand_entries_kernel(int64_t mb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
+                                          const int32_t *__restrict__ browptr,
+                                          const int32_t *__restrict__ bcolind, const T *__restrict__ val,
+                                          int row_major_blocks, int32_t *__restrict__ colind,
+                                          T *__restrict__ out)
+{
+    const int64_t bb = b1 * b2, total = nnzb * bb;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total;
+         e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t q = e / bb, w = e % bb;
+        const int64_t r = w / b2, s = w % b2;           // the entry's row and column in its block
+        int64_t lo = 0, hi = mb - 1;                    // last R with browptr[R] - origin <= q
+        while (lo < hi) {
+            const int64_t mid = (lo + hi + 1) >> 1;
+            if ((int64_t)browptr[mid] - origin <= q) lo = mid; else hi = mid - 1;
+        }
+        const int64_t q0 = (int64_t)browptr[lo] - origin, q1 = (int64_t)browptr[lo + 1] - origin;
+        if (q < q0 || q >= q1) continue;
+        const int64_t pos = q0 * bb + r * (q1 - q0) * b2 + (q - q0) * b2 + s;
+        if (pos < 0 || pos >= total) continue;
+        colind[pos] = (int32_t)(((int64_t)bcolind[q] - origin) * b2 + s + origin);
+        out[pos] = row_major_blocks ? val[q * bb + r * b2 + s] : val[q * bb + s * b1 + r];
+    }
+}
+
+int bsr_expand_csr(int64_t mb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin, const int32_t *browptr,
+                   const int32_t *bcolind, const void *val, int value_type, int row_major_blocks,
+                   int32_t *rowptr, int32_t *colind, void *val_out, jlust_stream_t stream)
+{
+    clear_error();
+    if (mb < 0 || b1 <= 0 || b2 <= 0 || nnzb < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_expand_csr: negative extent or block size");
+    if (value_type != 0 && value_type != 1)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE,
+                    "bsr_expand_csr: value_type %d (0 = Float64, 1 = Float32)", value_type);
+    if (int st = check_origin(origin)) return st;
+    if (mb * b1 >= INT32_MAX || nnzb * b1 * b2 >= (int64_t)INT32_MAX - 1)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_expand_csr: the expansion exceeds the Int32 index range");
+    const int64_t total = nnzb * b1 * b2;
+    if (!browptr || !rowptr || bad_ptr(bcolind, nnzb) || bad_ptr(val, total) || bad_ptr(colind, total) ||
+        bad_ptr(val_out, total))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_expand_csr: null device pointer");
+    if (int st = require_device(nullptr)) return st;
+    hipStream_t s = (hipStream_t)stream;
+    // browptr must run from origin to origin + nnzb (two scalars read back).
+    int32_t ends[2] = {0, 0};
+    JLUST_HIP_TRY(hipMemcpyAsync(&ends[0], browptr, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    JLUST_HIP_TRY(hipMemcpyAsync(&ends[1], browptr + mb, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+    JLUST_HIP_TRY(hipStreamSynchronize(s));
+    if (ends[0] != origin || (int64_t)ends[1] != nnzb + origin)
+        return fail(JLUST_STATUS_NONCANONICAL_STORAGE,
+                    "bsr_expand_csr: browptr runs from %d to %d, expected %d to %lld", ends[0], ends[1], origin,
+                    (long long)(nnzb + origin));
+    const int64_t rows = mb * b1 + 1;
+    hipLaunchKernelGGL(bsr_expand_rowptr_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, mb, b1,
+                       b2, origin, browptr, rowptr);
+    if (int st = check_launch("bsr_expand_rowptr_kernel")) return st;
+    if (total == 0) return JLUST_STATUS_SUCCESS;
+    const int64_t blocks = min((total + 255) / 256, (int64_t)65536);
+    if (value_type == 0)
+        hipLaunchKernelGGL((bsr_expand_entries_kernel<double>), dim3((unsigned)blocks), dim3(256), 0, s, mb, b1,
+                           b2, nnzb, origin, browptr, bcolind, (const double *)val, row_major_blocks, colind,
+                           (double *)val_out);
+    else
+        hipLaunchKernelGGL((bsr_expand_entries_kernel<float>), dim3((unsigned)blocks), dim3(256), 0, s, mb, b1,
+                           b2, nnzb, origin, browptr, bcolind, (const float *)val, row_major_blocks, colind,
+                           (float *)val_out);
+    return check_launch("bsr_expand_entries_kernel");
+}
+
 int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
              const int32_t *browptr, const int32_t *bcolind, const float *val,
              int row_major_blocks, int64_t k, float alpha, const float *B, int64_t ldb,
@@ -474,4 +570,13 @@ extern "C" int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs, in
 {
     return jlust::bsr_spmm(mb, nb, bs, nnzb, origin, browptr, bcolind, val, row_major_blocks, k,
                            alpha, B, ldb, beta, C, ldc, stream);
+}
+
+extern "C" int jlust_hip_bsr_expand_csr_i32(int64_t mb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
+                                            const int32_t *browptr, const int32_t *bcolind, const void *val,
+                                            int value_type, int row_major_blocks, int32_t *rowptr,
+                                            int32_t *colind, void *val_out, jlust_stream_t stream)
+{
+    return jlust::bsr_expand_csr(mb, b1, b2, nnzb, origin, browptr, bcolind, val, value_type,
+                                 row_major_blocks, rowptr, colind, val_out, stream);
 }

@@ -55,12 +55,12 @@ def _supports(op: Op) -> bool:
     f = op.formats
     if op.tag == "SpMV" and len(f) == 3:
         return (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_csc_shaped(f[0]) or
-                is_shifted_diag(f[0]) or f[0] == Formats.DCSR or is_periodic_csr(f[0])) and \
+                is_shifted_diag(f[0]) or f[0] == Formats.DCSR or is_periodic_csr(f[0]) or
+                is_bsr(f[0])) and \
             _dense_fmt(f[1]) and \
             _dense_fmt(f[2]) and f[1].ndims == 1 and f[2].ndims == 1
     if op.tag == "SpMM" and len(f) == 3:
-        a_ok = is_csr_shaped(f[0]) or f[0] == Formats.DCSR or \
-            (is_bsr(f[0]) and bsr_blocksize(f[0])[:2] == (16, 16))
+        a_ok = is_csr_shaped(f[0]) or f[0] == Formats.DCSR or is_bsr(f[0])
         return a_ok and _dense_fmt(f[1]) and _dense_fmt(f[2]) and f[1].ndims == 2 and \
             f[2].ndims == 2
     if op.tag == "SDDMM" and len(f) == 3:
@@ -185,6 +185,9 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     if is_periodic_csr(u_A.format):
         _periodic_spmv(u_A, x, y, alpha, beta)
         return u_y
+    if is_bsr(u_A.format):
+        _spmv(_bsr_as_csr(u_A), u_x, u_y, alpha, beta)
+        return u_y
     if is_shifted_diag(u_A.format):
         lv = u_A.format.levels[1]
         dev = _check_same_device(x, y)
@@ -299,6 +302,44 @@ def _dcsr_product(u_A: USTensor, u_X: USTensor, u_Y: USTensor, alpha, beta):
     return u_Y
 
 
+def _bsr_parts(u: USTensor):
+    """(b1, b2, row_major, browptr, bcolind, mb, nb) of a BSR tensor, checked."""
+    b1, b2, row_major = bsr_blocksize(u.format)
+    browptr, bcolind = u.pos_buffers[1], u.crd_buffers[1]
+    if browptr is None or bcolind is None:
+        raise NonCanonicalStorage(f"{u.format}: missing level-2 pos/crd buffer")
+    _check_index(u, browptr, bcolind)
+    m, n = u.extents
+    if m % b1 or n % b2:
+        raise IncompatibleExtents(f"BSR extents {m}x{n} are not multiples of {b1}x{b2}")
+    mb, nb = m // b1, n // b2
+    if browptr.numel() != mb + 1 or nnz(u) != bcolind.numel() * b1 * b2:
+        raise NonCanonicalStorage("BSR: browptr must have mb+1 entries and val nnzb*b1*b2")
+    return b1, b2, row_major, browptr, bcolind, mb, nb
+
+
+def _bsr_as_csr(u: USTensor) -> USTensor:
+    """The BSR tensor expanded to CSR on the device (jlust_hip_bsr_expand_csr_i32):
+    scalar rows in block order, every stored entry kept, the same origin."""
+    suf = _value_suffix(u)
+    b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u)
+    v = nonzeros(u)
+    if not v.is_contiguous():
+        raise NonCanonicalStorage("value buffers must be contiguous")
+    dev = _check_same_device(browptr, bcolind, v)
+    total = bcolind.numel() * b1 * b2
+    rowptr = torch.empty(mb * b1 + 1, dtype=torch.int32, device=dev)
+    colind = torch.empty(total, dtype=torch.int32, device=dev)
+    val = torch.empty(total, dtype=v.dtype, device=dev)
+    with _on(dev):
+        st = _lib.lib().jlust_hip_bsr_expand_csr_i32(
+            mb, b1, b2, bcolind.numel(), u.origin.offset, _ptr(browptr), _ptr(bcolind), _ptr(v),
+            0 if suf == "f64" else 1, int(row_major), _ptr(rowptr), _ptr(colind), _ptr(val),
+            _stream(dev))
+    _lib.check(st, "bsr_expand_csr", u.format, _BE, v.dtype)
+    return USTensor(u.extents, Formats.CSR, (None, rowptr), (None, colind), val, None, u.origin)
+
+
 def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_rows=False):
     suf = _value_suffix(u_A)
     T = nonzeros(u_A).dtype
@@ -317,16 +358,11 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
     if u_A.format == Formats.DCSR:
         return _dcsr_product(u_A, u_B, u_C, alpha, beta)
     if is_bsr(u_A.format):
-        b1, b2, row_major = bsr_blocksize(u_A.format)
-        if suf != "f32":
-            raise UnsupportedValueType(T, _BE, "BSR SpMM runs on fp32 MFMA")
-        browptr, bcolind = u_A.pos_buffers[1], u_A.crd_buffers[1]
-        _check_index(u_A, browptr, bcolind)
-        mb, nb = -(-m // b1), -(-n // b2)
-        if m % b1 or n % b2:
-            raise IncompatibleExtents(f"BSR extents {m}x{n} are not multiples of {b1}x{b2}")
-        if browptr.numel() != mb + 1 or nnz(u_A) != bcolind.numel() * b1 * b2:
-            raise NonCanonicalStorage("BSR: browptr must have mb+1 entries and val nnzb*b1*b2")
+        b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
+        if (b1, b2) != (16, 16) or suf != "f32":
+            # Blocks other than 16 x 16, or Float64: the CSR expansion and the
+            # CSR SpMM (the fp32 MFMA kernel serves 16 x 16 only).
+            return _spmm(_bsr_as_csr(u_A), u_B, u_C, alpha, beta, skip_empty_rows)
         dev = _check_same_device(browptr, bcolind, nonzeros(u_A), B, C)
         with _on(dev):
             st = L.jlust_hip_bsr_spmm_f32_i32(

@@ -393,38 +393,41 @@ DEF_SDDMM_ABSREF(f32, float)
  * BSRLeft.  The reference has no sound BSR compute path (its walker never
  * advances through the inner Dense levels), so the operator is pinned by its
  * mathematical definition: expand to CSR and run the CSR path.
- * Expansion: scalar row bs*R + r lists, for each stored block q of block-row R
- * in storage order, columns bs*bcol[q] + s for s = 0..bs-1 (ascending when the
- * block-columns are sorted).  Every stored entry is kept (explicit zeros too).
- * Output CSR uses the input's origin.  rowptr has mb*bs + 1 entries, colind and
- * val nnzb*bs*bs entries.
+ * Expansion (b1 x b2 blocks): scalar row b1*R + r lists, for each stored block
+ * q of block-row R in storage order, columns b2*bcol[q] + s for s = 0..b2-1
+ * (ascending when the block-columns are sorted).  Every stored entry is kept
+ * (explicit zeros too).  Output CSR uses the input's origin.  rowptr has
+ * mb*b1 + 1 entries, colind and val nnzb*b1*b2 entries.  Block q's entry
+ * (r, s) is bval[q*b1*b2 + r*b2 + s] for row-major blocks and
+ * bval[q*b1*b2 + s*b1 + r] for column-major ones.
  */
 #define DEF_BSR2CSR(SUF, T)                                                    \
-void oracle_bsr_to_csr_##SUF(int32_t mb, int32_t bs, int32_t origin,           \
-                             const int32_t *browptr, const int32_t *bcolind,   \
-                             const T *bval, int row_major_blocks,              \
-                             int32_t *rowptr, int32_t *colind, T *val)         \
+void oracle_bsr_to_csr_##SUF(int32_t mb, int32_t b1, int32_t b2,               \
+                             int32_t origin, const int32_t *browptr,           \
+                             const int32_t *bcolind, const T *bval,            \
+                             int row_major_blocks, int32_t *rowptr,            \
+                             int32_t *colind, T *val)                          \
 {                                                                              \
-    int64_t bb = (int64_t)bs * bs;                                             \
+    int64_t bb = (int64_t)b1 * b2;                                             \
     rowptr[0] = origin;                                                        \
     for (int64_t R = 0; R < mb; ++R) {                                         \
         int64_t q0 = (int64_t)browptr[R] - origin;                             \
         int64_t q1 = (int64_t)browptr[R + 1] - origin;                         \
         int64_t nb_row = q1 - q0;                                              \
-        for (int64_t r = 0; r < bs; ++r) {                                     \
-            int64_t row = R * bs + r;                                          \
+        for (int64_t r = 0; r < b1; ++r) {                                     \
+            int64_t row = R * b1 + r;                                          \
             int64_t base = (int64_t)rowptr[row] - origin;                      \
             int64_t w = 0;                                                     \
             for (int64_t q = q0; q < q1; ++q) {                                \
                 int64_t bc = (int64_t)bcolind[q] - origin;                     \
-                for (int64_t s = 0; s < bs; ++s) {                             \
-                    colind[base + w] = (int32_t)(bc * bs + s + origin);        \
-                    val[base + w] = row_major_blocks ? bval[q * bb + r * bs + s] \
-                                                     : bval[q * bb + s * bs + r]; \
+                for (int64_t s = 0; s < b2; ++s) {                             \
+                    colind[base + w] = (int32_t)(bc * b2 + s + origin);        \
+                    val[base + w] = row_major_blocks ? bval[q * bb + r * b2 + s] \
+                                                     : bval[q * bb + s * b1 + r]; \
                     ++w;                                                       \
                 }                                                              \
             }                                                                  \
-            rowptr[row + 1] = (int32_t)(rowptr[row] + nb_row * bs);            \
+            rowptr[row + 1] = (int32_t)(rowptr[row] + nb_row * b2);            \
         }                                                                      \
     }                                                                          \
 }

@@ -70,7 +70,7 @@ def lib():
                 _I32, _I32, _P, _P, _I64, _D, _P, _I64, _P, _I64, _D, _P, _P,
                 _P, _INT]
             getattr(L, f"oracle_bsr_to_csr_{suf}").argtypes = [
-                _I32, _I32, _I32, _P, _P, _P, _INT, _P, _P, _P]
+                _I32, _I32, _I32, _I32, _P, _P, _P, _INT, _P, _P, _P]
             for name, args in (
                     ("csr_to_csc", [_I32, _I32, _I32, _P, _P, _P, _P, _P, _P]),
                     ("csr_to_coo", [_I32, _I32, _P, _P, _P, _P, _P, _P, _P]),
@@ -319,30 +319,33 @@ def csr_sddmm_absref(rowptr, colind, A, B, alpha=1.0, beta=0.0, C0=None,
     return out
 
 
-def bsr_to_csr(browptr, bcolind, bval, bs, origin=1, row_major_blocks=True):
-    """Bit-exact expansion of a BSR matrix (block values flat, nnzb*bs*bs)."""
+def bsr_to_csr(browptr, bcolind, bval, bs, origin=1, row_major_blocks=True, b2=None):
+    """Bit-exact expansion of a BSR matrix of bs x b2 blocks (b2 = bs when
+    None; block values flat, nnzb*bs*b2), every stored entry kept."""
     L = lib()
     dt = np.asarray(bval).dtype
     suf = _suf(dt)
+    b1 = bs
+    b2 = bs if b2 is None else b2
     browptr = _c(browptr, np.int32)
     bcolind = _c(bcolind, np.int32)
     bval = _c(bval, dt).reshape(-1)
     mb = browptr.size - 1
     nnzb = bcolind.size
-    rowptr = np.empty(mb * bs + 1, np.int32)
-    colind = np.empty(nnzb * bs * bs, np.int32)
-    val = np.empty(nnzb * bs * bs, dt)
+    rowptr = np.empty(mb * b1 + 1, np.int32)
+    colind = np.empty(nnzb * b1 * b2, np.int32)
+    val = np.empty(nnzb * b1 * b2, dt)
     getattr(L, f"oracle_bsr_to_csr_{suf}")(
-        mb, bs, origin, _ptr(browptr), _ptr(bcolind), _ptr(bval),
+        mb, b1, b2, origin, _ptr(browptr), _ptr(bcolind), _ptr(bval),
         int(bool(row_major_blocks)), _ptr(rowptr), _ptr(colind), _ptr(val))
     return rowptr, colind, val
 
 
 def bsr_spmm(browptr, bcolind, bval, bs, B, alpha=1.0, beta=0.0, C0=None,
-             origin=1, row_major_blocks=True, nthreads=None):
+             origin=1, row_major_blocks=True, nthreads=None, b2=None):
     """BSR SpMM pinned by its definition: expand to CSR, run the CSR path."""
     rp, ci, v = bsr_to_csr(browptr, bcolind, bval, bs, origin,
-                           row_major_blocks)
+                           row_major_blocks, b2)
     return csr_spmm(rp, ci, v, B, alpha, beta, C0, origin,
                     nthreads=nthreads)[0]
 

@@ -151,12 +151,93 @@ def test_bsr_config5_full_sampled_block_rows(J, O):
     assert_within(C[rows], ref, absref, np.float32, cfg["name"])
 
 
-def test_bsr_unsupported_block_size(J):
+def test_bsr_mfma_entry_rejects_other_block_sizes(J):
+    """The fp32 MFMA entry point serves 16 x 16 blocks only and says so; the
+    host routes other shapes through the CSR expansion (tests below)."""
     import torch
-    A = J.bsr_tensor(dev(np.array([1, 2], np.int32)), dev(np.array([1], np.int32)),
-                     dev(np.ones(64, np.float32)), (8, 8), (8, 8))
-    with pytest.raises(J.UnsupportedFormat):
-        J.execute(J.SpMMOp, A, dev(np.ones((8, 4), np.float32)), J.dense_matrix(8, 4, dtype=torch.float32))
+    from jlust_amd import _lib
+    bp = dev(np.array([1, 2], np.int32))
+    bc = dev(np.array([1], np.int32))
+    v = dev(np.ones(64, np.float32))
+    B = dev(np.ones((8, 4), np.float32))
+    C = J.dense_matrix(8, 4, dtype=torch.float32)
+    st = _lib.lib().jlust_hip_bsr_spmm_f32_i32(
+        1, 1, 8, 1, 1, bp.data_ptr(), bc.data_ptr(), v.data_ptr(), 1, 4, 1.0, B.data_ptr(), 8, 0.0,
+        C.data_ptr(), 8, torch.cuda.current_stream().cuda_stream)
+    assert _lib.STATUS[st] == "UNSUPPORTED_FORMAT"
+
+
+def _random_rect_bsr(mb, nb, b1, b2, per_row, seed, dtype, row_major, origin=1, zeros=True):
+    """Random BSR of b1 x b2 blocks; small integers (exact sums) with some
+    stored zeros.  Returns browptr, bcolind, the flat values in the block order
+    asked for, and the same blocks row-major as (nnzb, b1, b2)."""
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(0, per_row + 1, mb)
+    bcols = [np.sort(rng.choice(nb, min(c, nb), replace=False)) for c in counts]
+    browptr = (np.r_[0, np.cumsum([c.size for c in bcols])] + origin).astype(np.int32)
+    bcolind = (np.concatenate(bcols) + origin).astype(np.int32) if bcols else np.zeros(0, np.int32)
+    blocks = rng.integers(-4, 5, (bcolind.size, b1, b2)).astype(dtype)
+    if zeros:
+        blocks[blocks == 4] = 0
+    flat = blocks.reshape(-1) if row_major else blocks.transpose(0, 2, 1).reshape(-1)
+    return browptr, bcolind, np.ascontiguousarray(flat), blocks
+
+
+@pytest.mark.parametrize("b1,b2", [(2, 2), (4, 8), (3, 5), (16, 16), (1, 7)])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("row_major", [True, False])
+def test_bsr_any_block_shape_spmm_and_spmv(J, O, b1, b2, dtype, row_major):
+    """BSR of any block shape and value type (16 x 16 fp32 excepted, the MFMA
+    path): SpMM and SpMV through the device CSR expansion against the oracle's
+    expansion + CSR path, with alpha/beta; integer data, so the results are
+    exact in both precisions."""
+    import torch
+    if (b1, b2) == (16, 16) and dtype == np.float32:
+        pytest.skip("16 x 16 fp32 is the MFMA kernel (tested above)")
+    mb, nb, k = 37, 29, 9
+    origin = 1 if row_major else 0
+    bp, bc, flat, _ = _random_rect_bsr(mb, nb, b1, b2, 5, 100 + b1 * 7 + b2, dtype, row_major, origin)
+    A = J.bsr_tensor(dev(bp), dev(bc), dev(flat), (mb * b1, nb * b2), (b1, b2), row_major,
+                     J.OneBased() if origin == 1 else J.ZeroBased())
+    rng = np.random.default_rng(5)
+    B = np.asfortranarray(rng.integers(-3, 4, (nb * b2, k)).astype(dtype))
+    C0 = np.asfortranarray(rng.integers(-3, 4, (mb * b1, k)).astype(dtype))
+    C = J.dense_matrix(mb * b1, k, dtype=torch.float64 if dtype == np.float64 else torch.float32)
+    C.copy_(dev(C0))
+    J.execute(J.SpMMOp, A, dev(B), C, alpha=2.0, beta=-1.0)
+    ref = O.bsr_spmm(bp, bc, flat, b1, B, 2.0, -1.0, C0, origin=origin, row_major_blocks=row_major, b2=b2)
+    np.testing.assert_array_equal(host(C), ref)
+    x = rng.integers(-3, 4, nb * b2).astype(dtype)
+    y0 = rng.integers(-3, 4, mb * b1).astype(dtype)
+    y = dev(y0.copy())
+    J.execute(J.SpMVOp, A, dev(x), y, alpha=0.5, beta=2.0)
+    rp, ci, v = O.bsr_to_csr(bp, bc, flat, b1, origin, row_major, b2)
+    yref = O.csr_spmv(rp, ci, v, x, 0.5, 2.0, y0, origin)
+    np.testing.assert_array_equal(host(y), yref)
+
+
+def test_bsr_expansion_keeps_stored_zeros_and_matches_oracle_arrays(J, O):
+    """jlust_hip_bsr_expand_csr_i32 itself: rowptr, colind and values equal
+    the oracle's expansion array for array (explicit zeros kept)."""
+    from jlust_amd import hip_backend as HB
+    b1, b2 = 3, 4
+    bp, bc, flat, _ = _random_rect_bsr(11, 13, b1, b2, 4, 77, np.float64, False)
+    A = J.bsr_tensor(dev(bp), dev(bc), dev(flat), (11 * b1, 13 * b2), (b1, b2), False)
+    E = HB._bsr_as_csr(A)
+    rp, ci, v = O.bsr_to_csr(bp, bc, flat, b1, 1, False, b2)
+    assert np.array_equal(host(E.pos_buffers[1]), rp)
+    assert np.array_equal(host(E.crd_buffers[1]), ci)
+    assert np.array_equal(host(J.nonzeros(E)).view(np.uint64), v.view(np.uint64))
+    assert (v == 0).any()
+
+
+def test_bsr_expansion_rejects_bad_browptr(J):
+    import torch
+    bp = dev(np.array([1, 2, 5], np.int32))           # ends at 5, but only 2 blocks are stored
+    bc = dev(np.array([1, 2], np.int32))
+    A = J.bsr_tensor(bp, bc, dev(np.ones(2 * 4, np.float64)), (4, 4), (2, 2))
+    with pytest.raises(J.NonCanonicalStorage):
+        J.execute(J.SpMVOp, A, dev(np.ones(4)), torch.zeros(4, dtype=torch.float64, device="cuda"))
 
 
 @pytest.mark.parametrize("beta", [0.0, -0.5])

@@ -58,7 +58,10 @@ def test_supports_backend_table():
     assert not J.supports_backend(be, J.SpMMOp(d2, d2, d2))
     assert J.supports_backend(be, J.SpMMOp(J.Formats.BSRRight((16, 16)), d2, d2))
     assert J.supports_backend(be, J.SpMMOp(J.Formats.BSRLeft((16, 16)), d2, d2))
-    assert not J.supports_backend(be, J.SpMMOp(J.Formats.BSRRight((8, 8)), d2, d2))
+    # Other block shapes and BSR SpMV go through the device CSR expansion.
+    assert J.supports_backend(be, J.SpMMOp(J.Formats.BSRRight((8, 8)), d2, d2))
+    assert J.supports_backend(be, J.SpMMOp(J.Formats.BSRLeft((2, 3)), d2, d2))
+    assert J.supports_backend(be, J.SpMVOp(J.Formats.BSRRight((4, 8)), d1, d1))
     assert J.supports_backend(be, J.SDDMMOp(d2, d2, J.Formats.CSR))
     assert not J.supports_backend(be, J.SDDMMOp(J.Formats.CSR, d2, J.Formats.CSR))
     assert not J.supports_backend(object(), J.SpMVOp(J.Formats.CSR, d1, d1))

@@ -253,6 +253,33 @@ def test_bsr_equals_dense_block_product():
     np.testing.assert_array_equal(O.bsr_spmm(browptr, bcolind, val, bs, B), D @ B)
 
 
+@pytest.mark.parametrize("b1,b2", [(2, 2), (4, 8), (3, 5), (1, 7)])
+@pytest.mark.parametrize("row_major", [True, False])
+def test_bsr_rectangular_expansion_against_scipy(b1, b2, row_major):
+    """Rectangular blocks, both block orders: the expansion keeps every stored
+    entry (explicit zeros too) and equals scipy's bsr_matrix densely; the
+    product equals the dense product exactly on small integers."""
+    import scipy.sparse as sp
+    rng = np.random.default_rng(40 + b1 * 10 + b2)
+    mb, nb, k = 7, 6, 5
+    counts = rng.integers(0, 4, mb)
+    bcol = [np.sort(rng.choice(nb, c, replace=False)) for c in counts]
+    indptr = np.r_[0, np.cumsum(counts)].astype(np.int32)
+    indices = np.concatenate(bcol).astype(np.int32)
+    blocks = rng.integers(-3, 4, (indices.size, b1, b2)).astype(np.float64)
+    blocks[blocks == 3] = 0.0              # explicit zeros stay stored
+    flat = blocks.reshape(-1) if row_major else blocks.transpose(0, 2, 1).reshape(-1)
+    rp, ci, v = O.bsr_to_csr(indptr + 1, indices + 1, flat, b1, 1, row_major, b2)
+    assert rp.size == mb * b1 + 1 and v.size == indices.size * b1 * b2
+    ref = sp.bsr_matrix((blocks, indices, indptr), shape=(mb * b1, nb * b2)).toarray()
+    got = sp.csr_matrix((v, ci - 1, rp - 1), shape=(mb * b1, nb * b2)).toarray()
+    np.testing.assert_array_equal(got, ref)
+    B = np.asfortranarray(rng.integers(-3, 4, (nb * b2, k)).astype(np.float64))
+    np.testing.assert_array_equal(
+        O.bsr_spmm(indptr + 1, indices + 1, flat, b1, B, row_major_blocks=row_major, b2=b2),
+        ref @ B)
+
+
 # -------------------------------------------------------- strategy semantics
 
 def test_spmm_strategy_selection():
