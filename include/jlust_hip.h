@@ -54,6 +54,7 @@ typedef struct jlust_spmv_graph *jlust_spmv_graph_t;
 typedef struct jlust_convert *jlust_convert_t;
 typedef struct jlust_spmm_plan *jlust_spmm_plan_t;
 typedef struct jlust_sddmm_plan *jlust_sddmm_plan_t;
+typedef struct jlust_bsr_plan *jlust_bsr_plan_t;
 
 /*
  * Status codes.  The Julia side maps them onto the reference's exception
@@ -542,6 +543,44 @@ int jlust_hip_bsr_expand_csr_i32(int64_t mb, int64_t b1, int64_t b2,
                                  int value_type, int row_major_blocks,
                                  int32_t *rowptr, int32_t *colind,
                                  void *val_out, jlust_stream_t stream);
+
+/*
+ * Prepared BSR SpMM, the BSR analyse handle (the cuSPARSE SpMM handle
+ * contract, ext/CUDAExt/ops/spmm.jl:8-70: analysis and workspace once,
+ * execute many times, update_values! for new values of the same pattern).
+ * 16 x 16 Float32 blocks (16-byte aligned values for BSRRight) keep the MFMA
+ * kernels and read the caller's buffers in place.  Any other b1 x b2 shape,
+ * or Float64, is expanded to CSR once (jlust_hip_bsr_expand_csr_i32's
+ * layout; the plan owns it) and runs through a CSR SpMM plan over it for k
+ * columns.  create synchronises `stream` (browptr's ends are read back and
+ * the CSR plan analyses its rows); update_values re-expands only the values,
+ * stream-ordered, on the expansion path, and is a pointer swap on the MFMA
+ * path.  execute: B (nb*b2) x k (ldb), C (mb*b1) x k (ldc), column-major;
+ * C = alpha*A*B + beta*C (beta == 0: C write-only).  info: path 0 = MFMA,
+ * 1 = CSR expansion.  The plan keeps browptr, bcolind (and, on the MFMA path,
+ * the values) by pointer: the caller keeps them alive.
+ */
+int jlust_hip_bsr_spmm_plan_create(int64_t mb, int64_t nb, int64_t b1,
+                                   int64_t b2, int64_t nnzb, int32_t origin,
+                                   int value_type, int row_major_blocks,
+                                   const int32_t *browptr,
+                                   const int32_t *bcolind, const void *val,
+                                   int64_t k, jlust_stream_t stream,
+                                   jlust_bsr_plan_t *plan_out);
+int jlust_hip_bsr_spmm_plan_update_values(jlust_bsr_plan_t plan,
+                                          const void *val,
+                                          jlust_stream_t stream);
+int jlust_hip_bsr_spmm_plan_execute_f32(jlust_bsr_plan_t plan, float alpha,
+                                        const float *B, int64_t ldb,
+                                        float beta, float *C, int64_t ldc,
+                                        jlust_stream_t stream);
+int jlust_hip_bsr_spmm_plan_execute_f64(jlust_bsr_plan_t plan, double alpha,
+                                        const double *B, int64_t ldb,
+                                        double beta, double *C, int64_t ldc,
+                                        jlust_stream_t stream);
+int jlust_hip_bsr_spmm_plan_info(jlust_bsr_plan_t plan, int32_t *path);
+/* Drains the device, then frees the plan's expansion and CSR plan. */
+int jlust_hip_bsr_spmm_plan_destroy(jlust_bsr_plan_t plan);
 
 /* ----------------------------------------------------------- conversions */
 

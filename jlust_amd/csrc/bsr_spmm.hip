@@ -25,6 +25,7 @@
 #include "common.hpp"
 
 #include <cstdlib>
+#include <memory>
 
 namespace jlust {
 namespace {
@@ -415,7 +416,8 @@ __global__ void bsr_expand_rowptr_kernel(int64_t mb, int64_t b1, int64_t b2, int
     rowptr[row] = (int32_t)(v + origin);
 }
 
-// Columns and values: one thread per stored block entry (q, r, s).  The
+// Columns and values (values only when colind is null): one thread per
+// stored block entry (q, r, s).  The
 // block-row of block q is found by binary search of browptr; an entry whose
 // target position falls outside [0, total) -- possible only for a browptr
 // that is not non-decreasing -- is not written.
@@ -440,9 +442,27 @@ __global__ void bsr_expand_entries_kernel(int64_t mb, int64_t b1, int64_t b2, in
         if (q < q0 || q >= q1) continue;
         const int64_t pos = q0 * bb + r * (q1 - q0) * b2 + (q - q0) * b2 + s;
         if (pos < 0 || pos >= total) continue;
-        colind[pos] = (int32_t)(((int64_t)bcolind[q] - origin) * b2 + s + origin);
+        if (colind) colind[pos] = (int32_t)(((int64_t)bcolind[q] - origin) * b2 + s + origin);
         out[pos] = row_major_blocks ? val[q * bb + r * b2 + s] : val[q * bb + s * b1 + r];
     }
+}
+
+int bsr_expand_entries(int64_t mb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin, const int32_t *browptr,
+                       const int32_t *bcolind, const void *val, int value_type, int row_major_blocks,
+                       int32_t *colind, void *val_out, hipStream_t s)
+{
+    const int64_t total = nnzb * b1 * b2;
+    if (total == 0) return JLUST_STATUS_SUCCESS;
+    const int64_t blocks = min((total + 255) / 256, (int64_t)65536);
+    if (value_type == 0)
+        hipLaunchKernelGGL((bsr_expand_entries_kernel<double>), dim3((unsigned)blocks), dim3(256), 0, s, mb, b1,
+                           b2, nnzb, origin, browptr, bcolind, (const double *)val, row_major_blocks, colind,
+                           (double *)val_out);
+    else
+        hipLaunchKernelGGL((bsr_expand_entries_kernel<float>), dim3((unsigned)blocks), dim3(256), 0, s, mb, b1,
+                           b2, nnzb, origin, browptr, bcolind, (const float *)val, row_major_blocks, colind,
+                           (float *)val_out);
+    return check_launch("bsr_expand_entries_kernel");
 }
 
 int bsr_expand_csr(int64_t mb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin, const int32_t *browptr,
@@ -477,17 +497,8 @@ int bsr_expand_csr(int64_t mb, int64_t b1, int64_t b2, int64_t nnzb, int32_t ori
     hipLaunchKernelGGL(bsr_expand_rowptr_kernel, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, s, mb, b1,
                        b2, origin, browptr, rowptr);
     if (int st = check_launch("bsr_expand_rowptr_kernel")) return st;
-    if (total == 0) return JLUST_STATUS_SUCCESS;
-    const int64_t blocks = min((total + 255) / 256, (int64_t)65536);
-    if (value_type == 0)
-        hipLaunchKernelGGL((bsr_expand_entries_kernel<double>), dim3((unsigned)blocks), dim3(256), 0, s, mb, b1,
-                           b2, nnzb, origin, browptr, bcolind, (const double *)val, row_major_blocks, colind,
-                           (double *)val_out);
-    else
-        hipLaunchKernelGGL((bsr_expand_entries_kernel<float>), dim3((unsigned)blocks), dim3(256), 0, s, mb, b1,
-                           b2, nnzb, origin, browptr, bcolind, (const float *)val, row_major_blocks, colind,
-                           (float *)val_out);
-    return check_launch("bsr_expand_entries_kernel");
+    return bsr_expand_entries(mb, b1, b2, nnzb, origin, browptr, bcolind, val, value_type, row_major_blocks,
+                              colind, val_out, s);
 }
 
 int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
@@ -579,4 +590,161 @@ extern "C" int jlust_hip_bsr_expand_csr_i32(int64_t mb, int64_t b1, int64_t b2, 
 {
     return jlust::bsr_expand_csr(mb, b1, b2, nnzb, origin, browptr, bcolind, val, value_type,
                                  row_major_blocks, rowptr, colind, val_out, stream);
+}
+
+// ------------------------------------------------------------------- plans
+
+// A prepared BSR SpMM (the analyse-once handle of the C ABI; the cuSPARSE SpMM
+// handle contract, ext/CUDAExt/ops/spmm.jl:8-70, for BSR).  16 x 16 fp32
+// blocks keep the MFMA kernels and the caller's buffers.  Any other block
+// shape, or Float64, is expanded to CSR once (the plan owns the expansion)
+// and runs through a CSR SpMM plan over it; update_values re-expands the
+// values only, on the stream.
+static size_t bsr_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+struct jlust_bsr_plan {
+    int64_t mb = 0, nb = 0, b1 = 0, b2 = 0, nnzb = 0, k = 0;
+    int32_t origin = 0;
+    int value_type = 0, row_major = 1, device = 0;
+    const int32_t *browptr = nullptr;
+    const int32_t *bcolind = nullptr;
+    const void *val = nullptr;
+    bool mfma = false;
+    void *mem = nullptr;                // expansion: rowptr | colind | values
+    int32_t *rowptr = nullptr;
+    int32_t *colind = nullptr;
+    void *cval = nullptr;
+    jlust_spmm_plan_t csr = nullptr;
+};
+
+extern "C" int jlust_hip_bsr_spmm_plan_create(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
+                                              int32_t origin, int value_type, int row_major_blocks,
+                                              const int32_t *browptr, const int32_t *bcolind, const void *val,
+                                              int64_t k, jlust_stream_t stream, jlust_bsr_plan_t *plan_out)
+{
+    using namespace jlust;
+    clear_error();
+    if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_create: null plan_out");
+    *plan_out = nullptr;
+    if (mb < 0 || nb < 0 || b1 <= 0 || b2 <= 0 || nnzb < 0 || k < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_create: negative extent or block size");
+    if (value_type != 0 && value_type != 1)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE,
+                    "bsr_spmm_plan_create: value_type %d (0 = Float64, 1 = Float32)", value_type);
+    if (int st = check_origin(origin)) return st;
+    if (mb * b1 >= INT32_MAX || nb * b2 >= INT32_MAX || nnzb * b1 * b2 >= (int64_t)INT32_MAX - 1)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_create: extents exceed the Int32 index range");
+    const int64_t total = nnzb * b1 * b2;
+    if (!browptr || bad_ptr(bcolind, nnzb) || bad_ptr(val, total))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_create: null device pointer");
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    std::unique_ptr<jlust_bsr_plan> p(new jlust_bsr_plan());
+    p->mb = mb;
+    p->nb = nb;
+    p->b1 = b1;
+    p->b2 = b2;
+    p->nnzb = nnzb;
+    p->k = k;
+    p->origin = origin;
+    p->value_type = value_type;
+    p->row_major = row_major_blocks ? 1 : 0;
+    p->device = dev;
+    p->browptr = browptr;
+    p->bcolind = bcolind;
+    p->val = val;
+    p->mfma = b1 == BSR_BS && b2 == BSR_BS && value_type == 1 &&
+              (!row_major_blocks || (uintptr_t)val % 16 == 0);
+    if (!p->mfma) {
+        const size_t tsz = value_type == 0 ? sizeof(double) : sizeof(float);
+        const size_t nz = (size_t)(total > 0 ? total : 1);
+        const size_t sz_rp = bsr_align_up(sizeof(int32_t) * (size_t)(mb * b1 + 1), 256);
+        const size_t sz_ci = bsr_align_up(sizeof(int32_t) * nz, 256);
+        JLUST_HIP_TRY(hipMalloc(&p->mem, sz_rp + sz_ci + bsr_align_up(tsz * nz, 256)));
+        char *b = (char *)p->mem;
+        p->rowptr = (int32_t *)b;
+        p->colind = (int32_t *)(b + sz_rp);
+        p->cval = b + sz_rp + sz_ci;
+        int st = bsr_expand_csr(mb, b1, b2, nnzb, origin, browptr, bcolind, val, value_type, p->row_major,
+                                p->rowptr, p->colind, p->cval, stream);
+        if (!st)
+            st = jlust_hip_csr_spmm_plan_create(mb * b1, nb * b2, k, total, origin, value_type, p->rowptr,
+                                                p->colind, p->cval, stream, &p->csr);
+        if (st) {
+            (void)hipStreamSynchronize((hipStream_t)stream);
+            (void)hipFree(p->mem);
+            return st;
+        }
+    }
+    *plan_out = p.release();
+    return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_bsr_spmm_plan_update_values(jlust_bsr_plan_t plan, const void *val, jlust_stream_t stream)
+{
+    using namespace jlust;
+    clear_error();
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_update_values: null plan");
+    const int64_t total = plan->nnzb * plan->b1 * plan->b2;
+    if (bad_ptr(val, total)) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_update_values: null values");
+    if (plan->mfma && plan->row_major && (uintptr_t)val % 16 != 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_update_values: block values must be 16-byte aligned");
+    plan->val = val;
+    if (plan->mfma) return JLUST_STATUS_SUCCESS;     // the kernels read the values in place
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    if (dev != plan->device)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "bsr_spmm_plan_update_values: plan belongs to device %d, current device is %d", plan->device, dev);
+    return bsr_expand_entries(plan->mb, plan->b1, plan->b2, plan->nnzb, plan->origin, plan->browptr, plan->bcolind,
+                              val, plan->value_type, plan->row_major, nullptr, plan->cval, (hipStream_t)stream);
+}
+
+extern "C" int jlust_hip_bsr_spmm_plan_execute_f32(jlust_bsr_plan_t plan, float alpha, const float *B, int64_t ldb,
+                                                   float beta, float *C, int64_t ldc, jlust_stream_t stream)
+{
+    using namespace jlust;
+    clear_error();
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_execute: null plan");
+    if (plan->value_type != 1)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE, "bsr_spmm_plan_execute: plan was created for Float64 values");
+    if (!plan->mfma)
+        return jlust_hip_csr_spmm_plan_execute_f32(plan->csr, alpha, B, ldb, beta, C, ldc, 0, stream);
+    return bsr_spmm(plan->mb, plan->nb, BSR_BS, plan->nnzb, plan->origin, plan->browptr, plan->bcolind,
+                    (const float *)plan->val, plan->row_major, plan->k, alpha, B, ldb, beta, C, ldc, stream);
+}
+
+extern "C" int jlust_hip_bsr_spmm_plan_execute_f64(jlust_bsr_plan_t plan, double alpha, const double *B, int64_t ldb,
+                                                   double beta, double *C, int64_t ldc, jlust_stream_t stream)
+{
+    using namespace jlust;
+    clear_error();
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_execute: null plan");
+    if (plan->value_type != 0)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE, "bsr_spmm_plan_execute: plan was created for Float32 values");
+    return jlust_hip_csr_spmm_plan_execute_f64(plan->csr, alpha, B, ldb, beta, C, ldc, 0, stream);
+}
+
+extern "C" int jlust_hip_bsr_spmm_plan_info(jlust_bsr_plan_t plan, int32_t *path)
+{
+    jlust::clear_error();
+    if (!plan) return jlust::fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_info: null plan");
+    if (path) *path = plan->mfma ? 0 : 1;
+    return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_bsr_spmm_plan_destroy(jlust_bsr_plan_t plan)
+{
+    jlust::clear_error();
+    if (!plan) return JLUST_STATUS_SUCCESS;
+    // Work queued on any stream may still read the plan's buffers.
+    hipError_t e = hipDeviceSynchronize();
+    int st = plan->csr ? jlust_hip_csr_spmm_plan_destroy(plan->csr) : JLUST_STATUS_SUCCESS;
+    if (plan->mem) {
+        const hipError_t e2 = hipFree(plan->mem);
+        if (e == hipSuccess) e = e2;
+    }
+    delete plan;
+    if (e != hipSuccess) return jlust::hip_fail(e, "bsr_spmm_plan_destroy");
+    return st;
 }

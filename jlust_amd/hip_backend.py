@@ -813,6 +813,123 @@ class HIPSpMMHandle(AbstractKernelHandle):
         self._destroy()
 
 
+class HIPBSRSpMMHandle(AbstractKernelHandle):
+    """Prepared BSR SpMM (jlust_hip_bsr_spmm_plan_*): prepare(HIPBackend(),
+    SpMMOp, A::BSR; n_cols=k) -> execute(h, B, C) -> update_values!(h, A), the
+    cuSPARSE SpMM handle contract (ext/CUDAExt/ops/spmm.jl:8-70) for BSR.
+    16 x 16 Float32 blocks run the MFMA kernels on A's buffers; any other
+    block shape, or Float64, is expanded to CSR once and runs through a CSR
+    SpMM plan over the expansion.  A's values are read as they are at the
+    call: on the expansion path, values written in place through torch since
+    the plan last read them (the value tensor's version counter moved) are
+    expanded again, in stream order, before the product.  B with another
+    number of columns than the plan's rebuilds the plan."""
+
+    def __init__(self, u_A: USTensor, n_cols=None):
+        if not is_bsr(u_A.format):
+            raise UnsupportedFormat(u_A.format, _BE, "prepared BSR SpMM plans take BSR")
+        self.suf = _value_suffix(u_A)
+        self.T = nonzeros(u_A).dtype
+        b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
+        _check_values(u_A, self.T)
+        self.dev = _check_same_device(browptr, bcolind, nonzeros(u_A))
+        self.u_A = u_A
+        self._plan = ctypes.c_void_p(0)
+        self.k = None
+        self._vals = nonzeros(u_A)
+        self._ver = self._vals._version
+        if n_cols is not None:
+            self._make(int(n_cols))
+
+    def _make(self, k: int):
+        self._destroy()
+        b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(self.u_A)
+        plan = ctypes.c_void_p(0)
+        with _on(self.dev):
+            st = _lib.lib().jlust_hip_bsr_spmm_plan_create(
+                mb, nb, b1, b2, bcolind.numel(), self.u_A.origin.offset, 0 if self.suf == "f64" else 1,
+                int(row_major), _ptr(browptr), _ptr(bcolind), _ptr(self._vals), k, _stream(self.dev),
+                ctypes.byref(plan))
+        _lib.check(st, "bsr_spmm_plan_create", self.u_A.format, _BE, self.T)
+        self._plan, self.k = plan, k
+        self._ver = self._vals._version
+
+    def execute(self, *ts, alpha=1.0, beta=0.0):
+        """execute(h, B, C) or execute(h, A, B, C); returns C (a USTensor)."""
+        ts = tuple(t if isinstance(t, USTensor) else ust(t) for t in ts)
+        if len(ts) == 3:
+            u_A, u_B, u_C = ts
+            if nonzeros(u_A) is not self._vals:
+                self.update_values(u_A)
+        elif len(ts) == 2:
+            u_B, u_C = ts
+        else:
+            raise TypeError("execute(handle, [A,] B, C)")
+        B, C = nonzeros(u_B), nonzeros(u_C)
+        m, n = self.u_A.extents
+        if B.dtype != self.T or C.dtype != self.T:
+            raise UnsupportedValueType(B.dtype if B.dtype != self.T else C.dtype, _BE)
+        if B.dim() != 2 or C.dim() != 2 or B.shape[0] != n or C.shape[0] != m or \
+                B.shape[1] != C.shape[1]:
+            raise IncompatibleExtents(
+                f"SpMM: A is {m}x{n}, B is {tuple(B.shape)}, C is {tuple(C.shape)}")
+        for t, nm in ((B, "B"), (C, "C")):
+            if t.shape[0] > 1 and t.shape[1] > 0 and t.stride(0) != 1:
+                raise NonCanonicalStorage(f"SpMM: {nm} must be column-major (stride(0) == 1)")
+        _check_same_device(self._vals, B, C)
+        k = B.shape[1]
+        if self.k != k:
+            self._make(k)
+        elif self._vals._version != self._ver:
+            self._refresh()
+        with _on(self.dev):
+            st = getattr(_lib.lib(), f"jlust_hip_bsr_spmm_plan_execute_{self.suf}")(
+                self._plan, float(alpha), _ptr(B), leading_dim(B), float(beta), _ptr(C),
+                leading_dim(C), _stream(self.dev))
+        _lib.check(st, "bsr_spmm_plan_execute", self.u_A.format, _BE, self.T)
+        return u_C
+
+    def _refresh(self):
+        """Point the plan at self._vals and re-read them (stream-ordered)."""
+        if self._plan.value:
+            with _on(self.dev):
+                st = _lib.lib().jlust_hip_bsr_spmm_plan_update_values(self._plan, _ptr(self._vals),
+                                                                      _stream(self.dev))
+            _lib.check(st, "bsr_spmm_plan_update_values", self.u_A.format, _BE, self.T)
+        self._ver = self._vals._version
+
+    def update_values(self, u_A: USTensor):
+        if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A) or u_A.format != self.u_A.format:
+            raise IncompatibleExtents("update_values!: the sparsity structure must not change")
+        _check_values(u_A, self.T)
+        _check_same_device(nonzeros(u_A), self._vals)
+        self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
+                            self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+        self._vals = nonzeros(u_A)
+        self._refresh()
+        return self
+
+    def info(self) -> dict:
+        """The path the plan chose: "mfma" or "csr_expansion"."""
+        if not self._plan.value:
+            return {}
+        path = ctypes.c_int32()
+        st = _lib.lib().jlust_hip_bsr_spmm_plan_info(self._plan, ctypes.byref(path))
+        _lib.check(st, "bsr_spmm_plan_info", self.u_A.format, _BE, self.T)
+        return {"path": "mfma" if path.value == 0 else "csr_expansion"}
+
+    def _destroy(self):
+        plan, self._plan = getattr(self, "_plan", None), ctypes.c_void_p(0)
+        if plan is not None and plan.value:
+            try:
+                _lib.lib().jlust_hip_bsr_spmm_plan_destroy(plan)
+            except Exception:
+                pass
+
+    def __del__(self):
+        self._destroy()
+
+
 class HIPSDDMMHandle(AbstractKernelHandle):
     """Prepared SDDMM (jlust_hip_sddmm_plan_*): prepare(HIPBackend(), SDDMMOp,
     A, B, C) -> execute(h, A, B, C) -> update_values!(h, C), the cuSPARSE
@@ -922,6 +1039,8 @@ def prepare(optype, u_A: USTensor, *more, **kw):
             raise TypeError(f"prepare(SpMMOp): unexpected keywords {sorted(bad)} or tensors ({len(more)})")
         if is_csr_shaped(u_A.format):
             return HIPSpMMHandle(u_A, kw.get("n_cols"), kw.get("skip_empty_rows", False))
+        if is_bsr(u_A.format) and not kw.get("skip_empty_rows"):
+            return HIPBSRSpMMHandle(u_A, kw.get("n_cols"))
         kw.pop("n_cols", None)
         return HIPOpHandle(SpMMOp, u_A, **kw)
     if tag == "SDDMM":

@@ -285,3 +285,72 @@ def test_csc_spmv_input_fn_and_output_fn(J, O):
     assert_within(host(y), ref, absref, np.float64, "csc input_fn")
     with pytest.raises(J.UnsupportedFormat, match="output_fn"):
         J.execute(J.SpMVOp, A, dev(x), y, output_fn=J.abs_fn)
+
+
+# ------------------------------------------------------------- BSR plans
+
+def _rect_bsr(mb, nb, b1, b2, per_row, seed, dtype, row_major, origin=1):
+    """Random BSR of b1 x b2 blocks with small-integer values (exact sums),
+    some stored zeros; flat values in the block order asked for."""
+    rng = np.random.default_rng(seed)
+    counts = rng.integers(0, per_row + 1, mb)
+    bcols = [np.sort(rng.choice(nb, min(c, nb), replace=False)) for c in counts]
+    browptr = (np.r_[0, np.cumsum([c.size for c in bcols])] + origin).astype(np.int32)
+    bcolind = (np.concatenate(bcols) + origin).astype(np.int32)
+    blocks = rng.integers(-4, 5, (bcolind.size, b1, b2)).astype(dtype)
+    blocks[blocks == 4] = 0
+    flat = blocks.reshape(-1) if row_major else blocks.transpose(0, 2, 1).reshape(-1)
+    return browptr, bcolind, np.ascontiguousarray(flat)
+
+
+@pytest.mark.parametrize("b1,b2,dtype,row_major,path", [
+    (16, 16, np.float32, True, "mfma"),
+    (16, 16, np.float32, False, "mfma"),
+    (4, 8, np.float64, True, "csr_expansion"),
+    (3, 5, np.float32, False, "csr_expansion"),
+    (16, 16, np.float64, True, "csr_expansion"),
+])
+def test_bsr_spmm_plan(J, O, b1, b2, dtype, row_major, path):
+    """prepare(SpMMOp, A::BSR; n_cols=k): the chosen path, the product
+    against the oracle (exact on integer data), bit-identity with the plain
+    call, values written in place seen by the next execute, update_values_
+    with another tensor, and a k change rebuilding the plan."""
+    import torch
+    mb, nb, k = 45, 38, 20
+    bp, bc, flat = _rect_bsr(mb, nb, b1, b2, 6, 300 + b1 + 10 * b2, dtype, row_major)
+    vals = dev(flat)
+    A = J.bsr_tensor(dev(bp), dev(bc), vals, (mb * b1, nb * b2), (b1, b2), row_major)
+    tdt = torch.float64 if dtype == np.float64 else torch.float32
+    rng = np.random.default_rng(9)
+    B = np.asfortranarray(rng.integers(-3, 4, (nb * b2, k)).astype(dtype))
+    C0 = np.asfortranarray(rng.integers(-3, 4, (mb * b1, k)).astype(dtype))
+
+    def ref(v, Bm, a, b):
+        return O.bsr_spmm(bp, bc, v, b1, Bm, a, b, C0[:, :Bm.shape[1]].copy(order="F"),
+                          row_major_blocks=row_major, b2=b2)
+
+    h = J.prepare(J.HIPBackend(), J.SpMMOp, A, n_cols=k)
+    assert h.info()["path"] == path
+    C = J.dense_matrix(mb * b1, k, dtype=tdt)
+    C.copy_(dev(C0))
+    J.execute(J.SpMMOp, h, dev(B), C, alpha=1.5, beta=-1.0)
+    np.testing.assert_array_equal(host(C), ref(flat, B, 1.5, -1.0))
+    C2 = J.dense_matrix(mb * b1, k, dtype=tdt)
+    C2.copy_(dev(C0))
+    J.execute(J.SpMMOp, A, dev(B), C2, alpha=1.5, beta=-1.0)
+    assert np.array_equal(host(C2), host(C))
+    # values written in place
+    vals.mul_(-2)
+    J.execute(J.SpMMOp, h, dev(B), C, alpha=1.0, beta=0.0)
+    np.testing.assert_array_equal(host(C), ref(-2 * flat, B, 1.0, 0.0))
+    # another value tensor through update_values_, then execute(h, A, B, C)
+    flat3 = np.ascontiguousarray(flat + 1).astype(dtype)
+    A3 = J.bsr_tensor(dev(bp), dev(bc), dev(flat3), (mb * b1, nb * b2), (b1, b2), row_major)
+    J.update_values_(h, A3)
+    J.execute(J.SpMMOp, h, dev(B), C, alpha=1.0, beta=0.0)
+    np.testing.assert_array_equal(host(C), ref(flat3, B, 1.0, 0.0))
+    # a different k rebuilds the plan
+    B5 = np.asfortranarray(B[:, :5])
+    C5 = J.dense_matrix(mb * b1, 5, dtype=tdt)
+    J.execute(J.SpMMOp, h, A, dev(B5), C5, alpha=1.0, beta=0.0)
+    np.testing.assert_array_equal(host(C5), ref(-2 * flat, B5, 1.0, 0.0))
