@@ -136,3 +136,64 @@ def test_plan_capture_launch(J, kind, monkeypatch):
         h.capture(x[:-1], y)
     del g
     torch.cuda.synchronize()
+
+
+def test_graph_spmm_plan_with_split_rows(J):
+    """The prepared CSR SpMM plan (rows longer than 1024 entries split into
+    segments, their partial rows reduced by a third kernel) captured and
+    replayed: the plan's execute allocates nothing and synchronises nothing."""
+    import torch
+    m, n, k = 3000, 6000, 24
+    lens = np.random.default_rng(11).integers(0, 30, m)
+    lens[[5, 777, 2999]] = [5000, 2500, 1100]
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=12)
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    h = J.prepare(J.HIPBackend(), J.SpMMOp, A, n_cols=k)
+    assert h.info()["split_rows"] == 3
+    B = J.dense_matrix(n, k, dtype=torch.float64)
+    C = J.dense_matrix(m, k, dtype=torch.float64)
+    C0 = torch.randn(k, m, dtype=torch.float64, device="cuda").t()
+    check_replays(lambda: J.execute(J.SpMMOp, h, B, C, alpha=1.25, beta=-0.5), B, C, C0)
+
+
+@pytest.mark.parametrize("mask", ["csr", "coo_unsorted"])
+def test_graph_sddmm_plan(J, mask):
+    import torch
+    m, n, K = 2000, 1500, 40
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(13).integers(0, 25, m),
+                                     seed=14, dtype=np.float32)
+    out = dev(val.copy())
+    if mask == "csr":
+        Cs = J.csr_tensor(dev(rowptr), dev(colind), out, (m, n))
+    else:
+        rows = np.repeat(np.arange(m, dtype=np.int32), np.diff(rowptr)) + 1
+        perm = np.random.default_rng(15).permutation(rows.size)
+        out = dev(val[perm].copy())
+        Cs = J.coo_tensor(dev(rows[perm]), dev(colind[perm]), out, (m, n))
+    h = J.prepare(J.HIPBackend(), J.SDDMMOp, Cs, n_inner=K)
+    A = torch.zeros(K, m, dtype=torch.float32, device="cuda").t()
+    Bm = torch.randn(n, K, dtype=torch.float32, device="cuda").t()
+    c0 = out.clone()
+    check_replays(lambda: J.execute(J.SDDMMOp, h, A, Bm, Cs, alpha=0.5, beta=2.0), A, out, c0)
+
+
+@pytest.mark.parametrize("b1,b2,dtype", [(16, 16, np.float32), (4, 8, np.float64)])
+def test_graph_bsr_plan(J, b1, b2, dtype):
+    """The prepared BSR SpMM plan on both of its paths (MFMA kernels; CSR
+    expansion + CSR SpMM plan) captured and replayed."""
+    import torch
+    mb, nb, k = 60, 50, 32
+    rng = np.random.default_rng(16)
+    counts = rng.integers(0, 6, mb)
+    bcols = [np.sort(rng.choice(nb, c, replace=False)) for c in counts]
+    bp = (np.r_[0, np.cumsum(counts)] + 1).astype(np.int32)
+    bc = (np.concatenate(bcols) + 1).astype(np.int32)
+    vals = rng.standard_normal(bc.size * b1 * b2).astype(dtype)
+    A = J.bsr_tensor(dev(bp), dev(bc), dev(vals), (mb * b1, nb * b2), (b1, b2))
+    h = J.prepare(J.HIPBackend(), J.SpMMOp, A, n_cols=k)
+    assert h.info()["path"] == ("mfma" if b1 == 16 and dtype == np.float32 else "csr_expansion")
+    tdt = torch.float64 if dtype == np.float64 else torch.float32
+    B = J.dense_matrix(nb * b2, k, dtype=tdt)
+    C = J.dense_matrix(mb * b1, k, dtype=tdt)
+    C0 = torch.randn(k, mb * b1, dtype=tdt, device="cuda").t()
+    check_replays(lambda: J.execute(J.SpMMOp, h, B, C, alpha=0.75, beta=1.5), B, C, C0)
