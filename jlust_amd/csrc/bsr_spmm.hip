@@ -230,35 +230,60 @@ __global__ __launch_bounds__(256) void bsr16_spmm_rowwave_kernel(
     }
 }
 
-// Strip kernel (row-major blocks, B and C float4-aligned).  A workgroup owns
-// BSR_SR consecutive block-rows, one wave each, with the row's blocks (up to
-// BSR_QCHUNK) held as MFMA A operands in registers for all of k.  For each
-// 16-column tile the strip's window of B -- block-rows [J_min, J_max] of all
-// its blocks, each of the 16 columns one contiguous run of (J_max - J_min +
-// 1) * 64 bytes -- is copied into LDS with direct global-to-LDS loads
-// (global_load_lds_dwordx4: 64 lanes x 16 bytes of one column per
-// instruction, whole 128-byte lines, no registers), then every wave runs its
-// row's MFMAs from it.  A block used by several rows of the strip is fetched
-// from L2 once instead of once per row, in whole lines instead of 64-byte
-// column pieces: at the banded config the L1-to-L2 read requests fall from
-// 124.7M to 54.8M per call and the address unit's busy time from 86 % to
-// about a third.  The window buffer is single (78 KB), so two workgroups
-// share a CU and each computes while the other waits for its copies (a
-// double-buffered 156 KB window leaves one workgroup per CU with its copy
-// latency exposed: 1.32 ms against 1.15 ms).  Columns sit BSR_CS bytes apart
-// (a 16-byte pad per column), so the 16 lanes of an operand read (16
-// columns, one row group) hit distinct banks.  A strip whose rows hold more
-// than BSR_QCHUNK blocks or whose window exceeds BSR_WMAX block-rows computes
-// its rows with direct operand loads instead (same arithmetic).
+// Strip kernel (row-major blocks, B and C float4-aligned, byte offsets of B
+// and C below 2^31).  A workgroup owns BSR_SR consecutive block-rows, one
+// wave each, with the row's blocks (up to BSR_QCHUNK) held as MFMA A operands
+// in registers for all of k.  For each 16-column tile the strip's window of B
+// -- block-rows [J_min, J_max] of all its blocks, each of the 16 columns one
+// contiguous run of (J_max - J_min + 1) * 64 bytes -- sits in LDS, copied
+// there with direct global-to-LDS loads (buffer_load_dwordx4 ... lds: 64
+// lanes x 16 bytes of one column per instruction, whole 128-byte lines, no
+// registers).  Per tile every wave reads all of its row's B operands from the
+// window into registers; after a barrier the window is free, so the next
+// tile's copies are issued at once and land while the waves run this tile's
+// MFMAs from registers and store C.  One wait + barrier per tile finds the
+// copies done (vmcnt(1): all but the C store just issued; an explicit
+// s_barrier, since a fence would wait for everything).  The window buffer is
+// single (78 KB) and the kernel fits 80 VGPRs (buffer resources keep the
+// addresses of B and C in SGPRs), so two workgroups share a CU and each has
+// a window in flight: one workgroup's copies alone are latency-bound at about
+// half the rate of two.  Columns sit BSR_CS bytes apart (a 16-byte pad per
+// column), so the 16 lanes of an operand read (16 columns, one row group)
+// spread over the banks.  A strip whose rows hold more than BSR_QCHUNK blocks
+// or whose window exceeds BSR_WMAX block-rows computes its rows with direct
+// operand loads instead (same arithmetic).
 constexpr int BSR_SR = 12;                        // block-rows (waves) per workgroup
 constexpr int BSR_WMAX = BSR_SR + 64;             // window block-rows (a +-32 band)
 constexpr int BSR_CS = BSR_WMAX * 64 + 16;        // LDS bytes per column of a window
 constexpr int BSR_BUF = 16 * BSR_CS;              // the window buffer
 
 typedef __attribute__((address_space(3))) void lds_void;
+typedef int int32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer intrinsics (MUBUF with a 128-bit resource in SGPRs).
+__device__ void raw_buffer_load_lds(int32x4 rsrc, lds_void *lds, int size, int voffset, int soffset, int offset,
+                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ void raw_buffer_store_v4f32(floatx4 data, int32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.store.v4f32");
+__device__ floatx4 raw_buffer_load_v4f32(int32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+
+// A buffer resource over [p, p + 4 GB): base address, stride 0, no range
+// limit, the gfx9 default format word.
+__device__ __forceinline__ int32x4 buffer_resource(const void *p)
+{
+    const uint64_t a = (uint64_t)p;
+    int32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffff));
+    r.z = -1;
+    r.w = 0x00020000;
+    return r;
+}
 
 template <bool BZ>
-__global__ __launch_bounds__(64 * BSR_SR) void bsr16_spmm_strip_kernel(
+__global__ __launch_bounds__(64 * BSR_SR) __attribute__((amdgpu_waves_per_eu(6))) 
+void bsr16_spmm_strip_kernel(
     int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
     const int32_t *__restrict__ bcolind, const float *__restrict__ val, int64_t k, float alpha,
     const float *__restrict__ B, int64_t ldb, float beta, float *__restrict__ C, int64_t ldc)
@@ -270,14 +295,16 @@ __global__ __launch_bounds__(64 * BSR_SR) void bsr16_spmm_strip_kernel(
     const int64_t strip = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
     const int64_t R0 = strip * BSR_SR;
     if (R0 >= mb) return;                  // whole workgroup
-    const int wave = threadIdx.x >> 6;
+    // Wave-uniform values go to SGPRs (readfirstlane), which keeps the kernel
+    // within the 80 VGPRs two workgroups per CU need.
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int i = lane & 15;               // MFMA: A row / B, C column in the tile
     const int g = lane >> 4;               // MFMA: contraction group / C row group
     const int64_t R = R0 + wave;
     const bool live = R < mb;
-    const int64_t q0 = live ? (int64_t)browptr[R] - origin : 0;
-    const int64_t q1 = live ? (int64_t)browptr[R + 1] - origin : 0;
+    const int64_t q0 = live ? (int64_t)__builtin_amdgcn_readfirstlane(browptr[R]) - origin : 0;
+    const int64_t q1 = live ? (int64_t)__builtin_amdgcn_readfirstlane(browptr[R + 1]) - origin : 0;
     const int nq = (int)(q1 - q0);
     const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
 
@@ -308,15 +335,26 @@ __global__ __launch_bounds__(64 * BSR_SR) void bsr16_spmm_strip_kernel(
         jw1 = max(jw1, s_jmax[w]);
         lmax = max(lmax, s_len[w]);
     }
+    jw0 = __builtin_amdgcn_readfirstlane(jw0);
+    jw1 = __builtin_amdgcn_readfirstlane(jw1);
+    lmax = __builtin_amdgcn_readfirstlane(lmax);
     const int32_t nwin = jw1 >= jw0 ? jw1 - jw0 + 1 : 0;
     const int64_t crow = R * BSR_BS + 4 * g;
 
+    auto store_tile = [&](floatx4 acc, int64_t c0) {
+        const int64_t col = c0 + i;
+        if (col < k) {
+            floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + col * ldc);
+            floatx4 out = alpha * acc;
+            if (!BZ) out += beta * *dst;
+            *dst = out;
+        }
+    };
     if (lmax > BSR_QCHUNK || nwin > BSR_WMAX) {
         // Direct operand loads (any row length, any window).
         if (!live) return;
         for (int64_t c0 = 0; c0 < k; c0 += 16) {
-            const int64_t col = c0 + i;
-            const int64_t colc = col < k ? col : k - 1;
+            const int64_t colc = c0 + i < k ? c0 + i : k - 1;
             floatx4 acc = zero;
             for (int64_t q = q0; q < q1; ++q) {
                 const floatx4 a = *reinterpret_cast<const floatx4 *>(val + q * 256 + i * 16 + 4 * g);
@@ -325,23 +363,18 @@ __global__ __launch_bounds__(64 * BSR_SR) void bsr16_spmm_strip_kernel(
 #pragma unroll
                 for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
             }
-            if (col < k) {
-                floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + col * ldc);
-                floatx4 out = alpha * acc;
-                if (!BZ) out += beta * *dst;
-                *dst = out;
-            }
+            store_tile(acc, c0);
         }
         return;
     }
 
-    // A operands and window-relative block rows of this wave's row.
+    // A operands and window-relative block rows (wave-uniform) of this row.
     floatx4 a[BSR_QCHUNK];
     int32_t jrel[BSR_QCHUNK];
 #pragma unroll
     for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
         a[qq] = qq < nq ? *reinterpret_cast<const floatx4 *>(val + (q0 + qq) * 256 + i * 16 + 4 * g) : zero;
-        jrel[qq] = qq < nq ? bcolind[q0 + qq] - origin - jw0 : 0;
+        jrel[qq] = qq < nq ? __builtin_amdgcn_readfirstlane(bcolind[q0 + qq] - origin - jw0) : 0;
     }
     // Window copy of one tile: instruction ii = (column j, part p) moves the
     // column's floats [256 p, 256 p + 256) of the window; lanes past the
@@ -350,39 +383,60 @@ __global__ __launch_bounds__(64 * BSR_SR) void bsr16_spmm_strip_kernel(
     const int ninst = 16 * npc;
     const int64_t wfloats = (int64_t)nwin * 16;
     const float *bwin = B + (int64_t)jw0 * BSR_BS;
-    const char *col_i = win + i * BSR_CS + 16 * g;
-    for (int64_t c0 = 0; c0 < k; c0 += 16) {
+    const uint32_t col_off = (uint32_t)(i * BSR_CS + 16 * g);
+    const int lane16 = lane * 16;
+    const int32x4 rs_b = buffer_resource(bwin);  // B's window: lane offset in a VGPR, the rest in an SGPR
+    auto copy_tile = [&](int64_t c0) {
         for (int ii = wave; ii < ninst; ii += BSR_SR) {
             const int j = ii / npc, p = ii % npc;
-            const int64_t f = (int64_t)p * 256 + 4 * lane;
-            if (f < wfloats && c0 + j < k) {
-                __builtin_amdgcn_global_load_lds((const void *)(bwin + f + (c0 + j) * ldb),
-                                                 (lds_void *)(win + j * BSR_CS + p * 1024), 16, 0, 0);
-            }
+            if (c0 + j >= k) continue;
+            const int fu = p * 256;                        // floats, wave-uniform
+            const int so = (int)((fu + (c0 + j) * ldb) * 4); // bytes, wave-uniform
+            if (fu + 4 * lane < wfloats)
+                raw_buffer_load_lds(rs_b, (lds_void *)(win + j * BSR_CS + p * 1024), 16, lane16, so, 0, 0);
         }
-        __builtin_amdgcn_s_waitcnt(0);     // this wave's copies are in LDS
-        __syncthreads();                   // ... and every wave's
+    };
+    const int32x4 rs_c = buffer_resource(C);
+    const int c_lane = (4 * g + i * (int)ldc) * 4;
+    copy_tile(0);
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("s_barrier" ::: "memory");
+    for (int64_t c0 = 0; c0 < k; c0 += 16) {
+        // This tile's B operands into registers; then the window is free.
+        floatx4 b[BSR_QCHUNK];
+        uint32_t co = col_off;
+        asm volatile("" : "+v"(co));           // the read addresses are formed per tile, not kept
+#pragma unroll
+        for (int qq = 0; qq < BSR_QCHUNK; ++qq) b[qq] = *reinterpret_cast<const floatx4 *>(win + co + jrel[qq] * 64);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (c0 + 16 < k) copy_tile(c0 + 16);
+        asm volatile("" ::: "memory");        // the copies are issued before the MFMAs and the store
+        floatx4 acc = zero;
         if (live) {
-            floatx4 acc = zero;
 #pragma unroll
             for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
                 if (qq < nq) {
-                    const floatx4 b = *reinterpret_cast<const floatx4 *>(col_i + jrel[qq] * 64);
 #pragma unroll
                     for (int u = 0; u < 4; ++u)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[qq][u], b[u], acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[qq][u], b[qq][u], acc, 0, 0, 0);
                 }
             }
-            const int64_t col = c0 + i;
-            if (col < k) {
-                floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + col * ldc);
-                floatx4 out = alpha * acc;
-                if (!BZ) out += beta * *dst;
-                *dst = out;
-            }
         }
-        __syncthreads();                   // every wave is done reading before the next copies
+        if (live) {
+            // C's lane part (4 g + i ldc) * 4 bytes in a VGPR, the rest in an SGPR.
+            if (c0 + i < k) {
+                const int so_c = (int)((R * BSR_BS + c0 * ldc) * 4);
+                floatx4 out = alpha * acc;
+                if (!BZ) out += beta * raw_buffer_load_v4f32(rs_c, c_lane, so_c, 0);
+                raw_buffer_store_v4f32(out, rs_c, c_lane, so_c, 0);
+            }
+            __builtin_amdgcn_s_waitcnt(0x0001);   // vmcnt(1): every copy; the C store may be in flight
+        } else {
+            __builtin_amdgcn_s_waitcnt(0);
+        }
+        asm volatile("s_barrier" ::: "memory");
     }
+    __builtin_amdgcn_s_waitcnt(0);
 }
 
 // JLUST_HIP_BSR_STRIP=0 keeps the row-wave kernel.
@@ -539,7 +593,10 @@ int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
     const bool rm = row_major_blocks && vals_aligned;
     if (row_major_blocks && !vals_aligned)
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: block values must be 16-byte aligned");
-    if (rm && vec && bsr_strip()) {
+    // The strip kernel addresses B and C through 32-bit buffer offsets.
+    const bool offsets_fit = ((uint64_t)(nrows + k * ldb) + 2048) * 4 < ((uint64_t)1 << 31) &&
+                             ((uint64_t)(mrows + (k + 16) * ldc)) * 4 < ((uint64_t)1 << 31);
+    if (rm && vec && offsets_fit && bsr_strip()) {
         const int64_t strips = (mb + BSR_SR - 1) / BSR_SR;
         const int64_t grids = (strips + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
         if (beta == 0.f)
