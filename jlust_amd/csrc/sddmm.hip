@@ -13,11 +13,13 @@
 // lanes, one nonzero per group at a time: each lane multiplies a 16-byte
 // slice of B[:, j] (one vector load; the group reads the column as contiguous
 // 128-byte lines) with the matching slice of the staged A row, and the group
-// reduces its G partial dots with xor-shuffles.  G = 8 for K above 8 slices;
-// for smaller K, G is the smallest power of two whose slices cover K, and
-// each group takes U nonzeros per step with their loads issued together
-// (indices clamped into the block's nonzeros, results of the clamped copies
-// dropped), so K = 1 puts 64 nonzeros on a wave per load instead of 8.
+// reduces its G partial dots with xor-shuffles.  G = 8 for K above 8 slices
+// (K of 16, 32 or 64 slices: the lane's 2, 4 or 8 loads of B are issued
+// together, the rest loop); for smaller K, G is the smallest power of two
+// whose slices cover K, and each group takes U nonzeros per step with their
+// loads issued together (indices clamped into the block's nonzeros, results
+// of the clamped copies dropped), so K = 1 puts 64 nonzeros on a wave per
+// load instead of 8.
 #include <memory>
 #include <vector>
 
@@ -45,10 +47,11 @@ __device__ __forceinline__ T group_sum(T v)
     return v;
 }
 
-// VECB: B columns and the LDS rows allow 16-byte vector access.  ONE: a
-// group's G slices cover all of K (one step per nonzero), so U nonzeros per
-// group can be loaded at once; otherwise U = 1 and the lanes loop over K.
-template <typename T, bool VECB, int G, int U, bool ONE>
+// VECB: B columns and the LDS rows allow 16-byte vector access.  KS >= 1: a
+// group covers K in exactly KS steps of its G slices (KS = 1: at most one
+// step, lanes past K idle), so all KS loads of U nonzeros are issued before
+// any arithmetic; KS = 0: U = 1 and the lanes loop over K.
+template <typename T, bool VECB, int G, int U, int KS>
 __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     int64_t m, int64_t K, int32_t origin, const int32_t *__restrict__ rowptr,
     const int32_t *__restrict__ colind, T alpha, const T *__restrict__ A, int64_t lda,
@@ -56,7 +59,8 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     const T *mask, int R, int64_t lds_ld, const int32_t *__restrict__ items, int64_t chunk,
     const int32_t *__restrict__ perm)
 {
-    static_assert(ONE || U == 1, "several nonzeros per group need one step over K");
+    static_assert(KS >= 1 || U == 1, "several nonzeros per group need a fixed step count over K");
+    static_assert(KS <= 1 || VECB, "several steps over K need vector loads");
     constexpr int GROUPS = SD_BLOCK / G;
     constexpr int NE = VECB ? V16<T>::N : 1;   // elements per lane load
     extern __shared__ unsigned char sd_smem[];
@@ -112,17 +116,26 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
             arow[u] = s_a + lo * lds_ld;
         }
         T dot[U];
-        if (ONE) {
+        if (KS >= 1) {
             if (VECB) {
-                V16<T> bv[U];
+                // Step s of lane q covers K elements (s*G + q)*NE ..+NE, the order of
+                // the looping form below, so both give the same sums.
+                constexpr int KS1 = KS >= 1 ? KS : 1;
+                V16<T> bv[U][KS1];
 #pragma unroll
-                for (int u = 0; u < U; ++u) bv[u] = *reinterpret_cast<const V16<T> *>(B + j[u] * ldb + k1c);
+                for (int u = 0; u < U; ++u)
+#pragma unroll
+                    for (int st = 0; st < KS1; ++st)
+                        bv[u][st] = *reinterpret_cast<const V16<T> *>(B + j[u] * ldb + k1c + st * G * NE);
 #pragma unroll
                 for (int u = 0; u < U; ++u) {
-                    const V16<T> av = *reinterpret_cast<const V16<T> *>(arow[u] + k1c);
                     T d = T(0);
 #pragma unroll
-                    for (int e = 0; e < NE; ++e) d += av.v[e] * bv[u].v[e];
+                    for (int st = 0; st < KS1; ++st) {
+                        const V16<T> av = *reinterpret_cast<const V16<T> *>(arow[u] + k1c + st * G * NE);
+#pragma unroll
+                        for (int e = 0; e < NE; ++e) d += av.v[e] * bv[u][st].v[e];
+                    }
                     dot[u] = k1_ok ? d : T(0);
                 }
             } else {
@@ -248,20 +261,25 @@ int sddmm_launch(int64_t m, int64_t K, int32_t origin, const int32_t *rowptr, co
     const dim3 grid((unsigned)(items ? nitems : (m + R - 1) / R));
     // Lane loads that cover K: G = the smallest power of two >= that, up to 8.
     const int64_t slices = vecb ? K / N : K;
-#define JLUST_SD(V, G, U, ONE)                                                                        \
-    hipLaunchKernelGGL((csr_sddmm_kernel<T, V, G, U, ONE>), grid, dim3(SD_BLOCK), smem, s, m, K, origin, \
+#define JLUST_SD(V, G, U, KS)                                                                         \
+    hipLaunchKernelGGL((csr_sddmm_kernel<T, V, G, U, KS>), grid, dim3(SD_BLOCK), smem, s, m, K, origin, \
                        rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, R, lds_ld, items,  \
                        chunk, perm)
 #define JLUST_SD_V(V)                                                                                 \
     do {                                                                                              \
-        if (slices == 0) JLUST_SD(V, 8, 1, false);     /* K = 0: no loads of B at all */             \
-        else if (slices <= 1) JLUST_SD(V, 1, 4, true);                                                \
-        else if (slices <= 2) JLUST_SD(V, 2, 4, true);                                                \
-        else if (slices <= 4) JLUST_SD(V, 4, 2, true);                                                \
-        else if (slices <= 8) JLUST_SD(V, 8, 1, true);                                                \
-        else JLUST_SD(V, 8, 1, false);                                                                \
+        if (slices == 0) JLUST_SD(V, 8, 1, 0);     /* K = 0: no loads of B at all */                 \
+        else if (slices <= 1) JLUST_SD(V, 1, 4, 1);                                                   \
+        else if (slices <= 2) JLUST_SD(V, 2, 4, 1);                                                   \
+        else if (slices <= 4) JLUST_SD(V, 4, 2, 1);                                                   \
+        else if (slices <= 8) JLUST_SD(V, 8, 1, 1);                                                   \
+        else JLUST_SD(V, 8, 1, 0);                                                                    \
     } while (0)
-    if (vecb) JLUST_SD_V(true);
+    // K a multiple of 2, 4 or 8 whole steps of 8 lanes: every load of the column
+    // issued at once (one nonzero per group; two per group measured slower).
+    if (vecb && slices == 16) JLUST_SD(true, 8, 1, 2);
+    else if (vecb && slices == 32) JLUST_SD(true, 8, 1, 4);
+    else if (vecb && slices == 64) JLUST_SD(true, 8, 1, 8);
+    else if (vecb) JLUST_SD_V(true);
     else JLUST_SD_V(false);
 #undef JLUST_SD_V
 #undef JLUST_SD

@@ -139,7 +139,7 @@ def test_sddmm_reference_fixture(J, dtype):
     np.testing.assert_array_equal(out, np.array(c["cval"], dtype))
 
 
-@pytest.mark.parametrize("K", [1, 2, 3, 4, 8, 12, 16, 32, 64, 128, 130, 512])
+@pytest.mark.parametrize("K", [1, 2, 3, 4, 8, 12, 16, 32, 64, 128, 130, 256, 512])
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 def test_sddmm_random(J, O, K, dtype):
     m, n = 2000, 1500
