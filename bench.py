@@ -76,6 +76,9 @@ def parse():
                         "matrix, sorted and shuffled, beside the oracle's COO SpMV on this host")
     p.add_argument("--gather-floor", action="store_true",
                    help="only time the random-row gathers of configs 3 and 4 alone (their floor)")
+    p.add_argument("--gather-overlap", action="store_true",
+                   help="only time config 3's chunk gathers alone, a 256 MB transpose alone, and the "
+                        "two on two streams at once")
     p.add_argument("--mall-probe", action="store_true",
                    help="only measure whether a just-written buffer reads back faster than a cold one")
     p.add_argument("--cold", action="store_true",
@@ -449,6 +452,70 @@ def gather_floor():
             del out
         del src, idx
         torch.cuda.empty_cache()
+    return res
+
+
+def gather_overlap():
+    """Would config 3's second column chunk cost less if its transpose ran
+    while the first chunk's gathers do?  Times the chunk's gathers
+    (rows_probe_kernel, 64 rows per wave, as in gather_floor) alone, the
+    transpose of a 64-column chunk of a column-major 1M x 128 B into a
+    row-major 1M x 64 copy (torch's strided copy) alone, the two back to back,
+    and the two at once on two streams of default priority joined by events."""
+    import ctypes
+    import torch
+    lib = probe_lib()
+    lib.jlust_probe_rows_f32.restype = ctypes.c_int
+    lib.jlust_probe_rows_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    nrows, row, count, per_wave = 1_000_000, 64, 32_000_000, 64
+    g = torch.Generator(device="cuda").manual_seed(3)
+    src = torch.randn(nrows * row, dtype=torch.float32, device="cuda")
+    idx = torch.randint(0, nrows, (count,), generator=g, device="cuda", dtype=torch.int64).to(torch.int32)
+    out = torch.empty(((count + per_wave - 1) // per_wave) * 64, dtype=torch.float32, device="cuda")
+    bt = torch.randn(128, nrows, device="cuda")       # B column-major: row c of bt is column c of B
+    dst = torch.empty(nrows, 64, device="cuda")
+    cur = torch.cuda.current_stream()
+    s1, s2 = torch.cuda.Stream(), torch.cuda.Stream()
+
+    def gather(st):
+        assert lib.jlust_probe_rows_f32(src.data_ptr(), nrows, row, idx.data_ptr(), count, per_wave,
+                                        out.data_ptr(), st.cuda_stream) == 0
+
+    def transpose(st):
+        with torch.cuda.stream(st):
+            dst.copy_(bt[64:128].t())
+
+    def concurrent():
+        e0 = torch.cuda.Event()
+        e0.record(cur)
+        s1.wait_event(e0)
+        s2.wait_event(e0)
+        gather(s1)
+        transpose(s2)
+        for st in (s1, s2):
+            e = torch.cuda.Event()
+            e.record(st)
+            cur.wait_event(e)
+
+    cases = (("gathers alone", lambda: gather(cur)), ("transpose alone", lambda: transpose(cur)),
+             ("gathers then transpose, one stream", lambda: (gather(cur), transpose(cur))),
+             ("gathers and transpose on two streams", concurrent))
+    res = []
+    for name, fn in cases:
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 10
+        a.record(cur)
+        for _ in range(reps):
+            fn()
+        b.record(cur)
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / reps
+        res.append({"case": name, "ms": round(ms, 4)})
+        log(f"{name}: {ms:.3f} ms")
     return res
 
 
@@ -1012,6 +1079,9 @@ def main():
         return
     if args.gather_floor:
         print(json.dumps({"gather_floor": gather_floor()}), flush=True)
+        return
+    if args.gather_overlap:
+        print(json.dumps({"gather_overlap": gather_overlap()}), flush=True)
         return
     if args.mall_probe:
         print(json.dumps({"mall_probe": mall_probe()}), flush=True)
