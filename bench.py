@@ -79,6 +79,8 @@ def parse():
     p.add_argument("--gather-overlap", action="store_true",
                    help="only time config 3's chunk gathers alone, a 256 MB transpose alone, and the "
                         "two on two streams at once")
+    p.add_argument("--gather-cpol", action="store_true",
+                   help="only time 8-byte random gathers as buffer loads under each cache policy")
     p.add_argument("--mall-probe", action="store_true",
                    help="only measure whether a just-written buffer reads back faster than a cold one")
     p.add_argument("--cold", action="store_true",
@@ -620,6 +622,52 @@ def gather_probe():
     return res
 
 
+def gather_cpol():
+    """The 8-byte gathers of gather_probe (whole source) as buffer loads with
+    each cache-policy setting (bench_probes.hip, gather_cpol_kernel), from
+    1, 4 and 32 MB sources: whether bypassing the L1 (sc0), the streaming
+    hint (nt) or system scope (sc1) changes the rate at which random 8-byte
+    values come from the L2s or the MALL."""
+    import ctypes
+    import torch
+    lib = probe_lib()
+    lib.jlust_probe_gather_cpol_f64.restype = ctypes.c_int
+    lib.jlust_probe_gather_cpol_f64.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p,
+                                                ctypes.c_void_p, ctypes.c_int64, ctypes.c_uint32, ctypes.c_int,
+                                                ctypes.c_void_p]
+    total = 64 * 2**20
+    nthreads = total // 8
+    idx = torch.empty(total, dtype=torch.int32, device="cuda")
+    out = torch.empty(nthreads, dtype=torch.float64, device="cuda")
+    stream = torch.cuda.current_stream()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    names = {0: "default", 1: "sc0", 2: "nt", 3: "sc0 nt", 16: "sc1", 17: "sc0 sc1"}
+    res = []
+    for mb in (1, 4, 32):
+        n = mb * 2**20 // 8
+        src = torch.rand(n, dtype=torch.float64, device="cuda")
+        idx.random_(0, n, generator=g)
+        for cpol, name in names.items():
+            call = lambda: lib.jlust_probe_gather_cpol_f64(src.data_ptr(), n, idx.data_ptr(),  # noqa: E731
+                                                           out.data_ptr(), nthreads, n, cpol, stream.cuda_stream)
+            for _ in range(3):
+                assert call() == 0
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            reps = 10
+            s.record(stream)
+            for _ in range(reps):
+                call()
+            e.record(stream)
+            torch.cuda.synchronize()
+            t = s.elapsed_time(e) / reps * 1e-3
+            res.append({"source_MB": mb, "cpol": name, "gathers": total, "ms": round(t * 1e3, 4),
+                        "Ggathers_per_s": round(total / t / 1e9, 2)})
+            log(f"{mb} MB, {name}: {t * 1e3:.4f} ms, {total / t / 1e9:.1f} G gathers/s")
+        del src
+    return res
+
+
 def _wall_ms(fn, reps=10, warm=3):
     import torch
     for _ in range(warm):
@@ -1079,6 +1127,9 @@ def main():
         return
     if args.gather_floor:
         print(json.dumps({"gather_floor": gather_floor()}), flush=True)
+        return
+    if args.gather_cpol:
+        print(json.dumps({"gather_cpol": gather_cpol()}), flush=True)
         return
     if args.gather_overlap:
         print(json.dumps({"gather_overlap": gather_overlap()}), flush=True)

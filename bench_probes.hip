@@ -28,6 +28,11 @@
 
 #include <cstdint>
 
+typedef int probe_int32x4 __attribute__((ext_vector_type(4)));
+
+__device__ double probe_buffer_load_f64(probe_int32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.f64");
+
 namespace {
 
 constexpr int PROBE_U = 8;
@@ -47,6 +52,39 @@ __global__ __launch_bounds__(256) void gather_probe_kernel(const double *__restr
     double s = 0;
 #pragma unroll
     for (int u = 0; u < PROBE_U; ++u) s += src[base + id[u]];
+    out[t] = s;
+}
+
+// Buffer resource over p (wave-uniform): base in dwords 0-1, no stride,
+// num_records 0xffffffff bytes, gfx9 data format in dword 3.
+__device__ __forceinline__ probe_int32x4 probe_resource(const void *p)
+{
+    const uint64_t a = (uint64_t)p;
+    probe_int32x4 r;
+    r.x = __builtin_amdgcn_readfirstlane((int)(uint32_t)a);
+    r.y = __builtin_amdgcn_readfirstlane((int)((uint32_t)(a >> 32) & 0xffff));
+    r.z = -1;
+    r.w = 0x00020000;
+    return r;
+}
+
+// 1b. The gathers of 1. (whole source) as buffer loads carrying cache-policy
+// bits CPOL (bit 0 sc0, bit 1 nt, bit 4 sc1): which form moves an 8-byte
+// gather from the L2 fastest.
+template <int CPOL>
+__global__ __launch_bounds__(256) void gather_cpol_kernel(const double *__restrict__ src,
+                                                          const uint32_t *__restrict__ idx,
+                                                          double *__restrict__ out, int64_t nthreads)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nthreads) return;
+    const probe_int32x4 rsrc = probe_resource(src);
+    uint32_t id[PROBE_U];
+#pragma unroll
+    for (int u = 0; u < PROBE_U; ++u) id[u] = __builtin_nontemporal_load(idx + t + u * nthreads);
+    double s = 0;
+#pragma unroll
+    for (int u = 0; u < PROBE_U; ++u) s += probe_buffer_load_f64(rsrc, (int)(id[u] * 8u), 0, CPOL);
     out[t] = s;
 }
 
@@ -181,5 +219,31 @@ extern "C" int jlust_probe_gather_f64(const double *src, int64_t src_len, const 
     const unsigned grid = (unsigned)((nthreads + 255) / 256);
     hipLaunchKernelGGL(gather_probe_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, idx,
                        out, nthreads, xcd_slice, range);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// The gathers of jlust_probe_gather_f64 (whole source) as buffer loads with
+// cache-policy bits cpol: 0, 1 (sc0), 2 (nt), 3 (sc0 nt), 16 (sc1) or 17
+// (sc0 sc1).  idx holds 8*nthreads values below range <= src_len, and
+// src_len * 8 < 2^31.  Returns 0, 1 on invalid arguments, 2 on a launch error.
+extern "C" int jlust_probe_gather_cpol_f64(const double *src, int64_t src_len, const uint32_t *idx,
+                                           double *out, int64_t nthreads, uint32_t range, int cpol,
+                                           void *stream)
+{
+    if (!src || !idx || !out || nthreads <= 0 || range == 0 || range > (uint64_t)src_len) return 1;
+    if (src_len * 8 >= ((int64_t)1 << 31)) return 1;
+    const unsigned grid = (unsigned)((nthreads + 255) / 256);
+    const hipStream_t st = (hipStream_t)stream;
+#define PROBE_CPOL(C) hipLaunchKernelGGL(gather_cpol_kernel<C>, dim3(grid), dim3(256), 0, st, src, idx, out, nthreads)
+    switch (cpol) {
+    case 0: PROBE_CPOL(0); break;
+    case 1: PROBE_CPOL(1); break;
+    case 2: PROBE_CPOL(2); break;
+    case 3: PROBE_CPOL(3); break;
+    case 16: PROBE_CPOL(16); break;
+    case 17: PROBE_CPOL(17); break;
+    default: return 1;
+    }
+#undef PROBE_CPOL
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
