@@ -414,15 +414,18 @@ def gather_floor():
     rows_probe_kernel): config 3's SpMM gathers, per 64-column chunk, one
     256-byte row of the 256 MB row-major copy of B for each of its 32M
     nonzeros; config 4's SDDMM gathers one 512-byte column of B (256 MB) for
-    each of its 16M nonzeros.  Uniform random rows, 8 in flight per wave,
-    a wave per 32 (or 64) consecutive indices; the time bounds any kernel
-    making those gathers."""
+    each of its 16M nonzeros.  Uniform random rows, a wave per 32 or 64
+    (or 128) consecutive indices, 8 load instructions in flight per wave:
+    with 4/8-byte lanes one row per instruction, with 16-byte lanes
+    (rows_wide_probe_kernel) 4 or 2 rows per instruction.  The time bounds
+    any kernel making those gathers."""
     import ctypes
     import torch
     lib = probe_lib()
-    lib.jlust_probe_rows_f32.restype = ctypes.c_int
-    lib.jlust_probe_rows_f32.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
-                                         ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
+    for f in (lib.jlust_probe_rows_f32, lib.jlust_probe_rows_wide_f32):
+        f.restype = ctypes.c_int
+        f.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                      ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p]
     stream = torch.cuda.current_stream()
     g = torch.Generator(device="cuda").manual_seed(3)
     res = []
@@ -432,11 +435,12 @@ def gather_floor():
                                      16_000_000)):
         src = torch.randn(nrows * row, dtype=torch.float32, device="cuda")
         idx = torch.randint(0, nrows, (count,), generator=g, device="cuda", dtype=torch.int64).to(torch.int32)
-        for per_wave in (32, 64):
+        for lanes, per_wave in (("4/8-byte", 32), ("4/8-byte", 64), ("16-byte", 64), ("16-byte", 128)):
             waves = (count + per_wave - 1) // per_wave
             out = torch.empty(waves * 64, dtype=torch.float32, device="cuda")
-            call = lambda: lib.jlust_probe_rows_f32(src.data_ptr(), nrows, row, idx.data_ptr(), count,  # noqa: E731
-                                                    per_wave, out.data_ptr(), stream.cuda_stream)
+            fn = lib.jlust_probe_rows_f32 if lanes == "4/8-byte" else lib.jlust_probe_rows_wide_f32
+            call = lambda: fn(src.data_ptr(), nrows, row, idx.data_ptr(), count,  # noqa: E731
+                              per_wave, out.data_ptr(), stream.cuda_stream)
             for _ in range(3):
                 assert call() == 0
             torch.cuda.synchronize()
@@ -448,9 +452,10 @@ def gather_floor():
             e.record(stream)
             torch.cuda.synchronize()
             t = s.elapsed_time(e) / reps * 1e-3
-            res.append({"case": name, "rows_per_wave": per_wave, "gathers": count, "row_bytes": row * 4,
-                        "ms": round(t * 1e3, 4), "gathered_TBps": round(count * row * 4 / t / 1e12, 3)})
-            log(f"{name}, {per_wave} per wave: {t * 1e3:.3f} ms")
+            res.append({"case": name, "lanes": lanes, "rows_per_wave": per_wave, "gathers": count,
+                        "row_bytes": row * 4, "ms": round(t * 1e3, 4),
+                        "gathered_TBps": round(count * row * 4 / t / 1e12, 3)})
+            log(f"{name}, {lanes} lanes, {per_wave} per wave: {t * 1e3:.3f} ms")
             del out
         del src, idx
         torch.cuda.empty_cache()

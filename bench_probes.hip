@@ -19,7 +19,8 @@
 // pattern of the SpMM kernel's gathers from the row-major copy of B (256-byte
 // rows) and of the SDDMM kernel's gathers of B's columns (512-byte rows),
 // without their arithmetic or outputs.  Its time bounds any kernel that
-// makes those gathers.
+// makes those gathers.  3b: the same with 16-byte lanes, several rows per
+// wave instruction.
 //
 // 4. Streaming write and read of a buffer (16-byte lanes, grid-stride), for
 // the question whether data written by one kernel is read back by the next
@@ -141,6 +142,37 @@ __global__ __launch_bounds__(256) void rows_probe_kernel(const float *__restrict
     if (p0 < count) out[wave * 64 + lane] = s;
 }
 
+// 3b. The same gathers with 16-byte lanes: LPR lanes cover a row (16 for
+// 256-byte rows, 32 for 512-byte rows), so one wave instruction reads 64/LPR
+// rows and ROWS_U instructions keep ROWS_U * 64/LPR rows in flight per wave.
+template <int LPR>
+__global__ __launch_bounds__(256) void rows_wide_probe_kernel(const float *__restrict__ src, int64_t row,
+                                                              const uint32_t *__restrict__ idx, int64_t count,
+                                                              int64_t per_wave, float *__restrict__ out)
+{
+    typedef float vec_t __attribute__((ext_vector_type(4)));
+    constexpr int RPI = 64 / LPR;
+    const int lane = threadIdx.x & 63;
+    const int sub = lane / LPR, l = lane % LPR;
+    const int64_t wave = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+    const int64_t p0 = wave * per_wave;
+    const int64_t p1 = p0 + per_wave < count ? p0 + per_wave : count;
+    vec_t acc = {};
+    for (int64_t p = p0; p < p1; p += ROWS_U * RPI) {
+        vec_t v[ROWS_U];
+#pragma unroll
+        for (int u = 0; u < ROWS_U; ++u) {
+            const int64_t q0 = p + u * RPI + sub;
+            const int64_t q = q0 < p1 ? q0 : p1 - 1;
+            const uint64_t r = idx[q];
+            v[u] = *reinterpret_cast<const vec_t *>(src + r * row + l * 4);
+        }
+#pragma unroll
+        for (int u = 0; u < ROWS_U; ++u) acc += v[u];
+    }
+    if (p0 < count) out[wave * 64 + lane] = acc[0] + acc[1] + acc[2] + acc[3];
+}
+
 typedef double probe_double2 __attribute__((ext_vector_type(2)));
 
 __global__ __launch_bounds__(256) void write_probe_kernel(probe_double2 *__restrict__ dst, int64_t n, double v)
@@ -179,6 +211,23 @@ extern "C" int jlust_probe_rows_f32(const float *src, int64_t nrows, int64_t row
     else
         hipLaunchKernelGGL(rows_probe_kernel<2>, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, row, idx,
                            count, per_wave, out);
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// As jlust_probe_rows_f32, with 16-byte lanes (rows_wide_probe_kernel).
+extern "C" int jlust_probe_rows_wide_f32(const float *src, int64_t nrows, int64_t row, const uint32_t *idx,
+                                         int64_t count, int64_t per_wave, float *out, void *stream)
+{
+    if (!src || !idx || !out || nrows <= 0 || count <= 0 || per_wave <= 0) return 1;
+    if (row != 64 && row != 128) return 1;
+    const int64_t waves = (count + per_wave - 1) / per_wave;
+    const unsigned grid = (unsigned)((waves + 3) / 4);
+    if (row == 64)
+        hipLaunchKernelGGL(rows_wide_probe_kernel<16>, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, row,
+                           idx, count, per_wave, out);
+    else
+        hipLaunchKernelGGL(rows_wide_probe_kernel<32>, dim3(grid), dim3(256), 0, (hipStream_t)stream, src, row,
+                           idx, count, per_wave, out);
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
 
