@@ -222,3 +222,75 @@ def test_coo_random(J, O, sorted_rows, dtype):
     rp = np.r_[0, np.cumsum(cnt)].astype(np.int32) + 1
     absref = O.csr_spmv_absref(rp, colind[order], val[order], x, 1.5, 0.5, y0)
     assert_within(host(y), ref, absref, dtype, "coo")
+
+
+# ------------------------------------------------- strided dense operands
+
+def _colmajor_view(J, a, pad, fill=float("nan")):
+    """A view of the column-major array a inside a larger column-major buffer
+    whose leading dimension is rows + pad (the padding rows hold `fill`)."""
+    import torch
+    from jlust_amd.tensor import leading_dim
+    r, c = a.shape
+    big = np.full((r + pad, c), fill, dtype=a.dtype, order="F")
+    big[:r] = a
+    v = dev(big)[:r]
+    assert v.stride(0) == 1 and leading_dim(v) == r + pad
+    del torch
+    return v
+
+
+@pytest.mark.parametrize("pad", [1, 4, 7])
+@pytest.mark.parametrize("k", [5, 40, 128])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_spmm_strided_views(J, O, pad, k, dtype):
+    """B and C as column views of larger buffers (ldb = n + pad, ldc = m + pad;
+    pad 4 keeps 16-byte alignment, 1 and 7 do not): the plain call and the
+    prepared plan, beta != 0, and the padding rows of C left untouched."""
+    m, n = 1500, 1300
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(k).integers(0, 30, m),
+                                     seed=20 + pad, dtype=dtype)
+    rng = np.random.default_rng(21)
+    B = np.asfortranarray(rng.standard_normal((n, k)).astype(dtype))
+    C0 = np.asfortranarray(rng.standard_normal((m, k)).astype(dtype))
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    ref, _ = O.csr_spmm(rowptr, colind, val, B, 0.5, -1.5, C0)
+    absref = O.csr_spmm_absref(rowptr, colind, val, B, 0.5, -1.5, C0)
+    for how in ("plain", "plan"):
+        Bv = _colmajor_view(J, B, pad)
+        Cv = _colmajor_view(J, C0, pad, fill=7.0)
+        if how == "plain":
+            J.execute(J.SpMMOp, A, Bv, Cv, alpha=0.5, beta=-1.5)
+        else:
+            h = J.prepare(J.HIPBackend(), J.SpMMOp, A, n_cols=k)
+            J.execute(h, Bv, Cv, alpha=0.5, beta=-1.5)
+        assert_within(host(Cv), ref, absref, dtype, f"spmm {how} k={k} pad={pad}")
+        base = Cv.as_strided((m + pad, k), (1, m + pad))     # the whole buffer
+        assert (host(base)[m:] == 7.0).all(), f"spmm {how} wrote into the padding rows"
+
+
+@pytest.mark.parametrize("pad", [1, 4, 7])
+@pytest.mark.parametrize("K", [3, 64, 128])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_sddmm_strided_views(J, O, pad, K, dtype):
+    """A (m x K, lda = m + pad) and B (K x n, ldb = K + pad) as column views of
+    larger buffers: the plain call and the prepared plan."""
+    m, n = 1200, 900
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(K).integers(0, 40, m),
+                                     seed=30 + pad, dtype=dtype)
+    rng = np.random.default_rng(31)
+    A = np.asfortranarray(rng.standard_normal((m, K)).astype(dtype))
+    Bm = np.asfortranarray(rng.standard_normal((K, n)).astype(dtype))
+    c0 = rng.standard_normal(colind.size).astype(dtype)
+    ref = O.csr_sddmm(rowptr, colind, A, Bm, 2.0, 0.25, c0)
+    absref = O.csr_sddmm_absref(rowptr, colind, A, Bm, 2.0, 0.25, c0)
+    for how in ("plain", "plan"):
+        cv = dev(c0)
+        Cs = J.csr_tensor(dev(rowptr), dev(colind), cv, (m, n))
+        Av, Bv = _colmajor_view(J, A, pad), _colmajor_view(J, Bm, pad)
+        if how == "plain":
+            J.execute(J.SDDMMOp, Av, Bv, Cs, alpha=2.0, beta=0.25)
+        else:
+            h = J.prepare(J.HIPBackend(), J.SDDMMOp, Cs, n_inner=K)
+            J.execute(J.SDDMMOp, h, Av, Bv, Cs, alpha=2.0, beta=0.25)
+        assert_within(host(cv), ref, absref, dtype, f"sddmm {how} K={K} pad={pad}")
