@@ -138,7 +138,17 @@ def spmv_with_fns(spmv, u_A, u_x, u_y, alpha=1.0, beta=0.0, input_fn=None, outpu
     """y = alpha*output_fn(A*input_fn.(x)) + beta*y (spmv.jl:371-374) around a
     plain SpMV `spmv(u_A, u_x, u_y, alpha, beta)`: in_fn.(x) into a new
     vector, the product into a row-sum vector when output_fn is given, then
-    the row write on the device (jlust_amd/elementwise.py)."""
+    the row write on the device (jlust_amd/elementwise.py).  Strided
+    vectors (a row of a column-major matrix, a stepped slice), which the
+    reference's ust takes as any AbstractVector (src/interop.jl:36-46), pass
+    through contiguous device copies, and y is copied back into its view."""
+    x0, y0 = nonzeros(u_x), nonzeros(u_y)
+    if (x0.dim() == 1 and not x0.is_contiguous()) or (y0.dim() == 1 and not y0.is_contiguous()):
+        yc = y0.contiguous()
+        spmv_with_fns(spmv, u_A, ust(x0.contiguous()), ust(yc), alpha, beta, input_fn, output_fn)
+        if yc is not y0:
+            y0.copy_(yc)
+        return u_y
     if input_fn is None and output_fn is None:
         return spmv(u_A, u_x, u_y, alpha, beta)
     from .elementwise import apply_fn, is_identity
