@@ -20,6 +20,7 @@
 // loads issued together (indices clamped into the block's nonzeros, results
 // of the clamped copies dropped), so K = 1 puts 64 nonzeros on a wave per
 // load instead of 8.
+#include <algorithm>
 #include <memory>
 #include <vector>
 
@@ -34,6 +35,7 @@ constexpr int SD_BLOCK = 256;
 constexpr int SD_GROUP = 8;
 constexpr int SD_GROUPS = SD_BLOCK / SD_GROUP;
 constexpr size_t SD_LDS_BUDGET = 48 * 1024;
+constexpr int64_t SD_GRID_MAX = 1 << 20;     // grid cap of the grid-stride kernels
 
 template <typename T> struct V16;
 template <> struct alignas(16) V16<float> { float v[4]; static constexpr int N = 4; };
@@ -186,21 +188,22 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_direct_kernel(
     const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval, const T *mask,
     const int32_t *__restrict__ perm)
 {
-    const int64_t i = blockIdx.x;
-    if (i >= m) return;
     const int g = threadIdx.x / SD_GROUP, q = threadIdx.x % SD_GROUP;
-    const int64_t lo = (int64_t)rowptr[i] - origin, hi = (int64_t)rowptr[i + 1] - origin;
-    for (int64_t p = lo + g; p < hi; p += SD_GROUPS) {
-        const int64_t j = (int64_t)colind[p] - origin;
-        T dot = T(0);
-        for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
-        dot = group_sum<SD_GROUP>(dot);
-        if (q == 0) {
-            const int64_t o = perm ? (int64_t)perm[p] : p;
-            T out = alpha * dot;
-            if (mask) out = mask[o] * out;
-            if (!beta_zero) out += beta * Cval[o];
-            Cval[o] = out;
+    // Rows by grid stride: the grid is capped, so any m launches.
+    for (int64_t i = blockIdx.x; i < m; i += gridDim.x) {
+        const int64_t lo = (int64_t)rowptr[i] - origin, hi = (int64_t)rowptr[i + 1] - origin;
+        for (int64_t p = lo + g; p < hi; p += SD_GROUPS) {
+            const int64_t j = (int64_t)colind[p] - origin;
+            T dot = T(0);
+            for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
+            dot = group_sum<SD_GROUP>(dot);
+            if (q == 0) {
+                const int64_t o = perm ? (int64_t)perm[p] : p;
+                T out = alpha * dot;
+                if (mask) out = mask[o] * out;
+                if (!beta_zero) out += beta * Cval[o];
+                Cval[o] = out;
+            }
         }
     }
 }
@@ -214,17 +217,18 @@ __global__ __launch_bounds__(SD_BLOCK) void coo_sddmm_kernel(
     const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval, const T *mask)
 {
     const int g = threadIdx.x / SD_GROUP, q = threadIdx.x % SD_GROUP;
-    const int64_t p = (int64_t)blockIdx.x * SD_GROUPS + g;
-    if (p >= nnz) return;
-    const int64_t i = (int64_t)rows[p] - origin, j = (int64_t)cols[p] - origin;
-    T dot = T(0);
-    for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
-    dot = group_sum<SD_GROUP>(dot);
-    if (q == 0) {
-        T out = alpha * dot;
-        if (mask) out = mask[p] * out;
-        if (!beta_zero) out += beta * Cval[p];
-        Cval[p] = out;
+    // Entries by grid stride (the grid is capped); the 8 lanes of a group share p.
+    for (int64_t p = (int64_t)blockIdx.x * SD_GROUPS + g; p < nnz; p += (int64_t)gridDim.x * SD_GROUPS) {
+        const int64_t i = (int64_t)rows[p] - origin, j = (int64_t)cols[p] - origin;
+        T dot = T(0);
+        for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
+        dot = group_sum<SD_GROUP>(dot);
+        if (q == 0) {
+            T out = alpha * dot;
+            if (mask) out = mask[p] * out;
+            if (!beta_zero) out += beta * Cval[p];
+            Cval[p] = out;
+        }
     }
 }
 
@@ -252,7 +256,8 @@ int sddmm_launch(int64_t m, int64_t K, int32_t origin, const int32_t *rowptr, co
     int64_t lds_ld = 0;
     const int R = sddmm_rows<T>(K, &lds_ld);
     if (R < 1) {
-        hipLaunchKernelGGL((csr_sddmm_direct_kernel<T>), dim3((unsigned)m), dim3(SD_BLOCK), 0, s, m,
+        hipLaunchKernelGGL((csr_sddmm_direct_kernel<T>), dim3((unsigned)std::min<int64_t>(m, SD_GRID_MAX)),
+                           dim3(SD_BLOCK), 0, s, m,
                            K, origin, rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, perm);
         return check_launch("csr_sddmm_direct_kernel");
     }
@@ -337,7 +342,8 @@ int coo_sddmm(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin, cons
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "coo_sddmm: entries in an empty matrix");
     if (int st = require_device(nullptr)) return st;
     if (nnz == 0) return JLUST_STATUS_SUCCESS;
-    hipLaunchKernelGGL((coo_sddmm_kernel<T>), dim3((unsigned)((nnz + SD_GROUPS - 1) / SD_GROUPS)), dim3(SD_BLOCK),
+    hipLaunchKernelGGL((coo_sddmm_kernel<T>),
+                       dim3((unsigned)std::min<int64_t>((nnz + SD_GROUPS - 1) / SD_GROUPS, SD_GRID_MAX)), dim3(SD_BLOCK),
                        0, (hipStream_t)stream, nnz, K, origin, rows, cols, alpha, A, lda, B, ldb, beta,
                        (int)(beta == T(0)), Cval, mask);
     return check_launch("coo_sddmm_kernel");

@@ -294,3 +294,34 @@ def test_sddmm_strided_views(J, O, pad, K, dtype):
             h = J.prepare(J.HIPBackend(), J.SDDMMOp, Cs, n_inner=K)
             J.execute(J.SDDMMOp, h, Av, Bv, Cs, alpha=2.0, beta=0.25)
         assert_within(host(cv), ref, absref, dtype, f"sddmm {how} K={K} pad={pad}")
+
+
+@pytest.mark.parametrize("mask_kind", ["csr", "coo"])
+@pytest.mark.parametrize("dtype,K", [(np.float64, 6500), (np.float32, 13000)])
+def test_sddmm_k_beyond_lds(J, O, mask_kind, dtype, K):
+    """K too large for a 32-row block of A in 48 KB of LDS (f64 K > 6110,
+    f32 K > 12222): the direct kernel, which reads A's rows with stride lda;
+    plain call and prepared plan, CSR and shuffled COO masks."""
+    m, n = 300, 200
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(K).integers(0, 9, m),
+                                     seed=50, dtype=dtype)
+    rng = np.random.default_rng(51)
+    A = np.asfortranarray(rng.uniform(-1, 1, (m, K)).astype(dtype))
+    Bm = np.asfortranarray(rng.uniform(-1, 1, (K, n)).astype(dtype))
+    c0 = rng.uniform(-1, 1, colind.size).astype(dtype)
+    ref = O.csr_sddmm(rowptr, colind, A, Bm, 0.5, 1.5, c0)
+    absref = O.csr_sddmm_absref(rowptr, colind, A, Bm, 0.5, 1.5, c0)
+    rows = np.repeat(np.arange(1, m + 1, dtype=np.int32), np.diff(rowptr))
+    perm = rng.permutation(colind.size) if mask_kind == "coo" else np.arange(colind.size)
+    for how in ("plain", "plan"):
+        cv = dev(c0[perm])
+        if mask_kind == "csr":
+            Cs = J.csr_tensor(dev(rowptr), dev(colind), cv, (m, n))
+        else:
+            Cs = J.coo_tensor(dev(rows[perm]), dev(colind[perm]), cv, (m, n))
+        if how == "plain":
+            J.execute(J.SDDMMOp, dev(A), dev(Bm), Cs, alpha=0.5, beta=1.5)
+        else:
+            h = J.prepare(J.HIPBackend(), J.SDDMMOp, Cs, n_inner=K)
+            J.execute(J.SDDMMOp, h, dev(A), dev(Bm), Cs, alpha=0.5, beta=1.5)
+        assert_within(host(cv), ref[perm], absref[perm], dtype, f"{mask_kind} {how} K={K}")
