@@ -439,14 +439,13 @@ void bsr16_spmm_strip_kernel(
     __builtin_amdgcn_s_waitcnt(0);
 }
 
-// JLUST_HIP_BSR_STRIP=0 keeps the row-wave kernel.
+// JLUST_HIP_BSR_STRIP=0 keeps the row-wave kernel (read at each call, so a
+// test can run both kernels in one process; the row-wave kernel is also the
+// one for B or C whose byte offsets reach 2^31).
 bool bsr_strip()
 {
-    static const bool on = [] {
-        const char *e = getenv("JLUST_HIP_BSR_STRIP");
-        return !(e && e[0] == '0');
-    }();
-    return on;
+    const char *e = getenv("JLUST_HIP_BSR_STRIP");
+    return !(e && e[0] == '0');
 }
 
 // ------------------------------------------------- expansion to CSR

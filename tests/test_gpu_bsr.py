@@ -131,6 +131,28 @@ def test_bsr_config5_scaled(J, O):
     assert_within(C, ref, absref, np.float32, cfg["name"] + " /32")
 
 
+@pytest.mark.parametrize("beta", [0.0, 0.5])
+def test_bsr_rowwave_kernel(J, O, monkeypatch, beta):
+    """JLUST_HIP_BSR_STRIP=0 runs the row-wave kernel, the one taken when B's
+    or C's byte offsets reach 2^31: config 5's pattern at 1/32 scale, a
+    scattered pattern and long block-rows, against the oracle."""
+    from jlust_amd import workloads as W
+    monkeypatch.setenv("JLUST_HIP_BSR_STRIP", "0")
+    cfg = W.make(5, scale=32)
+    cases = [(cfg["browptr"], cfg["bcolind"], cfg["val"], cfg["B"], cfg["mb"], cfg["nb"], "config 5 /32")]
+    for per_row, nb, name in ((4, 300, "scattered"), (19, 40, "long block-rows")):
+        bp, bc, bv = random_bsr(30, nb, per_row, seed=60 + per_row)
+        B = np.asfortranarray(np.random.default_rng(61).standard_normal((nb * 16, 40)).astype(np.float32))
+        cases.append((bp, bc, bv, B, 30, nb, name))
+    for bp, bc, bv, B, mb, nb, name in cases:
+        C0 = np.asfortranarray(np.random.default_rng(62).standard_normal((mb * 16, B.shape[1])).astype(np.float32))
+        C = run_bsr(J, bp, bc, bv, B, mb, nb, alpha=1.25, beta=beta, C0=C0 if beta else None)
+        ref = O.bsr_spmm(bp, bc, bv, 16, B, 1.25, beta, C0 if beta else None)
+        rp, ci, v = O.bsr_to_csr(bp, bc, bv, 16)
+        absref = O.csr_spmm_absref(rp, ci, v, B, 1.25, beta, C0 if beta else None)
+        assert_within(C, ref, absref, np.float32, f"row-wave kernel, {name}, beta={beta}")
+
+
 def test_bsr_config5_full_sampled_block_rows(J, O):
     from jlust_amd import workloads as W
     cfg = W.make(5)
