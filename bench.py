@@ -81,6 +81,8 @@ def parse():
                         "two on two streams at once")
     p.add_argument("--gather-cpol", action="store_true",
                    help="only time 8-byte random gathers as buffer loads under each cache policy")
+    p.add_argument("--structured", action="store_true",
+                   help="only time SpMV on structured matrices (2D/3D Laplacians, a random band)")
     p.add_argument("--mall-probe", action="store_true",
                    help="only measure whether a just-written buffer reads back faster than a cold one")
     p.add_argument("--cold", action="store_true",
@@ -775,6 +777,85 @@ def sweep_spmv():
     return res
 
 
+def _stencil_csr(shape, offsets):
+    """CSR (Int32, 1-based) of a grid operator: row i = grid point p, its
+    columns p + o for the stencil offsets o that stay inside the grid, values
+    uniform in [-1, 1].  Columns are sorted because the offsets are."""
+    rng = np.random.default_rng(7)
+    dims = np.array(shape)
+    m = int(np.prod(dims))
+    coords = np.stack(np.unravel_index(np.arange(m), shape), axis=1)
+    cols, valid = [], []
+    for off in offsets:
+        c = coords + np.array(off)
+        ok = np.all((c >= 0) & (c < dims), axis=1)
+        cols.append(np.ravel_multi_index(tuple(np.clip(c, 0, dims - 1).T), shape))
+        valid.append(ok)
+    cols, valid = np.stack(cols, axis=1), np.stack(valid, axis=1)
+    lens = valid.sum(axis=1)
+    rp = np.zeros(m + 1, np.int64)
+    np.cumsum(lens, out=rp[1:])
+    ci = cols[valid]
+    return (rp + 1).astype(np.int32), (ci + 1).astype(np.int32), rng.uniform(-1, 1, ci.size), m
+
+
+def structured_spmv():
+    """SpMV (f64) on structured matrices of config 2's size, the kind the
+    reference's SuiteSparse benchmark runs (bench_suitesparse.jl): a 2D
+    5-point and a 3D 7-point Laplacian, and random columns in a band of
+    +-256 around the diagonal (16 per row).  The plain call and the plan's own
+    choice, per call from HIP events over 50 back-to-back calls, in effective
+    GB/s by the reference's byte formula (12 nnz + 4 (m + 1) + 8 (n + m))."""
+    import torch
+    import jlust_amd as J
+    res = []
+    cases = []
+    rp, ci, v, m = _stencil_csr((2048, 2048), [(-1, 0), (0, -1), (0, 0), (0, 1), (1, 0)])
+    cases.append(("2D 5-point Laplacian 2048^2", rp, ci, v, m, m))
+    rp, ci, v, m = _stencil_csr((160, 160, 160), [(-1, 0, 0), (0, -1, 0), (0, 0, -1), (0, 0, 0), (0, 0, 1),
+                                                  (0, 1, 0), (1, 0, 0)])
+    cases.append(("3D 7-point Laplacian 160^3", rp, ci, v, m, m))
+    rng = np.random.default_rng(8)
+    m = 4_000_000
+    offs = np.sort(rng.choice(513, (m, 16), replace=True) - 256, axis=1)
+    cols = np.clip(np.arange(m)[:, None] + offs, 0, m - 1)
+    cols = np.sort(cols, axis=1)
+    keep = np.ones_like(cols, bool)
+    keep[:, 1:] = cols[:, 1:] != cols[:, :-1]          # distinct columns per row
+    lens = keep.sum(axis=1)
+    rp = np.zeros(m + 1, np.int64)
+    np.cumsum(lens, out=rp[1:])
+    ci = cols[keep]
+    cases.append(("random band +-256, 16 per row, 4M", (rp + 1).astype(np.int32), (ci + 1).astype(np.int32),
+                  rng.uniform(-1, 1, ci.size), m, m))
+    for name, rp, ci, v, m, n in cases:
+        nnz = ci.size
+        nbytes = 12 * nnz + 4 * (m + 1) + 8 * (n + m)
+        A = J.csr_tensor(dev(rp), dev(ci), dev(v), (m, n))
+        x = dev(np.random.default_rng(9).uniform(-1, 1, n))
+        y = torch.empty(m, dtype=torch.float64, device="cuda")
+        h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+        e = {"matrix": name, "m": m, "nnz": int(nnz), "algorithmic_bytes": int(nbytes), "plan_kernel": h.kernel()}
+        for key, fn in (("plain", lambda: J.execute(J.SpMVOp, A, x, y)), ("plan", lambda: J.execute(h, x, y))):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(50):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            ms = a.elapsed_time(b) / 50
+            e[f"{key}_us"] = round(ms * 1e3, 1)
+            e[f"{key}_GBps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        res.append(e)
+        log(f"{name}: {e}")
+        del A, x, y, h
+        torch.cuda.empty_cache()
+    return res
+
+
 def stream_ceiling():
     """Attainable HBM streaming rates on this box for a 2 GiB f64 tensor: a
     device copy (read + write), a read-only reduction and a fill, in TB/s of
@@ -1132,6 +1213,9 @@ def main():
         return
     if args.gather_floor:
         print(json.dumps({"gather_floor": gather_floor()}), flush=True)
+        return
+    if args.structured:
+        print(json.dumps({"structured_spmv": structured_spmv()}), flush=True)
         return
     if args.gather_cpol:
         print(json.dumps({"gather_cpol": gather_cpol()}), flush=True)
