@@ -240,21 +240,23 @@ __global__ __launch_bounds__(256) void bsr16_spmm_rowwave_kernel(
 // lanes x 16 bytes of one column per instruction, whole 128-byte lines, no
 // registers).  Per tile every wave reads all of its row's B operands from the
 // window into registers; after a barrier the window is free, so the next
-// tile's copies are issued at once and land while the waves run this tile's
-// MFMAs from registers and store C.  One wait + barrier per tile finds the
+// tile's copies are issued during this tile's MFMAs -- one copy instruction
+// before each block's four MFMAs, so they issue in the MFMA chain's
+// dependency stalls -- and land while the waves finish the MFMAs and store C.  One wait + barrier per tile finds the
 // copies done (vmcnt(1): all but the C store just issued; an explicit
 // s_barrier, since a fence would wait for everything).  The window buffer is
 // single (78 KB) and the kernel fits 80 VGPRs (buffer resources keep the
 // addresses of B and C in SGPRs), so two workgroups share a CU and each has
 // a window in flight: one workgroup's copies alone are latency-bound at about
-// half the rate of two.  Columns sit BSR_CS bytes apart (a 16-byte pad per
-// column), so the 16 lanes of an operand read (16 columns, one row group)
-// spread over the banks.  A strip whose rows hold more than BSR_QCHUNK blocks
+// half the rate of two.  Columns sit BSR_CS bytes apart (a 32-byte pad per
+// column), so the 16-byte operand reads of the 64 lanes (16 columns x 4 row
+// groups) meet no bank conflict; the 16-byte pad that a 16-lane count
+// suggests costs 4 conflict cycles per read (measured by SQ_LDS_BANK_CONFLICT).  A strip whose rows hold more than BSR_QCHUNK blocks
 // or whose window exceeds BSR_WMAX block-rows computes its rows with direct
 // operand loads instead (same arithmetic).
 constexpr int BSR_SR = 12;                        // block-rows (waves) per workgroup
 constexpr int BSR_WMAX = BSR_SR + 64;             // window block-rows (a +-32 band)
-constexpr int BSR_CS = BSR_WMAX * 64 + 16;        // LDS bytes per column of a window
+constexpr int BSR_CS = BSR_WMAX * 64 + 32;        // LDS bytes per column of a window
 constexpr int BSR_BUF = 16 * BSR_CS;              // the window buffer
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -386,15 +388,16 @@ void bsr16_spmm_strip_kernel(
     const uint32_t col_off = (uint32_t)(i * BSR_CS + 16 * g);
     const int lane16 = lane * 16;
     const int32x4 rs_b = buffer_resource(bwin);  // B's window: lane offset in a VGPR, the rest in an SGPR
+    auto copy_one = [&](int64_t c0, int ii) {
+        const int j = ii / npc, p = ii % npc;
+        if (c0 + j >= k) return;
+        const int fu = p * 256;                        // floats, wave-uniform
+        const int so = (int)((fu + (c0 + j) * ldb) * 4); // bytes, wave-uniform
+        if (fu + 4 * lane < wfloats)
+            raw_buffer_load_lds(rs_b, (lds_void *)(win + j * BSR_CS + p * 1024), 16, lane16, so, 0, 0);
+    };
     auto copy_tile = [&](int64_t c0) {
-        for (int ii = wave; ii < ninst; ii += BSR_SR) {
-            const int j = ii / npc, p = ii % npc;
-            if (c0 + j >= k) continue;
-            const int fu = p * 256;                        // floats, wave-uniform
-            const int so = (int)((fu + (c0 + j) * ldb) * 4); // bytes, wave-uniform
-            if (fu + 4 * lane < wfloats)
-                raw_buffer_load_lds(rs_b, (lds_void *)(win + j * BSR_CS + p * 1024), 16, lane16, so, 0, 0);
-        }
+        for (int ii = wave; ii < ninst; ii += BSR_SR) copy_one(c0, ii);
     };
     const int32x4 rs_c = buffer_resource(C);
     const int c_lane = (4 * g + i * (int)ldc) * 4;
@@ -409,19 +412,27 @@ void bsr16_spmm_strip_kernel(
 #pragma unroll
         for (int qq = 0; qq < BSR_QCHUNK; ++qq) b[qq] = *reinterpret_cast<const floatx4 *>(win + co + jrel[qq] * 64);
         asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (c0 + 16 < k) copy_tile(c0 + 16);
-        asm volatile("" ::: "memory");        // the copies are issued before the MFMAs and the store
+        // One copy instruction of the next tile before each block's MFMAs (the
+        // branches keep the order), the rest after: the copies issue in the
+        // MFMA chain's dependency stalls instead of ahead of it.
         floatx4 acc = zero;
-        if (live) {
+        const bool more = c0 + 16 < k;
+        int ii = wave;
 #pragma unroll
-            for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
-                if (qq < nq) {
+        for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+            if (more && ii < ninst) {
+                copy_one(c0 + 16, ii);
+                ii += BSR_SR;
+            }
+            asm volatile("" ::: "memory");
+            if (live && qq < nq) {
 #pragma unroll
-                    for (int u = 0; u < 4; ++u)
-                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[qq][u], b[qq][u], acc, 0, 0, 0);
-                }
+                for (int u = 0; u < 4; ++u)
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[qq][u], b[qq][u], acc, 0, 0, 0);
             }
         }
+        for (; more && ii < ninst; ii += BSR_SR) copy_one(c0 + 16, ii);
+        asm volatile("" ::: "memory");        // every copy is issued before the store
         if (live) {
             // C's lane part (4 g + i ldc) * 4 bytes in a VGPR, the rest in an SGPR.
             if (c0 + i < k) {
