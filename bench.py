@@ -750,7 +750,7 @@ def sweep_spmv():
     rng = np.random.default_rng(0)
     res = []
     for m, n in ((4_000_000, 4_000_000), (1_000_000, 4_000_000), (4_000_000, 1_000_000),
-                 (4_000_000, 500_000)):
+                 (4_000_000, 500_000), (1_000_000, 1_000_000), (2_000_000, 2_000_000)):
         for L in (1, 2, 4, 6, 8, 12, 16):
             rp = (np.arange(m + 1, dtype=np.int64) * L + 1).astype(np.int32)
             ci = rng.integers(0, n, (m, L))

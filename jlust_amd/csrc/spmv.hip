@@ -1035,16 +1035,18 @@ int mostly_local(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_
 // ~5-6 and ~9 entries, so slicing needs nnz >= L * m with L by x's size.
 enum Layout { LAYOUT_ROWS = 0, LAYOUT_SLICED = 1, LAYOUT_BINNED = 2 };
 
-// The LDS-binned layout costs a fixed ~85 us (its bin pass is a chain of one
-// step per column slice) plus ~4-5 ns per 1000 entries; scattered gathers of
-// an x beyond the L2 cost the row-order kernels ~16 ns per 1000 entries at
-// 32 MB and ~7 ns at 4 MB.  Measured crossovers (f64, random columns): 7M
-// entries for x >= 24 MB, 12M for x >= 6 MB, 20M above 2 MB.
+// The LDS-binned layout costs a fixed time (its bin pass is a chain of one
+// step per column slice: ~85 us with 256 slices, ~35 us with the 31-123 wide
+// slices of an x of 4-16 MB) plus ~3.5-5 ns per 1000 entries; scattered
+// gathers of an x beyond the L2 cost the row-order kernels ~16 ns per 1000
+// entries at 32 MB, ~11 ns at 8 MB and ~6 ns at 4 MB.  Measured crossovers
+// (f64, random columns): 7M entries for x >= 24 MB, 6M for x >= 6 MB, 12M
+// above 2 MB.
 constexpr size_t BINNED_MIN_X_BYTES = (size_t)2 << 20;
 
 int64_t binned_min_nnz(size_t xbytes)
 {
-    return xbytes >= ((size_t)24 << 20) ? 7000000 : xbytes >= ((size_t)6 << 20) ? 12000000 : 20000000;
+    return xbytes >= ((size_t)24 << 20) ? 7000000 : xbytes >= ((size_t)6 << 20) ? 6000000 : 12000000;
 }
 
 // The layout of a prepared plan.  JLUST_HIP_SPMV_SLICE: 0 = row order, 1 =

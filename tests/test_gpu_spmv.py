@@ -281,14 +281,16 @@ def test_plan_sliced_full_config2_deterministic(J, O, monkeypatch):
     np.testing.assert_array_equal(host(y2), y)
 
 
-@pytest.mark.parametrize("per_row,expect", [(2, "vector"), (8, "binned")])
-def test_plan_slicing_threshold(J, O, per_row, expect, monkeypatch):
-    """x of 25.6 MB with random columns: the LDS-binned layout pays from ~4
-    entries per row; shorter rows keep the vector kernel.  Both plans match
-    the oracle."""
+@pytest.mark.parametrize("n,per_row,expect", [(3_200_000, 2, "vector"), (3_200_000, 8, "binned"),
+                                               (1_000_000, 4, "vector"), (1_000_000, 8, "binned")])
+def test_plan_slicing_threshold(J, O, n, per_row, expect, monkeypatch):
+    """Random columns, n x n: with x of 25.6 MB the LDS-binned layout pays
+    from 7M entries, with x of 8 MB (wide slices shared by several workgroups)
+    from 6M; fewer entries keep the vector kernel.  Both plans match the
+    oracle."""
     monkeypatch.delenv("JLUST_HIP_SPMV_SLICE", raising=False)
     monkeypatch.delenv("JLUST_HIP_SPMV_VECTOR", raising=False)
-    m = n = 3_200_000
+    m = n
     rng = np.random.default_rng(per_row)
     colind = np.sort(rng.integers(0, n, (m, per_row)), axis=1)
     colind = (colind.reshape(-1) + 1).astype(np.int32)

@@ -97,9 +97,30 @@ def test_binned_long_runs(J, O, dtype, monkeypatch):
 
 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("n", [300_000, 1_100_000])
+def test_binned_wide_slices(J, O, dtype, n, monkeypatch):
+    """x small enough for at most 128 slices of 128 KB: slices as wide as LDS
+    allows, several workgroups per slice (f64 n = 300k: 19 slices of 15,808
+    columns, 13 workgroups each; f32: 10 slices, 25 workgroups; n = 1.1M f64:
+    68 slices, 3 workgroups; f32: 34 slices, 7 workgroups).  Rows of 0-40
+    entries, alpha/beta, bit-identical on a second execute."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m = 250_000
+    lens = np.random.default_rng(n % 97).integers(0, 41, m)
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=n % 89, dtype=dtype)
+    x = np.random.default_rng(41).uniform(-1, 1, n).astype(dtype)
+    y0 = np.random.default_rng(42).uniform(-1, 1, m).astype(dtype)
+    y, h, A = check(J, O, rowptr, colind, val, x, m, n, dtype, f"binned wide n={n}",
+                    alpha=0.5, beta=-2.0, y0=y0)
+    y2 = dev(y0)
+    J.execute(h, dev(x), y2, alpha=0.5, beta=-2.0)
+    np.testing.assert_array_equal(host(y2), y)
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
 def test_binned_many_slices_few_rows(J, O, dtype, monkeypatch):
-    """300 rows over 4M columns: 256 slices (several workgroups per slice when
-    slices are fewer than CUs is covered by the shapes above), one bin."""
+    """300 rows over 4M columns: 256 slices, one workgroup per slice, one
+    bin."""
     monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
     m, n = 300, 4_000_000
     lens = np.random.default_rng(8).integers(0, 3000, m)
