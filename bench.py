@@ -1059,6 +1059,30 @@ def timed(step, steps, warmup):
     return wall * 1e3 / steps, e0.elapsed_time(e1) / steps
 
 
+def timed_samples(step, est_ms, n=20, min_sample_ms=0.5):
+    """Min and median of n samples (the @belapsed statistics of the
+    reference's benchmarks, benchmark/bench_suitesparse.jl:174-177), warm:
+    each sample is B back-to-back steps between one pair of HIP events, with
+    B chosen so that a sample lasts at least min_sample_ms and the two event
+    records (about 2 us) stay a small part of it.  Returns (min, median, B)
+    in ms per step."""
+    import torch
+    b = max(1, int(np.ceil(min_sample_ms / max(est_ms, 1e-6))))
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    pairs = []
+    for _ in range(n):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(b):
+            step()
+        e1.record(stream)
+        pairs.append((e0, e1))
+    torch.cuda.synchronize()
+    t = np.array([e0.elapsed_time(e1) / b for e0, e1 in pairs])
+    return float(t.min()), float(np.median(t)), b
+
+
 def timed_cold(step, steps):
     """Each of K steps timed alone (an event pair around it) right after a
     1 GiB read that evicts the operands from the L2s and the 256 MB MALL.
@@ -1134,6 +1158,12 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
         del pkeep
     log(f"config {config}: {steps} steps: wall {ms_per_step:.4f} ms/step, events "
         f"{per_launch_ms:.4f} ms/step")
+    s_min, s_med, s_b = timed_samples(step, per_launch_ms)
+    samples = {"n": 20, "steps_per_sample": s_b, "min_ms_per_step": round(s_min, 6),
+               "median_ms_per_step": round(s_med, 6),
+               "cache": "warm: back-to-back steps, operands left in the L2s and the MALL by the "
+                        "previous step (--cold times steps after a 1 GiB flush)"}
+    log(f"config {config}: 20 samples of {s_b} step(s): min {s_min:.4f}, median {s_med:.4f} ms/step")
     cold_res = None
     if cold:
         c_mean, c_min = timed_cold(step, steps)
@@ -1181,7 +1211,8 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
         "gflops": round(nflops / (ms_per_step * 1e-3) / 1e9, 3),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 3),
         "algorithmic_bytes": int(nbytes), "flops": int(nflops),
-        "roofline": roof, "plain_call": plain, "plan_build_ms": plan_build_ms, "cpu_baseline": cpu,
+        "roofline": roof, "samples": samples, "plain_call": plain, "plan_build_ms": plan_build_ms,
+        "cpu_baseline": cpu,
     }
     if cold_res is not None:
         out["cold"] = cold_res
@@ -1269,7 +1300,7 @@ def main():
                                  no_cpu=args.no_cpu_baseline)
             rows.append({k: e[k] for k in ("config", "value", "unit", "ms_per_step", "gflops",
                                            "pct_hbm_peak", "dtype", "algorithmic_bytes", "flops",
-                                           "roofline", "plain_call", "plan_build_ms",
+                                           "roofline", "samples", "plain_call", "plan_build_ms",
                                            "cpu_baseline")})
         out["all_configs"] = rows
     print(json.dumps(out), flush=True)
