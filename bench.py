@@ -1104,15 +1104,21 @@ def timed_cold(step, steps):
     return float(np.mean(times)), float(np.min(times))
 
 
-def traffic_for(workload):
+def counters_for(workload):
+    """(traffic bytes, counter readings) of a workload's committed rocprofv3
+    --pmc passes (profiles/pmc_traffic.json): L2-miss bytes per step, and the
+    L2 hit rate per kernel and MFMA utilisation where they were collected."""
     path = os.path.join(ROOT, "profiles", "pmc_traffic.json")
     try:
         with open(path) as f:
             d = json.load(f)
         e = d.get(workload)
-        return None if e is None else int(e["traffic_bytes"])
+        if e is None:
+            return None, None
+        extra = {k: e[k] for k in ("l2_hit_pct", "mfma_busy_pct") if k in e}
+        return int(e["traffic_bytes"]), extra or None
     except (OSError, ValueError, KeyError):
-        return None
+        return None, None
 
 
 def host_info():
@@ -1184,7 +1190,9 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
         achieved = nflops / (k_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": MFMA_F32_PEAK_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / MFMA_F32_PEAK_TFLOPS, 5)}
-    roof["traffic"] = traffic_for(cfg["name"] + (":plan" if use_plan else ""))
+    roof["traffic"], counters = counters_for(cfg["name"] + (":plan" if use_plan else ""))
+    if counters:
+        roof["counters"] = counters
     roof["traffic_counts"] = ("L2-miss bytes (FETCH_SIZE x 2.0 + WRITE_SIZE, rocprofv3 --pmc): "
                               "requests leaving the L2s, served by the MALL or by HBM")
     roof["kernel"] = kname
