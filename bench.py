@@ -76,6 +76,9 @@ def parse():
                         "matrix, sorted and shuffled, beside the oracle's COO SpMV on this host")
     p.add_argument("--gather-floor", action="store_true",
                    help="only time the random-row gathers of configs 3 and 4 alone (their floor)")
+    p.add_argument("--spmv-parts", action="store_true",
+                   help="config 1's SpMV step taken apart: with its x gathers, with a coalesced x "
+                        "read in their place, without x, y only (bench_probes.hip)")
     p.add_argument("--gather-overlap", action="store_true",
                    help="only time config 3's chunk gathers alone, a 256 MB transpose alone, and the "
                         "two on two streams at once")
@@ -461,6 +464,56 @@ def gather_floor():
             del out
         del src, idx
         torch.cuda.empty_cache()
+    return res
+
+
+def spmv_parts():
+    """Config 1's SpMV step taken apart (bench_probes.hip, spmv_parts_kernel:
+    the library's vector-kernel shape at config 1, 4 lanes per row): with the
+    random x gathers, with a coalesced read of x[row] in their place, with no
+    x, and writing y only.  HIP events over 400 back-to-back launches, best
+    of 3 rounds, in us per launch (the 400 launches are made in a C loop,
+    since a launch from Python takes longer on the host than these kernels
+    on the GPU)."""
+    import ctypes
+    import torch
+    from jlust_amd import workloads as W
+    lib = probe_lib()
+    f = lib.jlust_probe_spmv_parts_f64
+    f.restype = ctypes.c_int
+    f.argtypes = [ctypes.c_int64, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32, ctypes.c_void_p,
+                  ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                  ctypes.c_void_p]
+    cfg = W.make(1)
+    m, n = cfg["m"], cfg["n"]
+    nnz = int(cfg["rowptr"][-1]) - 1
+    if nnz != 16 * m:
+        raise RuntimeError("config 1 rows are expected to hold 16 entries each")
+    colind, val, x = dev(cfg["colind"]), dev(cfg["val"]), dev(cfg["x"])
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    stream = torch.cuda.current_stream()
+    names = {0: "x[col] gathers (the kernel's step)", 1: "x[row], coalesced, in place of the gathers",
+             2: "no x (value x column index)", 3: "y written only"}
+    best = {}
+    for _ in range(3):
+        for mode in names:
+            call = lambda reps: f(m, n, 16, 1, colind.data_ptr(), val.data_ptr(),  # noqa: E731
+                                  x.data_ptr(), y.data_ptr(), mode, reps, stream.cuda_stream)
+            assert call(20) == 0
+            torch.cuda.synchronize()
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            assert call(400) == 0
+            e.record(stream)
+            torch.cuda.synchronize()
+            us = s.elapsed_time(e) / 400 * 1e3
+            best[mode] = min(best.get(mode, us), us)
+    res = [{"mode": names[k], "us_per_launch": round(v, 3)} for k, v in best.items()]
+    for r in res:
+        log(f"spmv parts: {r['mode']}: {r['us_per_launch']} us")
+    gathers = best[0] - best[1]
+    res.append({"gathers_us": round(gathers, 3), "gathers": nnz,
+                "gathers_per_s": round(nnz / (gathers * 1e-6) / 1e9, 1)})
     return res
 
 
@@ -1258,6 +1311,9 @@ def main():
         return
     if args.gather_cpol:
         print(json.dumps({"gather_cpol": gather_cpol()}), flush=True)
+        return
+    if args.spmv_parts:
+        print(json.dumps({"spmv_parts": spmv_parts()}), flush=True)
         return
     if args.gather_overlap:
         print(json.dumps({"gather_overlap": gather_overlap()}), flush=True)

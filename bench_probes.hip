@@ -25,6 +25,14 @@
 // 4. Streaming write and read of a buffer (16-byte lanes, grid-stride), for
 // the question whether data written by one kernel is read back by the next
 // from the MALL faster than from HBM.
+//
+// 5. The parts of a uniform-row CSR SpMV step (rows of exactly `ulen`
+// entries, 4 lanes per row, 4 entries per lane at a time: the shape of the
+// library's vector kernel at config 1): mode 0 multiplies by x[col], the
+// random gathers; mode 1 by x[row], a coalesced read of the same bytes;
+// mode 2 by the column index itself, no x; mode 3 writes y only.  The
+// differences between the modes split the step into its gathers, its stream
+// of A and its launch.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
@@ -194,6 +202,43 @@ __global__ __launch_bounds__(256) void read_probe_kernel(const probe_double2 *__
 
 }  // namespace
 
+template <int MODE>
+__global__ __launch_bounds__(256) void spmv_parts_kernel(int64_t m, int32_t ulen, int32_t origin,
+                                                         const int32_t *__restrict__ colind,
+                                                         const double *__restrict__ val,
+                                                         const double *__restrict__ x, double *__restrict__ y)
+{
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int64_t row = t >> 2;
+    const int sub = (int)(t & 3);
+    const int64_t r = row < m ? row : m - 1;
+    const int64_t lo = r * ulen, hi = row < m ? lo + ulen : lo;
+    double acc = 0.0;
+    if (MODE != 3) {
+        for (int64_t p0 = lo + sub; p0 < hi; p0 += 16) {
+            int32_t c[4];
+            double v[4], xv[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int64_t p = min(p0 + 4 * u, hi - 1);
+                c[u] = colind[p];
+                v[u] = val[p];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                xv[u] = MODE == 0 ? x[c[u] - origin] : MODE == 1 ? x[r] : (double)c[u];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const double a = acc + v[u] * xv[u];
+                acc = p0 + 4 * u < hi ? a : acc;
+            }
+        }
+    }
+    acc += __shfl_xor(acc, 1, 4);
+    acc += __shfl_xor(acc, 2, 4);
+    if (sub == 0 && row < m) y[row] = acc;
+}
+
 // src holds nrows x row floats (row-major, 16-byte aligned), idx holds count
 // row indices below nrows, out holds 64 * waves floats with waves =
 // ceil(count / per_wave); row is 64 (4-byte lanes) or 128 (8-byte lanes).
@@ -294,5 +339,32 @@ extern "C" int jlust_probe_gather_cpol_f64(const double *src, int64_t src_len, c
     default: return 1;
     }
 #undef PROBE_CPOL
+    return hipGetLastError() == hipSuccess ? 0 : 2;
+}
+
+// The parts of a uniform-row SpMV step (probe 5), launched `reps` times back
+// to back from here (a launch from Python costs more host time than these
+// kernels take): colind/val hold m*ulen entries with columns in
+// [origin, origin + n), x holds n values (mode 0) or m (mode 1), y holds m.
+// Returns 0, 1 on invalid arguments, 2 on a launch error.
+extern "C" int jlust_probe_spmv_parts_f64(int64_t m, int64_t n, int32_t ulen, int32_t origin,
+                                          const int32_t *colind, const double *val, const double *x,
+                                          double *y, int mode, int reps, void *stream)
+{
+    if (m <= 0 || n <= 0 || ulen <= 0 || m * ulen > ((int64_t)1 << 31) || !colind || !val || !x || !y ||
+        reps < 1)
+        return 1;
+    if (mode == 1 && n < m) return 1;
+    const unsigned grid = (unsigned)((m * 4 + 255) / 256);
+    const hipStream_t st = (hipStream_t)stream;
+    for (int r = 0; r < reps; ++r) {
+        switch (mode) {
+        case 0: hipLaunchKernelGGL(spmv_parts_kernel<0>, dim3(grid), dim3(256), 0, st, m, ulen, origin, colind, val, x, y); break;
+        case 1: hipLaunchKernelGGL(spmv_parts_kernel<1>, dim3(grid), dim3(256), 0, st, m, ulen, origin, colind, val, x, y); break;
+        case 2: hipLaunchKernelGGL(spmv_parts_kernel<2>, dim3(grid), dim3(256), 0, st, m, ulen, origin, colind, val, x, y); break;
+        case 3: hipLaunchKernelGGL(spmv_parts_kernel<3>, dim3(grid), dim3(256), 0, st, m, ulen, origin, colind, val, x, y); break;
+        default: return 1;
+        }
+    }
     return hipGetLastError() == hipSuccess ? 0 : 2;
 }
