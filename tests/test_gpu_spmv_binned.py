@@ -117,6 +117,25 @@ def test_binned_wide_slices(J, O, dtype, n, monkeypatch):
     np.testing.assert_array_equal(host(y2), y)
 
 
+@pytest.mark.parametrize("dtype,n", [(np.float64, 2_097_152), (np.float64, 2_097_153),
+                                     (np.float32, 4_194_304), (np.float32, 4_194_305)],
+                         ids=["f64-128-wide", "f64-per-cu", "f32-128-wide", "f32-per-cu"])
+def test_binned_geometry_switch(J, O, dtype, n, monkeypatch):
+    """Both sides of the switch between wide slices and one slice per CU on a
+    256-CU device: 128 slices of 128 KB (two workgroups each) at n = 2^21
+    (f64) / 2^22 (f32); one column more needs 129 wide slices, more than half
+    the CUs, and the plan takes ~n/256-column slices instead.  Rows of 0-40
+    entries, 0-based, alpha/beta."""
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m = 30_000
+    lens = np.random.default_rng(n % 101).integers(0, 41, m)
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=n % 83, origin=0, dtype=dtype)
+    x = np.random.default_rng(43).uniform(-1, 1, n).astype(dtype)
+    y0 = np.random.default_rng(44).uniform(-1, 1, m).astype(dtype)
+    check(J, O, rowptr, colind, val, x, m, n, dtype, f"binned geometry n={n}", origin=0,
+          alpha=1.5, beta=0.25, y0=y0)
+
+
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 def test_binned_many_slices_few_rows(J, O, dtype, monkeypatch):
     """300 rows over 4M columns: 256 slices, one workgroup per slice, one
