@@ -11,8 +11,9 @@
 // queues on the L1/L2 miss capacity; even x cut into eight 4 MB slices, one per
 // XCD L2, gathers at only ~190 G/s.  Here no gather ever leaves a CU's LDS:
 //
-//   slice pass (one workgroup per column slice c of W columns, W*sizeof(T) =
-//   128 KB of LDS): x[cW, (c+1)W) is copied into LDS; the slice's entries,
+//   slice pass (G workgroups per column slice c of W columns, W*sizeof(T) <=
+//   128 KB of LDS; G = 1 unless x is small, see geometry()): x[cW, (c+1)W) is
+//   copied into each workgroup's LDS; the slice's entries,
 //   stored slice-major and inside a slice in (row bin, row, k) order, are
 //   streamed once (value + 16-bit local column), multiplied by their x from LDS
 //   and summed per row with a wave64 segmented scan.  Each (row, slice) pair
