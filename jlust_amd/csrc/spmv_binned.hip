@@ -19,7 +19,7 @@
 //   and summed per row with a wave64 segmented scan.  Each (row, slice) pair
 //   with entries yields one partial sum, written contiguously.
 //
-//   bin pass (one workgroup per bin b of H rows, H*sizeof(T) = 128 KB of
+//   bin pass (one workgroup per bin b of H rows, H*sizeof(T) <= 128 KB of
 //   LDS): the partials of bin b come in S runs, one per slice, each run sorted
 //   by row with every row at most once.  Runs are added into an LDS copy of
 //   y[bH, (b+1)H) in slice order, a workgroup barrier between runs (so no two
