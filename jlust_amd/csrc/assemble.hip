@@ -288,9 +288,9 @@ int assemble(int64_t m, const std::vector<Piece> &ps, int32_t *rowptr, int32_t *
 
 using namespace jlust;
 
-extern "C" int jlust_hip_csr_assemble(int64_t m, int64_t n, int32_t nplacements, const jlust_placement *placements,
-                                      int value_type, int32_t *rowptr, int32_t *colind, void *val, int64_t nnz,
-                                      jlust_stream_t stream)
+static int csr_assemble_body(int64_t m, int64_t n, int32_t nplacements, const jlust_placement *placements,
+                             int value_type, int32_t *rowptr, int32_t *colind, void *val, int64_t nnz,
+                             jlust_stream_t stream)
 {
     clear_error();
     if (m < 0 || n < 0 || m >= INT32_MAX || n > INT32_MAX || nnz < 0 || nnz > INT32_MAX)
@@ -314,6 +314,15 @@ extern "C" int jlust_hip_csr_assemble(int64_t m, int64_t n, int32_t nplacements,
     hipStream_t s = (hipStream_t)stream;
     return value_type == 0 ? assemble<double>(m, ps, rowptr, colind, (double *)val, nnz, s)
                            : assemble<float>(m, ps, rowptr, colind, (float *)val, nnz, s);
+}
+
+extern "C" int jlust_hip_csr_assemble(int64_t m, int64_t n, int32_t nplacements, const jlust_placement *placements,
+                                      int value_type, int32_t *rowptr, int32_t *colind, void *val, int64_t nnz,
+                                      jlust_stream_t stream)
+{
+    return jlust::host_guard("csr_assemble", [&] {
+        return csr_assemble_body(m, n, nplacements, placements, value_type, rowptr, colind, val, nnz, stream);
+    });
 }
 
 extern "C" int jlust_hip_scatter_values(void *dst, int64_t dst_len, const int32_t *slots, const void *src,

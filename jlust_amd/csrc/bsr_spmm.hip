@@ -684,10 +684,10 @@ struct jlust_bsr_plan {
     jlust_spmm_plan_t csr = nullptr;
 };
 
-extern "C" int jlust_hip_bsr_spmm_plan_create(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
-                                              int32_t origin, int value_type, int row_major_blocks,
-                                              const int32_t *browptr, const int32_t *bcolind, const void *val,
-                                              int64_t k, jlust_stream_t stream, jlust_bsr_plan_t *plan_out)
+static int bsr_spmm_plan_create_body(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
+                                     int32_t origin, int value_type, int row_major_blocks,
+                                     const int32_t *browptr, const int32_t *bcolind, const void *val,
+                                     int64_t k, jlust_stream_t stream, jlust_bsr_plan_t *plan_out)
 {
     using namespace jlust;
     clear_error();
@@ -745,6 +745,17 @@ extern "C" int jlust_hip_bsr_spmm_plan_create(int64_t mb, int64_t nb, int64_t b1
     }
     *plan_out = p.release();
     return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_bsr_spmm_plan_create(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
+                                              int32_t origin, int value_type, int row_major_blocks,
+                                              const int32_t *browptr, const int32_t *bcolind, const void *val,
+                                              int64_t k, jlust_stream_t stream, jlust_bsr_plan_t *plan_out)
+{
+    return jlust::host_guard("bsr_spmm_plan_create", [&] {
+        return bsr_spmm_plan_create_body(mb, nb, b1, b2, nnzb, origin, value_type, row_major_blocks,
+                                         browptr, bcolind, val, k, stream, plan_out);
+    });
 }
 
 extern "C" int jlust_hip_bsr_spmm_plan_update_values(jlust_bsr_plan_t plan, const void *val, jlust_stream_t stream)

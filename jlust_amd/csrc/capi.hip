@@ -19,7 +19,11 @@ int fail(int code, const char *fmt, ...)
     va_start(ap, fmt);
     vsnprintf(buf, sizeof buf, fmt, ap);
     va_end(ap);
-    g_last_error = buf;
+    try {
+        g_last_error = buf;
+    } catch (const std::bad_alloc &) {
+        g_last_error.clear();   // the status code still reports the failure
+    }
     return code;
 }
 
@@ -104,18 +108,21 @@ int scratch(jlust_stream_t stream, size_t bytes, void **out)
     int dev = 0;
     int st = require_device(&dev);
     if (st) return st;
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    ScratchBuf &b = g_scratch[{dev, stream}];
-    if (b.bytes < bytes) {
-        const size_t want = bytes + bytes / 4 + 4096;
-        void *p = nullptr;
-        JLUST_HIP_TRY(hipMalloc(&p, want));
-        if (b.ptr) g_scratch_retired.push_back(b.ptr);
-        b.ptr = p;
-        b.bytes = want;
-    }
-    *out = b.ptr;
-    return JLUST_STATUS_SUCCESS;
+    return host_guard("scratch", [&]() -> int {
+        std::lock_guard<std::mutex> lk(g_scratch_mu);
+        ScratchBuf &b = g_scratch[{dev, stream}];
+        if (b.bytes < bytes) {
+            const size_t want = bytes + bytes / 4 + 4096;
+            if (b.ptr) g_scratch_retired.reserve(g_scratch_retired.size() + 1);   // before the hipMalloc
+            void *p = nullptr;
+            JLUST_HIP_TRY(hipMalloc(&p, want));
+            if (b.ptr) g_scratch_retired.push_back(b.ptr);
+            b.ptr = p;
+            b.bytes = want;
+        }
+        *out = b.ptr;
+        return JLUST_STATUS_SUCCESS;
+    });
 }
 
 }  // namespace jlust

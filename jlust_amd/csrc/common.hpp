@@ -7,6 +7,7 @@
 
 #include <cstdint>
 #include <cstdio>
+#include <new>
 #include <string>
 
 #include "../../include/jlust_hip.h"
@@ -21,6 +22,20 @@ void clear_error();
 
 // Maps a failed HIP call onto JLUST_STATUS_HIP_ERROR / OUT_OF_MEMORY.
 int hip_fail(hipError_t e, const char *what);
+
+// Runs f() and turns a host allocation failure (std::bad_alloc from the
+// library's host-side tables) into JLUST_STATUS_OUT_OF_MEMORY, so that no C++
+// exception crosses the C ABI.  The guarded code makes its host allocations
+// before its device ones, so such a failure leaks no device memory.
+template <typename F>
+int host_guard(const char *what, F &&f)
+{
+    try {
+        return f();
+    } catch (const std::bad_alloc &) {
+        return fail(JLUST_STATUS_OUT_OF_MEMORY, "%s: out of host memory", what);
+    }
+}
 
 #define JLUST_HIP_TRY(expr)                                      \
     do {                                                         \
@@ -53,8 +68,9 @@ const DeviceInfo &device_info(int device);
 // ---------------------------------------------------------------- scratch
 
 // Returns a device buffer of at least `bytes` owned by the library and
-// private to (current device, stream).  It grows on demand (the old buffer is
-// released after the stream drains) and lives until process exit.
+// private to (current device, stream).  It grows on demand; an outgrown
+// buffer is kept until process exit, since queued work or a captured graph
+// may still read it.
 int scratch(jlust_stream_t stream, size_t bytes, void **out);
 
 // out[i] = sum(in[0..i)) over n int32 counts (in == out allowed); stream-ordered.

@@ -141,9 +141,9 @@ int coo_row_order(int64_t m, int64_t nnz, int32_t origin, const int32_t *rows, c
 
 using namespace jlust;
 
-extern "C" int jlust_hip_coo_spmv_plan_create(int64_t m, int64_t n, int64_t nnz, int32_t origin, int value_type,
-                                             const int32_t *rows, const int32_t *cols, const void *val,
-                                             jlust_stream_t stream, jlust_spmv_plan_t *plan_out)
+static int coo_spmv_plan_create_body(int64_t m, int64_t n, int64_t nnz, int32_t origin, int value_type,
+                                     const int32_t *rows, const int32_t *cols, const void *val,
+                                     jlust_stream_t stream, jlust_spmv_plan_t *plan_out)
 {
     clear_error();
     if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "coo_spmv_plan_create: null plan_out");
@@ -196,4 +196,13 @@ extern "C" int jlust_hip_coo_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
     own.p = nullptr;
     *plan_out = plan;
     return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_coo_spmv_plan_create(int64_t m, int64_t n, int64_t nnz, int32_t origin, int value_type,
+                                             const int32_t *rows, const int32_t *cols, const void *val,
+                                             jlust_stream_t stream, jlust_spmv_plan_t *plan_out)
+{
+    return jlust::host_guard("coo_spmv_plan_create", [&] {
+        return coo_spmv_plan_create_body(m, n, nnz, origin, value_type, rows, cols, val, stream, plan_out);
+    });
 }

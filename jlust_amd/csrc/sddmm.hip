@@ -415,10 +415,10 @@ struct jlust_sddmm_plan {
     void *mem = nullptr;
 };
 
-extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64_t n, int64_t K, int64_t nnz,
-                                           int32_t origin, int value_type, const int32_t *idx1,
-                                           const int32_t *idx2, jlust_stream_t stream,
-                                           jlust_sddmm_plan_t *plan_out)
+static int sddmm_plan_create_body(int32_t mask_format, int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                  int32_t origin, int value_type, const int32_t *idx1,
+                                  const int32_t *idx2, jlust_stream_t stream,
+                                  jlust_sddmm_plan_t *plan_out)
 {
     clear_error();
     if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: null plan_out");
@@ -457,6 +457,12 @@ extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64
     const size_t sz_i = coo ? align_up(4 * nz, 256) : 0;
     const int64_t max_items = nblk + nnz / SD_CHUNK + 1;
     const size_t sz_items = align_up(8 * (size_t)max_items, 256);
+    // Host tables before the device allocation (a failed host allocation then
+    // leaks nothing): the row pointers and the work items (row block, part).
+    const bool analyse = R >= 1 && m > 0;
+    std::vector<int32_t> rp(analyse ? (size_t)(m + 1) : 0);
+    std::vector<int32_t> items;
+    if (analyse) items.reserve(2 * (size_t)max_items);
     JLUST_HIP_TRY(hipMalloc(&p->mem, sz_rp + 2 * sz_i + sz_items));
     char *b = (char *)p->mem;
     int st = JLUST_STATUS_SUCCESS;
@@ -474,8 +480,7 @@ extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64
     }
     p->items = (int32_t *)(b + sz_rp + 2 * sz_i);
     // Work items from the row pointers of each row block (host analysis).
-    if (!st && R >= 1 && m > 0) {
-        std::vector<int32_t> rp((size_t)(m + 1));
+    if (!st && analyse) {
         hipError_t e = hipMemcpyAsync(rp.data(), p->rowptr, sizeof(int32_t) * (size_t)(m + 1),
                                       hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -484,7 +489,6 @@ extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64
             st = fail(JLUST_STATUS_NONCANONICAL_STORAGE,
                       "sddmm_plan_create: rowptr runs from %d to %d, expected %d to %lld", rp[0], rp[m], origin,
                       (long long)(nnz + origin));
-        std::vector<int32_t> items;
         for (int64_t rb = 0; !st && rb < nblk; ++rb) {
             const int64_t r1 = min((rb + 1) * (int64_t)R, m);
             const int64_t cnt = (int64_t)rp[r1] - rp[rb * R];
@@ -493,13 +497,16 @@ extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64
                           (long long)(rb * R));
                 break;
             }
-            for (int64_t part = 0; part * SD_CHUNK < cnt; ++part) {
+            for (int64_t part = 0; !st && part * SD_CHUNK < cnt; ++part) {
+                if ((int64_t)items.size() >= 2 * max_items) {   // stays within the reserved tables
+                    st = fail(JLUST_STATUS_HIP_ERROR, "sddmm_plan_create: item overflow");
+                    break;
+                }
                 items.push_back((int32_t)rb);
                 items.push_back((int32_t)part);
             }
         }
         p->nitems = (int64_t)items.size() / 2;
-        if (!st && p->nitems > max_items) st = fail(JLUST_STATUS_HIP_ERROR, "sddmm_plan_create: item overflow");
         if (!st && p->nitems > 0) {
             e = hipMemcpyAsync(p->items, items.data(), sizeof(int32_t) * items.size(), hipMemcpyHostToDevice, s);
             if (e == hipSuccess) e = hipStreamSynchronize(s);
@@ -513,6 +520,17 @@ extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64
     }
     *plan_out = p.release();
     return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                           int32_t origin, int value_type, const int32_t *idx1,
+                                           const int32_t *idx2, jlust_stream_t stream,
+                                           jlust_sddmm_plan_t *plan_out)
+{
+    return jlust::host_guard("sddmm_plan_create", [&] {
+        return sddmm_plan_create_body(mask_format, m, n, K, nnz, origin, value_type, idx1, idx2, stream,
+                                      plan_out);
+    });
 }
 
 template <typename T>

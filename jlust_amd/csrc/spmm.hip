@@ -502,10 +502,10 @@ struct jlust_spmm_plan {
     int64_t nnz_rows = 0;           // entries of the rows that are not split
 };
 
-extern "C" int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
-                                              int value_type, const int32_t *rowptr, const int32_t *colind,
-                                              const void *val, jlust_stream_t stream,
-                                              jlust_spmm_plan_t *plan_out)
+static int csr_spmm_plan_create_body(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
+                                     int value_type, const int32_t *rowptr, const int32_t *colind,
+                                     const void *val, jlust_stream_t stream,
+                                     jlust_spmm_plan_t *plan_out)
 {
     clear_error();
     if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmm_plan_create: null plan_out");
@@ -560,6 +560,8 @@ extern "C" int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k, i
     seg_first.push_back((int32_t)seg_lo.size());
     p->nlong = (int64_t)long_rows.size();
     p->nseg = (int64_t)seg_lo.size();
+    std::vector<uint8_t> skip(p->nlong ? (size_t)m : 0, 0);   // host tables before the device allocation
+    for (int32_t r : long_rows) skip[(size_t)r] = 1;
 
     // One allocation: B copy, row flags, segment tables, partial rows.
     const int64_t ldt_max = (min(p->kc, k > 0 ? k : 1) + 3) / 4 * 4;
@@ -579,8 +581,6 @@ extern "C" int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k, i
     if (p->nseg) p->part = b;
     int st = JLUST_STATUS_SUCCESS;
     if (p->nlong) {
-        std::vector<uint8_t> skip((size_t)m, 0);
-        for (int32_t r : long_rows) skip[(size_t)r] = 1;
         hipError_t e = hipMemcpyAsync(p->row_skip, skip.data(), (size_t)m, hipMemcpyHostToDevice, s);
         if (e == hipSuccess)
             e = hipMemcpyAsync(p->long_rows, long_rows.data(), sizeof(int32_t) * long_rows.size(),
@@ -602,6 +602,17 @@ extern "C" int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k, i
     }
     *plan_out = p.release();
     return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
+                                              int value_type, const int32_t *rowptr, const int32_t *colind,
+                                              const void *val, jlust_stream_t stream,
+                                              jlust_spmm_plan_t *plan_out)
+{
+    return jlust::host_guard("csr_spmm_plan_create", [&] {
+        return csr_spmm_plan_create_body(m, n, k, nnz, origin, value_type, rowptr, colind, val, stream,
+                                         plan_out);
+    });
 }
 
 extern "C" int jlust_hip_csr_spmm_plan_update_values(jlust_spmm_plan_t plan, const void *val)

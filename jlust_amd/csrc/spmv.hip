@@ -1281,10 +1281,10 @@ static int plan_build_sliced(jlust_spmv_plan *p, jlust_stream_t stream)
     return JLUST_STATUS_SUCCESS;
 }
 
-extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz, int32_t origin,
-                                              int value_type, const int32_t *rowptr,
-                                              const int32_t *colind, const void *val,
-                                              jlust_stream_t stream, jlust_spmv_plan_t *plan_out)
+static int csr_spmv_plan_create_body(int64_t m, int64_t n, int64_t nnz, int32_t origin,
+                                     int value_type, const int32_t *rowptr,
+                                     const int32_t *colind, const void *val,
+                                     jlust_stream_t stream, jlust_spmv_plan_t *plan_out)
 {
     clear_error();
     if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_create: null plan_out");
@@ -1389,6 +1389,17 @@ extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
     }
     *plan_out = p;
     return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz, int32_t origin,
+                                              int value_type, const int32_t *rowptr,
+                                              const int32_t *colind, const void *val,
+                                              jlust_stream_t stream, jlust_spmv_plan_t *plan_out)
+{
+    return jlust::host_guard("csr_spmv_plan_create", [&] {
+        return csr_spmv_plan_create_body(m, n, nnz, origin, value_type, rowptr, colind, val, stream,
+                                         plan_out);
+    });
 }
 
 namespace jlust {
