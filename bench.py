@@ -79,6 +79,9 @@ def parse():
     p.add_argument("--spmv-parts", action="store_true",
                    help="config 1's SpMV step taken apart: with its x gathers, with a coalesced x "
                         "read in their place, without x, y only (bench_probes.hip)")
+    p.add_argument("--bsr-f64", action="store_true",
+                   help="config 5's BSR pattern in Float64: the fp64 MFMA kernel against the CSR "
+                        "expansion path")
     p.add_argument("--gather-overlap", action="store_true",
                    help="only time config 3's chunk gathers alone, a 256 MB transpose alone, and the "
                         "two on two streams at once")
@@ -514,6 +517,50 @@ def spmv_parts():
     gathers = best[0] - best[1]
     res.append({"gathers_us": round(gathers, 3), "gathers": nnz,
                 "gathers_per_s": round(nnz / (gathers * 1e-6) / 1e9, 1)})
+    return res
+
+
+def bsr_f64():
+    """Config 5's banded BSR pattern (65,536 block-rows of 16 x 16 blocks,
+    8 per block-row within +-32, k = 256) in Float64: the fp64 MFMA kernel
+    (jlust_hip_bsr_spmm_f64_i32) against the same product through the
+    device CSR expansion and the CSR SpMM, which is how Float64 BSR ran before
+    that kernel.  HIP events over 10 calls after 2 warm-up calls."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    from jlust_amd.hip_backend import _bsr_as_csr
+    cfg = W.make(5)
+    mb, nb, k = cfg["mb"], cfg["nb"], cfg["B"].shape[1]
+    A = J.bsr_tensor(dev(cfg["browptr"]), dev(cfg["bcolind"]), dev(cfg["val"].astype(np.float64)),
+                     (mb * 16, nb * 16), (16, 16))
+    B = dev(np.asfortranarray(cfg["B"].astype(np.float64)))
+    del cfg
+    C = J.dense_matrix(mb * 16, k, dtype=torch.float64)
+    flops = 2.0 * 16 * 16 * k * int(A.crd_buffers[1].numel())
+    stream = torch.cuda.current_stream()
+
+    def ms(fn, reps=10):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / reps
+
+    t_mfma = ms(lambda: J.execute(J.SpMMOp, A, B, C))
+    Acsr = _bsr_as_csr(A)
+    t_csr = ms(lambda: J.execute(J.SpMMOp, Acsr, B, C), reps=3)
+    res = {"workload": "bsr16_spmm_f64_banded_65536x8_k256", "flops": flops,
+           "mfma_ms": round(t_mfma, 4), "mfma_tflops": round(flops / (t_mfma * 1e-3) / 1e12, 2),
+           "mfma_pct_of_fp64_peak": round(100 * flops / (t_mfma * 1e-3) / 78.6e12, 1),
+           "csr_expansion_ms": round(t_csr, 3),
+           "csr_expansion_tflops": round(flops / (t_csr * 1e-3) / 1e12, 2)}
+    log(f"bsr f64: {res}")
     return res
 
 
@@ -1311,6 +1358,9 @@ def main():
         return
     if args.gather_cpol:
         print(json.dumps({"gather_cpol": gather_cpol()}), flush=True)
+        return
+    if args.bsr_f64:
+        print(json.dumps({"bsr_f64": bsr_f64()}), flush=True)
         return
     if args.spmv_parts:
         print(json.dumps({"spmv_parts": spmv_parts()}), flush=True)

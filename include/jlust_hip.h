@@ -520,6 +520,16 @@ int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs,
                                int64_t k, float alpha, const float *B,
                                int64_t ldb, float beta, float *C, int64_t ldc,
                                jlust_stream_t stream);
+/* The same for Float64 values on the fp64 matrix cores (16 x 16 blocks; any
+ * alignment, element access where values, B or C are not 32-byte aligned or
+ * ldb, ldc are not multiples of 4).  Same reference operator as above. */
+int jlust_hip_bsr_spmm_f64_i32(int64_t mb, int64_t nb, int64_t bs,
+                               int64_t nnzb, int32_t origin,
+                               const int32_t *browptr, const int32_t *bcolind,
+                               const double *val, int row_major_blocks,
+                               int64_t k, double alpha, const double *B,
+                               int64_t ldb, double beta, double *C, int64_t ldc,
+                               jlust_stream_t stream);
 
 /*
  * BSR of any b1 x b2 block shape and value type, expanded to CSR for the CSR
@@ -548,9 +558,9 @@ int jlust_hip_bsr_expand_csr_i32(int64_t mb, int64_t b1, int64_t b2,
  * Prepared BSR SpMM, the BSR analyse handle (the cuSPARSE SpMM handle
  * contract, ext/CUDAExt/ops/spmm.jl:8-70: analysis and workspace once,
  * execute many times, update_values! for new values of the same pattern).
- * 16 x 16 Float32 blocks (16-byte aligned values for BSRRight) keep the MFMA
- * kernels and read the caller's buffers in place.  Any other b1 x b2 shape,
- * or Float64, is expanded to CSR once (jlust_hip_bsr_expand_csr_i32's
+ * 16 x 16 blocks keep the MFMA kernels (fp32, with 16-byte aligned values
+ * for BSRRight, or fp64) and read the caller's buffers in place.  Any other
+ * b1 x b2 shape is expanded to CSR once (jlust_hip_bsr_expand_csr_i32's
  * layout; the plan owns it) and runs through a CSR SpMM plan over it for k
  * columns.  create synchronises `stream` (browptr's ends are read back and
  * the CSR plan analyses its rows); update_values re-expands only the values,

@@ -122,6 +122,107 @@ __global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_mfma_kernel(
     }
 }
 
+// Float64 blocks: the same tiling on the fp64 matrix cores
+// (v_mfma_f64_16x16x4_f64).  Each step takes one double of A and one of B per
+// lane (A row lane % 16, B column lane % 16, contraction index lane / 16, as
+// in the fp32 step) and accumulates a 16 x 16 double tile held as four
+// doubles per lane; but where the fp32 step leaves rows 4g .. 4g+3 in lane
+// (j, g), the fp64 step leaves rows g, g+4, g+8, g+12 (register v: row
+// g + 4v; checked on gfx950 with a one-wave probe).  Lane (i, g) therefore
+// feeds A's row p(i) = 4 (i % 4) + i / 4: the step's output row g + 4v is
+// then A's row 4g + v, and lane (j, g) holds rows 16R + 4g .. +3 of column
+// c0 + j as in the fp32 kernel, one contiguous double4 of C.  The
+// contraction split s = 4g + step is the fp32 kernel's, so lane (i, g) needs
+// V_q[p(i)][4g .. 4g+3] and B[16*bcol + 4g .. +3, c0 + i], 32 contiguous
+// bytes each.  VEC: values, B and C 32-byte aligned and ldb, ldc multiples
+// of 4 (double4 access); otherwise element loads and stores.
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+
+template <bool ROW_MAJOR, bool VEC>
+__global__ __launch_bounds__(64 * BSR_WAVES) void bsr16_spmm_f64_kernel(
+    int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
+    const int32_t *__restrict__ bcolind, const double *__restrict__ val, int64_t k, double alpha,
+    const double *__restrict__ B, int64_t ldb, double beta, int beta_zero, double *__restrict__ C,
+    int64_t ldc)
+{
+    const int64_t per_xcd = (int64_t)gridDim.x / NUM_XCD;
+    const int64_t R = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+    if (R >= mb) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int i = lane & 15;
+    const int g = lane >> 4;
+    const int ar = 4 * (i & 3) + (i >> 2);     // the A row this lane feeds
+    const int64_t q0 = (int64_t)browptr[R] - origin;
+    const int64_t q1 = (int64_t)browptr[R + 1] - origin;
+    const int64_t crow = R * BSR_BS + 4 * g;
+    const doublex4 zero = {0.0, 0.0, 0.0, 0.0};
+
+    for (int64_t pass = 0; pass < k; pass += BSR_PASS) {
+        const int64_t c0 = pass + (int64_t)wave * 16 * BSR_WTILES;
+        if (c0 >= k) continue;
+        doublex4 acc[BSR_WTILES];
+#pragma unroll
+        for (int t = 0; t < BSR_WTILES; ++t) acc[t] = zero;
+
+        for (int64_t q = q0; q < q1; ++q) {
+            const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
+            const double *vb = val + q * (BSR_BS * BSR_BS);
+            doublex4 a;
+            if (ROW_MAJOR && VEC) {
+                a = *reinterpret_cast<const doublex4 *>(vb + ar * BSR_BS + 4 * g);
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    a[u] = ROW_MAJOR ? vb[ar * BSR_BS + 4 * g + u] : vb[(4 * g + u) * BSR_BS + ar];
+            }
+            doublex4 b[BSR_WTILES];
+#pragma unroll
+            for (int t = 0; t < BSR_WTILES; ++t) {
+                const int64_t col = c0 + 16 * t + i;
+                if (col < k) {
+                    const double *src = B + brow + col * ldb;
+                    if (VEC) {
+                        b[t] = *reinterpret_cast<const doublex4 *>(src);
+                    } else {
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) b[t][u] = src[u];
+                    }
+                } else {
+                    b[t] = zero;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int t = 0; t < BSR_WTILES; ++t)
+                    acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], b[t][u], acc[t], 0, 0, 0);
+        }
+#pragma unroll
+        for (int t = 0; t < BSR_WTILES; ++t) {
+            const int64_t col = c0 + 16 * t + i;
+            if (col >= k) continue;
+            double *dst = C + crow + col * ldc;
+            doublex4 out = acc[t] * alpha;
+            if (!beta_zero) {
+                doublex4 old;
+                if (VEC) old = *reinterpret_cast<const doublex4 *>(dst);
+                else
+#pragma unroll
+                    for (int u = 0; u < 4; ++u) old[u] = dst[u];
+                out += beta * old;
+            }
+            if (VEC) {
+                *reinterpret_cast<doublex4 *>(dst) = out;
+            } else {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) dst[u] = out[u];
+            }
+        }
+    }
+}
+
 // Row-wave kernel (row-major blocks, B and C float4-aligned).  One wave owns
 // one block-row.  Column-major B with a large ldb puts every column in its own
 // memory page, so loading B in the MFMA operand layout (16 columns per
@@ -636,8 +737,60 @@ int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
     return check_launch("bsr16_spmm_mfma_kernel");
 }
 
+int bsr_spmm_f64(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
+                 const int32_t *browptr, const int32_t *bcolind, const double *val,
+                 int row_major_blocks, int64_t k, double alpha, const double *B, int64_t ldb,
+                 double beta, double *C, int64_t ldc, jlust_stream_t stream)
+{
+    clear_error();
+    if (mb < 0 || nb < 0 || bs <= 0 || nnzb < 0 || k < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: negative extent or block size");
+    if (bs != BSR_BS)
+        return fail(JLUST_STATUS_UNSUPPORTED_FORMAT,
+                    "bsr_spmm: block size %lld x %lld (the MFMA path supports 16 x 16)",
+                    (long long)bs, (long long)bs);
+    if (mb * bs > INT32_MAX || nb * bs > INT32_MAX || nnzb > INT32_MAX)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: extents exceed the Int32 index range");
+    if (int st = check_origin(origin)) return st;
+    const int64_t mrows = mb * bs, nrows = nb * bs;
+    if (ldb < (nrows > 0 ? nrows : 1) || ldc < (mrows > 0 ? mrows : 1))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "bsr_spmm: leading dimensions too small (ldb=%lld < %lld or ldc=%lld < %lld)",
+                    (long long)ldb, (long long)nrows, (long long)ldc, (long long)mrows);
+    if ((mb > 0 && !browptr) || bad_ptr(bcolind, nnzb) || bad_ptr(val, nnzb) ||
+        bad_ptr(B, (nnzb > 0 && k > 0) ? nrows : 0) || bad_ptr(C, mrows * k))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm: null device pointer");
+    if (int st = require_device(nullptr)) return st;
+    if (mb == 0 || k == 0) return JLUST_STATUS_SUCCESS;
+    const bool vec = (ldb % 4 == 0) && (ldc % 4 == 0) && ((uintptr_t)B % 32 == 0) &&
+                     ((uintptr_t)C % 32 == 0) && ((uintptr_t)val % 32 == 0);
+    const int64_t grid = (mb + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+    hipStream_t s = (hipStream_t)stream;
+    const int bz = beta == 0.0;
+#define JLUST_BSR64_LAUNCH(RM, V)                                                                   \
+    hipLaunchKernelGGL((bsr16_spmm_f64_kernel<RM, V>), dim3((unsigned)grid), dim3(64 * BSR_WAVES), \
+                       0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, bz, C, ldc)
+    if (row_major_blocks && vec) JLUST_BSR64_LAUNCH(true, true);
+    else if (row_major_blocks) JLUST_BSR64_LAUNCH(true, false);
+    else if (vec) JLUST_BSR64_LAUNCH(false, true);
+    else JLUST_BSR64_LAUNCH(false, false);
+#undef JLUST_BSR64_LAUNCH
+    return check_launch("bsr16_spmm_f64_kernel");
+}
+
 }  // namespace
 }  // namespace jlust
+
+extern "C" int jlust_hip_bsr_spmm_f64_i32(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb,
+                                          int32_t origin, const int32_t *browptr,
+                                          const int32_t *bcolind, const double *val,
+                                          int row_major_blocks, int64_t k, double alpha,
+                                          const double *B, int64_t ldb, double beta, double *C,
+                                          int64_t ldc, jlust_stream_t stream)
+{
+    return jlust::bsr_spmm_f64(mb, nb, bs, nnzb, origin, browptr, bcolind, val, row_major_blocks, k,
+                               alpha, B, ldb, beta, C, ldc, stream);
+}
 
 extern "C" int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb,
                                           int32_t origin, const int32_t *browptr,
@@ -720,8 +873,10 @@ static int bsr_spmm_plan_create_body(int64_t mb, int64_t nb, int64_t b1, int64_t
     p->browptr = browptr;
     p->bcolind = bcolind;
     p->val = val;
-    p->mfma = b1 == BSR_BS && b2 == BSR_BS && value_type == 1 &&
-              (!row_major_blocks || (uintptr_t)val % 16 == 0);
+    // 16 x 16 blocks run the MFMA kernels on A's buffers (fp32 row-major
+    // blocks need 16-byte aligned values; fp64 takes any alignment).
+    p->mfma = b1 == BSR_BS && b2 == BSR_BS &&
+              (value_type == 0 || !row_major_blocks || (uintptr_t)val % 16 == 0);
     if (!p->mfma) {
         const size_t tsz = value_type == 0 ? sizeof(double) : sizeof(float);
         const size_t nz = (size_t)(total > 0 ? total : 1);
@@ -765,7 +920,7 @@ extern "C" int jlust_hip_bsr_spmm_plan_update_values(jlust_bsr_plan_t plan, cons
     if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_update_values: null plan");
     const int64_t total = plan->nnzb * plan->b1 * plan->b2;
     if (bad_ptr(val, total)) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_update_values: null values");
-    if (plan->mfma && plan->row_major && (uintptr_t)val % 16 != 0)
+    if (plan->mfma && plan->value_type == 1 && plan->row_major && (uintptr_t)val % 16 != 0)
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_update_values: block values must be 16-byte aligned");
     plan->val = val;
     if (plan->mfma) return JLUST_STATUS_SUCCESS;     // the kernels read the values in place
@@ -800,7 +955,10 @@ extern "C" int jlust_hip_bsr_spmm_plan_execute_f64(jlust_bsr_plan_t plan, double
     if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmm_plan_execute: null plan");
     if (plan->value_type != 0)
         return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE, "bsr_spmm_plan_execute: plan was created for Float32 values");
-    return jlust_hip_csr_spmm_plan_execute_f64(plan->csr, alpha, B, ldb, beta, C, ldc, 0, stream);
+    if (!plan->mfma)
+        return jlust_hip_csr_spmm_plan_execute_f64(plan->csr, alpha, B, ldb, beta, C, ldc, 0, stream);
+    return bsr_spmm_f64(plan->mb, plan->nb, BSR_BS, plan->nnzb, plan->origin, plan->browptr, plan->bcolind,
+                        (const double *)plan->val, plan->row_major, plan->k, alpha, B, ldb, beta, C, ldc, stream);
 }
 
 extern "C" int jlust_hip_bsr_spmm_plan_info(jlust_bsr_plan_t plan, int32_t *path)

@@ -369,13 +369,13 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
         return _dcsr_product(u_A, u_B, u_C, alpha, beta)
     if is_bsr(u_A.format):
         b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
-        if (b1, b2) != (16, 16) or suf != "f32":
-            # Blocks other than 16 x 16, or Float64: the CSR expansion and the
-            # CSR SpMM (the fp32 MFMA kernel serves 16 x 16 only).
+        if (b1, b2) != (16, 16):
+            # Blocks other than 16 x 16: the CSR expansion and the CSR SpMM
+            # (the MFMA kernels serve 16 x 16 blocks only).
             return _spmm(_bsr_as_csr(u_A), u_B, u_C, alpha, beta, skip_empty_rows)
         dev = _check_same_device(browptr, bcolind, nonzeros(u_A), B, C)
         with _on(dev):
-            st = L.jlust_hip_bsr_spmm_f32_i32(
+            st = getattr(L, f"jlust_hip_bsr_spmm_{suf}_i32")(
                 mb, nb, b1, bcolind.numel(), u_A.origin.offset, _ptr(browptr), _ptr(bcolind),
                 _ptr(nonzeros(u_A)), int(row_major), k, float(alpha), _ptr(B), leading_dim(B),
                 float(beta), _ptr(C), leading_dim(C), _stream(dev))
@@ -827,9 +827,9 @@ class HIPBSRSpMMHandle(AbstractKernelHandle):
     """Prepared BSR SpMM (jlust_hip_bsr_spmm_plan_*): prepare(HIPBackend(),
     SpMMOp, A::BSR; n_cols=k) -> execute(h, B, C) -> update_values!(h, A), the
     cuSPARSE SpMM handle contract (ext/CUDAExt/ops/spmm.jl:8-70) for BSR.
-    16 x 16 Float32 blocks run the MFMA kernels on A's buffers; any other
-    block shape, or Float64, is expanded to CSR once and runs through a CSR
-    SpMM plan over the expansion.  A's values are read as they are at the
+    16 x 16 blocks run the MFMA kernels (fp32 or fp64) on A's buffers; any
+    other block shape is expanded to CSR once and runs through a CSR SpMM
+    plan over the expansion.  A's values are read as they are at the
     call: on the expansion path, values written in place through torch since
     the plan last read them (the value tensor's version counter moved) are
     expanded again, in stream order, before the product.  B with another

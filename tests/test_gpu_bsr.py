@@ -209,10 +209,11 @@ def _random_rect_bsr(mb, nb, b1, b2, per_row, seed, dtype, row_major, origin=1, 
 @pytest.mark.parametrize("dtype", [np.float64, np.float32])
 @pytest.mark.parametrize("row_major", [True, False])
 def test_bsr_any_block_shape_spmm_and_spmv(J, O, b1, b2, dtype, row_major):
-    """BSR of any block shape and value type (16 x 16 fp32 excepted, the MFMA
-    path): SpMM and SpMV through the device CSR expansion against the oracle's
-    expansion + CSR path, with alpha/beta; integer data, so the results are
-    exact in both precisions."""
+    """BSR of any block shape and value type (16 x 16 fp32 excepted, tested
+    above): SpMM through the device CSR expansion, or for 16 x 16 fp64 blocks
+    the fp64 MFMA kernel, and SpMV through the expansion, against the
+    oracle's expansion + CSR path, with alpha/beta; integer data, so the
+    results are exact in both precisions."""
     import torch
     if (b1, b2) == (16, 16) and dtype == np.float32:
         pytest.skip("16 x 16 fp32 is the MFMA kernel (tested above)")

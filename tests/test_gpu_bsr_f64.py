@@ -1,0 +1,138 @@
+"""GPU parity of the fp64 16 x 16 BSR SpMM (v_mfma_f64_16x16x4_f64 kernel,
+jlust_hip_bsr_spmm_f64_i32) against the CPU oracle, which expands the BSR
+matrix to CSR bit-exactly and runs the CSR SpMM.  Bar: |C - C_ref| <=
+1e-12 x (|alpha||A||B| + |beta||C0|) elementwise; integer-valued cases are
+compared bit for bit."""
+import numpy as np
+import pytest
+
+from tests._util import assert_within, dev, host
+from tests.test_gpu_bsr import dense_of_bsr, random_bsr
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def J():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import jlust_amd
+    return jlust_amd
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+def _bsr64(J, browptr, bcolind, val, mb, nb, origin=1, row_major=True):
+    return J.bsr_tensor(dev(browptr), dev(bcolind), dev(val), (mb * 16, nb * 16), (16, 16),
+                        row_major_blocks=row_major,
+                        origin=J.OneBased() if origin == 1 else J.ZeroBased())
+
+
+def _run(J, A, B, C0=None, alpha=1.0, beta=0.0):
+    import torch
+    k = B.shape[1]
+    if C0 is None:
+        C = J.dense_matrix(A.extents[0], k, dtype=torch.float64, fill=float("nan"))
+    else:
+        C = dev(np.asfortranarray(C0))
+    J.execute(J.SpMMOp, A, dev(np.asfortranarray(B)), C, alpha=alpha, beta=beta)
+    return host(C)
+
+
+def _check(O, C, browptr, bcolind, val, B, alpha, beta, C0, what, origin=1, row_major=True):
+    ref = O.bsr_spmm(browptr, bcolind, val, 16, B, alpha, beta, C0, origin=origin,
+                     row_major_blocks=row_major)
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16, origin=origin, row_major_blocks=row_major)
+    absref = O.csr_spmm_absref(rp, ci, v, B, alpha, beta, C0, origin=origin)
+    assert_within(C, ref, absref, np.float64, what)
+
+
+@pytest.mark.parametrize("row_major", [True, False])
+def test_bsr_f64_single_block_exact_layout(J, row_major):
+    """One block whose entries make any operand-layout mix-up (row/column
+    swap, contraction-group order, output row groups) change the result;
+    small integers, so every product and sum is exact."""
+    browptr = np.array([1, 2], np.int32)
+    bcolind = np.array([1], np.int32)
+    blk = (np.arange(256) % 7 - 3).astype(np.float64)          # V[r][s] = blk[16r+s]
+    val = blk if row_major else blk.reshape(16, 16).T.reshape(-1).copy()
+    B = np.asfortranarray((np.arange(16 * 48) % 5 - 2).astype(np.float64).reshape(16, 48))
+    C = _run(J, _bsr64(J, browptr, bcolind, val, 1, 1, row_major=row_major), B)
+    np.testing.assert_array_equal(C, blk.reshape(16, 16) @ B)
+
+
+@pytest.mark.parametrize("k", [1, 16, 40, 256, 300])
+@pytest.mark.parametrize("row_major", [True, False])
+def test_bsr_f64_random(J, O, k, row_major):
+    """Random blocks, k across the 16-column tiles and the 256-column passes,
+    alpha/beta; also against the dense product."""
+    mb, nb = 37, 29
+    browptr, bcolind, val32 = random_bsr(mb, nb, 5, seed=k + 7)
+    val = val32.astype(np.float64)
+    rng = np.random.default_rng(k)
+    B = np.asfortranarray(rng.standard_normal((nb * 16, k)))
+    C0 = np.asfortranarray(rng.standard_normal((mb * 16, k)))
+    C = _run(J, _bsr64(J, browptr, bcolind, val, mb, nb, row_major=row_major), B, C0, 1.25, -0.5)
+    _check(O, C, browptr, bcolind, val, B, 1.25, -0.5, C0, f"bsr f64 k={k}", row_major=row_major)
+    D = dense_of_bsr(browptr, bcolind, val, mb, nb, row_major=row_major)
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16, row_major_blocks=row_major)
+    absref = O.csr_spmm_absref(rp, ci, v, B, 1.25, -0.5, C0)
+    assert_within(C, 1.25 * (D @ B) - 0.5 * C0, absref, np.float64, "bsr f64 vs dense")
+
+
+def test_bsr_f64_zero_based_long_and_empty_rows(J, O):
+    """ZeroBased, BSRLeft, block-rows of 0 to 12 blocks (beyond the fp32
+    kernels' 8-block register chunk) with empty ones, beta = 0 and beta != 0."""
+    mb, nb, k = 40, 40, 48
+    rng = np.random.default_rng(3)
+    counts = rng.integers(0, 13, mb)
+    counts[::5] = 0
+    bcols = [np.sort(rng.choice(nb, c, replace=False)) for c in counts]
+    browptr = np.r_[0, np.cumsum(counts)].astype(np.int32)
+    bcolind = np.concatenate(bcols).astype(np.int32)
+    val = rng.standard_normal(bcolind.size * 256)
+    A = _bsr64(J, browptr, bcolind, val, mb, nb, origin=0, row_major=False)
+    B = np.asfortranarray(rng.standard_normal((nb * 16, k)))
+    C0 = np.asfortranarray(rng.standard_normal((mb * 16, k)))
+    for beta in (0.0, 0.75):
+        C = _run(J, A, B, C0 if beta else None, 2.0, beta)
+        _check(O, C, browptr, bcolind, val, B, 2.0, beta, C0 if beta else None,
+               f"BSRLeft ZeroBased beta={beta}", origin=0, row_major=False)
+
+
+def test_bsr_f64_unaligned_operands(J, O):
+    """ldb and ldc not multiples of 4 and block values at an odd offset (8-byte
+    aligned only): the element-access kernel."""
+    import torch
+    mb, nb, k = 9, 11, 24
+    browptr, bcolind, val32 = random_bsr(mb, nb, 3, seed=21)
+    val = val32.astype(np.float64)
+    vbuf = dev(np.r_[0.0, val])
+    vview = vbuf[1:]
+    assert vview.data_ptr() % 32 != 0
+    A = J.bsr_tensor(dev(browptr), dev(bcolind), vview, (mb * 16, nb * 16), (16, 16))
+    Bbig = np.asfortranarray(np.random.default_rng(7).standard_normal((nb * 16 + 1, k)))
+    Bd = dev(Bbig)[: nb * 16]
+    Cbig = torch.full((k, mb * 16 + 3), float("nan"), dtype=torch.float64, device="cuda").t()
+    Cd = Cbig[: mb * 16]
+    from jlust_amd.tensor import leading_dim
+    assert leading_dim(Bd) == nb * 16 + 1 and leading_dim(Cd) == mb * 16 + 3
+    J.execute(J.SpMMOp, A, Bd, Cd)
+    _check(O, host(Cd), browptr, bcolind, val, np.asfortranarray(Bbig[: nb * 16]), 1.0, 0.0, None,
+           "unaligned f64 operands")
+
+
+def test_bsr_f64_banded_scaled(J, O):
+    """Config 5's banded pattern at 1/32 scale (2,048 block-rows, 8 blocks
+    within +-32, k = 256) in Float64."""
+    from jlust_amd import workloads as W
+    cfg = W.make(5, scale=32)
+    val = cfg["val"].astype(np.float64)
+    B = np.asfortranarray(cfg["B"].astype(np.float64))
+    A = _bsr64(J, cfg["browptr"], cfg["bcolind"], val, cfg["mb"], cfg["nb"])
+    C = _run(J, A, B)
+    _check(O, C, cfg["browptr"], cfg["bcolind"], val, B, 1.0, 0.0, None, cfg["name"] + " f64 /32")

@@ -308,7 +308,8 @@ def _rect_bsr(mb, nb, b1, b2, per_row, seed, dtype, row_major, origin=1):
     (16, 16, np.float32, False, "mfma"),
     (4, 8, np.float64, True, "csr_expansion"),
     (3, 5, np.float32, False, "csr_expansion"),
-    (16, 16, np.float64, True, "csr_expansion"),
+    (16, 16, np.float64, True, "mfma"),
+    (16, 16, np.float64, False, "mfma"),
 ])
 def test_bsr_spmm_plan(J, O, b1, b2, dtype, row_major, path):
     """prepare(SpMMOp, A::BSR; n_cols=k): the chosen path, the product
