@@ -532,9 +532,32 @@ int jlust_hip_bsr_spmm_f64_i32(int64_t mb, int64_t nb, int64_t bs,
                                jlust_stream_t stream);
 
 /*
+ * y = alpha*A*x + beta*y for BSR of any b1 x b2 block shape (A (mb*b1) x
+ * (nb*b2), storage as for jlust_hip_bsr_spmm_f32_i32 with bs = b1 x b2
+ * blocks).  The reference's EmitterBackend claims SpMV for every sparse
+ * format (KernelAbstractionsExt.jl:31-37).  Each scalar row sums its entries
+ * in the order of its row in the CSR expansion below.  Block ranges and block
+ * columns are clamped to the stored blocks and to [0, nb), so a malformed
+ * browptr or bcolind gives wrong sums, never an out-of-bounds read; they are
+ * not validated here (the expansion validates browptr's ends).
+ */
+int jlust_hip_bsr_spmv_f64_i32(int64_t mb, int64_t nb, int64_t b1, int64_t b2,
+                               int64_t nnzb, int32_t origin,
+                               const int32_t *browptr, const int32_t *bcolind,
+                               const double *val, int row_major_blocks,
+                               double alpha, const double *x, double beta,
+                               double *y, jlust_stream_t stream);
+int jlust_hip_bsr_spmv_f32_i32(int64_t mb, int64_t nb, int64_t b1, int64_t b2,
+                               int64_t nnzb, int32_t origin,
+                               const int32_t *browptr, const int32_t *bcolind,
+                               const float *val, int row_major_blocks,
+                               float alpha, const float *x, float beta,
+                               float *y, jlust_stream_t stream);
+
+/*
  * BSR of any b1 x b2 block shape and value type, expanded to CSR for the CSR
- * kernels: the route of BSR SpMV, and of BSR SpMM where the MFMA path above does
- * not apply (blocks other than 16 x 16, or Float64).  The reference's
+ * kernels: the route of BSR SpMM where the MFMA path above does not apply
+ * (blocks other than 16 x 16).  The reference's
  * EmitterBackend claims SpMV and SpMM for every sparse format
  * (KernelAbstractionsExt.jl:31-37); its BSR layout is Formats.BSRRight /
  * BSRLeft((b1, b2)) (src/named_formats.jl:106-128).  Scalar row b1*R + r lists, for

@@ -84,6 +84,10 @@ SIGNATURES = {
                                           _P, _I64, _F, _P, _I64, _P]),
     "jlust_hip_bsr_spmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _INT, _I64, _D,
                                           _P, _I64, _D, _P, _I64, _P]),
+    "jlust_hip_bsr_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _INT, _D, _P, _D,
+                                          _P, _P]),
+    "jlust_hip_bsr_spmv_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _INT, _F, _P, _F,
+                                          _P, _P]),
     "jlust_hip_bsr_expand_csr_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _INT, _INT, _P, _P,
                                             _P, _P]),
     "jlust_hip_bsr_spmm_plan_create": (_INT, [_I64, _I64, _I64, _I64, _I64, _I32, _INT, _INT, _P, _P, _P, _I64,

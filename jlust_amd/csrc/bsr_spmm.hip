@@ -560,6 +560,71 @@ bool bsr_strip()
     return !(e && e[0] == '0');
 }
 
+// ------------------------------------------------------------- BSR SpMV
+
+// y = alpha*A*x + beta*y for BSR of any b1 x b2 blocks: one thread per
+// scalar row 16R + r walks the blocks of its block-row in storage order and
+// each block's row r in column order -- the order of the row's entries in the
+// CSR expansion, so the sum is the expanded CSR row's.  x[16 bcol + s] is the
+// same for every thread of a block-row (one broadcast load per wave).  Block
+// ranges are clamped into [0, nnzb) and block columns into [0, nb), so a
+// malformed browptr or bcolind cannot take a read out of bounds.
+template <typename T, bool ROW_MAJOR, bool BZ>
+__global__ __launch_bounds__(256) void bsr_spmv_kernel(int64_t mb, int64_t nb, int64_t b1, int64_t b2,
+                                                      int64_t nnzb, int32_t origin,
+                                                      const int32_t *__restrict__ browptr,
+                                                      const int32_t *__restrict__ bcolind,
+                                                      const T *__restrict__ val, T alpha,
+                                                      const T *__restrict__ x, T beta, T *__restrict__ y)
+{
+    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= mb * b1) return;
+    const int64_t R = row / b1, r = row % b1, bb = b1 * b2;
+    const int64_t q0 = min(max((int64_t)browptr[R] - origin, (int64_t)0), nnzb);
+    const int64_t q1 = min(max((int64_t)browptr[R + 1] - origin, q0), nnzb);
+    T acc = T(0);
+    for (int64_t q = q0; q < q1; ++q) {
+        const int64_t c = min(max((int64_t)bcolind[q] - origin, (int64_t)0), nb - 1) * b2;
+        const T *v = val + q * bb + (ROW_MAJOR ? r * b2 : r);
+        for (int64_t s = 0; s < b2; ++s) acc += v[ROW_MAJOR ? s : s * b1] * x[c + s];
+    }
+    y[row] = BZ ? alpha * acc : alpha * acc + beta * y[row];
+}
+
+template <typename T>
+int bsr_spmv(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
+             const int32_t *browptr, const int32_t *bcolind, const T *val, int row_major_blocks, T alpha,
+             const T *x, T beta, T *y, jlust_stream_t stream)
+{
+    clear_error();
+    if (mb < 0 || nb < 0 || b1 <= 0 || b2 <= 0 || nnzb < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv: negative extent or block size");
+    if (mb * b1 > INT32_MAX || nb * b2 > INT32_MAX || nnzb * b1 * b2 > INT32_MAX)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv: extents exceed the Int32 index range");
+    if (int st = check_origin(origin)) return st;
+    if ((mb > 0 && !browptr) || bad_ptr(bcolind, nnzb) || bad_ptr(val, nnzb * b1 * b2) ||
+        (nnzb > 0 && !x) || bad_ptr(y, mb * b1))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv: null device pointer");
+    if (nnzb > 0 && nb == 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv: blocks stored in a matrix with no columns");
+    if (int st = require_device(nullptr)) return st;
+    const int64_t m = mb * b1;
+    if (m == 0) return JLUST_STATUS_SUCCESS;
+    const dim3 grid((unsigned)((m + 255) / 256));
+    hipStream_t s = (hipStream_t)stream;
+#define JLUST_BSRMV(RM, Z)                                                                             \
+    hipLaunchKernelGGL((bsr_spmv_kernel<T, RM, Z>), grid, dim3(256), 0, s, mb, nb, b1, b2, nnzb, origin, \
+                       browptr, bcolind, val, alpha, x, beta, y)
+    const bool bz = beta == T(0);
+    if (row_major_blocks) {
+        if (bz) JLUST_BSRMV(true, true); else JLUST_BSRMV(true, false);
+    } else {
+        if (bz) JLUST_BSRMV(false, true); else JLUST_BSRMV(false, false);
+    }
+#undef JLUST_BSRMV
+    return check_launch("bsr_spmv_kernel");
+}
+
 // ------------------------------------------------- expansion to CSR
 
 // rowptr of the expansion: scalar row b1*R + r starts after the entries of
@@ -801,6 +866,24 @@ extern "C" int jlust_hip_bsr_spmm_f32_i32(int64_t mb, int64_t nb, int64_t bs, in
 {
     return jlust::bsr_spmm(mb, nb, bs, nnzb, origin, browptr, bcolind, val, row_major_blocks, k,
                            alpha, B, ldb, beta, C, ldc, stream);
+}
+
+extern "C" int jlust_hip_bsr_spmv_f64_i32(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
+                                          int32_t origin, const int32_t *browptr, const int32_t *bcolind,
+                                          const double *val, int row_major_blocks, double alpha,
+                                          const double *x, double beta, double *y, jlust_stream_t stream)
+{
+    return jlust::bsr_spmv<double>(mb, nb, b1, b2, nnzb, origin, browptr, bcolind, val, row_major_blocks,
+                                   alpha, x, beta, y, stream);
+}
+
+extern "C" int jlust_hip_bsr_spmv_f32_i32(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
+                                          int32_t origin, const int32_t *browptr, const int32_t *bcolind,
+                                          const float *val, int row_major_blocks, float alpha,
+                                          const float *x, float beta, float *y, jlust_stream_t stream)
+{
+    return jlust::bsr_spmv<float>(mb, nb, b1, b2, nnzb, origin, browptr, bcolind, val, row_major_blocks,
+                                  alpha, x, beta, y, stream);
 }
 
 extern "C" int jlust_hip_bsr_expand_csr_i32(int64_t mb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,

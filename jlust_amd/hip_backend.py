@@ -196,7 +196,15 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
         _periodic_spmv(u_A, x, y, alpha, beta)
         return u_y
     if is_bsr(u_A.format):
-        _spmv(_bsr_as_csr(u_A), u_x, u_y, alpha, beta)
+        b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
+        _check_values(u_A, nonzeros(u_A).dtype)
+        dev = _check_same_device(browptr, bcolind, nonzeros(u_A), x, y)
+        with _on(dev):
+            st = getattr(L, f"jlust_hip_bsr_spmv_{suf}_i32")(
+                mb, nb, b1, b2, bcolind.numel(), u_A.origin.offset, _ptr(browptr), _ptr(bcolind),
+                _ptr(nonzeros(u_A)), int(row_major), float(alpha), _ptr(x), float(beta), _ptr(y),
+                _stream(dev))
+        _lib.check(st, "bsr_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
         return u_y
     if is_shifted_diag(u_A.format):
         lv = u_A.format.levels[1]

@@ -255,12 +255,13 @@ def test_bsr_expansion_keeps_stored_zeros_and_matches_oracle_arrays(J, O):
 
 
 def test_bsr_expansion_rejects_bad_browptr(J):
-    import torch
+    """The CSR expansion (the SpMM route of 2 x 2 blocks) reads browptr's ends
+    back and rejects a pointer array that does not end at nnzb."""
     bp = dev(np.array([1, 2, 5], np.int32))           # ends at 5, but only 2 blocks are stored
     bc = dev(np.array([1, 2], np.int32))
     A = J.bsr_tensor(bp, bc, dev(np.ones(2 * 4, np.float64)), (4, 4), (2, 2))
     with pytest.raises(J.NonCanonicalStorage):
-        J.execute(J.SpMVOp, A, dev(np.ones(4)), torch.zeros(4, dtype=torch.float64, device="cuda"))
+        J.execute(J.SpMMOp, A, dev(np.asfortranarray(np.ones((4, 3)))), J.dense_matrix(4, 3))
 
 
 @pytest.mark.parametrize("beta", [0.0, -0.5])
@@ -333,3 +334,30 @@ def test_bsr_block_patterns(J, O, case):
         rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
         absref = O.csr_spmm_absref(rp, ci, v, B, 1.5, beta, C0)
         assert_within(C, ref, absref, np.float32, f"{case} beta={beta}")
+
+
+@pytest.mark.parametrize("b1,b2", [(16, 16), (3, 5), (1, 9), (7, 1)])
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+@pytest.mark.parametrize("row_major", [True, False])
+def test_bsr_spmv_direct(J, O, b1, b2, dtype, row_major):
+    """BSR SpMV (jlust_hip_bsr_spmv_*, one thread per scalar row, no
+    expansion): random values, empty block-rows, ZeroBased for BSRLeft,
+    alpha/beta, against the oracle's expansion + CSR SpMV."""
+    import torch
+    mb, nb = 53, 41
+    origin = 1 if row_major else 0
+    bp, bc, flat, _ = _random_rect_bsr(mb, nb, b1, b2, 6, 500 + b1 * 11 + b2, dtype, row_major, origin)
+    rng = np.random.default_rng(b1 + 31 * b2)
+    flat = rng.standard_normal(flat.size).astype(dtype)
+    A = J.bsr_tensor(dev(bp), dev(bc), dev(flat), (mb * b1, nb * b2), (b1, b2), row_major,
+                     J.OneBased() if origin == 1 else J.ZeroBased())
+    x = rng.uniform(-1, 1, nb * b2).astype(dtype)
+    y0 = rng.uniform(-1, 1, mb * b1).astype(dtype)
+    rp, ci, v = O.bsr_to_csr(bp, bc, flat, b1, origin, row_major, b2)
+    for alpha, beta in ((1.0, 0.0), (-0.5, 1.5)):
+        y = dev(y0.copy()) if beta else torch.full((mb * b1,), float("nan"), dtype=A.dtype, device="cuda")
+        J.execute(J.SpMVOp, A, dev(x), y, alpha=alpha, beta=beta)
+        yb = y0 if beta else None
+        ref = O.csr_spmv(rp, ci, v, x, alpha, beta, yb, origin)
+        absref = O.csr_spmv_absref(rp, ci, v, x, alpha, beta, yb, origin)
+        assert_within(host(y), ref, absref, dtype, f"bsr spmv {b1}x{b2} beta={beta}")
