@@ -10,6 +10,10 @@
  *     execute, destroy;
  *   - SpMM of the same A with B = [e1, 2 e2 + e3]: C = [A e1, 2 A e2 + A e3];
  *   - SDDMM over A's pattern with A = I and B = ones: every entry 1;
+ *   - BSR SpMV (fp32, 2 x 2 blocks) of diag([1 2; 3 4], [5 6; 7 8]) times
+ *     ones: [3, 7, 11, 15];
+ *   - BSR SpMM (fp64, one 16 x 16 block V[r][s] = r + s) times B with columns
+ *     1 and s: C[r] = [16 r + 120, 120 r + 1240];
  *   - the error path: origin 2 gives JLUST_STATUS_INDEX_ORIGIN and a message.
  *
  * jlust_c_harness_run(msg, len) returns 0 when every check holds, else the
@@ -50,7 +54,7 @@ static int from_dev(void *h, const void *d, size_t bytes)
 int jlust_c_harness_run(char *msg, size_t len)
 {
     int rc = 0;
-    void *d[16] = {0};
+    void *d[32] = {0};
     int nd = 0;
     jlust_spmv_plan_t plan = NULL;
     snprintf(msg, len, "ok");
@@ -140,6 +144,56 @@ int jlust_c_harness_run(char *msg, size_t len)
         CHECK(st == JLUST_STATUS_SUCCESS, 14, "csr_sddmm: status %d (%s)", st, jlust_hip_last_error());
         CHECK(hipDeviceSynchronize() == hipSuccess && from_dev(cv, dcv, sizeof cv) == 0, 4, "copy back failed");
         for (int i = 0; i < 5; ++i) CHECK(cv[i] == 1, 15, "csr_sddmm: Cval[%d] = %g, want 1", i, cv[i]);
+    }
+
+    /* BSR SpMV, fp32, two 2 x 2 blocks on the diagonal, row-major, 1-based. */
+    {
+        const int32_t bp[3] = {1, 2, 3}, bc[2] = {1, 2};
+        const float bv[8] = {1, 2, 3, 4, 5, 6, 7, 8}, bx[4] = {1, 1, 1, 1};
+        float by[4] = {-1, -1, -1, -1};
+        int32_t *dbp = (int32_t *)to_dev(bp, sizeof bp), *dbc = (int32_t *)to_dev(bc, sizeof bc);
+        float *dbv = (float *)to_dev(bv, sizeof bv), *dbx = (float *)to_dev(bx, sizeof bx),
+              *dby = (float *)to_dev(by, sizeof by);
+        d[nd++] = dbp;
+        d[nd++] = dbc;
+        d[nd++] = dbv;
+        d[nd++] = dbx;
+        d[nd++] = dby;
+        CHECK(dbp && dbc && dbv && dbx && dby, 1, "device allocation failed");
+        int st = jlust_hip_bsr_spmv_f32_i32(2, 2, 2, 2, 2, 1, dbp, dbc, dbv, 1, 1.0f, dbx, 0.0f, dby, NULL);
+        CHECK(st == JLUST_STATUS_SUCCESS, 18, "bsr_spmv: status %d (%s)", st, jlust_hip_last_error());
+        CHECK(hipDeviceSynchronize() == hipSuccess && from_dev(by, dby, sizeof by) == 0, 4, "copy back failed");
+        CHECK(by[0] == 3 && by[1] == 7 && by[2] == 11 && by[3] == 15, 19,
+              "bsr_spmv: y = [%g, %g, %g, %g], want [3, 7, 11, 15]", by[0], by[1], by[2], by[3]);
+    }
+
+    /* BSR SpMM, fp64 matrix cores: one 16 x 16 block V[r][s] = r + s,
+     * B = [ones, (0..15)] (16 x 2, column-major). */
+    {
+        const int32_t bp[2] = {1, 2}, bc[1] = {1};
+        double bv[256], bB[32], bC[32];
+        for (int r = 0; r < 16; ++r)
+            for (int c = 0; c < 16; ++c) bv[r * 16 + c] = r + c;
+        for (int r = 0; r < 16; ++r) {
+            bB[r] = 1;
+            bB[16 + r] = r;
+        }
+        int32_t *dbp = (int32_t *)to_dev(bp, sizeof bp), *dbc = (int32_t *)to_dev(bc, sizeof bc);
+        double *dbv = (double *)to_dev(bv, sizeof bv), *dbB = (double *)to_dev(bB, sizeof bB),
+               *dbC = (double *)to_dev(bB, sizeof bB);
+        d[nd++] = dbp;
+        d[nd++] = dbc;
+        d[nd++] = dbv;
+        d[nd++] = dbB;
+        d[nd++] = dbC;
+        CHECK(dbp && dbc && dbv && dbB && dbC, 1, "device allocation failed");
+        int st = jlust_hip_bsr_spmm_f64_i32(1, 1, 16, 1, 1, dbp, dbc, dbv, 1, 2, 1.0, dbB, 16, 0.0, dbC, 16, NULL);
+        CHECK(st == JLUST_STATUS_SUCCESS, 20, "bsr_spmm_f64: status %d (%s)", st, jlust_hip_last_error());
+        CHECK(hipDeviceSynchronize() == hipSuccess && from_dev(bC, dbC, sizeof bC) == 0, 4, "copy back failed");
+        for (int r = 0; r < 16; ++r)
+            CHECK(bC[r] == 16.0 * r + 120 && bC[16 + r] == 120.0 * r + 1240, 21,
+                  "bsr_spmm_f64: C[%d] = [%g, %g], want [%g, %g]", r, bC[r], bC[16 + r], 16.0 * r + 120,
+                  120.0 * r + 1240);
     }
 
     /* Error path: origin 2 is neither 0 nor 1. */
