@@ -27,6 +27,19 @@
 #include <cstdlib>
 #include <memory>
 
+// Raw buffer intrinsics (MUBUF with a 128-bit resource in SGPRs), bound to
+// the LLVM intrinsics by name; declared at file scope, since a declaration
+// with internal linkage would have to be defined.
+typedef __attribute__((address_space(3))) void bsr_lds_void;
+typedef int bsr_int32x4 __attribute__((ext_vector_type(4)));
+typedef float bsr_floatx4 __attribute__((ext_vector_type(4)));
+__device__ void raw_buffer_load_lds(bsr_int32x4 rsrc, bsr_lds_void *lds, int size, int voffset, int soffset,
+                                    int offset, int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ void raw_buffer_store_v4f32(bsr_floatx4 data, bsr_int32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.store.v4f32");
+__device__ bsr_floatx4 raw_buffer_load_v4f32(bsr_int32x4 rsrc, int voffset, int soffset, int aux)
+    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+
 namespace jlust {
 namespace {
 
@@ -360,16 +373,8 @@ constexpr int BSR_WMAX = BSR_SR + 64;             // window block-rows (a +-32 b
 constexpr int BSR_CS = BSR_WMAX * 64 + 32;        // LDS bytes per column of a window
 constexpr int BSR_BUF = 16 * BSR_CS;              // the window buffer
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef int int32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer intrinsics (MUBUF with a 128-bit resource in SGPRs).
-__device__ void raw_buffer_load_lds(int32x4 rsrc, lds_void *lds, int size, int voffset, int soffset, int offset,
-                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
-__device__ void raw_buffer_store_v4f32(floatx4 data, int32x4 rsrc, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.store.v4f32");
-__device__ floatx4 raw_buffer_load_v4f32(int32x4 rsrc, int voffset, int soffset, int aux)
-    __asm("llvm.amdgcn.raw.buffer.load.v4f32");
+typedef bsr_lds_void lds_void;
+typedef bsr_int32x4 int32x4;
 
 // A buffer resource over [p, p + 4 GB): base address, stride 0, no range
 // limit, the gfx9 default format word.
