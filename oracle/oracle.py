@@ -18,7 +18,10 @@ import subprocess
 import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-_LIBPATH = os.path.join(_HERE, "libjlust_oracle.so")
+# JLUST_ORACLE_LIB points the loader at another build of jlust_cpu.c, such as
+# the AddressSanitizer one (`make -C oracle asan`; run with the sanitizer's
+# runtime in LD_PRELOAD).
+_LIBPATH = os.environ.get("JLUST_ORACLE_LIB") or os.path.join(_HERE, "libjlust_oracle.so")
 _lib = None
 
 _P = ctypes.c_void_p
