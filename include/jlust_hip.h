@@ -46,7 +46,7 @@
 extern "C" {
 #endif
 
-#define JLUST_HIP_ABI_VERSION 1
+#define JLUST_HIP_ABI_VERSION 2
 
 typedef void *jlust_stream_t;                 /* hipStream_t */
 typedef struct jlust_spmv_plan *jlust_spmv_plan_t;
@@ -80,7 +80,9 @@ enum jlust_status {
 
 /* ---------------------------------------------------------------- library */
 
-/* ABI version (JLUST_HIP_ABI_VERSION of the build). */
+/* ABI version (JLUST_HIP_ABI_VERSION of the build).  Version 2: the
+ * update_values entry points of the SpMV and SpMM plans take a stream and
+ * are stream-ordered. */
 int jlust_hip_version(void);
 
 /* Message of the last failing call on this thread ("" if none). */
@@ -100,6 +102,54 @@ int jlust_hip_device_arch(char *buf, size_t len);
 int jlust_hip_check_csr(int64_t m, int64_t n, int64_t nnz, int32_t origin,
                         const int32_t *rowptr_host, const int32_t *colind_host,
                         int require_sorted);
+
+/*
+ * Device-side checks of index arrays already on the GPU (the same opt-in deep
+ * checks beside validate_storage, src/backends.jl:309-316; no counterpart in
+ * the reference's kernels).  check_pos: pos[nouter+1] starts at origin, ends
+ * at nnz + origin and never decreases (a CSR rowptr, CSC colptr, DCSR or BSR
+ * segment pointer).  check_crd: len coordinates within [origin, extent +
+ * origin), strictly increasing when strictly_increasing != 0 (a DCSR's stored
+ * rows).  Either returns JLUST_STATUS_NONCANONICAL_STORAGE on a violation.
+ * Synchronises `stream` (one flag word read back).
+ */
+int jlust_hip_check_pos_i32(int64_t nouter, int64_t nnz, int32_t origin,
+                            const int32_t *pos, jlust_stream_t stream);
+int jlust_hip_check_crd_i32(int64_t len, int64_t extent, int32_t origin,
+                            int strictly_increasing, const int32_t *crd,
+                            jlust_stream_t stream);
+
+/*
+ * Index passes of the COO/CSC operators (no counterpart in the reference's
+ * interface; the steps its scatter and atomic paths avoid by adding in place,
+ * ext/KernelAbstractionsExt/ops/spmm.jl:412-416):
+ *  - expand_pos: crd_out[p] = the outer coordinate of entry p --
+ *    outer_crd[s] for the segment s of pos holding p, or s + origin when
+ *    outer_crd is NULL (a CSC colptr into one column per entry).  pos is
+ *    checked as by check_pos first (synchronises `stream`).
+ *  - row_order: the row order of COO (format JLUST_FORMAT_COO, idx1 = rows,
+ *    idx2 = cols) or CSC (JLUST_FORMAT_CSC, idx1 = colptr[n+1], idx2 =
+ *    rowind) entries: rowptr[m+1] (origin-based) always; perm[q] = the source
+ *    position of row-ordered entry q (a stable order: ties keep storage
+ *    order) and cols[q] = its column, with *reordered = 1, unless the COO rows
+ *    were already non-decreasing (*reordered = 0, perm and cols untouched).
+ *    Caller-owned outputs: rowptr m+1, perm and cols nnz entries.
+ *    Synchronises `stream`.
+ *  - gather: dst[i] = src[perm[i]], i < n (values into a row order), on
+ *    `stream`.
+ */
+int jlust_hip_expand_pos_i32(int64_t nouter, int64_t nnz, int32_t origin,
+                             const int32_t *pos, const int32_t *outer_crd,
+                             int32_t *crd_out, jlust_stream_t stream);
+int jlust_hip_row_order_i32(int32_t format, int64_t m, int64_t n, int64_t nnz,
+                            int32_t origin, const int32_t *idx1,
+                            const int32_t *idx2, int32_t *rowptr,
+                            int32_t *perm, int32_t *cols, int32_t *reordered,
+                            jlust_stream_t stream);
+int jlust_hip_gather_f64(int64_t n, const int32_t *perm, const double *src,
+                         double *dst, jlust_stream_t stream);
+int jlust_hip_gather_f32(int64_t n, const int32_t *perm, const float *src,
+                         float *dst, jlust_stream_t stream);
 
 /* ----------------------------------------------------------------- SpMV */
 
@@ -157,7 +207,8 @@ int jlust_hip_csr_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
                                    jlust_stream_t stream,
                                    jlust_spmv_plan_t *plan_out);
 int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan,
-                                          const void *val);
+                                          const void *val,
+                                          jlust_stream_t stream);
 int jlust_hip_csr_spmv_plan_execute_f64(jlust_spmv_plan_t plan, double alpha,
                                         const double *x, double beta,
                                         double *y, jlust_stream_t stream);
@@ -181,10 +232,13 @@ int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan);
  * are when the call's work runs on `stream`, whatever the plan kind: a copy
  * is refreshed on `stream` before the product (one gather of the values
  * through the stored permutation), and `val` becomes the plan's values for
- * later executes.  update_values does the same refresh but orders it against
- * every stream of the device (it synchronises the device twice).
- * Executes of one plan on different streams must be ordered by the caller:
- * they share the plan's partial sums and value copy.
+ * later executes.  update_values makes `val` the plan's values with the same
+ * refresh enqueued on `stream` and no product, like the reference's
+ * descriptor swap (ext/CUDAExt/ops/spmv.jl:40-43): nothing is waited for on
+ * the host or on other streams, and executes ordered after it on `stream`
+ * see the new values.  Executes and updates of one plan on different streams
+ * must be ordered by the caller: they share the plan's partial sums and
+ * value copy.
  */
 int jlust_hip_csr_spmv_plan_execute_values_f64(jlust_spmv_plan_t plan,
                                                const double *val, double alpha,
@@ -385,8 +439,10 @@ int jlust_hip_csr_spmm_f32_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
  * allocates nothing.  Results equal jlust_hip_csr_spmm_* bit for bit on rows
  * that are not split, and are deterministic run to run.  The plan records
  * rowptr, colind and val (read in place at each execute: values stored into
- * val are seen); update_values points it at another value buffer.
- * value_type: 0 = f64, 1 = f32.  Synchronises `stream` (the row analysis
+ * val are seen); update_values points it at another value buffer (a plan of
+ * jlust_hip_coo_spmm_plan_create whose entries were reordered gathers the
+ * values into its row order on `stream` instead; executes ordered after it
+ * on `stream` see them).  value_type: 0 = f64, 1 = f32.  Synchronises `stream` (the row analysis
  * reads rowptr on the host).  Executes of one plan must not overlap in time.
  */
 int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k,
@@ -396,7 +452,8 @@ int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k,
                                    jlust_stream_t stream,
                                    jlust_spmm_plan_t *plan_out);
 int jlust_hip_csr_spmm_plan_update_values(jlust_spmm_plan_t plan,
-                                          const void *val);
+                                          const void *val,
+                                          jlust_stream_t stream);
 int jlust_hip_csr_spmm_plan_execute_f64(jlust_spmm_plan_t plan, double alpha,
                                         const double *B, int64_t ldb,
                                         double beta, double *C, int64_t ldc,
@@ -408,11 +465,74 @@ int jlust_hip_csr_spmm_plan_execute_f32(jlust_spmm_plan_t plan, float alpha,
                                         int skip_empty_rows,
                                         jlust_stream_t stream);
 /* What the analysis found (no counterpart in the reference; diagnostics):
- * rows split into segments, segments, columns per pass. */
+ * rows split into segments, segments, columns per pass, and whether the
+ * entries of a COO/CSC plan were reordered (the plan then holds a copy of the
+ * values in its row order). */
 int jlust_hip_csr_spmm_plan_info(jlust_spmm_plan_t plan, int64_t *split_rows,
-                                 int64_t *segments, int64_t *cols_per_pass);
+                                 int64_t *segments, int64_t *cols_per_pass,
+                                 int32_t *reordered);
 /* Drains the device, then frees the plan's workspace. */
 int jlust_hip_csr_spmm_plan_destroy(jlust_spmm_plan_t plan);
+
+/*
+ * SpMM with a COO A (idx1 = rows[nnz], idx2 = cols[nnz], rows in any order)
+ * or a CSC A (idx1 = colptr[n+1], idx2 = rowind[nnz]): C = alpha*A*B +
+ * beta*C with B n x k (ldb), C m x k (ldc), column-major; beta == 0 makes C
+ * write-only.  The reference runs COO as ColFirst and CSC in the walker's
+ * scatter direction, pre-scaling C by beta and adding alpha*val*B[col, :]
+ * into C[row, :] with atomics (execute(::EmitterBackend, ::Op{:SpMM}),
+ * ext/KernelAbstractionsExt/ops/spmm.jl:331-335, 412-416).  Here the entries
+ * are put in row order (a stable sort, only for COO rows that are not already
+ * non-decreasing; always for CSC) into temporaries and the CSR SpMM runs on
+ * them: each output is summed in one fixed order, so the result is the
+ * same product, deterministic run to run.  A COO row outside [origin,
+ * m + origin) or a CSC colptr that is not canonical is NONCANONICAL_STORAGE.
+ * Synchronises `stream` (the analysis reads flags on the host and the
+ * temporaries are freed on return).
+ */
+int jlust_hip_coo_spmm_f64_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                               int32_t origin, const int32_t *rows,
+                               const int32_t *cols, const double *val,
+                               double alpha, const double *B, int64_t ldb,
+                               double beta, double *C, int64_t ldc,
+                               jlust_stream_t stream);
+int jlust_hip_coo_spmm_f32_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                               int32_t origin, const int32_t *rows,
+                               const int32_t *cols, const float *val,
+                               float alpha, const float *B, int64_t ldb,
+                               float beta, float *C, int64_t ldc,
+                               jlust_stream_t stream);
+int jlust_hip_csc_spmm_f64_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                               int32_t origin, const int32_t *colptr,
+                               const int32_t *rowind, const double *val,
+                               double alpha, const double *B, int64_t ldb,
+                               double beta, double *C, int64_t ldc,
+                               jlust_stream_t stream);
+int jlust_hip_csc_spmm_f32_i32(int64_t m, int64_t n, int64_t k, int64_t nnz,
+                               int32_t origin, const int32_t *colptr,
+                               const int32_t *rowind, const float *val,
+                               float alpha, const float *B, int64_t ldb,
+                               float beta, float *C, int64_t ldc,
+                               jlust_stream_t stream);
+
+/*
+ * Prepared COO or CSC SpMM (format JLUST_FORMAT_COO: idx1 = rows, idx2 =
+ * cols; JLUST_FORMAT_CSC: idx1 = colptr, idx2 = rowind): the row order of the
+ * entries once, into memory the plan owns, then a CSR SpMM plan over it --
+ * the cuSPARSE SpMM handle contract (ext/CUDAExt/ops/spmm.jl:8-70) for the
+ * formats the reference's SpMM takes (spmm.jl:412-416).  Returns a plan of
+ * the jlust_hip_csr_spmm_plan_{execute,update_values,info,destroy} entry
+ * points; update_values takes values in the caller's storage order and, when
+ * the entries were reordered, gathers them into the plan's order on its
+ * stream.  When COO rows were already non-decreasing the plan keeps `idx2`
+ * and `val` by pointer (they must outlive it).  Synchronises `stream`.
+ */
+int jlust_hip_coo_spmm_plan_create(int32_t format, int64_t m, int64_t n,
+                                   int64_t k, int64_t nnz, int32_t origin,
+                                   int value_type, const int32_t *idx1,
+                                   const int32_t *idx2, const void *val,
+                                   jlust_stream_t stream,
+                                   jlust_spmm_plan_t *plan_out);
 
 /* ---------------------------------------------------------------- SDDMM */
 
@@ -460,14 +580,65 @@ int jlust_hip_coo_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
                                 const float *mask, jlust_stream_t stream);
 
 /*
+ * SDDMM with a DCSR mask (rows[nout] stored rows, increasing; pos[nout+1];
+ * cols[nnz]; src/named_formats.jl:27): the reference's walker with the
+ * compressed outer level binding the stored row (execute(::EmitterBackend,
+ * ::Op{:SDDMM}), ext/KernelAbstractionsExt/ops/sddmm.jl:49-65, outer walk
+ * _walker.jl:323-392).  The CSR kernel runs over the stored rows, reading A's
+ * row rows[r] for stored row r (clamped into [0, m)); outputs in the mask's
+ * storage order.  Rows that are not stored have no outputs.
+ */
+int jlust_hip_dcsr_sddmm_f64_i32(int64_t m, int64_t n, int64_t K, int64_t nout,
+                                 int64_t nnz, int32_t origin,
+                                 const int32_t *rows, const int32_t *pos,
+                                 const int32_t *cols, double alpha,
+                                 const double *A, int64_t lda, const double *B,
+                                 int64_t ldb, double beta, double *Cval,
+                                 const double *mask, jlust_stream_t stream);
+int jlust_hip_dcsr_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nout,
+                                 int64_t nnz, int32_t origin,
+                                 const int32_t *rows, const int32_t *pos,
+                                 const int32_t *cols, float alpha,
+                                 const float *A, int64_t lda, const float *B,
+                                 int64_t ldb, float beta, float *Cval,
+                                 const float *mask, jlust_stream_t stream);
+
+/*
+ * SDDMM with a CSC mask (colptr[n+1], rowind[nnz]): Cval[p] = alpha*dot(A[i,:],
+ * B[:,j]) (*mask[p]) + beta*Cval[p] for the stored entry p at row i = rowind[p]
+ * of column j, in the mask's storage order -- the operator's definition
+ * (C <- alpha*(A*B) o sparsity(C) + beta*C, ext/KernelAbstractionsExt/ops/
+ * sddmm.jl:1-6).  The reference's gather walker binds a CSC mask's outer
+ * level (the column) as the row instead (sddmm.jl:23-30 with _walker.jl:
+ * 271-314), computing dot(A[j,:], B[:,i]); that transposed reading is not
+ * reproduced.  colptr is checked (NONCANONICAL_STORAGE) and expanded into one
+ * column per entry, then the COO-mask kernel runs.  Synchronises `stream`.
+ */
+int jlust_hip_csc_sddmm_f64_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                int32_t origin, const int32_t *colptr,
+                                const int32_t *rowind, double alpha,
+                                const double *A, int64_t lda, const double *B,
+                                int64_t ldb, double beta, double *Cval,
+                                const double *mask, jlust_stream_t stream);
+int jlust_hip_csc_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nnz,
+                                int32_t origin, const int32_t *colptr,
+                                const int32_t *rowind, float alpha,
+                                const float *A, int64_t lda, const float *B,
+                                int64_t ldb, float beta, float *Cval,
+                                const float *mask, jlust_stream_t stream);
+
+/*
  * Prepared SDDMM for a mask pattern C (m x n) and inner dimension K:
  * prepare(backend, SDDMMOp, A, B, C) -> execute(h, A, B, C) ->
  * update_values!(h, C), the cuSPARSE SDDMM handle contract (ext/CUDAExt/ops/
  * sddmm.jl:10-76).  mask_format is JLUST_FORMAT_CSR (idx1 = rowptr[m+1],
- * idx2 = colind[nnz]) or JLUST_FORMAT_COO (idx1 = rows[nnz], idx2 =
- * cols[nnz]).  Analysis once: a COO mask is put in row order (rowptr, the
- * columns and the permutation back to storage order, owned by the plan; a
- * row outside [origin, m + origin) is NONCANONICAL_STORAGE); the row blocks
+ * idx2 = colind[nnz]), JLUST_FORMAT_COO (idx1 = rows[nnz], idx2 =
+ * cols[nnz]) or JLUST_FORMAT_CSC (idx1 = colptr[n+1], idx2 = rowind[nnz],
+ * with the semantics of jlust_hip_csc_sddmm_*); DCSR masks take
+ * jlust_hip_dcsr_sddmm_plan_create.  Analysis once: a COO or CSC mask is put
+ * in row order (rowptr, the columns and the permutation back to storage
+ * order, owned by the plan; a row outside [origin, m + origin) or a CSC
+ * colptr that is not canonical is NONCANONICAL_STORAGE); the row blocks
  * that hold entries become work items of at most 4096 entries, so blocks
  * without entries cost nothing and a block holding a long row is shared by
  * several workgroups.  execute writes Cval (and reads mask) in the mask's
@@ -481,6 +652,15 @@ int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64_t n,
                                 int value_type, const int32_t *idx1,
                                 const int32_t *idx2, jlust_stream_t stream,
                                 jlust_sddmm_plan_t *plan_out);
+/* Prepared SDDMM over a DCSR mask (the arrays of jlust_hip_dcsr_sddmm_*,
+ * kept by pointer): work items over the stored rows, pos checked
+ * (NONCANONICAL_STORAGE).  Used with the plan entry points above. */
+int jlust_hip_dcsr_sddmm_plan_create(int64_t m, int64_t n, int64_t K,
+                                     int64_t nout, int64_t nnz, int32_t origin,
+                                     int value_type, const int32_t *rows,
+                                     const int32_t *pos, const int32_t *cols,
+                                     jlust_stream_t stream,
+                                     jlust_sddmm_plan_t *plan_out);
 int jlust_hip_sddmm_plan_execute_f64(jlust_sddmm_plan_t plan, double alpha,
                                      const double *A, int64_t lda,
                                      const double *B, int64_t ldb, double beta,
@@ -781,6 +961,25 @@ int jlust_hip_shifted_diag_spmv_f64(int64_t m, int64_t n, int64_t shift,
 int jlust_hip_shifted_diag_spmv_f32(int64_t m, int64_t n, int64_t shift,
                                     float val, float alpha, const float *x,
                                     float beta, float *y,
+                                    jlust_stream_t stream);
+
+/*
+ * C = alpha*A*B + beta*C for the same shifted scaled identity A (m x n), B
+ * n x k (ldb), C m x k (ldc), column-major: the SpMM the reference's
+ * EmitterBackend takes for every non-dense A (ext/KernelAbstractionsExt/
+ * KernelAbstractionsExt.jl:35-37), with the nzval-less level's (r + shift,
+ * val) per row (src/backends.jl:223-227).  Rows whose column r + shift does
+ * not exist get alpha*0 + beta*C.  beta == 0 writes C without reading it.
+ */
+int jlust_hip_shifted_diag_spmm_f64(int64_t m, int64_t n, int64_t k,
+                                    int64_t shift, double val, double alpha,
+                                    const double *B, int64_t ldb, double beta,
+                                    double *C, int64_t ldc,
+                                    jlust_stream_t stream);
+int jlust_hip_shifted_diag_spmm_f32(int64_t m, int64_t n, int64_t k,
+                                    int64_t shift, float val, float alpha,
+                                    const float *B, int64_t ldb, float beta,
+                                    float *C, int64_t ldc,
                                     jlust_stream_t stream);
 
 #ifdef __cplusplus

@@ -18,6 +18,8 @@ from . import errors
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libjlust_hip.so")
 
+ABI_VERSION = 2          # JLUST_HIP_ABI_VERSION of include/jlust_hip.h
+
 _P = ctypes.c_void_p
 _I32 = ctypes.c_int32
 _I64 = ctypes.c_int64
@@ -31,13 +33,20 @@ SIGNATURES = {
     "jlust_hip_last_error": (ctypes.c_char_p, []),
     "jlust_hip_device_arch": (_INT, [ctypes.c_char_p, ctypes.c_size_t]),
     "jlust_hip_check_csr": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _INT]),
+    "jlust_hip_check_pos_i32": (_INT, [_I64, _I64, _I32, _P, _P]),
+    "jlust_hip_check_crd_i32": (_INT, [_I64, _I64, _I32, _INT, _P, _P]),
+    "jlust_hip_expand_pos_i32": (_INT, [_I64, _I64, _I32, _P, _P, _P, _P]),
+    "jlust_hip_row_order_i32": (_INT, [_I32, _I64, _I64, _I64, _I32, _P, _P, _P, _P, _P,
+                                       ctypes.POINTER(_I32), _P]),
+    "jlust_hip_gather_f64": (_INT, [_I64, _P, _P, _P, _P]),
+    "jlust_hip_gather_f32": (_INT, [_I64, _P, _P, _P, _P]),
     "jlust_hip_csr_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P, _P]),
     "jlust_hip_csr_spmv_f32_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _F, _P, _P]),
     "jlust_hip_csr_spmv_f64_i32_noalloc": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P,
                                                   _P]),
     "jlust_hip_csr_spmv_plan_create": (_INT, [_I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
                                               ctypes.POINTER(_P)]),
-    "jlust_hip_csr_spmv_plan_update_values": (_INT, [_P, _P]),
+    "jlust_hip_csr_spmv_plan_update_values": (_INT, [_P, _P, _P]),
     "jlust_hip_csr_spmv_plan_execute_f64": (_INT, [_P, _D, _P, _D, _P, _P]),
     "jlust_hip_csr_spmv_plan_execute_f32": (_INT, [_P, _F, _P, _F, _P, _P]),
     "jlust_hip_csr_spmv_plan_destroy": (_INT, [_P]),
@@ -62,18 +71,38 @@ SIGNATURES = {
                                            _I64, _F, _P, _P, _P]),
     "jlust_hip_csr_spmm_plan_create": (_INT, [_I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
                                               ctypes.POINTER(_P)]),
-    "jlust_hip_csr_spmm_plan_update_values": (_INT, [_P, _P]),
+    "jlust_hip_csr_spmm_plan_update_values": (_INT, [_P, _P, _P]),
     "jlust_hip_csr_spmm_plan_execute_f64": (_INT, [_P, _D, _P, _I64, _D, _P, _I64, _INT, _P]),
     "jlust_hip_csr_spmm_plan_execute_f32": (_INT, [_P, _F, _P, _I64, _F, _P, _I64, _INT, _P]),
     "jlust_hip_csr_spmm_plan_info": (_INT, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I64),
-                                            ctypes.POINTER(_I64)]),
+                                            ctypes.POINTER(_I64), ctypes.POINTER(_I32)]),
     "jlust_hip_csr_spmm_plan_destroy": (_INT, [_P]),
+    "jlust_hip_coo_spmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _I64, _D,
+                                          _P, _I64, _P]),
+    "jlust_hip_coo_spmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _I64, _F,
+                                          _P, _I64, _P]),
+    "jlust_hip_csc_spmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _I64, _D,
+                                          _P, _I64, _P]),
+    "jlust_hip_csc_spmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _P, _F, _P, _I64, _F,
+                                          _P, _I64, _P]),
+    "jlust_hip_coo_spmm_plan_create": (_INT, [_I32, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
+                                              ctypes.POINTER(_P)]),
     "jlust_hip_coo_sddmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _D, _P, _I64, _P,
                                            _I64, _D, _P, _P, _P]),
     "jlust_hip_coo_sddmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _F, _P, _I64, _P,
                                            _I64, _F, _P, _P, _P]),
+    "jlust_hip_dcsr_sddmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _D, _P,
+                                            _I64, _P, _I64, _D, _P, _P, _P]),
+    "jlust_hip_dcsr_sddmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I64, _I32, _P, _P, _P, _F, _P,
+                                            _I64, _P, _I64, _F, _P, _P, _P]),
+    "jlust_hip_csc_sddmm_f64_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _D, _P, _I64, _P,
+                                           _I64, _D, _P, _P, _P]),
+    "jlust_hip_csc_sddmm_f32_i32": (_INT, [_I64, _I64, _I64, _I64, _I32, _P, _P, _F, _P, _I64, _P,
+                                           _I64, _F, _P, _P, _P]),
     "jlust_hip_sddmm_plan_create": (_INT, [_I32, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P,
                                            ctypes.POINTER(_P)]),
+    "jlust_hip_dcsr_sddmm_plan_create": (_INT, [_I64, _I64, _I64, _I64, _I64, _I32, _INT, _P, _P, _P,
+                                                _P, ctypes.POINTER(_P)]),
     "jlust_hip_sddmm_plan_execute_f64": (_INT, [_P, _D, _P, _I64, _P, _I64, _D, _P, _P, _P]),
     "jlust_hip_sddmm_plan_execute_f32": (_INT, [_P, _F, _P, _I64, _P, _I64, _F, _P, _P, _P]),
     "jlust_hip_sddmm_plan_info": (_INT, [_P, ctypes.POINTER(_I64), ctypes.POINTER(_I32)]),
@@ -109,6 +138,10 @@ SIGNATURES = {
     "jlust_hip_bbm_periodic_spmv_f32": (_INT, [_I64, _I64, _I64, _I64, _P, _P, _P, _F, _P, _F, _P, _P]),
     "jlust_hip_shifted_diag_spmv_f64": (_INT, [_I64, _I64, _I64, _D, _D, _P, _D, _P, _P]),
     "jlust_hip_shifted_diag_spmv_f32": (_INT, [_I64, _I64, _I64, _F, _F, _P, _F, _P, _P]),
+    "jlust_hip_shifted_diag_spmm_f64": (_INT, [_I64, _I64, _I64, _I64, _D, _D, _P, _I64, _D, _P, _I64,
+                                               _P]),
+    "jlust_hip_shifted_diag_spmm_f32": (_INT, [_I64, _I64, _I64, _I64, _F, _F, _P, _I64, _F, _P, _I64,
+                                               _P]),
     "jlust_hip_apply_fn_f64": (_INT, [_I64, _I32, _D, _D, _P, _D, _D, _P, _P]),
     "jlust_hip_apply_fn_f32": (_INT, [_I64, _I32, _F, _F, _P, _F, _F, _P, _P]),
     "jlust_hip_gather_rows_f64": (_INT, [_I64, _I64, _I32, _P, _I64, _P, _I64, _P, _I64, _P]),
@@ -162,7 +195,7 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
-        if L.jlust_hip_version() != 1:
+        if L.jlust_hip_version() != ABI_VERSION:
             raise RuntimeError("libjlust_hip.so ABI version mismatch")
         _lib = L
     return _lib

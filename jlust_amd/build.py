@@ -24,7 +24,7 @@ WL_LIB = os.path.join(HERE, "libjlust_workloads.so")
 
 HIP_SOURCES = ["capi.hip", "scan.hip", "spmv.hip", "coo_spmv.hip", "spmm.hip", "sddmm.hip",
                "bsr_spmm.hip", "convert.hip", "assemble.hip", "fn.hip", "dcsr.hip", "coo_plan.hip",
-               "periodic.hip", "spmv_binned.hip"]
+               "periodic.hip", "spmv_binned.hip", "coo_csc.hip"]
 
 ARCH = os.environ.get("JLUST_HIP_ARCH", "gfx950")
 

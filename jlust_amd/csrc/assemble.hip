@@ -178,6 +178,42 @@ int shifted_diag_spmv(int64_t m, int64_t n, int64_t shift, T v, T alpha, const T
     return check_launch("shifted_diag_spmv_kernel");
 }
 
+// C = alpha*A*B + beta*C for the shifted diagonal A (m x n, A[r, r + shift] =
+// v where 0 <= r + shift < n), B n x k (ldb), C m x k (ldc): one thread per
+// (row, column) of C, rows fastest, so each column is read and written
+// contiguously.
+template <typename T>
+__global__ __launch_bounds__(AS_BLOCK) void shifted_diag_spmm_kernel(int64_t m, int64_t n, int64_t k,
+                                                                     int64_t shift, T v, T alpha,
+                                                                     const T *__restrict__ B, int64_t ldb, T beta,
+                                                                     T *__restrict__ C, int64_t ldc)
+{
+    const int64_t t = (int64_t)blockIdx.x * AS_BLOCK + threadIdx.x;
+    if (t >= m * k) return;
+    const int64_t r = t % m, col = t / m;
+    const int64_t c = r + shift;
+    const T acc = (c >= 0 && c < n) ? v * B[c + col * ldb] : T(0);
+    T *out = C + r + col * ldc;
+    *out = beta == T(0) ? alpha * acc : alpha * acc + beta * *out;
+}
+
+template <typename T>
+int shifted_diag_spmm(int64_t m, int64_t n, int64_t k, int64_t shift, T v, T alpha, const T *B, int64_t ldb,
+                      T beta, T *C, int64_t ldc, jlust_stream_t stream)
+{
+    clear_error();
+    if (m < 0 || n < 0 || k < 0) return fail(JLUST_STATUS_INVALID_ARGUMENT, "shifted_diag_spmm: negative extents");
+    if (k > 1 && (ldb < (n > 0 ? n : 1) || ldc < (m > 0 ? m : 1)))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "shifted_diag_spmm: leading dimensions too small");
+    if (bad_ptr(B, k > 0 ? n : 0) || bad_ptr(C, m * k))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "shifted_diag_spmm: null device pointer");
+    if (int st = require_device(nullptr)) return st;
+    if (m == 0 || k == 0) return JLUST_STATUS_SUCCESS;
+    hipLaunchKernelGGL((shifted_diag_spmm_kernel<T>), dim3(as_grid(m * k)), dim3(AS_BLOCK), 0,
+                       (hipStream_t)stream, m, n, k, shift, v, alpha, B, ldb, beta, C, ldc);
+    return check_launch("shifted_diag_spmm_kernel");
+}
+
 struct DevMem {
     void *p = nullptr;
     ~DevMem() { if (p) (void)hipFree(p); }
@@ -356,4 +392,18 @@ extern "C" int jlust_hip_shifted_diag_spmv_f32(int64_t m, int64_t n, int64_t shi
                                                const float *x, float beta, float *y, jlust_stream_t stream)
 {
     return shifted_diag_spmv<float>(m, n, shift, val, alpha, x, beta, y, stream);
+}
+
+extern "C" int jlust_hip_shifted_diag_spmm_f64(int64_t m, int64_t n, int64_t k, int64_t shift, double val,
+                                               double alpha, const double *B, int64_t ldb, double beta, double *C,
+                                               int64_t ldc, jlust_stream_t stream)
+{
+    return shifted_diag_spmm<double>(m, n, k, shift, val, alpha, B, ldb, beta, C, ldc, stream);
+}
+
+extern "C" int jlust_hip_shifted_diag_spmm_f32(int64_t m, int64_t n, int64_t k, int64_t shift, float val,
+                                               float alpha, const float *B, int64_t ldb, float beta, float *C,
+                                               int64_t ldc, jlust_stream_t stream)
+{
+    return shifted_diag_spmm<float>(m, n, k, shift, val, alpha, B, ldb, beta, C, ldc, stream);
 }

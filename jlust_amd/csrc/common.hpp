@@ -93,6 +93,30 @@ int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, 
 int coo_row_order(int64_t m, int64_t nnz, int32_t origin, const int32_t *rows, const int32_t *cols,
                   int32_t *rowptr, int32_t *perm, int32_t *cols_out, bool *sorted, hipStream_t s);
 
+// Checks a position array (coo_csc.hip): pos[0] == origin, pos[nouter] ==
+// nnz + origin, non-decreasing; NONCANONICAL_STORAGE otherwise.  Synchronises s.
+int check_pos(const char *who, int64_t nouter, int64_t nnz, int32_t origin, const int32_t *pos, hipStream_t s);
+
+// crd_out[p] = the outer coordinate of entry p (outer[s], or s + origin when
+// outer is null) after check_pos of pos (coo_csc.hip).
+int expand_pos(int64_t nouter, int64_t nnz, int32_t origin, const int32_t *pos, const int32_t *outer,
+               int32_t *crd_out, hipStream_t s);
+
+// Row order of COO (idx1 = rows, idx2 = cols) or CSC (idx1 = colptr, idx2 =
+// rowind) entries (coo_csc.hip): rowptr[m+1]; perm/cols written and
+// *reordered = 1 unless the source order already is the row order.
+int row_order(int32_t format, int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *idx1,
+              const int32_t *idx2, int32_t *rowptr, int32_t *perm, int32_t *cols, int32_t *reordered,
+              hipStream_t s);
+
+// dst[i] = src[perm[i]] for i < nnz (value_type 0 = f64, 1 = f32), on s.
+int perm_gather(int value_type, int64_t nnz, const int32_t *perm, const void *src, void *dst, hipStream_t s);
+
+// Hands a COO/CSC SpMM plan's owned row order to a CSR SpMM plan (spmm.hip):
+// mem is freed with the plan; perm/val_copy (or null) reorder new values on
+// update_values.
+int spmm_plan_adopt_reorder(jlust_spmm_plan_t plan, void *mem, const int32_t *perm, void *val_copy);
+
 // ------------------------------------------------------------ device code
 
 __device__ __forceinline__ int lane_id() { return __lane_id(); }

@@ -134,8 +134,11 @@ __device__ __forceinline__ int64_t csc_col_of(const int32_t *__restrict__ colptr
     return a;
 }
 
+// Memory-safe on a malformed colptr or rowind: the column search stays in
+// [0, n), entries past the end of the last column (colptr[n] - origin < nnz)
+// end the thread, and a row outside [0, m) is skipped.
 template <typename T>
-__global__ __launch_bounds__(COO_BLOCK) void csc_spmv_kernel(int64_t n, int64_t nnz, int32_t origin,
+__global__ __launch_bounds__(COO_BLOCK) void csc_spmv_kernel(int64_t m, int64_t n, int64_t nnz, int32_t origin,
                                                              const int32_t *__restrict__ colptr,
                                                              const int32_t *__restrict__ rowind,
                                                              const T *__restrict__ val, const T *__restrict__ x,
@@ -149,11 +152,15 @@ __global__ __launch_bounds__(COO_BLOCK) void csc_spmv_kernel(int64_t n, int64_t 
     T xc = x[c];
     for (int64_t p = lo; p < hi; ++p) {
         if (p >= cend) {
-            c = csc_col_of(colptr, origin, c + 1, n, p);
-            cend = (int64_t)colptr[c + 1] - origin;
+            while (p >= cend) {
+                if (c + 1 >= n) return;
+                c = csc_col_of(colptr, origin, c + 1, n, p);
+                cend = (int64_t)colptr[c + 1] - origin;
+            }
             xc = x[c];
         }
-        atomicAdd(&y[(int64_t)rowind[p] - origin], (alpha * val[p]) * xc);
+        const int64_t r = (int64_t)rowind[p] - origin;
+        if (r >= 0 && r < m) atomicAdd(&y[r], (alpha * val[p]) * xc);
     }
 }
 
@@ -182,7 +189,7 @@ int csc_spmv(int64_t m, int64_t n, int64_t nnz, int32_t origin, const int32_t *c
     if (nnz > 0) {
         const int64_t per_block = (int64_t)COO_BLOCK * COO_IPT;
         hipLaunchKernelGGL((csc_spmv_kernel<T>), dim3((unsigned)((nnz + per_block - 1) / per_block)),
-                           dim3(COO_BLOCK), 0, s, n, nnz, origin, colptr, rowind, val, x, y, alpha);
+                           dim3(COO_BLOCK), 0, s, m, n, nnz, origin, colptr, rowind, val, x, y, alpha);
         if (int st = check_launch("csc_spmv_kernel")) return st;
     }
     return JLUST_STATUS_SUCCESS;

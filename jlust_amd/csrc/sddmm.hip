@@ -59,7 +59,7 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     const int32_t *__restrict__ colind, T alpha, const T *__restrict__ A, int64_t lda,
     const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval,
     const T *mask, int R, int64_t lds_ld, const int32_t *__restrict__ items, int64_t chunk,
-    const int32_t *__restrict__ perm)
+    const int32_t *__restrict__ perm, const int32_t *__restrict__ rowmap, int64_t a_rows)
 {
     static_assert(KS >= 1 || U == 1, "several nonzeros per group need a fixed step count over K");
     static_assert(KS <= 1 || VECB, "several steps over K need vector loads");
@@ -68,6 +68,7 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     extern __shared__ unsigned char sd_smem[];
     T *s_a = reinterpret_cast<T *>(sd_smem);                       // R x lds_ld
     int32_t *s_rp = reinterpret_cast<int32_t *>(s_a + (int64_t)R * lds_ld);  // R + 1
+    int32_t *s_ar = s_rp + R + 1;            // R: A's row of each pattern row
 
     const int tid = threadIdx.x;
     const int g = tid / G;                   // group in block
@@ -80,10 +81,16 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_kernel(
     const int nr = (int)min((int64_t)R, m - i0);
 
     for (int r = tid; r <= nr; r += SD_BLOCK) s_rp[r] = rowptr[i0 + r] - origin;
+    // A DCSR mask walks its stored rows: pattern row i is A's row rowmap[i]
+    // (clamped into A, so a malformed row index reads no memory outside it).
+    for (int r = tid; r < nr; r += SD_BLOCK)
+        s_ar[r] = rowmap ? (int32_t)min(max((int64_t)rowmap[i0 + r] - origin, (int64_t)0), a_rows - 1)
+                         : (int32_t)(i0 + r);
+    __syncthreads();
     for (int64_t idx = tid; idx < (int64_t)nr * K; idx += SD_BLOCK) {
         const int rr = (int)(idx % nr);
         const int64_t kk = idx / nr;
-        s_a[rr * lds_ld + kk] = A[(i0 + rr) + kk * lda];
+        s_a[rr * lds_ld + kk] = A[(int64_t)s_ar[rr] + kk * lda];
     }
     __syncthreads();
 
@@ -186,16 +193,17 @@ __global__ __launch_bounds__(SD_BLOCK) void csr_sddmm_direct_kernel(
     int64_t m, int64_t K, int32_t origin, const int32_t *__restrict__ rowptr,
     const int32_t *__restrict__ colind, T alpha, const T *__restrict__ A, int64_t lda,
     const T *__restrict__ B, int64_t ldb, T beta, int beta_zero, T *Cval, const T *mask,
-    const int32_t *__restrict__ perm)
+    const int32_t *__restrict__ perm, const int32_t *__restrict__ rowmap, int64_t a_rows)
 {
     const int g = threadIdx.x / SD_GROUP, q = threadIdx.x % SD_GROUP;
     // Rows by grid stride: the grid is capped, so any m launches.
     for (int64_t i = blockIdx.x; i < m; i += gridDim.x) {
         const int64_t lo = (int64_t)rowptr[i] - origin, hi = (int64_t)rowptr[i + 1] - origin;
+        const int64_t ai = rowmap ? min(max((int64_t)rowmap[i] - origin, (int64_t)0), a_rows - 1) : i;
         for (int64_t p = lo + g; p < hi; p += SD_GROUPS) {
             const int64_t j = (int64_t)colind[p] - origin;
             T dot = T(0);
-            for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[i + kk * lda] * B[kk + j * ldb];
+            for (int64_t kk = q; kk < K; kk += SD_GROUP) dot += A[ai + kk * lda] * B[kk + j * ldb];
             dot = group_sum<SD_GROUP>(dot);
             if (q == 0) {
                 const int64_t o = perm ? (int64_t)perm[p] : p;
@@ -239,17 +247,20 @@ int sddmm_rows(int64_t K, int64_t *lds_ld)
 {
     constexpr int N = V16<T>::N;
     *lds_ld = (K + N - 1) / N * N + N;       // padded, keeps rows 16-byte aligned
-    int64_t R = (int64_t)((SD_LDS_BUDGET - 64 * sizeof(int32_t)) / (sizeof(T) * (size_t)*lds_ld));
+    int64_t R = (int64_t)((SD_LDS_BUDGET - 128 * sizeof(int32_t)) / (sizeof(T) * (size_t)*lds_ld));
     return (int)(R > 32 ? 32 : R);
 }
 
-// The SDDMM launch over the CSR pattern (rowptr, colind), plain or from a
-// plan: items/chunk cut row blocks into runs of nonzeros (null: one block per
-// row block), perm maps CSR positions to the output's (null: identity).
+// The SDDMM launch over the CSR pattern (rowptr, colind) of m rows, plain or
+// from a plan: items/chunk cut row blocks into runs of nonzeros (null: one
+// block per row block), perm maps CSR positions to the output's (null:
+// identity), rowmap gives A's row (of a_rows) of each pattern row (null:
+// the same row; a DCSR mask's stored rows otherwise).
 template <typename T>
 int sddmm_launch(int64_t m, int64_t K, int32_t origin, const int32_t *rowptr, const int32_t *colind, T alpha,
                  const T *A, int64_t lda, const T *B, int64_t ldb, T beta, T *Cval, const T *mask,
-                 const int32_t *items, int64_t nitems, int64_t chunk, const int32_t *perm, hipStream_t s)
+                 const int32_t *items, int64_t nitems, int64_t chunk, const int32_t *perm,
+                 const int32_t *rowmap, int64_t a_rows, hipStream_t s)
 {
     const int bz = beta == T(0);
     constexpr int N = V16<T>::N;
@@ -258,18 +269,19 @@ int sddmm_launch(int64_t m, int64_t K, int32_t origin, const int32_t *rowptr, co
     if (R < 1) {
         hipLaunchKernelGGL((csr_sddmm_direct_kernel<T>), dim3((unsigned)std::min<int64_t>(m, SD_GRID_MAX)),
                            dim3(SD_BLOCK), 0, s, m,
-                           K, origin, rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, perm);
+                           K, origin, rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, perm, rowmap,
+                           a_rows);
         return check_launch("csr_sddmm_direct_kernel");
     }
     const bool vecb = (K % N == 0) && (ldb % N == 0) && (((uintptr_t)B) % 16 == 0);
-    const size_t smem = sizeof(T) * (size_t)R * (size_t)lds_ld + sizeof(int32_t) * (size_t)(R + 1);
+    const size_t smem = sizeof(T) * (size_t)R * (size_t)lds_ld + sizeof(int32_t) * (size_t)(2 * R + 1);
     const dim3 grid((unsigned)(items ? nitems : (m + R - 1) / R));
     // Lane loads that cover K: G = the smallest power of two >= that, up to 8.
     const int64_t slices = vecb ? K / N : K;
 #define JLUST_SD(V, G, U, KS)                                                                         \
     hipLaunchKernelGGL((csr_sddmm_kernel<T, V, G, U, KS>), grid, dim3(SD_BLOCK), smem, s, m, K, origin, \
                        rowptr, colind, alpha, A, lda, B, ldb, beta, bz, Cval, mask, R, lds_ld, items,  \
-                       chunk, perm)
+                       chunk, perm, rowmap, a_rows)
 #define JLUST_SD_V(V)                                                                                 \
     do {                                                                                              \
         if (slices == 0) JLUST_SD(V, 8, 1, 0);     /* K = 0: no loads of B at all */                 \
@@ -325,7 +337,28 @@ int csr_sddmm(int64_t m, int64_t n, int64_t K, int64_t nnz, int32_t origin,
     if (int st = require_device(nullptr)) return st;
     if (m == 0 || nnz == 0) return JLUST_STATUS_SUCCESS;
     return sddmm_launch<T>(m, K, origin, rowptr, colind, alpha, A, lda, B, ldb, beta, Cval, mask, nullptr, 0, 0,
-                           nullptr, (hipStream_t)stream);
+                           nullptr, nullptr, m, (hipStream_t)stream);
+}
+
+// DCSR mask: the CSR kernel over the nout stored rows (pos, cols), reading A's
+// row rows[r] for stored row r; outputs in the mask's storage order.
+template <typename T>
+int dcsr_sddmm(int64_t m, int64_t n, int64_t K, int64_t nout, int64_t nnz, int32_t origin, const int32_t *rows,
+               const int32_t *pos, const int32_t *cols, T alpha, const T *A, int64_t lda, const T *B, int64_t ldb,
+               T beta, T *Cval, const T *mask, jlust_stream_t stream)
+{
+    clear_error();
+    if (int st = check_sddmm_extents("dcsr_sddmm", m, n, K, nnz, origin)) return st;
+    if (nout < 0 || nout > m)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "dcsr_sddmm: %lld stored rows in a matrix of %lld rows",
+                    (long long)nout, (long long)m);
+    if (int st = check_sddmm_dense("dcsr_sddmm", m, n, K, nnz, A, lda, B, ldb, Cval)) return st;
+    if (bad_ptr(rows, nout) || (nout > 0 && !pos) || bad_ptr(cols, nnz))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "dcsr_sddmm: null device pointer");
+    if (int st = require_device(nullptr)) return st;
+    if (nout == 0 || nnz == 0) return JLUST_STATUS_SUCCESS;
+    return sddmm_launch<T>(nout, K, origin, pos, cols, alpha, A, lda, B, ldb, beta, Cval, mask, nullptr, 0, 0,
+                           nullptr, rows, m, (hipStream_t)stream);
 }
 
 template <typename T>
@@ -390,6 +423,26 @@ extern "C" int jlust_hip_coo_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int6
     return coo_sddmm<float>(m, n, K, nnz, origin, rows, cols, alpha, A, lda, B, ldb, beta, Cval, mask, stream);
 }
 
+extern "C" int jlust_hip_dcsr_sddmm_f64_i32(int64_t m, int64_t n, int64_t K, int64_t nout, int64_t nnz,
+                                            int32_t origin, const int32_t *rows, const int32_t *pos,
+                                            const int32_t *cols, double alpha, const double *A, int64_t lda,
+                                            const double *B, int64_t ldb, double beta, double *Cval,
+                                            const double *mask, jlust_stream_t stream)
+{
+    return dcsr_sddmm<double>(m, n, K, nout, nnz, origin, rows, pos, cols, alpha, A, lda, B, ldb, beta, Cval,
+                              mask, stream);
+}
+
+extern "C" int jlust_hip_dcsr_sddmm_f32_i32(int64_t m, int64_t n, int64_t K, int64_t nout, int64_t nnz,
+                                            int32_t origin, const int32_t *rows, const int32_t *pos,
+                                            const int32_t *cols, float alpha, const float *A, int64_t lda,
+                                            const float *B, int64_t ldb, float beta, float *Cval,
+                                            const float *mask, jlust_stream_t stream)
+{
+    return dcsr_sddmm<float>(m, n, K, nout, nnz, origin, rows, pos, cols, alpha, A, lda, B, ldb, beta, Cval,
+                             mask, stream);
+}
+
 // ------------------------------------------------------------------- plans
 
 // A prepared SDDMM (the cuSPARSE SDDMM handle contract, ext/CUDAExt/ops/
@@ -404,21 +457,26 @@ constexpr int64_t SD_CHUNK = 4096;
 
 struct jlust_sddmm_plan {
     int64_t m = 0, n = 0, K = 0, nnz = 0;
+    int64_t nrows = 0;                 // pattern rows walked (m; a DCSR mask's stored rows)
     int32_t origin = 0;
     int value_type = 0;
     int device = 0;
-    const int32_t *rowptr = nullptr;   // CSR order: the caller's, or owned (COO)
+    const int32_t *rowptr = nullptr;   // CSR order: the caller's, or owned (COO, CSC)
     const int32_t *colind = nullptr;
     const int32_t *perm = nullptr;     // output position of CSR position q (null: q)
+    const int32_t *rowmap = nullptr;   // A's row of pattern row r (DCSR; null: r)
     int32_t *items = nullptr;          // [2 * nitems] (row block, part)
     int64_t nitems = 0;
     void *mem = nullptr;
 };
 
+// mask_format CSR: idx1 = rowptr, idx2 = colind; COO: idx1 = rows, idx2 =
+// cols; CSC: idx1 = colptr, idx2 = rowind; DCSR: dcsr_rows[nout] with idx1 =
+// pos[nout+1], idx2 = cols.
 static int sddmm_plan_create_body(int32_t mask_format, int64_t m, int64_t n, int64_t K, int64_t nnz,
                                   int32_t origin, int value_type, const int32_t *idx1,
-                                  const int32_t *idx2, jlust_stream_t stream,
-                                  jlust_sddmm_plan_t *plan_out)
+                                  const int32_t *idx2, int64_t nout, const int32_t *dcsr_rows,
+                                  jlust_stream_t stream, jlust_sddmm_plan_t *plan_out)
 {
     clear_error();
     if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: null plan_out");
@@ -426,11 +484,18 @@ static int sddmm_plan_create_body(int32_t mask_format, int64_t m, int64_t n, int
     if (value_type != 0 && value_type != 1)
         return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE,
                     "sddmm_plan_create: value_type %d (0 = Float64, 1 = Float32)", value_type);
-    if (mask_format != JLUST_FORMAT_CSR && mask_format != JLUST_FORMAT_COO)
-        return fail(JLUST_STATUS_UNSUPPORTED_FORMAT, "sddmm_plan_create: the mask must be CSR or COO");
+    if (mask_format != JLUST_FORMAT_CSR && mask_format != JLUST_FORMAT_COO && mask_format != JLUST_FORMAT_CSC &&
+        mask_format != JLUST_FORMAT_DCSR)
+        return fail(JLUST_STATUS_UNSUPPORTED_FORMAT, "sddmm_plan_create: the mask must be CSR, COO, CSC or DCSR");
     if (int st = check_sddmm_extents("sddmm_plan_create", m, n, K, nnz, origin)) return st;
-    const bool coo = mask_format == JLUST_FORMAT_COO;
-    if ((!coo && m > 0 && !idx1) || (coo && bad_ptr(idx1, nnz)) || bad_ptr(idx2, nnz))
+    const bool coo = mask_format == JLUST_FORMAT_COO, csc = mask_format == JLUST_FORMAT_CSC;
+    const bool dcsr = mask_format == JLUST_FORMAT_DCSR;
+    if (dcsr && (nout < 0 || nout > m))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: %lld stored rows in a matrix of %lld rows",
+                    (long long)nout, (long long)m);
+    const int64_t nrows = dcsr ? nout : m;
+    if ((!coo && nrows > 0 && !idx1) || (coo && bad_ptr(idx1, nnz)) || bad_ptr(idx2, nnz) ||
+        (dcsr && bad_ptr(dcsr_rows, nout)))
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: null device pointer");
     if (nnz > 0 && (m == 0 || n == 0))
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: entries in an empty matrix");
@@ -442,55 +507,70 @@ static int sddmm_plan_create_body(int32_t mask_format, int64_t m, int64_t n, int
     p->n = n;
     p->K = K;
     p->nnz = nnz;
+    p->nrows = nrows;
     p->origin = origin;
     p->value_type = value_type;
     p->device = dev;
     p->rowptr = idx1;
     p->colind = idx2;
+    p->rowmap = dcsr ? dcsr_rows : nullptr;
     int64_t lds_ld = 0;
     const int R = value_type == 0 ? sddmm_rows<double>(K, &lds_ld) : sddmm_rows<float>(K, &lds_ld);
-    const int64_t nblk = R >= 1 ? (m + R - 1) / R : 0;
+    const int64_t nblk = R >= 1 ? (nrows + R - 1) / R : 0;
     const size_t nz = (size_t)(nnz > 0 ? nnz : 1);
-    // Owned: [rowptr, perm, columns (COO)], items (at most 2 per block plus
-    // one per SD_CHUNK nonzeros).
-    const size_t sz_rp = coo ? align_up(4 * (size_t)(m + 1), 256) : 0;
-    const size_t sz_i = coo ? align_up(4 * nz, 256) : 0;
+    // Owned: [rowptr, perm, columns (COO, CSC), CSC's column per entry],
+    // items (at most 2 per block plus one per SD_CHUNK nonzeros).
+    const bool reorder = coo || csc;
+    const size_t sz_rp = reorder ? align_up(4 * (size_t)(m + 1), 256) : 0;
+    const size_t sz_i = reorder ? align_up(4 * nz, 256) : 0;
+    const size_t sz_ce = csc ? align_up(4 * nz, 256) : 0;
     const int64_t max_items = nblk + nnz / SD_CHUNK + 1;
     const size_t sz_items = align_up(8 * (size_t)max_items, 256);
     // Host tables before the device allocation (a failed host allocation then
     // leaks nothing): the row pointers and the work items (row block, part).
-    const bool analyse = R >= 1 && m > 0;
-    std::vector<int32_t> rp(analyse ? (size_t)(m + 1) : 0);
+    const bool analyse = R >= 1 && nrows > 0;
+    std::vector<int32_t> rp(analyse ? (size_t)(nrows + 1) : 0);
     std::vector<int32_t> items;
     if (analyse) items.reserve(2 * (size_t)max_items);
-    JLUST_HIP_TRY(hipMalloc(&p->mem, sz_rp + 2 * sz_i + sz_items));
+    JLUST_HIP_TRY(hipMalloc(&p->mem, sz_rp + 2 * sz_i + sz_ce + sz_items));
     char *b = (char *)p->mem;
     int st = JLUST_STATUS_SUCCESS;
-    if (coo) {
+    if (reorder) {
         int32_t *rowptr = (int32_t *)b;
         int32_t *perm = (int32_t *)(b + sz_rp);
         int32_t *cols_s = (int32_t *)(b + sz_rp + sz_i);
+        const int32_t *rows = idx1, *cols = idx2;
+        if (csc) {
+            // The column of every entry: the mask as COO (rowind, column) in storage order.
+            int32_t *ce = (int32_t *)(b + sz_rp + 2 * sz_i);
+            st = expand_pos(n, nnz, origin, idx1, nullptr, ce, s);
+            rows = idx2;
+            cols = ce;
+        }
         bool sorted = true;
-        st = coo_row_order(m, nnz, origin, idx1, idx2, rowptr, perm, cols_s, &sorted, s);
+        if (!st) st = coo_row_order(m, nnz, origin, rows, cols, rowptr, perm, cols_s, &sorted, s);
         p->rowptr = rowptr;
+        p->colind = cols;
         if (!sorted) {
             p->perm = perm;
             p->colind = cols_s;
         }
     }
-    p->items = (int32_t *)(b + sz_rp + 2 * sz_i);
+    p->items = (int32_t *)(b + sz_rp + 2 * sz_i + sz_ce);
     // Work items from the row pointers of each row block (host analysis).
+    if (!st && dcsr && nout > 0)
+        st = check_pos("sddmm_plan_create", nout, nnz, origin, p->rowptr, s);
     if (!st && analyse) {
-        hipError_t e = hipMemcpyAsync(rp.data(), p->rowptr, sizeof(int32_t) * (size_t)(m + 1),
+        hipError_t e = hipMemcpyAsync(rp.data(), p->rowptr, sizeof(int32_t) * (size_t)(nrows + 1),
                                       hipMemcpyDeviceToHost, s);
         if (e == hipSuccess) e = hipStreamSynchronize(s);
         if (e != hipSuccess) st = hip_fail(e, "sddmm_plan_create: rowptr copy");
-        if (!st && ((int64_t)rp[0] != origin || (int64_t)rp[m] - origin != nnz))
+        if (!st && ((int64_t)rp[0] != origin || (int64_t)rp[nrows] - origin != nnz))
             st = fail(JLUST_STATUS_NONCANONICAL_STORAGE,
-                      "sddmm_plan_create: rowptr runs from %d to %d, expected %d to %lld", rp[0], rp[m], origin,
+                      "sddmm_plan_create: rowptr runs from %d to %d, expected %d to %lld", rp[0], rp[nrows], origin,
                       (long long)(nnz + origin));
         for (int64_t rb = 0; !st && rb < nblk; ++rb) {
-            const int64_t r1 = min((rb + 1) * (int64_t)R, m);
+            const int64_t r1 = min((rb + 1) * (int64_t)R, nrows);
             const int64_t cnt = (int64_t)rp[r1] - rp[rb * R];
             if (cnt < 0) {
                 st = fail(JLUST_STATUS_NONCANONICAL_STORAGE, "sddmm_plan_create: rowptr decreases near row %lld",
@@ -527,9 +607,24 @@ extern "C" int jlust_hip_sddmm_plan_create(int32_t mask_format, int64_t m, int64
                                            const int32_t *idx2, jlust_stream_t stream,
                                            jlust_sddmm_plan_t *plan_out)
 {
+    if (mask_format == JLUST_FORMAT_DCSR) {
+        clear_error();
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "sddmm_plan_create: DCSR masks use jlust_hip_dcsr_sddmm_plan_create");
+    }
     return jlust::host_guard("sddmm_plan_create", [&] {
-        return sddmm_plan_create_body(mask_format, m, n, K, nnz, origin, value_type, idx1, idx2, stream,
+        return sddmm_plan_create_body(mask_format, m, n, K, nnz, origin, value_type, idx1, idx2, 0, nullptr, stream,
                                       plan_out);
+    });
+}
+
+extern "C" int jlust_hip_dcsr_sddmm_plan_create(int64_t m, int64_t n, int64_t K, int64_t nout, int64_t nnz,
+                                                int32_t origin, int value_type, const int32_t *rows,
+                                                const int32_t *pos, const int32_t *cols, jlust_stream_t stream,
+                                                jlust_sddmm_plan_t *plan_out)
+{
+    return jlust::host_guard("dcsr_sddmm_plan_create", [&] {
+        return sddmm_plan_create_body(JLUST_FORMAT_DCSR, m, n, K, nnz, origin, value_type, pos, cols, nout, rows,
+                                      stream, plan_out);
     });
 }
 
@@ -548,9 +643,10 @@ static int sddmm_plan_execute(jlust_sddmm_plan_t p, int want_type, T alpha, cons
     if (dev != p->device)
         return fail(JLUST_STATUS_INVALID_ARGUMENT,
                     "sddmm_plan_execute: plan belongs to device %d, current device is %d", p->device, dev);
-    if (p->m == 0 || p->nnz == 0) return JLUST_STATUS_SUCCESS;
-    return sddmm_launch<T>(p->m, p->K, p->origin, p->rowptr, p->colind, alpha, A, lda, B, ldb, beta, Cval, mask,
-                           p->nitems > 0 ? p->items : nullptr, p->nitems, SD_CHUNK, p->perm, (hipStream_t)stream);
+    if (p->nrows == 0 || p->nnz == 0) return JLUST_STATUS_SUCCESS;
+    return sddmm_launch<T>(p->nrows, p->K, p->origin, p->rowptr, p->colind, alpha, A, lda, B, ldb, beta, Cval,
+                           mask, p->nitems > 0 ? p->items : nullptr, p->nitems, SD_CHUNK, p->perm, p->rowmap, p->m,
+                           (hipStream_t)stream);
 }
 
 extern "C" int jlust_hip_sddmm_plan_execute_f64(jlust_sddmm_plan_t plan, double alpha, const double *A,

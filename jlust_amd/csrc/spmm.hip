@@ -500,7 +500,23 @@ struct jlust_spmm_plan {
     int32_t *seg_hi = nullptr;      // [nseg] segment end
     void *part = nullptr;           // nseg x kc partial rows, column-major (ld nseg)
     int64_t nnz_rows = 0;           // entries of the rows that are not split
+    // COO/CSC plans (coo_csc.hip): the row order the plan runs on is owned in
+    // own_mem; perm (null when the source was already in row order) maps its
+    // entries to the caller's, and val_copy holds the values in that order.
+    void *own_mem = nullptr;
+    const int32_t *perm = nullptr;
+    void *val_copy = nullptr;
 };
+
+namespace jlust {
+int spmm_plan_adopt_reorder(jlust_spmm_plan_t plan, void *mem, const int32_t *perm, void *val_copy)
+{
+    plan->own_mem = mem;
+    plan->perm = perm;
+    plan->val_copy = val_copy;
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust
 
 static int csr_spmm_plan_create_body(int64_t m, int64_t n, int64_t k, int64_t nnz, int32_t origin,
                                      int value_type, const int32_t *rowptr, const int32_t *colind,
@@ -615,13 +631,23 @@ extern "C" int jlust_hip_csr_spmm_plan_create(int64_t m, int64_t n, int64_t k, i
     });
 }
 
-extern "C" int jlust_hip_csr_spmm_plan_update_values(jlust_spmm_plan_t plan, const void *val)
+extern "C" int jlust_hip_csr_spmm_plan_update_values(jlust_spmm_plan_t plan, const void *val,
+                                                     jlust_stream_t stream)
 {
     clear_error();
     if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmm_plan_update_values: null plan");
     if (bad_ptr(val, plan->nnz)) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmm_plan_update_values: null values");
-    plan->val = val;        // the kernels read the values in place: nothing to copy
-    return JLUST_STATUS_SUCCESS;
+    if (!plan->perm) {
+        plan->val = val;    // the kernels read the values in place: nothing to copy
+        return JLUST_STATUS_SUCCESS;
+    }
+    // A reordered COO/CSC plan: the values into its row order, on the stream.
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    if (dev != plan->device)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                    "spmm_plan_update_values: plan belongs to device %d, current device is %d", plan->device, dev);
+    return perm_gather(plan->value_type, plan->nnz, plan->perm, val, plan->val_copy, (hipStream_t)stream);
 }
 
 template <typename T>
@@ -682,13 +708,14 @@ extern "C" int jlust_hip_csr_spmm_plan_execute_f32(jlust_spmm_plan_t plan, float
 }
 
 extern "C" int jlust_hip_csr_spmm_plan_info(jlust_spmm_plan_t plan, int64_t *split_rows, int64_t *segments,
-                                            int64_t *cols_per_pass)
+                                            int64_t *cols_per_pass, int32_t *reordered)
 {
     clear_error();
     if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmm_plan_info: null plan");
     if (split_rows) *split_rows = plan->nlong;
     if (segments) *segments = plan->nseg;
     if (cols_per_pass) *cols_per_pass = plan->kc;
+    if (reordered) *reordered = plan->perm != nullptr;
     return JLUST_STATUS_SUCCESS;
 }
 
@@ -698,8 +725,9 @@ extern "C" int jlust_hip_csr_spmm_plan_destroy(jlust_spmm_plan_t plan)
     if (!plan) return JLUST_STATUS_SUCCESS;
     // Work queued on any stream may still read the plan's buffers.
     hipError_t e = hipDeviceSynchronize();
-    if (plan->mem) {
-        const hipError_t e2 = hipFree(plan->mem);
+    for (void *m : {plan->mem, plan->own_mem}) {
+        if (!m) continue;
+        const hipError_t e2 = hipFree(m);
         if (e == hipSuccess) e = e2;
     }
     delete plan;

@@ -1439,21 +1439,25 @@ int plan_refresh(jlust_spmv_plan_t plan, const void *val, hipStream_t s)
 }
 }  // namespace jlust
 
-extern "C" int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan, const void *val)
+extern "C" int jlust_hip_csr_spmv_plan_update_values(jlust_spmv_plan_t plan, const void *val,
+                                                     jlust_stream_t stream)
 {
     clear_error();
     if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_update_values: null plan");
     if (bad_ptr(val, plan->nnz))
         return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_update_values: null values");
-    // Not tied to a stream: the new values are complete once every queued
-    // kernel on the device has finished, the plan's copies are refreshed on
-    // the null stream, and that is waited for, so the caller's next execute
-    // on any stream sees them.
-    const bool copies = plan->coo_perm || plan->binned || plan->sliced;
-    if (copies) JLUST_HIP_TRY(hipDeviceSynchronize());
-    if (int st = plan_refresh(plan, val, 0)) return st;
-    if (copies) JLUST_HIP_TRY(hipDeviceSynchronize());
-    return JLUST_STATUS_SUCCESS;
+    // Stream-ordered, like a descriptor swap followed by work on the stream:
+    // plans that copy the values (COO order, sliced and binned layouts) gather
+    // them on `stream`; nothing waits on the host or on other streams.
+    if (plan->coo_perm || plan->binned || plan->sliced) {
+        int dev = 0;
+        if (int st = require_device(&dev)) return st;
+        if (dev != plan->device)
+            return fail(JLUST_STATUS_INVALID_ARGUMENT,
+                        "spmv_plan_update_values: plan belongs to device %d, current device is %d",
+                        plan->device, dev);
+    }
+    return plan_refresh(plan, val, (hipStream_t)stream);
 }
 
 namespace jlust {

@@ -60,11 +60,13 @@ def _supports(op: Op) -> bool:
             _dense_fmt(f[1]) and \
             _dense_fmt(f[2]) and f[1].ndims == 1 and f[2].ndims == 1
     if op.tag == "SpMM" and len(f) == 3:
-        a_ok = is_csr_shaped(f[0]) or f[0] == Formats.DCSR or is_bsr(f[0])
+        a_ok = (is_csr_shaped(f[0]) or is_coo_shaped(f[0]) or is_csc_shaped(f[0]) or
+                f[0] == Formats.DCSR or is_bsr(f[0]) or is_shifted_diag(f[0]) or is_periodic_csr(f[0]))
         return a_ok and _dense_fmt(f[1]) and _dense_fmt(f[2]) and f[1].ndims == 2 and \
             f[2].ndims == 2
     if op.tag == "SDDMM" and len(f) == 3:
-        return _dense_fmt(f[0]) and _dense_fmt(f[1]) and (is_csr_shaped(f[2]) or is_coo_shaped(f[2]))
+        return _dense_fmt(f[0]) and _dense_fmt(f[1]) and \
+            (is_csr_shaped(f[2]) or is_coo_shaped(f[2]) or is_csc_shaped(f[2]) or f[2] == Formats.DCSR)
     return False
 
 
@@ -101,6 +103,41 @@ def _check_values(u: USTensor, T):
         raise UnsupportedValueType(v.dtype, _BE, f"operands must share the value type {T}")
     if not v.is_contiguous():
         raise NonCanonicalStorage("value buffers must be contiguous")
+
+
+def _checked_once(t: torch.Tensor, key, check):
+    """Run check() (a device-side structural check that raises on bad
+    storage) once per (tensor, key) and torch version of the tensor: an index
+    buffer written in place through torch is checked again, one that is not is
+    checked once.  The record lives on the tensor object."""
+    done = t.__dict__.get("_jlust_checked")
+    if done is not None and done.get(key) == t._version:
+        return
+    check()
+    if done is None:
+        done = t.__dict__["_jlust_checked"] = {}
+    done[key] = t._version
+
+
+def _check_pos_once(u: USTensor, pos: torch.Tensor, nouter: int, nnz_: int, dev):
+    """pos[nouter+1] from the origin to nnz + origin, never decreasing
+    (jlust_hip_check_pos_i32), checked once per version of pos."""
+    def run():
+        with _on(dev):
+            st = _lib.lib().jlust_hip_check_pos_i32(nouter, nnz_, u.origin.offset, _ptr(pos), _stream(dev))
+        _lib.check(st, "check_pos", u.format, _BE)
+    _checked_once(pos, ("pos", nouter, nnz_, u.origin.offset), run)
+
+
+def _check_crd_once(u: USTensor, crd: torch.Tensor, extent: int, strict: bool, dev):
+    """Coordinates within [origin, extent + origin) (strictly increasing when
+    `strict`; jlust_hip_check_crd_i32), checked once per version of crd."""
+    def run():
+        with _on(dev):
+            st = _lib.lib().jlust_hip_check_crd_i32(crd.numel(), extent, u.origin.offset, int(strict),
+                                                     _ptr(crd), _stream(dev))
+        _lib.check(st, "check_crd", u.format, _BE)
+    _checked_once(crd, ("crd", extent, bool(strict), u.origin.offset), run)
 
 
 def _csr_parts(u: USTensor):
@@ -199,6 +236,10 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
         b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
         _check_values(u_A, nonzeros(u_A).dtype)
         dev = _check_same_device(browptr, bcolind, nonzeros(u_A), x, y)
+        # The kernel clamps malformed block pointers into range; they are
+        # rejected here instead, once per version of the index buffers.
+        _check_pos_once(u_A, browptr, mb, bcolind.numel(), dev)
+        _check_crd_once(u_A, bcolind, nb, False, dev)
         with _on(dev):
             st = getattr(L, f"jlust_hip_bsr_spmv_{suf}_i32")(
                 mb, nb, b1, b2, bcolind.numel(), u_A.origin.offset, _ptr(browptr), _ptr(bcolind),
@@ -224,14 +265,9 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
         _lib.check(st, "csr_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
         return u_y
     if is_csc_shaped(u_A.format):
-        colptr, rowind = u_A.pos_buffers[1], u_A.crd_buffers[1]
-        if colptr is None or rowind is None:
-            raise NonCanonicalStorage("CSC: missing level-2 pos/crd buffer")
-        _check_index(u_A, colptr, rowind)
-        if colptr.numel() != n + 1 or rowind.numel() != nnz(u_A):
-            raise NonCanonicalStorage(f"CSC: colptr needs n+1 = {n + 1} entries (got {colptr.numel()}) "
-                                      f"and rowind nnz = {nnz(u_A)} (got {rowind.numel()})")
+        colptr, rowind = _csc_parts(u_A)
         dev = _check_same_device(colptr, rowind, nonzeros(u_A), x, y)
+        _check_pos_once(u_A, colptr, n, nnz(u_A), dev)
         with _on(dev):
             st = getattr(L, f"jlust_hip_csc_spmv_{suf}_i32")(
                 m, n, nnz(u_A), u_A.origin.offset, _ptr(colptr), _ptr(rowind), _ptr(nonzeros(u_A)),
@@ -246,6 +282,31 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
             float(alpha), _ptr(x), float(beta), _ptr(y), _stream(dev))
     _lib.check(st, "coo_spmv", u_A.format, _BE, nonzeros(u_A).dtype)
     return u_y
+
+
+def _csc_parts(u: USTensor):
+    colptr, rowind = u.pos_buffers[1], u.crd_buffers[1]
+    if colptr is None or rowind is None:
+        raise NonCanonicalStorage("CSC: missing level-2 pos/crd buffer")
+    _check_index(u, colptr, rowind)
+    n = u.extents[1]
+    if colptr.numel() != n + 1 or rowind.numel() != nnz(u):
+        raise NonCanonicalStorage(f"CSC: colptr needs n+1 = {n + 1} entries (got {colptr.numel()}) "
+                                  f"and rowind nnz = {nnz(u)} (got {rowind.numel()})")
+    return colptr, rowind
+
+
+def _dcsr_parts(u: USTensor):
+    rows, pos, cols = u.crd_buffers[0], u.pos_buffers[1], u.crd_buffers[1]
+    if rows is None or pos is None or cols is None:
+        raise NonCanonicalStorage("DCSR: missing level buffers")
+    _check_index(u, rows, pos, cols)
+    nout = rows.numel()
+    if pos.numel() != nout + 1 or cols.numel() != nnz(u):
+        raise NonCanonicalStorage(
+            f"DCSR: {nout} stored rows need {nout + 1} segment pointers (got {pos.numel()}) and "
+            f"{nnz(u)} columns (got {cols.numel()})")
+    return rows, pos, cols
 
 
 def _coo_parts(u: USTensor):
@@ -279,15 +340,8 @@ def _dcsr_product(u_A: USTensor, u_X: USTensor, u_Y: USTensor, alpha, beta):
     result, with y[rows] gathered first when beta != 0 and scattered back
     after, so rows that are not stored stay untouched (the walker writes
     stored rows only, spmv.jl:449-502; dcsr.hip)."""
-    rows, pos, cols = u_A.crd_buffers[0], u_A.pos_buffers[1], u_A.crd_buffers[1]
-    if rows is None or pos is None or cols is None:
-        raise NonCanonicalStorage("DCSR: missing level buffers")
-    _check_index(u_A, rows, pos, cols)
+    rows, pos, cols = _dcsr_parts(u_A)
     nout = rows.numel()
-    if pos.numel() != nout + 1 or cols.numel() != nnz(u_A):
-        raise NonCanonicalStorage(
-            f"DCSR: {nout} stored rows need {nout + 1} segment pointers (got {pos.numel()}) and "
-            f"{nnz(u_A)} columns (got {cols.numel()})")
     m, n = u_A.extents
     Y = nonzeros(u_Y)
     dev = _check_same_device(rows, pos, cols, nonzeros(u_A), nonzeros(u_X), Y)
@@ -375,11 +429,45 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
     L = _lib.lib()
     if u_A.format == Formats.DCSR:
         return _dcsr_product(u_A, u_B, u_C, alpha, beta)
+    if is_coo_shaped(u_A.format) or is_csc_shaped(u_A.format):
+        # COO (ColFirst) and CSC (scatter) in the reference, spmm.jl:331-335,
+        # 412-416: here in row order through the CSR kernels.
+        coo = is_coo_shaped(u_A.format)
+        idx1, idx2 = _coo_parts(u_A) if coo else _csc_parts(u_A)
+        dev = _check_same_device(idx1, idx2, nonzeros(u_A), B, C)
+        entry = f"jlust_hip_{'coo' if coo else 'csc'}_spmm_{suf}_i32"
+        with _on(dev):
+            st = getattr(L, entry)(m, n, k, nnz(u_A), u_A.origin.offset, _ptr(idx1), _ptr(idx2),
+                                   _ptr(nonzeros(u_A)), float(alpha), _ptr(B), leading_dim(B), float(beta),
+                                   _ptr(C), leading_dim(C), _stream(dev))
+        _lib.check(st, entry[10:], u_A.format, _BE, T)
+        return u_C
+    if is_shifted_diag(u_A.format):
+        lv = u_A.format.levels[1]
+        dev = _check_same_device(B, C)
+        with _on(dev):
+            st = getattr(L, f"jlust_hip_shifted_diag_spmm_{suf}")(
+                m, n, k, lv.shift, lv.val, float(alpha), _ptr(B), leading_dim(B), float(beta), _ptr(C),
+                leading_dim(C), _stream(dev))
+        _lib.check(st, "shifted_diag_spmm", u_A.format, _BE, T)
+        return u_C
+    if is_periodic_csr(u_A.format):
+        # kron(I(T), block) * B: the block's CSR SpMM on each period's rows of B and C.
+        lv = u_A.format.levels[0]
+        nper, nc = lv.periods, lv.n_cols
+        br = u_A.format.levels[1].size
+        block = USTensor((br, nc), Formats.CSR, (None, u_A.pos_buffers[2]), (None, u_A.crd_buffers[2]),
+                         nonzeros(u_A), u_A.owner, u_A.origin)
+        for t in range(nper):
+            _spmm(block, ust(B[t * nc:(t + 1) * nc, :]), ust(C[t * br:(t + 1) * br, :]), alpha, beta)
+        return u_C
     if is_bsr(u_A.format):
         b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
-        if (b1, b2) != (16, 16):
-            # Blocks other than 16 x 16: the CSR expansion and the CSR SpMM
-            # (the MFMA kernels serve 16 x 16 blocks only).
+        if (b1, b2) != (16, 16) or (suf == "f32" and row_major and nonzeros(u_A).data_ptr() % 16):
+            # Blocks other than 16 x 16 (the MFMA kernels serve 16 x 16 blocks
+            # only), and fp32 row-major blocks whose values are not 16-byte
+            # aligned (the fp32 MFMA kernels load a block row as one float4):
+            # the CSR expansion and the CSR SpMM, as the prepared BSR plan does.
             return _spmm(_bsr_as_csr(u_A), u_B, u_C, alpha, beta, skip_empty_rows)
         dev = _check_same_device(browptr, bcolind, nonzeros(u_A), B, C)
         with _on(dev):
@@ -406,11 +494,26 @@ def _sddmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, mask=None):
     A, B = _sddmm_dense_checks(u_A, u_B, u_C)
     m, n = u_C.extents
     K = A.shape[1]
-    coo = is_coo_shaped(u_C.format)
-    idx1, idx2 = _coo_parts(u_C) if coo else _csr_parts(u_C)
     mk = _sddmm_mask(mask, u_C, T)
+    if u_C.format == Formats.DCSR:
+        # The walker's compressed outer level binds the stored row
+        # (sddmm.jl:49-65 with _walker.jl:323-392).
+        rows, pos, cols = _dcsr_parts(u_C)
+        dev = _check_same_device(rows, pos, cols, nonzeros(u_C), A, B, mk)
+        _check_crd_once(u_C, rows, m, True, dev)
+        _check_pos_once(u_C, pos, rows.numel(), nnz(u_C), dev)
+        entry = f"jlust_hip_dcsr_sddmm_{suf}_i32"
+        with _on(dev):
+            st = getattr(_lib.lib(), entry)(
+                m, n, K, rows.numel(), nnz(u_C), u_C.origin.offset, _ptr(rows), _ptr(pos), _ptr(cols),
+                float(alpha), _ptr(A), leading_dim(A), _ptr(B), leading_dim(B), float(beta),
+                _ptr(nonzeros(u_C)), _ptr(mk), _stream(dev))
+        _lib.check(st, entry[10:], u_C.format, _BE, T)
+        return u_C
+    coo, csc = is_coo_shaped(u_C.format), is_csc_shaped(u_C.format)
+    idx1, idx2 = _coo_parts(u_C) if coo else _csc_parts(u_C) if csc else _csr_parts(u_C)
     dev = _check_same_device(idx1, idx2, nonzeros(u_C), A, B, mk)
-    entry = f"jlust_hip_{'coo' if coo else 'csr'}_sddmm_{suf}_i32"
+    entry = f"jlust_hip_{'coo' if coo else 'csc' if csc else 'csr'}_sddmm_{suf}_i32"
     with _on(dev):
         st = getattr(_lib.lib(), entry)(
             m, n, K, nnz(u_C), u_C.origin.offset, _ptr(idx1), _ptr(idx2), float(alpha),
@@ -627,7 +730,7 @@ class HIPSpMVHandle(AbstractKernelHandle):
         v = nonzeros(u_A)
         ver = v._version
         with _on(self.dev):
-            st = _lib.lib().jlust_hip_csr_spmv_plan_update_values(self._plan, _ptr(v))
+            st = _lib.lib().jlust_hip_csr_spmv_plan_update_values(self._plan, _ptr(v), _stream(self.dev))
         _lib.check(st, "csr_spmv_plan_update_values", u_A.format, _BE, self.T)
         self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
                             self.u_A.crd_buffers, v, self.u_A.owner, self.u_A.origin)
@@ -727,41 +830,64 @@ class HIPOpHandle(AbstractKernelHandle):
 
 
 class HIPSpMMHandle(AbstractKernelHandle):
-    """Prepared CSR SpMM (jlust_hip_csr_spmm_plan_*): prepare(HIPBackend(),
-    SpMMOp, A; n_cols=k) -> execute(h, B, C) -> update_values!(h, A), the
-    cuSPARSE SpMM handle contract (ext/CUDAExt/ops/spmm.jl:8-70).  The plan
-    analyses A once (column chunk per pass for k, long rows split into
-    segments) and owns the workspace.  It reads A's values in place, so
-    values written into them are seen; update_values_ or execute(h, A, B, C)
-    with another value tensor points the plan at it.  B with another number
-    of columns than the plan's rebuilds the plan."""
+    """Prepared CSR, COO or CSC SpMM (jlust_hip_csr_spmm_plan_*,
+    jlust_hip_coo_spmm_plan_create): prepare(HIPBackend(), SpMMOp, A;
+    n_cols=k) -> execute(h, B, C) -> update_values!(h, A), the cuSPARSE SpMM
+    handle contract (ext/CUDAExt/ops/spmm.jl:8-70).  The plan analyses A once
+    (COO/CSC entries put in row order; column chunk per pass for k, long rows
+    split into segments) and owns the workspace.  A CSR plan, and a COO plan
+    whose rows were already in order, read A's values in place; a reordered
+    COO/CSC plan holds them in its row order, and values written into A's
+    tensor through torch since the plan last read them (its version counter
+    moved) are gathered again, in stream order, before the product.
+    update_values_ or execute(h, A, B, C) with another value tensor points the
+    plan at it.  B with another number of columns than the plan's rebuilds
+    the plan.  skip_empty_rows applies to CSR (COO and CSC scale every row of
+    C by beta, as the reference's pre-scale does)."""
 
     def __init__(self, u_A: USTensor, n_cols=None, skip_empty_rows=False):
-        if not is_csr_shaped(u_A.format):
-            raise UnsupportedFormat(u_A.format, _BE, "prepared SpMM plans take CSR")
+        self.coo, self.csc = is_coo_shaped(u_A.format), is_csc_shaped(u_A.format)
+        if not (is_csr_shaped(u_A.format) or self.coo or self.csc):
+            raise UnsupportedFormat(u_A.format, _BE, "prepared SpMM plans take CSR, COO or CSC")
         self.suf = _value_suffix(u_A)
         self.T = nonzeros(u_A).dtype
-        rowptr, colind = _csr_parts(u_A)
-        self.dev = _check_same_device(rowptr, colind, nonzeros(u_A))
+        idx1, idx2 = self._index()
+        _check_values(u_A, self.T)
+        self.dev = _check_same_device(idx1, idx2, nonzeros(u_A))
         self.u_A = u_A
-        self.skip_empty_rows = bool(skip_empty_rows)
+        self.skip_empty_rows = bool(skip_empty_rows) and not (self.coo or self.csc)
         self._plan = ctypes.c_void_p(0)
         self.k = None
+        self._copies = False
+        self._ver = nonzeros(u_A)._version
         if n_cols is not None:
             self._make(int(n_cols))
+
+    def _index(self, u=None):
+        u = self.u_A if u is None else u
+        return _coo_parts(u) if self.coo else _csc_parts(u) if self.csc else _csr_parts(u)
 
     def _make(self, k: int):
         self._destroy()
         m, n = self.u_A.extents
-        rowptr, colind = _csr_parts(self.u_A)
+        idx1, idx2 = self._index()
+        vals = nonzeros(self.u_A)
+        vt = 0 if self.suf == "f64" else 1
         plan = ctypes.c_void_p(0)
         with _on(self.dev):
-            st = _lib.lib().jlust_hip_csr_spmm_plan_create(
-                m, n, k, nnz(self.u_A), self.u_A.origin.offset, 0 if self.suf == "f64" else 1,
-                _ptr(rowptr), _ptr(colind), _ptr(nonzeros(self.u_A)), _stream(self.dev),
-                ctypes.byref(plan))
-        _lib.check(st, "csr_spmm_plan_create", self.u_A.format, _BE, self.T)
+            if self.coo or self.csc:
+                st = _lib.lib().jlust_hip_coo_spmm_plan_create(
+                    2 if self.coo else 1, m, n, k, nnz(self.u_A), self.u_A.origin.offset, vt, _ptr(idx1),
+                    _ptr(idx2), _ptr(vals), _stream(self.dev), ctypes.byref(plan))
+            else:
+                st = _lib.lib().jlust_hip_csr_spmm_plan_create(
+                    m, n, k, nnz(self.u_A), self.u_A.origin.offset, vt, _ptr(idx1), _ptr(idx2),
+                    _ptr(vals), _stream(self.dev), ctypes.byref(plan))
+        _lib.check(st, "spmm_plan_create", self.u_A.format, _BE, self.T)
         self._plan, self.k = plan, k
+        self._ver = vals._version
+        # A reordered COO/CSC plan holds its own copy of the values.
+        self._copies = self.info()["reordered"]
 
     def execute(self, *ts, alpha=1.0, beta=0.0, skip_empty_rows=None):
         """execute(h, B, C) or execute(h, A, B, C); returns C (a USTensor)."""
@@ -789,7 +915,11 @@ class HIPSpMMHandle(AbstractKernelHandle):
         k = B.shape[1]
         if self.k != k:
             self._make(k)
+        elif self._copies and nonzeros(self.u_A)._version != self._ver:
+            self._refresh()
         skip = self.skip_empty_rows if skip_empty_rows is None else bool(skip_empty_rows)
+        if self.coo or self.csc:
+            skip = False
         with _on(self.dev):
             st = getattr(_lib.lib(), f"jlust_hip_csr_spmm_plan_execute_{self.suf}")(
                 self._plan, float(alpha), _ptr(B), leading_dim(B), float(beta), _ptr(C),
@@ -797,27 +927,37 @@ class HIPSpMMHandle(AbstractKernelHandle):
         _lib.check(st, "csr_spmm_plan_execute", self.u_A.format, _BE, self.T)
         return u_C
 
+    def _refresh(self):
+        """Make the plan read self.u_A's values now (stream-ordered: a pointer
+        swap, or a gather into a reordered plan's copy)."""
+        v = nonzeros(self.u_A)
+        if self._plan.value:
+            with _on(self.dev):
+                st = _lib.lib().jlust_hip_csr_spmm_plan_update_values(self._plan, _ptr(v), _stream(self.dev))
+            _lib.check(st, "csr_spmm_plan_update_values", self.u_A.format, _BE, self.T)
+        self._ver = v._version
+
     def update_values(self, u_A: USTensor):
         if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):
             raise IncompatibleExtents("update_values!: the sparsity structure must not change")
         _check_values(u_A, self.T)
         _check_same_device(nonzeros(u_A), nonzeros(self.u_A))
-        if self._plan.value:
-            st = _lib.lib().jlust_hip_csr_spmm_plan_update_values(self._plan, _ptr(nonzeros(u_A)))
-            _lib.check(st, "csr_spmm_plan_update_values", u_A.format, _BE, self.T)
         self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
                             self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+        self._refresh()
         return self
 
     def info(self) -> dict:
-        """What the plan's analysis found: split rows, their segments, columns per pass."""
+        """What the plan's analysis found: split rows, their segments, columns
+        per pass, and whether COO/CSC entries were reordered."""
         if not self._plan.value:
             return {}
-        a, b, c = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        a, b, c, r = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
         st = _lib.lib().jlust_hip_csr_spmm_plan_info(self._plan, ctypes.byref(a), ctypes.byref(b),
-                                                     ctypes.byref(c))
+                                                     ctypes.byref(c), ctypes.byref(r))
         _lib.check(st, "csr_spmm_plan_info", self.u_A.format, _BE, self.T)
-        return {"split_rows": a.value, "segments": b.value, "cols_per_pass": c.value}
+        return {"split_rows": a.value, "segments": b.value, "cols_per_pass": c.value,
+                "reordered": bool(r.value)}
 
     def _destroy(self):
         plan, self._plan = getattr(self, "_plan", None), ctypes.c_void_p(0)
@@ -953,34 +1093,50 @@ class HIPSDDMMHandle(AbstractKernelHandle):
     A, B, C) -> execute(h, A, B, C) -> update_values!(h, C), the cuSPARSE
     SDDMM handle contract (ext/CUDAExt/ops/sddmm.jl:10-76); prepare(...,
     SDDMMOp, C) also works, the inner dimension taken from the first A.  C
-    (CSR or COO) is the mask pattern; the plan holds its row order and work
-    items.  execute(h, A, B) writes into the handle's C; update_values_(h,
-    C2) makes C2 (same pattern) the handle's output."""
+    (CSR, COO, CSC or DCSR) is the mask pattern; the plan holds its row order
+    and work items.  execute(h, A, B) writes into the handle's C;
+    update_values_(h, C2) makes C2 (same pattern) the handle's output."""
+
+    # Mask formats of jlust_hip_sddmm_plan_create (enum jlust_format).
+    _FMT = {"CSR": 0, "CSC": 1, "COO": 2}
 
     def __init__(self, u_C: USTensor, n_inner=None):
-        self.coo = is_coo_shaped(u_C.format)
-        if not (is_csr_shaped(u_C.format) or self.coo):
-            raise UnsupportedFormat(u_C.format, _BE, "prepared SDDMM plans take a CSR or COO mask")
+        f = u_C.format
+        self.kind = ("COO" if is_coo_shaped(f) else "CSC" if is_csc_shaped(f) else
+                     "CSR" if is_csr_shaped(f) else "DCSR" if f == Formats.DCSR else None)
+        if self.kind is None:
+            raise UnsupportedFormat(u_C.format, _BE, "prepared SDDMM plans take a CSR, COO, CSC or DCSR mask")
         self.suf = _value_suffix(u_C)
         self.T = nonzeros(u_C).dtype
-        idx = _coo_parts(u_C) if self.coo else _csr_parts(u_C)
+        idx = self._index(u_C)
         self.dev = _check_same_device(*idx, nonzeros(u_C))
+        if self.kind == "DCSR":
+            _check_crd_once(u_C, idx[0], u_C.extents[0], True, self.dev)
         self.u_C = u_C
         self._plan = ctypes.c_void_p(0)
         self.K = None
         if n_inner is not None:
             self._make(int(n_inner))
 
+    def _index(self, u):
+        return {"COO": _coo_parts, "CSC": _csc_parts, "CSR": _csr_parts, "DCSR": _dcsr_parts}[self.kind](u)
+
     def _make(self, K: int):
         self._destroy()
         m, n = self.u_C.extents
-        idx1, idx2 = _coo_parts(self.u_C) if self.coo else _csr_parts(self.u_C)
+        idx = self._index(self.u_C)
+        vt = 0 if self.suf == "f64" else 1
         plan = ctypes.c_void_p(0)
         with _on(self.dev):
-            st = _lib.lib().jlust_hip_sddmm_plan_create(
-                2 if self.coo else 0, m, n, K, nnz(self.u_C), self.u_C.origin.offset,
-                0 if self.suf == "f64" else 1, _ptr(idx1), _ptr(idx2), _stream(self.dev),
-                ctypes.byref(plan))
+            if self.kind == "DCSR":
+                rows, pos, cols = idx
+                st = _lib.lib().jlust_hip_dcsr_sddmm_plan_create(
+                    m, n, K, rows.numel(), nnz(self.u_C), self.u_C.origin.offset, vt, _ptr(rows), _ptr(pos),
+                    _ptr(cols), _stream(self.dev), ctypes.byref(plan))
+            else:
+                st = _lib.lib().jlust_hip_sddmm_plan_create(
+                    self._FMT[self.kind], m, n, K, nnz(self.u_C), self.u_C.origin.offset, vt, _ptr(idx[0]),
+                    _ptr(idx[1]), _stream(self.dev), ctypes.byref(plan))
         _lib.check(st, "sddmm_plan_create", self.u_C.format, _BE, self.T)
         self._plan, self.K = plan, K
 
@@ -1055,7 +1211,7 @@ def prepare(optype, u_A: USTensor, *more, **kw):
         bad = set(kw) - {"n_cols", "skip_empty_rows"}
         if bad or more:
             raise TypeError(f"prepare(SpMMOp): unexpected keywords {sorted(bad)} or tensors ({len(more)})")
-        if is_csr_shaped(u_A.format):
+        if is_csr_shaped(u_A.format) or is_coo_shaped(u_A.format) or is_csc_shaped(u_A.format):
             return HIPSpMMHandle(u_A, kw.get("n_cols"), kw.get("skip_empty_rows", False))
         if is_bsr(u_A.format) and not kw.get("skip_empty_rows"):
             return HIPBSRSpMMHandle(u_A, kw.get("n_cols"))

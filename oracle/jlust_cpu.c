@@ -286,6 +286,73 @@ DEF_SPMM_ABSREF(f64, double)
 DEF_SPMM_ABSREF(f32, float)
 
 /* ------------------------------------------------------------------------- */
+/* COO and CSC SpMM (atomic / scatter modes)                                 */
+/* ------------------------------------------------------------------------- */
+/*
+ * C = alpha*A*B + beta*C for a COO A.  execute(::EmitterBackend, ::Op{:SpMM})
+ * pre-scales C by beta for COO-like and scatter formats, filling zero when
+ * beta == 0 (ext/KernelAbstractionsExt/ops/spmm.jl:412-416), then runs COO as
+ * ColFirst (spmm.jl:331-335): one thread per stored entry loops over the k
+ * columns of B with the atomic leaf
+ *   @atomic C[row, col] += alpha * nzval[p] * B[x, col]     (spmm.jl:32-33)
+ * (Julia evaluates alpha*nzval first).  The atomics' order is not fixed in the
+ * reference; this restatement applies them sequentially, entry by entry in
+ * storage order, then column by column, one of its admissible orders.
+ */
+#define DEF_COO_SPMM(SUF, T)                                                   \
+void oracle_coo_spmm_##SUF(int64_t nnz, int32_t m, int32_t origin,             \
+                           const int32_t *rows, const int32_t *cols,           \
+                           const T *val, int64_t k, T alpha, const T *B,       \
+                           int64_t ldb, T beta, T *C, int64_t ldc)             \
+{                                                                              \
+    for (int64_t c = 0; c < k; ++c)                                            \
+        for (int64_t i = 0; i < m; ++i) {                                      \
+            T *o = &C[i + c * ldc];                                            \
+            *o = beta == (T)0 ? (T)0 : *o * beta;                              \
+        }                                                                      \
+    for (int64_t p = 0; p < nnz; ++p) {                                        \
+        int64_t r = (int64_t)rows[p] - origin, j = (int64_t)cols[p] - origin;  \
+        T av = alpha * val[p];                                                 \
+        for (int64_t c = 0; c < k; ++c)                                        \
+            C[r + c * ldc] += av * B[j + c * ldb];                             \
+    }                                                                          \
+}
+DEF_COO_SPMM(f64, double)
+DEF_COO_SPMM(f32, float)
+
+/*
+ * CSC A (colptr[n+1], rowind): the same pre-scale, then the walker's scatter
+ * direction (_walker.jl:41-66: the dense outer level walks the input column
+ * j, the compressed inner level binds the output row) with the scatter leaf
+ *   @atomic C[rowind[p], col] += alpha * nzval[p] * B[j, col]  (spmm.jl:18-19)
+ * for every strategy _spmm_strategy picks under scatter (spmm.jl:329-349).
+ * Applied sequentially: column j in order, its entries in storage order,
+ * then the k columns of B.
+ */
+#define DEF_CSC_SPMM(SUF, T)                                                   \
+void oracle_csc_spmm_##SUF(int32_t m, int32_t n, int32_t origin,               \
+                           const int32_t *colptr, const int32_t *rowind,       \
+                           const T *val, int64_t k, T alpha, const T *B,       \
+                           int64_t ldb, T beta, T *C, int64_t ldc)             \
+{                                                                              \
+    for (int64_t c = 0; c < k; ++c)                                            \
+        for (int64_t i = 0; i < m; ++i) {                                      \
+            T *o = &C[i + c * ldc];                                            \
+            *o = beta == (T)0 ? (T)0 : *o * beta;                              \
+        }                                                                      \
+    for (int64_t j = 0; j < n; ++j)                                            \
+        for (int64_t p = (int64_t)colptr[j] - origin;                          \
+             p < (int64_t)colptr[j + 1] - origin; ++p) {                       \
+            int64_t r = (int64_t)rowind[p] - origin;                           \
+            T av = alpha * val[p];                                             \
+            for (int64_t c = 0; c < k; ++c)                                    \
+                C[r + c * ldc] += av * B[j + c * ldb];                         \
+        }                                                                      \
+}
+DEF_CSC_SPMM(f64, double)
+DEF_CSC_SPMM(f32, float)
+
+/* ------------------------------------------------------------------------- */
 /* CSR SDDMM                                                                 */
 /* ------------------------------------------------------------------------- */
 /*

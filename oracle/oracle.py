@@ -57,6 +57,10 @@ def lib():
                 _I64, _I32, _I32, _P, _P, _P, S, _P, S, _P]
             getattr(L, f"oracle_csc_spmv_{suf}").argtypes = [
                 _I32, _I32, _I32, _P, _P, _P, S, _P, S, _P]
+            getattr(L, f"oracle_coo_spmm_{suf}").argtypes = [
+                _I64, _I32, _I32, _P, _P, _P, _I64, S, _P, _I64, S, _P, _I64]
+            getattr(L, f"oracle_csc_spmm_{suf}").argtypes = [
+                _I32, _I32, _I32, _P, _P, _P, _I64, S, _P, _I64, S, _P, _I64]
             getattr(L, f"oracle_coo_sddmm_{suf}").argtypes = [
                 _I64, _I32, _P, _P, _I64, S, _P, _I64, _P, _I64, S, _P, _P]
             f = getattr(L, f"oracle_csr_spmm_{suf}")
@@ -226,6 +230,78 @@ def coo_sddmm(rows, cols, A, B, alpha=1.0, beta=0.0, C0=None, mask=None, origin=
         nnz, origin, _ptr(rows), _ptr(cols), A.shape[1], alpha, _ptr(A), max(A.shape[0], 1),
         _ptr(B), max(B.shape[0], 1), beta, _ptr(C), _ptr(mk))
     return C
+
+
+def coo_spmm(rows, cols, val, B, m, alpha=1.0, beta=0.0, C0=None, origin=1):
+    """COO SpMM as the reference's ColFirst atomic path computes it: C
+    pre-scaled by beta (zero fill when beta == 0), then C[row, :] +=
+    (alpha*val)*B[col, :] entry by entry in storage order (oracle_coo_spmm_*)."""
+    L = lib()
+    dt = np.asarray(val).dtype
+    suf = _suf(dt)
+    rows = _c(rows, np.int32)
+    cols = _c(cols, np.int32)
+    val = _c(val, dt)
+    B = _f(B, dt)
+    k = B.shape[1]
+    C = np.zeros((m, k), dt, order="F") if C0 is None else _f(C0, dt).copy(order="F")
+    getattr(L, f"oracle_coo_spmm_{suf}")(
+        val.size, m, origin, _ptr(rows), _ptr(cols), _ptr(val), k, alpha, _ptr(B),
+        max(B.shape[0], 1), beta, _ptr(C), max(m, 1))
+    return C
+
+
+def csc_spmm(colptr, rowind, val, B, m, alpha=1.0, beta=0.0, C0=None, origin=1):
+    """CSC SpMM in the reference's scatter direction: C pre-scaled by beta,
+    then column by column C[row, :] += (alpha*val)*B[col, :] (oracle_csc_spmm_*)."""
+    L = lib()
+    dt = np.asarray(val).dtype
+    suf = _suf(dt)
+    colptr = _c(colptr, np.int32)
+    rowind = _c(rowind, np.int32)
+    val = _c(val, dt)
+    B = _f(B, dt)
+    k = B.shape[1]
+    C = np.zeros((m, k), dt, order="F") if C0 is None else _f(C0, dt).copy(order="F")
+    getattr(L, f"oracle_csc_spmm_{suf}")(
+        m, colptr.size - 1, origin, _ptr(colptr), _ptr(rowind), _ptr(val), k, alpha, _ptr(B),
+        max(B.shape[0], 1), beta, _ptr(C), max(m, 1))
+    return C
+
+
+def expand_pos(pos, outer=None, origin=1):
+    """The outer coordinate of every stored entry of a compressed level:
+    outer[s] (or s + origin) repeated pos[s+1] - pos[s] times -- the
+    coordinate the walker binds at the outer level for each inner entry
+    (ext/KernelAbstractionsExt/ops/_walker.jl:271-392)."""
+    pos = np.asarray(pos, np.int64)
+    lens = np.diff(pos)
+    o = np.arange(lens.size, dtype=np.int64) + origin if outer is None else np.asarray(outer, np.int64)
+    return np.repeat(o, lens).astype(np.int32)
+
+
+def dcsr_sddmm(outer, pos, cols, A, B, alpha=1.0, beta=0.0, C0=None, mask=None, origin=1):
+    """SDDMM over a DCSR mask: the walker's compressed outer level binds the
+    stored row (sddmm.jl:23-30 with _walker.jl:323-392), so entry p of stored
+    row f is (outer[f], cols[p]); outputs in storage order."""
+    return coo_sddmm(expand_pos(pos, outer, origin), cols, A, B, alpha, beta, C0, mask, origin)
+
+
+def csc_sddmm(colptr, rowind, A, B, alpha=1.0, beta=0.0, C0=None, mask=None, origin=1):
+    """SDDMM over a CSC mask by the operator's definition (C <- alpha*(A*B) o
+    sparsity(C) + beta*C, sddmm.jl:1-6): entry p of column j is
+    (rowind[p], j); outputs in storage order."""
+    return coo_sddmm(rowind, expand_pos(colptr, None, origin), A, B, alpha, beta, C0, mask, origin)
+
+
+def row_order(rows, m, origin=1):
+    """(rowptr, perm): the stable row order of COO entries -- perm[q] is the
+    storage position of the q-th entry in row order (ties in storage order),
+    rowptr the origin-based row pointers of that order."""
+    r = np.asarray(rows, np.int64) - origin
+    perm = np.argsort(r, kind="stable").astype(np.int32)
+    rowptr = (np.searchsorted(r[perm], np.arange(m + 1), side="left") + origin).astype(np.int32)
+    return rowptr, perm
 
 
 def spmm_strategy(m, k, nnz, skip_empty_rows=False) -> str:

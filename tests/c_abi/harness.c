@@ -100,7 +100,7 @@ int jlust_c_harness_run(char *msg, size_t len)
               y[2]);
         const double val2[5] = {2, 4, 6, 8, 10};
         CHECK(hipMemcpy(dval, val2, sizeof val2, hipMemcpyHostToDevice) == hipSuccess, 4, "copy failed");
-        st = jlust_hip_csr_spmv_plan_update_values(plan, dval);
+        st = jlust_hip_csr_spmv_plan_update_values(plan, dval, NULL);
         CHECK(st == JLUST_STATUS_SUCCESS, 9, "plan_update_values: status %d (%s)", st, jlust_hip_last_error());
         st = jlust_hip_csr_spmv_plan_execute_f64(plan, 1.0, dx, 0.0, dy, NULL);
         CHECK(st == JLUST_STATUS_SUCCESS, 7, "plan_execute: status %d (%s)", st, jlust_hip_last_error());

@@ -46,7 +46,7 @@ def test_python_signatures_cover_header():
 def test_load_version_and_error_buffer():
     from jlust_amd import _lib
     L = _lib.lib()
-    assert L.jlust_hip_version() == 1
+    assert L.jlust_hip_version() == 2
     assert isinstance(_lib.last_error(), str)
 
 

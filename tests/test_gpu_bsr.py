@@ -361,3 +361,54 @@ def test_bsr_spmv_direct(J, O, b1, b2, dtype, row_major):
         ref = O.csr_spmv(rp, ci, v, x, alpha, beta, yb, origin)
         absref = O.csr_spmv_absref(rp, ci, v, x, alpha, beta, yb, origin)
         assert_within(host(y), ref, absref, dtype, f"bsr spmv {b1}x{b2} beta={beta}")
+
+
+def test_bsr_spmv_rejects_bad_browptr(J):
+    """BSR SpMV checks browptr (and the block columns) once per version of
+    the index buffers: a pointer array that ends past nnzb, or one that does
+    not start at the origin, is NonCanonicalStorage, as the CSR expansion
+    route reports it; the kernel itself would only clamp it."""
+    bc = dev(np.array([1, 2], np.int32))
+    x = dev(np.ones(4))
+    for bad in ([1, 2, 5], [2, 2, 3], [1, 3, 3 - 1]):
+        A = J.bsr_tensor(dev(np.array(bad, np.int32)), bc, dev(np.ones(2 * 4, np.float64)), (4, 4), (2, 2))
+        with pytest.raises(J.NonCanonicalStorage):
+            J.execute(J.SpMVOp, A, x, dev(np.zeros(4)))
+    A = J.bsr_tensor(dev(np.array([1, 2, 3], np.int32)), dev(np.array([1, 3], np.int32)),
+                     dev(np.ones(2 * 4, np.float64)), (4, 4), (2, 2))
+    with pytest.raises(J.NonCanonicalStorage):                       # block column 3 of 2
+        J.execute(J.SpMVOp, A, x, dev(np.zeros(4)))
+    good = J.bsr_tensor(dev(np.array([1, 2, 3], np.int32)), bc, dev(np.arange(8, dtype=np.float64)),
+                        (4, 4), (2, 2))
+    y = dev(np.zeros(4))
+    J.execute(J.SpMVOp, good, x, y)
+    np.testing.assert_array_equal(host(y), [1.0, 5.0, 9.0, 13.0])
+    # the index buffer written in place through torch is checked again
+    good.pos_buffers[1][2] = 7
+    with pytest.raises(J.NonCanonicalStorage):
+        J.execute(J.SpMVOp, good, x, y)
+
+
+def test_bsr_f32_unaligned_values_plain_and_plan(J, O):
+    """fp32 16 x 16 BSRRight values that are not 16-byte aligned (a view at an
+    odd element offset): the plain call takes the CSR expansion, as the
+    prepared plan does, and both match the definition."""
+    import torch
+    mb, nb, k = 24, 20, 40
+    browptr, bcolind, val = random_bsr(mb, nb, 5, seed=31)
+    store = torch.empty(val.size + 1, dtype=torch.float32, device="cuda")
+    store[1:] = torch.from_numpy(val).cuda()
+    vview = store[1:]
+    assert vview.data_ptr() % 16 != 0
+    A = J.bsr_tensor(dev(browptr), dev(bcolind), vview, (mb * 16, nb * 16), (16, 16))
+    B = np.asfortranarray(np.random.default_rng(32).standard_normal((nb * 16, k)).astype(np.float32))
+    C = J.dense_matrix(mb * 16, k, dtype=torch.float32, fill=float("nan"))
+    J.execute(J.SpMMOp, A, dev(B), C)
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
+    ref, _ = O.csr_spmm(rp, ci, v, B)
+    absref = O.csr_spmm_absref(rp, ci, v, B)
+    assert_within(host(C), ref, absref, np.float32, "unaligned plain")
+    h = J.prepare(J.HIPBackend(), J.SpMMOp, A, n_cols=k)
+    C2 = J.dense_matrix(mb * 16, k, dtype=torch.float32, fill=float("nan"))
+    J.execute(h, dev(B), C2)
+    assert_within(host(C2), ref, absref, np.float32, "unaligned plan")

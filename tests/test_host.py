@@ -67,6 +67,25 @@ def test_supports_backend_table():
     assert not J.supports_backend(object(), J.SpMVOp(J.Formats.CSR, d1, d1))
 
 
+def test_supports_backend_every_sparse_format():
+    """Every non-dense operand format the mirror defines, as the reference's
+    EmitterBackend claims them (ext/KernelAbstractionsExt/
+    KernelAbstractionsExt.jl:31-37: any non-dense A for SpMV/SpMM;
+    ops/sddmm.jl:12-14: any non-dense C for SDDMM, here the formats with
+    stored values per entry)."""
+    be = J.HIPBackend()
+    d1, d2 = J.Formats.DensedRight(1), J.Formats.DensedRight(2)
+    sparse = [J.Formats.CSR, J.Formats.CSC, J.Formats.COO, J.Formats.DCSR,
+              J.Formats.BSRRight((16, 16)), J.Formats.BSRLeft((2, 3)),
+              J.Formats.ShiftedDiag(torch.float64, shift=1), J.Formats.PeriodicCSR(3, 4, 5)]
+    for f in sparse:
+        assert J.supports_backend(be, J.SpMVOp(f, d1, d1)), f
+        assert J.supports_backend(be, J.SpMMOp(f, d2, d2)), f
+    for f in (J.Formats.CSR, J.Formats.CSC, J.Formats.COO, J.Formats.DCSR):
+        assert J.supports_backend(be, J.SDDMMOp(d2, d2, f)), f
+    assert not J.supports_backend(be, J.SDDMMOp(d2, d2, J.Formats.ShiftedDiag(torch.float64)))
+
+
 def fixture_csr(origin=1):
     c = GOLDEN["spmv"][0 if origin == 1 else 1]
     return J.csr_tensor(torch.tensor(c["rowptr"], dtype=torch.int32),
