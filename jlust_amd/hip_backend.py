@@ -851,7 +851,7 @@ class HIPSpMMHandle(AbstractKernelHandle):
             raise UnsupportedFormat(u_A.format, _BE, "prepared SpMM plans take CSR, COO or CSC")
         self.suf = _value_suffix(u_A)
         self.T = nonzeros(u_A).dtype
-        idx1, idx2 = self._index()
+        idx1, idx2 = self._index(u_A)
         _check_values(u_A, self.T)
         self.dev = _check_same_device(idx1, idx2, nonzeros(u_A))
         self.u_A = u_A
