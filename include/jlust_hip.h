@@ -88,6 +88,17 @@ int jlust_hip_version(void);
 /* Message of the last failing call on this thread ("" if none). */
 const char *jlust_hip_last_error(void);
 
+/*
+ * Loads the library's device code on the current device now (no counterpart
+ * in the reference; for callers that want the cost at start-up, such as
+ * servers).  The runtime otherwise loads each translation unit's code object,
+ * and each rocPRIM instantiation, at its first launch, which adds tens of
+ * milliseconds to the first call that needs it (the first prepared SpMV plan
+ * of a process: about 35 ms of its first build).  Runs a few tiny sorts and
+ * scans on `stream` and synchronises it; idempotent.
+ */
+int jlust_hip_preload(jlust_stream_t stream);
+
 /* Name of the current device's ISA, e.g. "gfx950", into buf. */
 int jlust_hip_device_arch(char *buf, size_t len);
 
@@ -279,7 +290,13 @@ int jlust_hip_spmv_graph_destroy(jlust_spmv_graph_t graph);
 /* The kernel a plan runs (no counterpart in the reference; for diagnostics
  * and benchmarks): merge-path tiles, the vector kernel for short even rows
  * (*lanes_per_row lanes per row), XCD column slices, or the LDS-binned
- * two-pass layout (x slices and y bins held in LDS). */
+ * two-pass layout (x slices and y bins held in LDS); *device_bytes (may be
+ * NULL) is the device memory the plan holds until it is destroyed.
+ * The sliced and binned layouts copy the matrix; a plan whose layout cannot
+ * be allocated (hipMalloc reports out of memory, or the layout with its
+ * build temporaries would exceed the byte limit in the environment variable
+ * JLUST_HIP_PLAN_MAX_BYTES, read at plan_create) uses the merge or vector
+ * kernel on the caller's arrays instead, with no error. */
 enum jlust_spmv_kernel {
     JLUST_SPMV_MERGE = 0,
     JLUST_SPMV_VECTOR = 1,
@@ -287,7 +304,8 @@ enum jlust_spmv_kernel {
     JLUST_SPMV_BINNED = 3
 };
 int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *kernel,
-                                 int32_t *lanes_per_row);
+                                 int32_t *lanes_per_row,
+                                 int64_t *device_bytes);
 
 /*
  * Prepared COO SpMV (rows[nnz], cols[nnz] as coo_tensor stores them,

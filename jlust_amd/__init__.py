@@ -27,6 +27,7 @@ from .elementwise import (ElementwiseFn, abs_fn, affine_fn, exp_fn, identity_fn,
                           sqrt_fn, square_fn)
 from .convert import (convert_format, convert_index_type, convert_value_type, csc_tensor,
                       dcsr_tensor, sparse_to_dense)
+from ._lib import preload
 from .tensor import (CPUDevice, HIPDevice, OneBased, USTensor, ZeroBased, bsr_tensor,
                      coo_tensor, coordinates, csr_tensor, dense_matrix, extents, format,
                      has_coordinates, has_positions, index_origin, materialize, nnz, nonzeros,

@@ -32,6 +32,7 @@ SIGNATURES = {
     "jlust_hip_version": (_INT, []),
     "jlust_hip_last_error": (ctypes.c_char_p, []),
     "jlust_hip_device_arch": (_INT, [ctypes.c_char_p, ctypes.c_size_t]),
+    "jlust_hip_preload": (_INT, [_P]),
     "jlust_hip_check_csr": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _INT]),
     "jlust_hip_check_pos_i32": (_INT, [_I64, _I64, _I32, _P, _P]),
     "jlust_hip_check_crd_i32": (_INT, [_I64, _I64, _I32, _INT, _P, _P]),
@@ -56,7 +57,8 @@ SIGNATURES = {
     "jlust_hip_csr_spmv_plan_capture_f32": (_INT, [_P, _F, _P, _F, _P, ctypes.POINTER(_P)]),
     "jlust_hip_spmv_graph_launch": (_INT, [_P, _P]),
     "jlust_hip_spmv_graph_destroy": (_INT, [_P]),
-    "jlust_hip_csr_spmv_plan_info": (_INT, [_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32)]),
+    "jlust_hip_csr_spmv_plan_info": (_INT, [_P, ctypes.POINTER(_I32), ctypes.POINTER(_I32),
+                                            ctypes.POINTER(_I64)]),
     "jlust_hip_coo_spmv_plan_create": (_INT, [_I64, _I64, _I64, _I32, _INT, _P, _P, _P, _P,
                                               ctypes.POINTER(_P)]),
     "jlust_hip_coo_spmv_f64_i32": (_INT, [_I64, _I64, _I64, _I32, _P, _P, _P, _D, _P, _D, _P, _P]),
@@ -225,3 +227,13 @@ def check(status: int, what: str, fmt=None, backend=None, T=None):
     if status == 8:
         raise MemoryError(msg)
     raise errors.HIPError(f"{STATUS.get(status, status)}: {msg}")
+
+
+def preload(device=None) -> None:
+    """Load the library's device code on `device` (default: the current one)
+    now rather than at the first call that needs each part
+    (jlust_hip_preload): a server pays the runtime's one-time code-object
+    loading at start-up instead of in its first prepared plan."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    with on_device(dev):
+        check(lib().jlust_hip_preload(stream_handle(dev)), "preload")

@@ -407,3 +407,11 @@ extern "C" int jlust_hip_shifted_diag_spmm_f32(int64_t m, int64_t n, int64_t k, 
 {
     return shifted_diag_spmm<float>(m, n, k, shift, val, alpha, B, ldb, beta, C, ldc, stream);
 }
+
+namespace jlust {
+int preload_assemble()
+{
+    JLUST_PRELOAD_KERNEL(row_len_kernel);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

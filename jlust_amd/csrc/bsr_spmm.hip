@@ -1072,3 +1072,11 @@ extern "C" int jlust_hip_bsr_spmm_plan_destroy(jlust_bsr_plan_t plan)
     if (e != hipSuccess) return jlust::hip_fail(e, "bsr_spmm_plan_destroy");
     return st;
 }
+
+namespace jlust {
+int preload_bsr()
+{
+    JLUST_PRELOAD_KERNEL(bsr_expand_rowptr_kernel);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

@@ -131,6 +131,19 @@ using namespace jlust;
 
 extern "C" int jlust_hip_version(void) { return JLUST_HIP_ABI_VERSION; }
 
+extern "C" int jlust_hip_preload(jlust_stream_t stream)
+{
+    clear_error();
+    if (int st = require_device(nullptr)) return st;
+    hipStream_t s = (hipStream_t)stream;
+    for (int (*f)() : {preload_spmv, preload_spmm, preload_sddmm, preload_bsr, preload_coo_spmv, preload_coo_csc,
+                       preload_assemble, preload_dcsr, preload_fn, preload_periodic, preload_scan})
+        if (int st = f()) return st;
+    for (int (*f)(hipStream_t) : {preload_binned, preload_coo_plan, preload_convert})
+        if (int st = f(s)) return st;
+    return JLUST_STATUS_SUCCESS;
+}
+
 extern "C" const char *jlust_hip_last_error(void) { return g_last_error.c_str(); }
 
 extern "C" int jlust_hip_device_arch(char *buf, size_t len)

@@ -82,7 +82,7 @@ constexpr int NUM_XCD = 8;   // MI355X: workgroup b runs on XCD b % 8
 // Hands a COO plan's owned buffers to a CSR SpMV plan (spmv.hip): mem is
 // freed with the plan; perm/val_copy (or null) reorder new values on
 // update_values.
-int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, void *val_copy);
+int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, void *val_copy, size_t bytes);
 
 // Row order of m x n COO entries (coo_plan.hip): rowptr[m+1] (origin-based)
 // of the entries in row order and, unless the rows were already
@@ -116,6 +116,37 @@ int perm_gather(int value_type, int64_t nnz, const int32_t *perm, const void *sr
 // mem is freed with the plan; perm/val_copy (or null) reorder new values on
 // update_values.
 int spmm_plan_adopt_reorder(jlust_spmm_plan_t plan, void *mem, const int32_t *perm, void *val_copy);
+
+// ---------------------------------------------------------------- preload
+
+// The runtime loads a translation unit's device code on the first launch of
+// one of its kernels (tens of milliseconds for the larger ones).  Each unit
+// defines preload_<unit>(), which asks for the attributes of one of its
+// kernels -- enough to make the runtime load that code object now -- and, in
+// the units that sort with rocPRIM, runs one tiny sort on the stream, since
+// rocPRIM's kernels are loaded at their first launch.  jlust_hip_preload()
+// calls them all.
+int preload_spmv();
+int preload_binned(hipStream_t s);
+int preload_coo_plan(hipStream_t s);
+int preload_convert(hipStream_t s);
+int preload_spmm();
+int preload_sddmm();
+int preload_bsr();
+int preload_coo_spmv();
+int preload_coo_csc();
+int preload_assemble();
+int preload_dcsr();
+int preload_fn();
+int preload_periodic();
+int preload_scan();
+
+#define JLUST_PRELOAD_KERNEL(KERNEL)                                                        \
+    do {                                                                                    \
+        hipFuncAttributes attr_;                                                            \
+        const hipError_t e_ = hipFuncGetAttributes(&attr_, reinterpret_cast<const void *>(KERNEL)); \
+        if (e_ != hipSuccess) return ::jlust::hip_fail(e_, "preload " #KERNEL);             \
+    } while (0)
 
 // ------------------------------------------------------------ device code
 

@@ -774,3 +774,41 @@ extern "C" int jlust_hip_shift_index(int32_t *dst, const int32_t *src, int64_t l
                        src, delta);
     return check_launch("shift_kernel");
 }
+
+namespace jlust {
+// The unit's device code plus the rocPRIM instantiations a conversion runs
+// (64-bit key sort, int32 scans), each launched once on 64 elements.
+int preload_convert(hipStream_t s)
+{
+    JLUST_PRELOAD_KERNEL(compact_kernel);
+    constexpr size_t n = 64;
+    size_t need_sort = 0, need_max = 0, need_ex = 0, need_in = 0;
+    uint64_t *kn = nullptr;
+    int32_t *vn = nullptr;
+    JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, need_sort, kn, kn, vn, vn, n, 0, 64, s));
+    JLUST_HIP_TRY(rocprim::inclusive_scan(nullptr, need_max, vn, vn, n, rocprim::maximum<int32_t>(), s));
+    JLUST_HIP_TRY(rocprim::exclusive_scan(nullptr, need_ex, vn, vn, 0, n, rocprim::plus<int32_t>(), s));
+    JLUST_HIP_TRY(rocprim::inclusive_scan(nullptr, need_in, vn, vn, n, rocprim::plus<int32_t>(), s));
+    const size_t need = std::max(std::max(need_sort, need_max), std::max(need_ex, need_in));
+    void *buf = nullptr;
+    JLUST_HIP_TRY(hipMalloc(&buf, 2 * n * 8 + 2 * n * 4 + (need + 255) / 256 * 256));
+    char *b = (char *)buf;
+    uint64_t *k0 = (uint64_t *)b, *k1 = (uint64_t *)(b + n * 8);
+    int32_t *v0 = (int32_t *)(b + 2 * n * 8), *v1 = (int32_t *)(b + 2 * n * 8 + n * 4);
+    void *tmp = b + 2 * n * 8 + 2 * n * 4;
+    hipError_t e = hipMemsetAsync(buf, 0, 2 * n * 8 + 2 * n * 4, s);
+    size_t t = need;
+    if (e == hipSuccess) e = rocprim::radix_sort_pairs(tmp, t, k0, k1, v0, v1, n, 0, 64, s);
+    t = need;
+    if (e == hipSuccess) e = rocprim::inclusive_scan(tmp, t, v0, v1, n, rocprim::maximum<int32_t>(), s);
+    t = need;
+    if (e == hipSuccess) e = rocprim::exclusive_scan(tmp, t, v0, v1, 0, n, rocprim::plus<int32_t>(), s);
+    t = need;
+    if (e == hipSuccess) e = rocprim::inclusive_scan(tmp, t, v0, v1, n, rocprim::plus<int32_t>(), s);
+    const hipError_t e2 = hipStreamSynchronize(s);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return hip_fail(e, "preload_convert");
+    if (e2 != hipSuccess) return hip_fail(e2, "preload_convert");
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

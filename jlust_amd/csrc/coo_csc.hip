@@ -466,3 +466,11 @@ extern "C" int jlust_hip_coo_spmm_plan_create(int32_t format, int64_t m, int64_t
                                          plan_out);
     });
 }
+
+namespace jlust {
+int preload_coo_csc()
+{
+    JLUST_PRELOAD_KERNEL(pos_check_kernel);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

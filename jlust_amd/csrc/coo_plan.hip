@@ -192,7 +192,7 @@ static int coo_spmv_plan_create_body(int64_t m, int64_t n, int64_t nnz, int32_t 
                                                 &plan))
         return st;
     JLUST_HIP_TRY(hipStreamSynchronize(s));
-    spmv_plan_adopt_coo(plan, own.p, sorted ? nullptr : perm, sorted ? nullptr : val_s);
+    spmv_plan_adopt_coo(plan, own.p, sorted ? nullptr : perm, sorted ? nullptr : val_s, sz_rp + 2 * sz_i + sz_v);
     own.p = nullptr;
     *plan_out = plan;
     return JLUST_STATUS_SUCCESS;
@@ -206,3 +206,35 @@ extern "C" int jlust_hip_coo_spmv_plan_create(int64_t m, int64_t n, int64_t nnz,
         return coo_spmv_plan_create_body(m, n, nnz, origin, value_type, rows, cols, val, stream, plan_out);
     });
 }
+
+namespace jlust {
+// A tiny sort of `n` (key, value) pairs through the instantiation `Sort`
+// uses, into a temporary that is freed after the stream drains.
+template <typename K, typename V>
+static int preload_radix_sort(hipStream_t s, int bits)
+{
+    constexpr size_t n = 64;
+    size_t need = 0;
+    JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, need, (K *)nullptr, (K *)nullptr, (V *)nullptr, (V *)nullptr,
+                                            n, 0, bits, s));
+    void *buf = nullptr;
+    const size_t sz = 4 * n * 8 + (need + 255) / 256 * 256;
+    JLUST_HIP_TRY(hipMalloc(&buf, sz));
+    char *b = (char *)buf;
+    K *k0 = (K *)b, *k1 = (K *)(b + n * 8);
+    V *v0 = (V *)(b + 2 * n * 8), *v1 = (V *)(b + 3 * n * 8);
+    hipError_t e = hipMemsetAsync(buf, 0, 4 * n * 8, s);
+    if (e == hipSuccess) e = rocprim::radix_sort_pairs(b + 4 * n * 8, need, k0, k1, v0, v1, n, 0, bits, s);
+    const hipError_t e2 = hipStreamSynchronize(s);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return hip_fail(e, "preload sort");
+    if (e2 != hipSuccess) return hip_fail(e2, "preload sort");
+    return JLUST_STATUS_SUCCESS;
+}
+
+int preload_coo_plan(hipStream_t s)
+{
+    JLUST_PRELOAD_KERNEL(coo_rowptr_kernel);
+    return preload_radix_sort<uint32_t, int32_t>(s, 20);
+}
+}  // namespace jlust

@@ -231,3 +231,11 @@ extern "C" int jlust_hip_csc_spmv_f32_i32(int64_t m, int64_t n, int64_t nnz, int
 {
     return csc_spmv<float>(m, n, nnz, origin, colptr, rowind, val, alpha, x, beta, y, stream);
 }
+
+namespace jlust {
+int preload_coo_spmv()
+{
+    JLUST_PRELOAD_KERNEL(scale_kernel<double>);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

@@ -73,3 +73,11 @@ JLUST_ROWS(jlust_hip_gather_rows_f32, float, true)
 JLUST_ROWS(jlust_hip_scatter_rows_f64, double, false)
 JLUST_ROWS(jlust_hip_scatter_rows_f32, float, false)
 #undef JLUST_ROWS
+
+namespace jlust {
+int preload_dcsr()
+{
+    JLUST_PRELOAD_KERNEL((rows_kernel<double, true>));
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

@@ -78,3 +78,11 @@ extern "C" int jlust_hip_apply_fn_f32(int64_t n, int32_t kind, float a, float b,
 {
     return jlust::apply_fn<float>(n, kind, a, b, src, alpha, beta, dst, stream);
 }
+
+namespace jlust {
+int preload_fn()
+{
+    JLUST_PRELOAD_KERNEL(apply_fn_kernel<double>);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

@@ -285,3 +285,11 @@ extern "C" int jlust_hip_bbm_periodic_spmv_f32(int64_t T, int64_t n_diag_rows, i
     return bbm_periodic<float>(T, n_diag_rows, n_off_rows, n_cols, diag, neg, pos, alpha, x, beta, y,
                                (hipStream_t)stream);
 }
+
+namespace jlust {
+int preload_periodic()
+{
+    JLUST_PRELOAD_KERNEL((bbm_periodic_spmv_kernel<double, 2, 4, true>));
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

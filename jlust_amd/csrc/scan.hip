@@ -113,3 +113,11 @@ int exclusive_scan_i32(const int32_t *in, int32_t *out, int64_t n, jlust_stream_
 }
 
 }  // namespace jlust
+
+namespace jlust {
+int preload_scan()
+{
+    JLUST_PRELOAD_KERNEL(scan_chunk_sums);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

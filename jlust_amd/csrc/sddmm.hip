@@ -685,3 +685,11 @@ extern "C" int jlust_hip_sddmm_plan_destroy(jlust_sddmm_plan_t plan)
     if (e != hipSuccess) return hip_fail(e, "sddmm_plan_destroy");
     return JLUST_STATUS_SUCCESS;
 }
+
+namespace jlust {
+int preload_sddmm()
+{
+    JLUST_PRELOAD_KERNEL(coo_sddmm_kernel<float>);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

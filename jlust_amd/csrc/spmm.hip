@@ -734,3 +734,11 @@ extern "C" int jlust_hip_csr_spmm_plan_destroy(jlust_spmm_plan_t plan)
     if (e != hipSuccess) return hip_fail(e, "spmm_plan_destroy");
     return JLUST_STATUS_SUCCESS;
 }
+
+namespace jlust {
+int preload_spmm()
+{
+    JLUST_PRELOAD_KERNEL(transpose_kernel<float>);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

@@ -1123,11 +1123,13 @@ struct jlust_spmv_plan {
     void *coo_val = nullptr;
     // LDS-binned layout (spmv_binned.hip), or null.
     jlust::BinnedLayout *binned = nullptr;
+    int64_t bytes = 0;               // device memory held by the plan
 };
 
 namespace jlust {
-int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, void *val_copy)
+int spmv_plan_adopt_coo(jlust_spmv_plan_t plan, void *mem, const int32_t *perm, void *val_copy, size_t bytes)
 {
+    plan->bytes += (int64_t)bytes;
     plan->coo_mem = mem;
     plan->coo_perm = perm;
     plan->coo_val = val_copy;
@@ -1214,6 +1216,30 @@ extern "C" int jlust_hip_csr_spmv_f64_i32_noalloc(int64_t m, int64_t n, int64_t 
     double *carry_val = (double *)((char *)base + sizeof(int64_t) * NOALLOC_MAX_BLOCKS);
     return spmv_launch<double>(m, nnz, origin, rowptr, colind, val, alpha, x, beta, y, g, ipt, nullptr,
                                carry_row, carry_val, (hipStream_t)stream);
+}
+
+// The byte limit of a plan's copied layout (JLUST_HIP_PLAN_MAX_BYTES; 0 or
+// unset: none), read at each plan_create.
+static int64_t plan_max_bytes()
+{
+    const char *e = getenv("JLUST_HIP_PLAN_MAX_BYTES");
+    return e ? (int64_t)strtoll(e, nullptr, 10) : 0;
+}
+
+// After an allocation that failed with out of memory: the runtime's sticky
+// last error and this thread's message are cleared before another layout is
+// tried (a later check_launch reads hipGetLastError).
+static void fallback_clear()
+{
+    (void)hipGetLastError();
+    clear_error();
+}
+
+// Temporaries of plan_build_sliced: block counts and checkpoints.
+static size_t sliced_build_temp_bytes(int64_t nnz)
+{
+    const int64_t nblk = (nnz + SB_E - 1) / SB_E, nck = (nnz + SB_CKPT - 1) / SB_CKPT;
+    return align_up(sizeof(int32_t) * NUM_XCD * (size_t)nblk, 256) + sizeof(int32_t) * NUM_XCD * (size_t)nck;
 }
 
 template <typename T>
@@ -1319,38 +1345,27 @@ static int csr_spmv_plan_create_body(int64_t m, int64_t n, int64_t nnz, int32_t 
         delete p;
         return st;
     }
-    p->sliced = layout == LAYOUT_SLICED;
+    // Layouts that copy the matrix (binned, sliced) fall back to the merge or
+    // vector kernels on the caller's arrays when they cannot be allocated:
+    // hipMalloc out of memory, or the layout with its build temporaries above
+    // JLUST_HIP_PLAN_MAX_BYTES.
+    const int64_t cap = plan_max_bytes();
     if (layout == LAYOUT_BINNED) {
-        st = binned_build(&p->binned, value_type, m, n, nnz, origin, rowptr, colind, val, s);
-        if (st) {
+        st = binned_build(&p->binned, value_type, m, n, nnz, origin, rowptr, colind, val, cap, s);
+        if (!st) {
+            p->bytes = binned_bytes(p->binned);
+            *plan_out = p;
+            return JLUST_STATUS_SUCCESS;
+        }
+        if (st != JLUST_STATUS_OUT_OF_MEMORY) {
             delete p;
             return st;
         }
-        *plan_out = p;
-        return JLUST_STATUS_SUCCESS;
+        fallback_clear();
+        layout = LAYOUT_ROWS;
     }
-    if (!p->sliced) {
-        if (m > 0) {
-            st = value_type == 0 ? spmv_grid<double>(m, nnz, p->ipt, &p->grid)
-                                 : spmv_grid<float>(m, nnz, p->ipt, &p->grid);
-            if (!st) st = vector_lanes(m, nnz, origin, rowptr, s, &p->vec_lpr, &p->vec_ulen);
-            if (st) { delete p; return st; }
-        }
-        const size_t nb = (size_t)(p->grid.nblocks > 0 ? p->grid.nblocks : 1);
-        const size_t sz_rows = align_up(sizeof(int64_t) * nb, 256);
-        hipError_t e = hipMalloc(&p->mem, 2 * sz_rows + tsz * nb);
-        if (e != hipSuccess) { delete p; return hip_fail(e, "hipMalloc(spmv plan)"); }
-        p->start_rows = (int64_t *)p->mem;
-        p->carry_row = (int64_t *)((char *)p->mem + sz_rows);
-        p->carry_val = (char *)p->mem + 2 * sz_rows;
-        if (m > 0 && p->vec_lpr == 0) {
-            hipLaunchKernelGGL(merge_start_kernel, dim3((unsigned)p->grid.nblocks), dim3(64), 0, s, m,
-                               nnz, origin, rowptr,
-                               p->grid.tiles_per_block * (int64_t)(SPMV_BLOCK * p->ipt),
-                               p->grid.nblocks, p->start_rows);
-            st = check_launch("merge_start_kernel");
-        }
-    } else {
+    p->sliced = layout == LAYOUT_SLICED;
+    if (p->sliced) {
         p->slice_w = (n + NUM_XCD - 1) / NUM_XCD;
         // Upper bound of blocks per slice: one tile each.
         const int64_t tile = (int64_t)SPMV_BLOCK * p->ipt;
@@ -1361,29 +1376,73 @@ static int csr_spmv_plan_create_body(int64_t m, int64_t n, int64_t nnz, int32_t 
         const size_t sz_y = align_up(tsz * NUM_XCD * (size_t)m, 256);
         const size_t sz_sr = align_up(sizeof(int64_t) * NUM_XCD * (size_t)nb_max, 256);
         const size_t sz_cv = align_up(tsz * NUM_XCD * (size_t)nb_max, 256);
-        hipError_t e = hipMalloc(&p->mem, sz_rp + 2 * sz_ci + sz_v + sz_y + 2 * sz_sr + sz_cv);
-        if (e != hipSuccess) { delete p; return hip_fail(e, "hipMalloc(sliced spmv plan)"); }
-        char *b = (char *)p->mem;
-        p->rowptr_all = (int32_t *)b;  b += sz_rp;
-        p->colind_all = (int32_t *)b;  b += sz_ci;
-        p->perm = (int32_t *)b;        b += sz_ci;
-        p->val_all = b;                b += sz_v;
-        p->ypart = b;                  b += sz_y;
-        p->start_rows = (int64_t *)b;  b += sz_sr;
-        p->carry_row = (int64_t *)b;   b += sz_sr;
-        p->carry_val = b;
-        st = value_type == 0 ? plan_build_sliced<double>(p, stream) : plan_build_sliced<float>(p, stream);
-        if (!st && p->nb > nb_max) st = fail(JLUST_STATUS_HIP_ERROR, "spmv plan: block count overflow");
+        const size_t total = sz_rp + 2 * sz_ci + sz_v + sz_y + 2 * sz_sr + sz_cv;
+        if (cap > 0 && (int64_t)(total + sliced_build_temp_bytes(nnz)) > cap) {
+            st = fail(JLUST_STATUS_OUT_OF_MEMORY, "sliced spmv layout: %lld bytes above JLUST_HIP_PLAN_MAX_BYTES",
+                      (long long)total);
+        } else {
+            const hipError_t e = hipMalloc(&p->mem, total);
+            if (e != hipSuccess) {
+                p->mem = nullptr;
+                st = hip_fail(e, "hipMalloc(sliced spmv plan)");
+            }
+        }
         if (!st) {
-            hipLaunchKernelGGL(sliced_start_kernel, dim3((unsigned)(NUM_XCD * p->nb)), dim3(64), 0, s,
-                               m, p->info, p->rowptr_all, p->nb, (int64_t)SPMV_BLOCK * p->ipt,
-                               p->start_rows);
-            st = check_launch("sliced_start_kernel");
+            char *b = (char *)p->mem;
+            p->rowptr_all = (int32_t *)b;  b += sz_rp;
+            p->colind_all = (int32_t *)b;  b += sz_ci;
+            p->perm = (int32_t *)b;        b += sz_ci;
+            p->val_all = b;                b += sz_v;
+            p->ypart = b;                  b += sz_y;
+            p->start_rows = (int64_t *)b;  b += sz_sr;
+            p->carry_row = (int64_t *)b;   b += sz_sr;
+            p->carry_val = b;
+            p->bytes = (int64_t)total;
+            st = value_type == 0 ? plan_build_sliced<double>(p, stream) : plan_build_sliced<float>(p, stream);
+            if (!st && p->nb > nb_max) st = fail(JLUST_STATUS_HIP_ERROR, "spmv plan: block count overflow");
+            if (!st) {
+                hipLaunchKernelGGL(sliced_start_kernel, dim3((unsigned)(NUM_XCD * p->nb)), dim3(64), 0, s,
+                                   m, p->info, p->rowptr_all, p->nb, (int64_t)SPMV_BLOCK * p->ipt,
+                                   p->start_rows);
+                st = check_launch("sliced_start_kernel");
+            }
+        }
+        if (st == JLUST_STATUS_OUT_OF_MEMORY) {
+            (void)hipStreamSynchronize(s);
+            if (p->mem) (void)hipFree(p->mem);
+            p->mem = nullptr;
+            p->bytes = 0;
+            p->sliced = false;
+            fallback_clear();
+            st = JLUST_STATUS_SUCCESS;
+        }
+    }
+    if (!st && !p->sliced) {
+        if (m > 0) {
+            st = value_type == 0 ? spmv_grid<double>(m, nnz, p->ipt, &p->grid)
+                                 : spmv_grid<float>(m, nnz, p->ipt, &p->grid);
+            if (!st) st = vector_lanes(m, nnz, origin, rowptr, s, &p->vec_lpr, &p->vec_ulen);
+            if (st) { delete p; return st; }
+        }
+        const size_t nb = (size_t)(p->grid.nblocks > 0 ? p->grid.nblocks : 1);
+        const size_t sz_rows = align_up(sizeof(int64_t) * nb, 256);
+        hipError_t e = hipMalloc(&p->mem, 2 * sz_rows + tsz * nb);
+        if (e != hipSuccess) { delete p; return hip_fail(e, "hipMalloc(spmv plan)"); }
+        p->bytes = (int64_t)(2 * sz_rows + tsz * nb);
+        p->start_rows = (int64_t *)p->mem;
+        p->carry_row = (int64_t *)((char *)p->mem + sz_rows);
+        p->carry_val = (char *)p->mem + 2 * sz_rows;
+        if (m > 0 && p->vec_lpr == 0) {
+            hipLaunchKernelGGL(merge_start_kernel, dim3((unsigned)p->grid.nblocks), dim3(64), 0, s, m,
+                               nnz, origin, rowptr,
+                               p->grid.tiles_per_block * (int64_t)(SPMV_BLOCK * p->ipt),
+                               p->grid.nblocks, p->start_rows);
+            st = check_launch("merge_start_kernel");
         }
     }
     if (st) {
         (void)hipStreamSynchronize(s);
-        (void)hipFree(p->mem);
+        if (p->mem) (void)hipFree(p->mem);
         delete p;
         return st;
     }
@@ -1697,7 +1756,8 @@ extern "C" int jlust_hip_spmv_graph_destroy(jlust_spmv_graph_t graph)
     return JLUST_STATUS_SUCCESS;
 }
 
-extern "C" int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *kernel, int32_t *lanes_per_row)
+extern "C" int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *kernel, int32_t *lanes_per_row,
+                                            int64_t *device_bytes)
 {
     clear_error();
     if (!plan || !kernel) return fail(JLUST_STATUS_INVALID_ARGUMENT, "spmv_plan_info: null argument");
@@ -1705,6 +1765,7 @@ extern "C" int jlust_hip_csr_spmv_plan_info(jlust_spmv_plan_t plan, int32_t *ker
               : plan->sliced ? JLUST_SPMV_SLICED
               : plan->vec_lpr > 0 ? JLUST_SPMV_VECTOR : JLUST_SPMV_MERGE;
     if (lanes_per_row) *lanes_per_row = plan->vec_lpr;
+    if (device_bytes) *device_bytes = plan->bytes;
     return JLUST_STATUS_SUCCESS;
 }
 
@@ -1720,3 +1781,11 @@ extern "C" int jlust_hip_csr_spmv_plan_destroy(jlust_spmv_plan_t plan)
     if (e != hipSuccess) return hip_fail(e, "hipFree(plan)");
     return JLUST_STATUS_SUCCESS;
 }
+
+namespace jlust {
+int preload_spmv()
+{
+    JLUST_PRELOAD_KERNEL(spmv_carry_fixup_kernel<double>);
+    return JLUST_STATUS_SUCCESS;
+}
+}  // namespace jlust

@@ -394,7 +394,7 @@ unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
 
 template <typename T>
 int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t *colind, const T *val,
-          hipStream_t s)
+          int64_t max_bytes, hipStream_t s)
 {
     const int64_t m = L->m, nnz = L->nnz;
     const int64_t R = (int64_t)L->S * L->B;
@@ -407,17 +407,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     const size_t sz_pr = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
     const size_t sz_rw = align_up(sizeof(uint16_t) * (size_t)(nnz + 1), 256);
     const size_t sz_pv = align_up(sizeof(T) * (size_t)(nnz + 1), 256);
-    JLUST_HIP_TRY(hipMalloc(&L->mem, sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_rw + sz_pv));
-    char *p = (char *)L->mem;
-    L->sval = p;                 p += sz_v;
-    L->scol = (uint16_t *)p;     p += sz_c;
-    L->perm = (int32_t *)p;      p += sz_p;
-    L->cst = (int32_t *)p;       p += sz_ch;
-    L->cpi = (int32_t *)p;       p += sz_ch;
-    L->pr = (int32_t *)p;        p += sz_pr;
-    L->prow = (uint16_t *)p;     p += sz_rw;
-    L->pval = p;
-
+    const size_t persistent = sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_rw + sz_pv;
     // Temporaries: row counts / rows (nnz + 1), keys, sorted keys, iota,
     // flags / partial indices (nnz + 1), run starts, sort storage.
     uint32_t *nk = nullptr;
@@ -428,8 +418,25 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
                                             (int32_t *)nullptr, (size_t)nnz, 0, bits, s));
     const size_t sz_i = align_up(sizeof(int32_t) * (size_t)(nnz + 1), 256);
     const size_t sz_r = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
+    const size_t temporary = 5 * sz_i + sz_r + align_up(sort_bytes, 256);
+    if (max_bytes > 0 && (int64_t)(persistent + temporary) > max_bytes)
+        return fail(JLUST_STATUS_OUT_OF_MEMORY,
+                    "binned spmv layout: %lld + %lld build bytes above JLUST_HIP_PLAN_MAX_BYTES (%lld)",
+                    (long long)persistent, (long long)temporary, (long long)max_bytes);
+    JLUST_HIP_TRY(hipMalloc(&L->mem, persistent));
+    L->bytes = (int64_t)persistent;
+    char *p = (char *)L->mem;
+    L->sval = p;                 p += sz_v;
+    L->scol = (uint16_t *)p;     p += sz_c;
+    L->perm = (int32_t *)p;      p += sz_p;
+    L->cst = (int32_t *)p;       p += sz_ch;
+    L->cpi = (int32_t *)p;       p += sz_ch;
+    L->pr = (int32_t *)p;        p += sz_pr;
+    L->prow = (uint16_t *)p;     p += sz_rw;
+    L->pval = p;
+
     void *tmp = nullptr;
-    JLUST_HIP_TRY(hipMalloc(&tmp, 5 * sz_i + sz_r + align_up(sort_bytes, 256)));
+    JLUST_HIP_TRY(hipMalloc(&tmp, temporary));
     char *q = (char *)tmp;
     int32_t *cnt = (int32_t *)q;    q += sz_i;
     uint32_t *key = (uint32_t *)q;  q += sz_i;
@@ -554,8 +561,11 @@ bool binned_fits(int value_type, int64_t m, int64_t n, int64_t nnz)
     return geometry(value_type, m, n, nnz, device_info(dev).cu_count, &W, &S, &G, &H, &B);
 }
 
+int64_t binned_bytes(const BinnedLayout *L) { return L ? L->bytes : 0; }
+
 int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64_t nnz, int32_t origin,
-                 const int32_t *rowptr, const int32_t *colind, const void *val, hipStream_t s)
+                 const int32_t *rowptr, const int32_t *colind, const void *val, int64_t max_bytes,
+                 hipStream_t s)
 {
     *out = nullptr;
     int dev = 0;
@@ -572,8 +582,8 @@ int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64
                     (long long)m, (long long)n, (long long)nnz);
     }
     L->nch = L->G * BN_WAVES;
-    const int st = value_type == 0 ? build<double>(L, origin, rowptr, colind, (const double *)val, s)
-                                   : build<float>(L, origin, rowptr, colind, (const float *)val, s);
+    const int st = value_type == 0 ? build<double>(L, origin, rowptr, colind, (const double *)val, max_bytes, s)
+                                   : build<float>(L, origin, rowptr, colind, (const float *)val, max_bytes, s);
     if (st) {
         binned_destroy(L);
         return st;
@@ -612,4 +622,36 @@ void binned_destroy(BinnedLayout *L)
     delete L;
 }
 
+}  // namespace jlust
+
+namespace jlust {
+// A tiny sort of `n` (key, value) pairs through the instantiation `Sort`
+// uses, into a temporary that is freed after the stream drains.
+template <typename K, typename V>
+static int preload_radix_sort(hipStream_t s, int bits)
+{
+    constexpr size_t n = 64;
+    size_t need = 0;
+    JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, need, (K *)nullptr, (K *)nullptr, (V *)nullptr, (V *)nullptr,
+                                            n, 0, bits, s));
+    void *buf = nullptr;
+    const size_t sz = 4 * n * 8 + (need + 255) / 256 * 256;
+    JLUST_HIP_TRY(hipMalloc(&buf, sz));
+    char *b = (char *)buf;
+    K *k0 = (K *)b, *k1 = (K *)(b + n * 8);
+    V *v0 = (V *)(b + 2 * n * 8), *v1 = (V *)(b + 3 * n * 8);
+    hipError_t e = hipMemsetAsync(buf, 0, 4 * n * 8, s);
+    if (e == hipSuccess) e = rocprim::radix_sort_pairs(b + 4 * n * 8, need, k0, k1, v0, v1, n, 0, bits, s);
+    const hipError_t e2 = hipStreamSynchronize(s);
+    (void)hipFree(buf);
+    if (e != hipSuccess) return hip_fail(e, "preload sort");
+    if (e2 != hipSuccess) return hip_fail(e2, "preload sort");
+    return JLUST_STATUS_SUCCESS;
+}
+
+int preload_binned(hipStream_t s)
+{
+    JLUST_PRELOAD_KERNEL(bn_rowmark_kernel);
+    return preload_radix_sort<uint32_t, int32_t>(s, 20);
+}
 }  // namespace jlust

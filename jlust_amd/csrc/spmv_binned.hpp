@@ -24,6 +24,7 @@ struct BinnedLayout {
     int32_t *pr = nullptr;     // [S*B + 1] first partial of run (slice c, bin b) at c*B + b
     uint16_t *prow = nullptr;  // [P + 1] bin-local row of each partial
     void *pval = nullptr;      // [P + 1] partial sums, rewritten by every execute
+    int64_t bytes = 0;         // size of mem
 };
 
 // Whether a matrix of this shape fits the binned layout (slice count, bin
@@ -34,7 +35,10 @@ bool binned_fits(int value_type, int64_t m, int64_t n, int64_t nnz);
 // stream, and waits for it.  val is read once; update refreshes it.
 int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64_t nnz,
                  int32_t origin, const int32_t *rowptr, const int32_t *colind, const void *val,
-                 hipStream_t s);
+                 int64_t max_bytes, hipStream_t s);
+
+// Device bytes the layout holds (its one allocation).
+int64_t binned_bytes(const BinnedLayout *L);
 
 // sval = val[perm] for new values with the same pattern (stream-ordered).
 int binned_update(BinnedLayout *L, const void *val, hipStream_t s);

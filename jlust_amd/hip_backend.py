@@ -9,6 +9,9 @@ CPU path here.
 from __future__ import annotations
 
 import ctypes
+import os
+import weakref
+from collections import OrderedDict
 
 import torch
 
@@ -258,6 +261,8 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
     if is_csr_shaped(u_A.format):
         rowptr, colind = _csr_parts(u_A)
         dev = _check_same_device(rowptr, colind, nonzeros(u_A), x, y)
+        if PLAN_CACHE.enabled and PLAN_CACHE.run(u_A, rowptr, colind, dev, alpha, x, beta, y):
+            return u_y
         with _on(dev):
             st = getattr(L, f"jlust_hip_csr_spmv_{suf}_i32")(
                 m, n, nnz(u_A), u_A.origin.offset, _ptr(rowptr), _ptr(colind),
@@ -276,6 +281,8 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
         return u_y
     rows, cols = _coo_parts(u_A)
     dev = _check_same_device(rows, cols, nonzeros(u_A), x, y)
+    if PLAN_CACHE.enabled and PLAN_CACHE.run(u_A, rows, cols, dev, alpha, x, beta, y):
+        return u_y
     with _on(dev):
         st = getattr(L, f"jlust_hip_coo_spmv_{suf}_i32")(
             m, n, nnz(u_A), u_A.origin.offset, _ptr(rows), _ptr(cols), _ptr(nonzeros(u_A)),
@@ -550,6 +557,184 @@ def _sddmm_dense_checks(u_A: USTensor, u_B: USTensor, u_C: USTensor):
     return A, B
 
 
+# ------------------------------------------------------------- plan cache
+
+class _CachedPlan:
+    """A prepared SpMV plan built for repeated plain calls on one matrix.  It
+    holds weak references to the matrix's buffers only, so the caller's
+    tensors are freed as usual; the plan is dropped when any of them is."""
+
+    __slots__ = ("plan", "suf", "copies", "refs", "pat_ver", "val_ver", "bytes", "dev", "kind",
+                 "_exec", "_exec_values", "__weakref__")
+
+    def __init__(self, u_A: USTensor, idx1, idx2, dev):
+        vals = nonzeros(u_A)
+        coo = is_coo_shaped(u_A.format)
+        self.suf = _value_suffix(u_A)
+        self.dev = dev
+        self.plan = ctypes.c_void_p(0)
+        m, n = u_A.extents
+        create = "jlust_hip_coo_spmv_plan_create" if coo else "jlust_hip_csr_spmv_plan_create"
+        with _on(dev):
+            st = getattr(_lib.lib(), create)(
+                m, n, nnz(u_A), u_A.origin.offset, 0 if self.suf == "f64" else 1, _ptr(idx1), _ptr(idx2),
+                _ptr(vals), _stream(dev), ctypes.byref(self.plan))
+        _lib.check(st, create[10:], u_A.format, _BE, vals.dtype)
+        k, lpr, nb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+        _lib.check(_lib.lib().jlust_hip_csr_spmv_plan_info(self.plan, ctypes.byref(k), ctypes.byref(lpr),
+                                                            ctypes.byref(nb)), "csr_spmv_plan_info")
+        self.kind = ("merge", "vector", "sliced", "binned")[k.value]
+        self.bytes = nb.value
+        # Sliced and binned layouts, and COO plans, run on a copy of the values.
+        self.copies = coo or self.kind in ("sliced", "binned")
+        self.refs = (weakref.ref(idx1), weakref.ref(idx2), weakref.ref(vals))
+        self.pat_ver = (idx1._version, idx2._version)
+        self.val_ver = vals._version
+        L = _lib.lib()
+        self._exec = getattr(L, f"jlust_hip_csr_spmv_plan_execute_{self.suf}")
+        self._exec_values = getattr(L, f"jlust_hip_csr_spmv_plan_execute_values_{self.suf}")
+
+    def valid(self, idx1, idx2, vals) -> bool:
+        r1, r2, r3 = self.refs
+        return (r1() is idx1 and r2() is idx2 and r3() is vals and
+                (idx1._version, idx2._version) == self.pat_ver)
+
+    def launch(self, alpha, x, beta, y, stream) -> int:
+        vals = self.refs[2]()
+        if self.copies and vals._version != self.val_ver:
+            st = self._exec_values(self.plan, vals.data_ptr() if vals.numel() else None, alpha, x, beta, y,
+                                   stream)
+            if st == 0:
+                self.val_ver = vals._version
+            return st
+        return self._exec(self.plan, alpha, x, beta, y, stream)
+
+    def destroy(self):
+        plan, self.plan = self.plan, ctypes.c_void_p(0)
+        if plan.value:
+            try:
+                _lib.lib().jlust_hip_csr_spmv_plan_destroy(plan)
+            except Exception:
+                pass
+
+
+class PlanCache:
+    """Prepared plans for repeated plain SpMV calls, execute(SpMVOp, A, x, y)
+    with a CSR or COO A -- the counterpart of the reference's per-matrix cache
+    of compiled views in its GPU mul! (ext/CUDAExt/ops/block_mul.jl:53,227,
+    327-357).  A matrix is recognised by its index and value tensors (the same
+    objects and device addresses, index tensors not written since: torch's
+    version counters).  Its first `after` plain calls run the plain kernels;
+    the next one builds a plan (the analysis a prepare would do) and every
+    later call runs it.  Values written in place into the value tensor are
+    read again as a prepared handle does; an index tensor written in place, a
+    new tensor, or a freed one drops the plan.  At most `max_plans` plans and
+    `max_bytes` bytes of plan memory are kept (least recently used first out).
+    A plan's kernel may sum a row in another order than the plain call's, so
+    results can change in their last bits, within the parity bar, at the call
+    that switches.  Environment: JLUST_HIP_PLAN_CACHE=0 turns it off;
+    JLUST_HIP_PLAN_CACHE_AFTER (default 2), JLUST_HIP_PLAN_CACHE_PLANS (8),
+    JLUST_HIP_PLAN_CACHE_BYTES (8 GiB)."""
+
+    def __init__(self):
+        env = os.environ.get
+        self.enabled = env("JLUST_HIP_PLAN_CACHE", "1") != "0"
+        self.after = int(env("JLUST_HIP_PLAN_CACHE_AFTER", "2"))
+        self.max_plans = int(env("JLUST_HIP_PLAN_CACHE_PLANS", "8"))
+        self.max_bytes = int(env("JLUST_HIP_PLAN_CACHE_BYTES", str(8 << 30)))
+        self._seen = OrderedDict()     # key -> (plain calls so far, weak refs of the buffers)
+        self._plans = OrderedDict()    # key -> _CachedPlan, least recently used first
+        self._bytes = 0
+
+    @staticmethod
+    def _key(u_A, idx1, idx2, vals, dev, stream):
+        # The stream is part of the key: a plan's partial sums are not shared
+        # between streams, as the plain call's scratch is not.
+        return (idx1.data_ptr(), idx2.data_ptr(), vals.data_ptr(), u_A.extents, nnz(u_A),
+                u_A.origin.offset, vals.dtype, dev.index, is_coo_shaped(u_A.format), stream.value)
+
+    def run(self, u_A: USTensor, idx1, idx2, dev, alpha, x, beta, y) -> bool:
+        """Run the product through a cached plan and return True, or return
+        False (the caller makes the plain call)."""
+        vals = nonzeros(u_A)
+        stream = _stream(dev)
+        key = self._key(u_A, idx1, idx2, vals, dev, stream)
+        ent = self._plans.get(key)
+        if ent is not None:
+            if not ent.valid(idx1, idx2, vals):
+                self._drop(key)
+                ent = None
+            else:
+                self._plans.move_to_end(key)
+        if ent is None:
+            seen = self._seen.get(key)
+            refs = (weakref.ref(idx1), weakref.ref(idx2), weakref.ref(vals))
+            if seen is None or not all(r() is t for r, t in zip(seen[1], (idx1, idx2, vals))) or \
+                    seen[2] != (idx1._version, idx2._version):
+                self._seen[key] = (1, refs, (idx1._version, idx2._version))
+                self._trim_seen()
+                return False
+            count = seen[0] + 1
+            if count <= self.after or torch.cuda.is_current_stream_capturing():
+                # (no plan is built while the stream is captured: a build allocates and synchronises)
+                self._seen[key] = (count, refs, seen[2])
+                return False
+            del self._seen[key]
+            ent = _CachedPlan(u_A, idx1, idx2, dev)
+            self._plans[key] = ent
+            self._bytes += ent.bytes
+            for t in (idx1, idx2, vals):
+                fin = weakref.finalize(t, _plan_cache_forget, weakref.ref(self), key, weakref.ref(ent))
+                fin.atexit = False             # nothing to give back at interpreter exit
+            self._trim()
+            if key not in self._plans:         # larger than the whole budget
+                return False
+        with _on(dev):
+            st = ent.launch(float(alpha), x.data_ptr(), float(beta), y.data_ptr(), stream)
+        _lib.check(st, "csr_spmv_plan_execute", u_A.format, _BE, vals.dtype)
+        return True
+
+    def _trim_seen(self):
+        while len(self._seen) > 64:
+            self._seen.popitem(last=False)
+
+    def _trim(self):
+        while self._plans and (len(self._plans) > self.max_plans or self._bytes > self.max_bytes):
+            self._drop(next(iter(self._plans)))
+
+    def _drop(self, key):
+        ent = self._plans.pop(key, None)
+        if ent is not None:
+            self._bytes -= ent.bytes
+            ent.destroy()
+
+    def forget(self, key, ent):
+        if self._plans.get(key) is ent:
+            self._drop(key)
+
+    def clear(self):
+        """Destroy every cached plan (their device memory is given back)."""
+        for key in list(self._plans):
+            self._drop(key)
+        self._seen.clear()
+
+    def info(self) -> list:
+        """One dict per cached plan: its kernel, device bytes and extents."""
+        return [{"kernel": e.kind, "device_bytes": e.bytes, "extents": k[3], "nnz": k[4]}
+                for k, e in self._plans.items()]
+
+
+def _plan_cache_forget(cache_ref, key, ent_ref):
+    """A buffer of a cached matrix was freed: drop its plan (weakref.finalize
+    callback; the cache and the entry are weakly held)."""
+    cache, ent = cache_ref(), ent_ref()
+    if cache is not None and ent is not None:
+        cache.forget(key, ent)
+
+
+PLAN_CACHE = PlanCache()
+
+
 # -------------------------------------------------------------------- handles
 
 class HIPSpMVHandle(AbstractKernelHandle):
@@ -716,12 +901,20 @@ class HIPSpMVHandle(AbstractKernelHandle):
         _lib.check(st, "csr_spmv_plan_capture", self.u_A.format, _BE, self.T)
         return g
 
+    def _info(self):
+        k, lpr, nb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
+        st = _lib.lib().jlust_hip_csr_spmv_plan_info(self._plan, ctypes.byref(k), ctypes.byref(lpr),
+                                                     ctypes.byref(nb))
+        _lib.check(st, "csr_spmv_plan_info", self.u_A.format, _BE, self.T)
+        return k.value, lpr.value, nb.value
+
     def kernel(self) -> str:
         """The kernel the plan runs: "merge", "vector", "sliced" or "binned"."""
-        k, lpr = ctypes.c_int32(), ctypes.c_int32()
-        st = _lib.lib().jlust_hip_csr_spmv_plan_info(self._plan, ctypes.byref(k), ctypes.byref(lpr))
-        _lib.check(st, "csr_spmv_plan_info", self.u_A.format, _BE, self.T)
-        return ("merge", "vector", "sliced", "binned")[k.value]
+        return ("merge", "vector", "sliced", "binned")[self._info()[0]]
+
+    def device_bytes(self) -> int:
+        """Device memory the plan holds until it is destroyed."""
+        return self._info()[2]
 
     def update_values(self, u_A: USTensor):
         if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A):

@@ -73,7 +73,59 @@ def test_graph_spmv_plan(J, kind, monkeypatch):
     check_replays(lambda: J.execute(h, x, y, alpha=1.5, beta=-0.5), x, y, y0)
 
 
-def test_graph_plain_spmv_and_spmm(J):
+@pytest.fixture()
+def no_plan_cache():
+    """The plain kernels themselves (repeated plain SpMV calls would switch to
+    a cached plan, whose sums may differ in the last bits)."""
+    from jlust_amd import hip_backend as HB
+    was = HB.PLAN_CACHE.enabled
+    HB.PLAN_CACHE.enabled = False
+    yield
+    HB.PLAN_CACHE.enabled = was
+
+
+def test_graph_plain_spmv_cached_plan(J):
+    """Plain SpMV calls that the plan cache has switched to a plan (three
+    calls on the capturing stream first) are captured and replayed; every
+    replay equals an eager call on the same stream, which runs the same
+    cached plan."""
+    import torch
+    from jlust_amd import hip_backend as HB
+    HB.PLAN_CACHE.clear()
+    m, n = 20000, 300000
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(8).integers(0, 60, m), seed=9)
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    x = torch.zeros(n, dtype=torch.float64, device="cuda")
+    y = torch.zeros(m, dtype=torch.float64, device="cuda")
+    y0 = dev(np.random.default_rng(10).uniform(-1, 1, m))
+    s = torch.cuda.Stream()
+    run = lambda: J.execute(J.SpMVOp, A, x, y, alpha=0.5, beta=2.0)  # noqa: E731
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(4):
+            run()
+    torch.cuda.synchronize()
+    assert len(HB.PLAN_CACHE.info()) == 1
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        run()
+    torch.cuda.synchronize()
+    for rep in range(4):
+        x.uniform_(-1.0, 1.0)
+        y.copy_(y0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        got = host(y).copy()
+        y.copy_(y0)
+        with torch.cuda.stream(s):
+            run()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got, host(y), err_msg=f"replay {rep}")
+    HB.PLAN_CACHE.clear()
+
+
+def test_graph_plain_spmv_and_spmm(J, no_plan_cache):
     import torch
     m, n, k = 5000, 4000, 24
     rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(3).integers(0, 40, m),

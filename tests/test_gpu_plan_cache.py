@@ -1,0 +1,156 @@
+"""Repeated plain SpMV calls reuse a cached plan (hip_backend.PLAN_CACHE, the
+counterpart of the reference's per-matrix cache in its GPU mul!,
+ext/CUDAExt/ops/block_mul.jl:53,227,327-357): every call matches the oracle,
+before and after the switch to the plan; the plan is dropped when an index
+tensor is written in place, when other tensors are passed, and when the
+matrix's tensors are freed (its device memory is given back); values written
+in place are seen."""
+import gc
+
+import numpy as np
+import pytest
+
+from tests._util import assert_within, dev, host, random_csr
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def J():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    import jlust_amd
+    return jlust_amd
+
+
+@pytest.fixture(scope="module")
+def O():
+    from oracle import oracle
+    return oracle
+
+
+@pytest.fixture()
+def cache():
+    from jlust_amd import hip_backend as HB
+    c = HB.PLAN_CACHE
+    saved = (c.enabled, c.after, c.max_plans, c.max_bytes)
+    c.clear()
+    c.enabled, c.after = True, 2
+    yield c
+    c.clear()
+    c.enabled, c.after, c.max_plans, c.max_bytes = saved
+
+
+def _powerlaw(m, n, seed):
+    rng = np.random.default_rng(seed)
+    lens = np.minimum((rng.pareto(1.8, m) + 1) * 6, n).astype(np.int64)
+    return random_csr(m, n, lengths=lens, seed=seed)
+
+
+@pytest.mark.parametrize("slice_mode", ["auto", "2"])
+def test_plain_calls_switch_to_a_plan(J, O, cache, slice_mode, monkeypatch):
+    import torch
+    if slice_mode == "2":
+        monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")     # the binned layout
+    m, n = 60000, 50000
+    rowptr, colind, val = _powerlaw(m, n, 90)
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    rng = np.random.default_rng(91)
+    for call in range(6):
+        x = rng.uniform(-1, 1, n)
+        y0 = rng.uniform(-1, 1, m)
+        y = dev(y0)
+        J.execute(J.SpMVOp, A, dev(x), y, alpha=1.5, beta=-0.5)
+        ref = O.csr_spmv(rowptr, colind, val, x, 1.5, -0.5, y0)
+        absref = O.csr_spmv_absref(rowptr, colind, val, x, 1.5, -0.5, y0)
+        assert_within(host(y), ref, absref, np.float64, f"call {call}")
+        assert len(cache.info()) == (1 if call >= 2 else 0), (call, cache.info())
+    if slice_mode == "2":
+        assert cache.info()[0]["kernel"] == "binned"
+        # values written in place through torch: the plan's copy is refreshed
+        J.nonzeros(A).mul_(2.0)
+        x = rng.uniform(-1, 1, n)
+        y = torch.empty(m, dtype=torch.float64, device="cuda")
+        J.execute(J.SpMVOp, A, dev(x), y)
+        assert_within(host(y), O.csr_spmv(rowptr, colind, 2.0 * val, x),
+                      O.csr_spmv_absref(rowptr, colind, 2.0 * val, x), np.float64, "in-place values")
+
+
+def test_cache_invalidation_and_release(J, O, cache):
+    import torch
+    m, n = 40000, 40000
+    rowptr, colind, val = _powerlaw(m, n, 92)
+    rp, ci, v = dev(rowptr), dev(colind), dev(val)
+    A = J.csr_tensor(rp, ci, v, (m, n))
+    x = np.random.default_rng(93).uniform(-1, 1, n)
+    xd = dev(x)
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    for _ in range(3):
+        J.execute(J.SpMVOp, A, xd, y)
+    assert len(cache.info()) == 1
+    # an index tensor written in place (another valid pattern): the plan is dropped
+    colind2 = colind.copy()
+    row0 = slice(rowptr[0] - 1, rowptr[1] - 1)
+    colind2[row0] = np.sort(np.random.default_rng(94).choice(n, size=row0.stop - row0.start,
+                                                              replace=False)) + 1
+    ci.copy_(dev(colind2))
+    J.execute(J.SpMVOp, A, xd, y)
+    assert len(cache.info()) == 0
+    assert_within(host(y), O.csr_spmv(rowptr, colind2, val, x), O.csr_spmv_absref(rowptr, colind2, val, x),
+                  np.float64, "after an in-place pattern write")
+    for _ in range(3):
+        J.execute(J.SpMVOp, A, xd, y)
+    assert len(cache.info()) == 1
+    # other tensors (copies of the same arrays) are another matrix
+    A2 = J.csr_tensor(rp.clone(), ci.clone(), v.clone(), (m, n))
+    J.execute(J.SpMVOp, A2, xd, y)
+    assert len(cache.info()) == 1
+    assert_within(host(y), O.csr_spmv(rowptr, colind2, val, x), O.csr_spmv_absref(rowptr, colind2, val, x),
+                  np.float64, "another matrix")
+    # freeing the matrix's tensors drops the plan and gives its memory back
+    torch.cuda.synchronize()
+    del A, A2, rp, ci, v
+    gc.collect()
+    torch.cuda.synchronize()
+    assert cache.info() == []
+
+
+def test_cache_budget_and_switch(J, O, cache):
+    import torch
+    m, n = 30000, 30000
+    mats = [_powerlaw(m, n, s) for s in (95, 96, 97)]
+    As = [J.csr_tensor(dev(a), dev(b), dev(c), (m, n)) for a, b, c in mats]
+    x = np.random.default_rng(98).uniform(-1, 1, n)
+    xd = dev(x)
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    cache.max_plans = 2
+    for A in As:
+        for _ in range(3):
+            J.execute(J.SpMVOp, A, xd, y)
+    assert len(cache.info()) == 2                        # the least recently used one is out
+    for (rowptr, colind, val), A in zip(mats, As):
+        J.execute(J.SpMVOp, A, xd, y)
+        assert_within(host(y), O.csr_spmv(rowptr, colind, val, x), O.csr_spmv_absref(rowptr, colind, val, x),
+                      np.float64, "budget")
+    cache.clear()
+    cache.enabled = False
+    for _ in range(4):
+        J.execute(J.SpMVOp, As[0], xd, y)
+    assert cache.info() == []
+
+
+def test_coo_plain_calls_switch_to_a_plan(J, O, cache):
+    import torch
+    m, n = 20000, 25000
+    rowptr, colind, val = _powerlaw(m, n, 99)
+    rows = np.repeat(np.arange(1, m + 1, dtype=np.int32), np.diff(rowptr))
+    p = np.random.default_rng(100).permutation(rows.size)
+    A = J.coo_tensor(dev(rows[p]), dev(colind[p]), dev(val[p]), (m, n))
+    x = np.random.default_rng(101).uniform(-1, 1, n)
+    ref = O.csr_spmv(rowptr, colind, val, x)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x)
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    for call in range(4):
+        J.execute(J.SpMVOp, A, dev(x), y)
+        assert_within(host(y), ref, absref, np.float64, f"COO call {call}")
+    assert len(cache.info()) == 1

@@ -82,3 +82,63 @@ def test_spmm_two_streams(J, O):
         for i in range(3):
             ref, absref = refs[s][i]
             assert_within(host(Cs[s][i]), ref, absref, np.float64, f"stream {s} call {i}")
+
+
+@pytest.mark.parametrize("kind", ["binned", "coo"])
+def test_update_values_is_stream_ordered(J, O, kind, monkeypatch):
+    """update_values_ on a plan that copies its values (the LDS-binned layout;
+    a COO plan whose entries were reordered) is enqueued on the caller's
+    stream (jlust_hip_csr_spmv_plan_update_values takes the stream): it returns
+    at once and its work, and a product after it, complete while long work
+    queued before it on another stream is still running.  The product then
+    sees the new values (parity against the oracle)."""
+    import time
+
+    import torch
+    if kind == "binned":
+        monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m, n = 200000, 150000
+    rowptr, colind, val = random_csr(m, n, lengths=np.full(m, 12), seed=76)
+    if kind == "coo":
+        rows = np.repeat(np.arange(1, m + 1, dtype=np.int32), np.diff(rowptr))
+        p = np.random.default_rng(77).permutation(rows.size)
+        rows, cols, v0 = rows[p], colind[p], val[p]
+        A = J.coo_tensor(dev(rows), dev(cols), dev(v0), (m, n))
+    else:
+        A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    if kind == "binned":
+        assert h.kernel() == "binned"
+    rng = np.random.default_rng(78)
+    x = rng.uniform(-1, 1, n)
+    newval = rng.uniform(-1, 1, val.size)
+    A2 = J.USTensor(A.extents, A.format, A.pos_buffers, A.crd_buffers, dev(newval), None, A.origin)
+    xd = dev(x)
+    y = torch.full((m,), float("nan"), dtype=torch.float64, device="cuda")
+    big = torch.randn(8192, 8192, device="cuda")
+    out = torch.empty_like(big)
+    sA, sB = torch.cuda.Stream(), torch.cuda.Stream()        # default priority
+    torch.cuda.synchronize()
+    with torch.cuda.stream(sB):
+        for _ in range(60):
+            torch.mm(big, big, out=out)
+    t0 = time.perf_counter()
+    with torch.cuda.stream(sA):
+        J.update_values_(h, A2)
+        J.execute(h, xd, y)
+        done = torch.cuda.Event()
+        done.record(sA)
+    host_s = time.perf_counter() - t0
+    done.synchronize()
+    b_running = not sB.query()
+    torch.cuda.synchronize()
+    assert b_running, "the update and product waited for the other stream's queued work"
+    assert host_s < 0.05, f"update_values_ + execute took {host_s * 1e3:.1f} ms on the host"
+    if kind == "coo":
+        r0 = np.repeat(np.arange(1, m + 1, dtype=np.int32), np.diff(rowptr))[p]
+        ref = O.coo_spmv(r0, cols, newval, x, m)
+        absref = O.csr_spmv_absref(rowptr, colind, np.abs(newval[np.argsort(p)]), np.abs(x))
+    else:
+        ref = O.csr_spmv(rowptr, colind, newval, x)
+        absref = O.csr_spmv_absref(rowptr, colind, newval, x)
+    assert_within(host(y), ref, absref, np.float64, f"{kind} plan after a stream-ordered update")
