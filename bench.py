@@ -1129,6 +1129,72 @@ def cpu_baseline(cfg, budget_s):
             round(W.flops(cfg) / tmin / 1e9, 3)}
 
 
+def plain_call_timings(cfg, steps, warmup):
+    """The plain call execute(SpMVOp, A, x, y) on the same matrix, as unchanged
+    JLUST code makes it: its first call (one synchronised call: the plain
+    kernels, no plan yet), its steady state (from the third call on the plan
+    cache runs a plan built for this matrix), and the steady state with the
+    cache off (the plain kernels every call)."""
+    import torch
+    from jlust_amd import hip_backend as HB
+    from jlust_amd import workloads as W
+    nbytes = W.algorithmic_bytes(cfg)
+    pstep, pkname, _, pkeep = build_step(cfg, use_plan=False)
+    HB.PLAN_CACHE.clear()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    pstep()
+    torch.cuda.synchronize()
+    first_ms = (time.perf_counter() - t0) * 1e3
+    p_ms, p_launch = timed(pstep, steps, warmup)
+    info = HB.PLAN_CACHE.info()
+    HB.PLAN_CACHE.clear()
+    HB.PLAN_CACHE.enabled = False
+    try:
+        u_ms, u_launch = timed(pstep, steps, warmup)
+    finally:
+        HB.PLAN_CACHE.enabled = True
+    del pkeep
+    return {"value": round(nbytes / (p_ms * 1e-3) / 1e9, 3), "ms_per_step": round(p_ms, 6),
+            "per_launch_ms": round(p_launch, 6),
+            "kernel": f"cached plan ({info[0]['kernel']})" if info else pkname,
+            "first_call_ms": round(first_ms, 4),
+            "cache": "calls 1-2 on a matrix run the plain kernels; the 3rd builds a plan for it "
+                     "(jlust_amd.hip_backend.PLAN_CACHE, JLUST_HIP_PLAN_CACHE=0 turns it off) and "
+                     "later calls run that plan; the warm-up covers the switch",
+            "uncached": {"value": round(nbytes / (u_ms * 1e-3) / 1e9, 3), "ms_per_step": round(u_ms, 6),
+                         "per_launch_ms": round(u_launch, 6), "kernel": pkname}}
+
+
+def emitter_handle_timing(cfg, keep, steps, warmup):
+    """The emitter-form handle call execute(h, A, x, y) as a binding without
+    torch's version counters makes it (the Julia ccall of INTEGRATION.md):
+    every call re-reads A's values into the plan -- a gather through the
+    plan's permutation for the copying layouts, a pointer for the others --
+    then runs the product (jlust_hip_csr_spmv_plan_execute_values_*)."""
+    import torch
+    from jlust_amd import _lib
+    from jlust_amd import workloads as W
+    A, x, y, h = keep
+    import jlust_amd as J
+    fn = getattr(_lib.lib(), f"jlust_hip_csr_spmv_plan_execute_values_{h.suf}")
+    vp, xp, yp = J.nonzeros(A).data_ptr(), x.data_ptr(), y.data_ptr()
+    stream = _lib.stream_handle(x.device)
+
+    def step():
+        st = fn(h._plan, vp, 1.0, xp, 0.0, yp, stream)
+        if st:
+            _lib.check(st, "csr_spmv_plan_execute_values")
+    e_ms, e_launch = timed(step, steps, warmup)
+    h.update_values(A)                # the handle's own record of the values it holds
+    torch.cuda.synchronize()
+    nbytes = W.algorithmic_bytes(cfg)
+    return {"value": round(nbytes / (e_ms * 1e-3) / 1e9, 3), "ms_per_step": round(e_ms, 6),
+            "per_launch_ms": round(e_launch, 6), "kernel": h.kernel(),
+            "refresh": "values re-read on every call (a gather through the plan's permutation for "
+                       "the binned and sliced layouts; nothing to copy for merge and vector plans)"}
+
+
 def timed(step, steps, warmup):
     """W untimed steps, then exactly K steps bracketed by synchronize() (the
     wall-clock pass), then K more steps between one pair of HIP events
@@ -1255,13 +1321,10 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
     step, kname, bound, keep = build_step(cfg, use_plan=use_plan)
     ms_per_step, per_launch_ms = timed(step, steps, warmup)
     plain = None
+    emitter = None
     if use_plan:
-        pstep, pkname, _, pkeep = build_step(cfg, use_plan=False)
-        p_ms, p_launch = timed(pstep, steps, warmup)
-        plain = {"value": round(W.algorithmic_bytes(cfg) / (p_ms * 1e-3) / 1e9, 3),
-                 "ms_per_step": round(p_ms, 6), "kernel": pkname,
-                 "per_launch_ms": round(p_launch, 6)}
-        del pkeep
+        plain = plain_call_timings(cfg, steps, warmup)
+        emitter = emitter_handle_timing(cfg, keep, steps, warmup)
     log(f"config {config}: {steps} steps: wall {ms_per_step:.4f} ms/step, events "
         f"{per_launch_ms:.4f} ms/step")
     s_min, s_med, s_b = timed_samples(step, per_launch_ms)
@@ -1293,6 +1356,8 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
     roof["traffic"], counters = counters_for(cfg["name"] + (":plan" if use_plan else ""))
     if counters:
         roof["counters"] = counters
+    roof["traffic_source"] = ("profiles/pmc_traffic.json: the committed rocprofv3 --pmc passes of this "
+                              "workload (read by bench.py, not measured in this run)")
     roof["traffic_counts"] = ("L2-miss bytes (FETCH_SIZE x 2.0 + WRITE_SIZE, rocprofv3 --pmc): "
                               "requests leaving the L2s, served by the MALL or by HBM")
     roof["kernel"] = kname
@@ -1320,7 +1385,7 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 3),
         "algorithmic_bytes": int(nbytes), "flops": int(nflops),
         "roofline": roof, "samples": samples, "plain_call": plain, "plan_build_ms": plan_build_ms,
-        "cpu_baseline": cpu,
+        "emitter_handle": emitter, "cpu_baseline": cpu,
     }
     if cold_res is not None:
         out["cold"] = cold_res
@@ -1333,6 +1398,9 @@ def bench_config(config, steps, warmup, cpu_seconds, no_plan=False, no_cpu=False
 # Steps per configuration when bench.py runs them all (the driver's default
 # run): enough events for a stable mean while the five fit in a few minutes.
 ALL_STEPS = {1: 200, 2: 200, 3: 30, 4: 30, 5: 30}
+# Configurations timed cold as well by default (config 1's figures are quoted
+# in both cache states: its operands fit the L2s and the MALL).
+COLD_CONFIGS = (1,)
 
 
 def main():
@@ -1401,8 +1469,19 @@ def main():
         return
     steps = args.steps if args.steps is not None else ALL_STEPS[args.config]
     warmup = args.warmup if args.warmup is not None else 5
+    # The library's device code loaded once, before anything is timed (what a
+    # server does at start-up): otherwise the first plan build of the process
+    # also pays the runtime's one-time code-object loading.
+    import jlust_amd as J
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    J.preload()
+    torch.cuda.synchronize()
+    preload_ms = (time.perf_counter() - t0) * 1e3
+    log(f"preload {preload_ms:.1f} ms")
     out = bench_config(args.config, steps, warmup, args.cpu_seconds, args.no_plan,
-                       args.no_cpu_baseline, args.cold)
+                       args.no_cpu_baseline, args.cold or args.config in COLD_CONFIGS)
+    out["preload_ms"] = round(preload_ms, 2)
     if not args.only:
         # Every BASELINE configuration in the same run, the headline first.
         rows = []
@@ -1411,11 +1490,11 @@ def main():
                 e = out
             else:
                 e = bench_config(c, ALL_STEPS[c], warmup, args.other_cpu_seconds,
-                                 no_cpu=args.no_cpu_baseline)
+                                 no_cpu=args.no_cpu_baseline, cold=args.cold or c in COLD_CONFIGS)
             rows.append({k: e[k] for k in ("config", "value", "unit", "ms_per_step", "gflops",
                                            "pct_hbm_peak", "dtype", "algorithmic_bytes", "flops",
                                            "roofline", "samples", "plain_call", "plan_build_ms",
-                                           "cpu_baseline")})
+                                           "emitter_handle", "cold", "cpu_baseline") if k in e})
         out["all_configs"] = rows
     print(json.dumps(out), flush=True)
 

@@ -33,4 +33,6 @@ from .tensor import (CPUDevice, HIPDevice, OneBased, USTensor, ZeroBased, bsr_te
                      has_coordinates, has_positions, index_origin, materialize, nnz, nonzeros,
                      periodic_csr_tensor, positions, shifted_diag_tensor, size, ust)
 
+from . import hip_backend as _hip_backend  # noqa: F401  (the backend, loaded with the package)
+
 __all__ = [n for n in dir() if not n.startswith("_")]

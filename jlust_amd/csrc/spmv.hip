@@ -1363,6 +1363,7 @@ static int csr_spmv_plan_create_body(int64_t m, int64_t n, int64_t nnz, int32_t 
         }
         fallback_clear();
         layout = LAYOUT_ROWS;
+        st = JLUST_STATUS_SUCCESS;
     }
     p->sliced = layout == LAYOUT_SLICED;
     if (p->sliced) {

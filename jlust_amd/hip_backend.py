@@ -601,7 +601,9 @@ class _CachedPlan:
 
     def launch(self, alpha, x, beta, y, stream) -> int:
         vals = self.refs[2]()
-        if self.copies and vals._version != self.val_ver:
+        if vals._version != self.val_ver:
+            # Written in place (or its storage replaced): a copying plan gathers
+            # the values again, the others take the address again.
             st = self._exec_values(self.plan, vals.data_ptr() if vals.numel() else None, alpha, x, beta, y,
                                    stream)
             if st == 0:
@@ -653,9 +655,10 @@ class PlanCache:
         return (idx1.data_ptr(), idx2.data_ptr(), vals.data_ptr(), u_A.extents, nnz(u_A),
                 u_A.origin.offset, vals.dtype, dev.index, is_coo_shaped(u_A.format), stream.value)
 
-    def run(self, u_A: USTensor, idx1, idx2, dev, alpha, x, beta, y) -> bool:
+    def run(self, u_A: USTensor, idx1, idx2, dev, alpha, x, beta, y, fast=None) -> bool:
         """Run the product through a cached plan and return True, or return
-        False (the caller makes the plain call)."""
+        False (the caller makes the plain call).  `fast`: the fast path's
+        record of this matrix, which keeps the plan it runs."""
         vals = nonzeros(u_A)
         stream = _stream(dev)
         key = self._key(u_A, idx1, idx2, vals, dev, stream)
@@ -689,6 +692,8 @@ class PlanCache:
             self._trim()
             if key not in self._plans:         # larger than the whole budget
                 return False
+        if fast is not None:
+            fast.key, fast.ent = key, ent
         with _on(dev):
             st = ent.launch(float(alpha), x.data_ptr(), float(beta), y.data_ptr(), stream)
         _lib.check(st, "csr_spmv_plan_execute", u_A.format, _BE, vals.dtype)
@@ -722,6 +727,88 @@ class PlanCache:
         """One dict per cached plan: its kernel, device bytes and extents."""
         return [{"kernel": e.kind, "device_bytes": e.bytes, "extents": k[3], "nnz": k[4]}
                 for k, e in self._plans.items()]
+
+
+class _SpMVFast:
+    """What the plain SpMV fast path keeps about one CSR/COO USTensor: its
+    buffers as checked once (identity-compared at every call), the device,
+    value type and entry point, and the cached plan it last ran."""
+
+    __slots__ = ("pos", "crd", "val", "fmt", "origin", "extents", "idx1", "idx2", "dev", "di", "T", "m",
+                 "n", "coo", "plain", "key", "ent")
+
+    def matches(self, u: USTensor) -> bool:
+        return (u.val is self.val and u.pos_buffers is self.pos and u.crd_buffers is self.crd and
+                u.format is self.fmt and u.origin is self.origin and u.extents is self.extents)
+
+
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+_DENSE1 = Formats.DensedRight(1)
+
+
+def spmv_fast(u_A: USTensor, x: torch.Tensor, y: torch.Tensor, alpha, beta):
+    """execute(SpMVOp, A, x, y; alpha, beta) for a CSR or COO A on the GPU and
+    plain contiguous device vectors of its value type: the checks of the
+    general path done once per matrix and then reduced to identity and
+    attribute compares, the plan cache consulted directly.  Returns the
+    output USTensor, or None when the call needs the general path (which then
+    raises or handles what this one does not)."""
+    st = u_A.__dict__.get("_hip_spmv")
+    if st is None or not st.matches(u_A):
+        st = _spmv_fast_state(u_A)
+        if st is None:
+            return None
+    di = st.di
+    if (x.dtype is not st.T or y.dtype is not st.T or x.get_device() != di or y.get_device() != di or
+            x.numel() != st.n or y.numel() != st.m or not x.is_contiguous() or not y.is_contiguous() or
+            _RAW_STREAM is None):
+        return None
+    if st.m == 0:
+        return None
+    stream = _RAW_STREAM(di)
+    with _on(st.dev):
+        ent = st.ent
+        if (ent is not None and ent.plan.value and (st.key[-1] or 0) == stream and PLAN_CACHE.enabled and
+                PLAN_CACHE._plans.get(st.key) is ent and ent.valid(st.idx1, st.idx2, st.val)):
+            PLAN_CACHE._plans.move_to_end(st.key)
+            status = ent.launch(float(alpha), x.data_ptr(), float(beta), y.data_ptr(), stream)
+            if status:
+                _lib.check(status, "csr_spmv_plan_execute", u_A.format, _BE, st.T)
+        elif not (PLAN_CACHE.enabled and
+                  PLAN_CACHE.run(u_A, st.idx1, st.idx2, st.dev, alpha, x, beta, y, fast=st)):
+            status = st.plain(st.m, st.n, st.val.numel(), st.origin.offset, st.idx1.data_ptr(),
+                              st.idx2.data_ptr(), st.val.data_ptr(), alpha, x.data_ptr(), beta,
+                              y.data_ptr(), stream)
+            if status:
+                _lib.check(status, "coo_spmv" if st.coo else "csr_spmv", u_A.format, _BE, st.T)
+    return USTensor((st.m,), _DENSE1, (None,), (None,), y, y)     # ust(y), built directly
+
+
+def _spmv_fast_state(u_A: USTensor):
+    """Check a matrix once for the fast path (the general path's checks) and
+    record it on the USTensor; None when the fast path does not apply."""
+    f = u_A.format
+    coo = is_coo_shaped(f)
+    if not (is_csr_shaped(f) or coo):
+        return None
+    try:
+        suf = _value_suffix(u_A)
+        idx1, idx2 = _coo_parts(u_A) if coo else _csr_parts(u_A)
+        _check_values(u_A, nonzeros(u_A).dtype)
+        dev = _check_same_device(idx1, idx2, nonzeros(u_A))
+    except Exception:
+        return None                           # the general path raises it
+    st = _SpMVFast()
+    st.pos, st.crd, st.val, st.fmt = u_A.pos_buffers, u_A.crd_buffers, u_A.val, u_A.format
+    st.origin, st.extents = u_A.origin, u_A.extents
+    st.idx1, st.idx2, st.dev, st.di = idx1, idx2, dev, dev.index
+    st.T = nonzeros(u_A).dtype
+    st.m, st.n = u_A.extents
+    st.coo = coo
+    st.plain = getattr(_lib.lib(), f"jlust_hip_{'coo' if coo else 'csr'}_spmv_{suf}_i32")
+    st.key, st.ent = None, None
+    u_A.__dict__["_hip_spmv"] = st
+    return st
 
 
 def _plan_cache_forget(cache_ref, key, ent_ref):
@@ -825,8 +912,11 @@ class HIPSpMVHandle(AbstractKernelHandle):
 
     def _stale(self) -> bool:
         """Whether the plan must read its value tensor again before a product:
-        a new tensor (_rebind), or one a copying plan holds written in place."""
-        return self._ver < 0 or (self._copies and self._vals._version != self._ver)
+        a new tensor (_rebind), or one whose torch version moved (written in
+        place: a copying plan gathers it again; for a plan that reads the
+        tensor in place only its address is taken again, in case its storage
+        was replaced)."""
+        return self._ver < 0 or self._vals._version != self._ver
 
     def _launch(self, alpha, x_ptr, beta, y_ptr, stream):
         """One plan execute on raw pointers; through execute_values when the

@@ -10,6 +10,8 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Tuple
 
+import torch
+
 from .errors import UnsupportedFormat
 from .formats import TensorFormat
 from .tensor import USTensor, device_of, nonzeros, ust
@@ -97,9 +99,21 @@ def _wrap(a):
     return a if isinstance(a, (USTensor, AbstractKernelHandle)) else ust(a)
 
 
+_ALPHA_BETA = frozenset(("alpha", "beta"))
+
+
 def execute(optype, *args, backend=None, **kw):
     """execute(OpType, tensors...; backend, kw...)   (src/convenience.jl:15-39)
     execute(handle, tensors...; kw...)             (handle-driven call)."""
+    if optype is SpMVOp and backend is None and len(args) == 3 and (not kw or kw.keys() <= _ALPHA_BETA):
+        # The plain SpMV call on device vectors: HIPBackend's fast path (the
+        # same checks, made once per matrix); anything it does not take goes on.
+        A, x, y = args
+        if type(A) is USTensor and type(x) is torch.Tensor and type(y) is torch.Tensor:
+            from . import hip_backend
+            r = hip_backend.spmv_fast(A, x, y, kw.get("alpha", 1.0), kw.get("beta", 0.0))
+            if r is not None:
+                return r
     if isinstance(optype, AbstractKernelHandle) or (args and isinstance(args[0], AbstractKernelHandle)):
         h, rest = (optype, args) if isinstance(optype, AbstractKernelHandle) else (args[0], args[1:])
         if getattr(h, "takes_raw", False):

@@ -207,3 +207,33 @@ def test_binned_slice_count_limit(J, O, dtype, n, fits, monkeypatch):
     ref = O.csr_spmv(rowptr, colind, val, x)
     absref = O.csr_spmv_absref(rowptr, colind, val, x)
     assert_within(y, ref, absref, dtype, f"slice limit n={n}")
+
+
+@pytest.mark.parametrize("mode", ["2", "1"])
+def test_copied_layout_falls_back_to_merge_when_over_budget(J, O, mode, monkeypatch):
+    """A plan whose copied layout (binned "2", sliced "1") with its build
+    temporaries would exceed JLUST_HIP_PLAN_MAX_BYTES -- the path an
+    allocation failure takes -- is built on the merge/vector kernels over the
+    caller's arrays instead, with no error, and computes the same product; the
+    layout is taken again once the budget allows it."""
+    import torch
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", mode)
+    m, n = 120000, 900000
+    rowptr, colind, val = random_csr(m, n, lengths=np.random.default_rng(3).integers(4, 30, m), seed=4)
+    A = J.csr_tensor(dev(rowptr), dev(colind), dev(val), (m, n))
+    x = np.random.default_rng(5).uniform(-1, 1, n)
+    ref = O.csr_spmv(rowptr, colind, val, x)
+    absref = O.csr_spmv_absref(rowptr, colind, val, x)
+    monkeypatch.setenv("JLUST_HIP_PLAN_MAX_BYTES", str(4 << 20))
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    assert h.kernel() in ("merge", "vector")
+    assert h.device_bytes() < (4 << 20)
+    y = torch.empty(m, dtype=torch.float64, device="cuda")
+    J.execute(h, dev(x), y)
+    assert_within(host(y), ref, absref, np.float64, "fallback plan")
+    monkeypatch.delenv("JLUST_HIP_PLAN_MAX_BYTES")
+    h2 = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    assert h2.kernel() == {"2": "binned", "1": "sliced"}[mode]
+    assert h2.device_bytes() > 12 * rowptr[-1]
+    J.execute(h2, dev(x), y)
+    assert_within(host(y), ref, absref, np.float64, "layout plan")
