@@ -553,13 +553,24 @@ def bsr_f64():
         return s.elapsed_time(e) / reps
 
     t_mfma = ms(lambda: J.execute(J.SpMMOp, A, B, C))
+    old = os.environ.get("JLUST_HIP_BSR_STRIP")
+    os.environ["JLUST_HIP_BSR_STRIP"] = "0"           # the per-row kernel the strip kernel replaced
+    try:
+        t_row = ms(lambda: J.execute(J.SpMMOp, A, B, C))
+    finally:
+        if old is None:
+            del os.environ["JLUST_HIP_BSR_STRIP"]
+        else:
+            os.environ["JLUST_HIP_BSR_STRIP"] = old
     Acsr = _bsr_as_csr(A)
     t_csr = ms(lambda: J.execute(J.SpMMOp, Acsr, B, C), reps=3)
+    tf = lambda t: round(flops / (t * 1e-3) / 1e12, 2)  # noqa: E731
     res = {"workload": "bsr16_spmm_f64_banded_65536x8_k256", "flops": flops,
-           "mfma_ms": round(t_mfma, 4), "mfma_tflops": round(flops / (t_mfma * 1e-3) / 1e12, 2),
+           "kernel": "bsr16_spmm_f64_strip_kernel",
+           "mfma_ms": round(t_mfma, 4), "mfma_tflops": tf(t_mfma),
            "mfma_pct_of_fp64_peak": round(100 * flops / (t_mfma * 1e-3) / 78.6e12, 1),
-           "csr_expansion_ms": round(t_csr, 3),
-           "csr_expansion_tflops": round(flops / (t_csr * 1e-3) / 1e12, 2)}
+           "row_kernel_ms": round(t_row, 4), "row_kernel_tflops": tf(t_row),
+           "csr_expansion_ms": round(t_csr, 3), "csr_expansion_tflops": tf(t_csr)}
     log(f"bsr f64: {res}")
     return res
 

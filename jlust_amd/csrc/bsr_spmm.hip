@@ -556,6 +556,274 @@ void bsr16_spmm_strip_kernel(
     __builtin_amdgcn_s_waitcnt(0);
 }
 
+// Float64 strip kernel (row-major blocks; values, B and C 32-byte aligned,
+// ldb and ldc multiples of 4; 16 columns of B or C span less than 2^31 bytes).
+// The fp32 strip kernel's design on v_mfma_f64_16x16x4_f64: a workgroup of
+// BSR64_SR waves owns that many consecutive block-rows, one wave each, with
+// the row's blocks (up to BSR_QCHUNK) held as A operands in registers for all
+// of k; for each 16-column tile the strip's window of B (block-rows
+// [J_min, J_max], each column one contiguous run of 128 bytes per block-row)
+// is copied to LDS with direct global-to-LDS loads; every wave reads its B
+// operands from the window, a barrier frees it, and the next tile's copies
+// are issued between this tile's MFMAs.  In Float64 a window is twice the
+// fp32 one (156 KB for a +-32 band), so one workgroup holds the CU's LDS and
+// there are twice the VGPRs per wave (three waves per SIMD).  Operand layout
+// (see bsr16_spmm_f64_kernel): lane (i, g) feeds A's row 4 (i % 4) + i / 4
+// and B rows 4g .. 4g+3 of column i, and holds C rows 4g .. 4g+3 of column i.
+// The buffer resources of B and C are rebased per tile (B at the window's
+// first row of column c0, C at column c0), so 32-bit offsets cover 16 columns
+// of any height.
+constexpr int BSR64_SR = 12;                      // block-rows (waves) per workgroup
+constexpr int BSR64_WMAX = BSR64_SR + 64;         // used window block-rows held in LDS
+constexpr int BSR64_SPAN = 128;                   // window block-rows the used-row mask covers
+#ifndef JLUST_BSR64_PAD
+#define JLUST_BSR64_PAD 32
+#endif
+constexpr int BSR64_PAD = JLUST_BSR64_PAD;        // bytes after each window column
+#ifndef JLUST_BSR64_CFRONT
+#define JLUST_BSR64_CFRONT 0
+#endif
+#ifndef JLUST_BSR64_CPB
+#define JLUST_BSR64_CPB 4
+#endif
+constexpr int BSR64_CFRONT = JLUST_BSR64_CFRONT;  // window copies issued before the first block's MFMAs
+constexpr int BSR64_CPB = JLUST_BSR64_CPB;        // window copies issued before each later block's MFMAs
+constexpr int BSR64_CS = BSR64_WMAX * 128 + BSR64_PAD;   // LDS bytes per window column
+constexpr int BSR64_BUF = 16 * BSR64_CS;          // the window buffer (156 KB)
+
+__device__ __forceinline__ void raw_store_d4(doublex4 v, int32x4 rs, int voff, int soff)
+{
+    const bsr_floatx4 *f = reinterpret_cast<const bsr_floatx4 *>(&v);
+    raw_buffer_store_v4f32(f[0], rs, voff, soff, 0);
+    raw_buffer_store_v4f32(f[1], rs, voff + 16, soff, 0);
+}
+
+__device__ __forceinline__ doublex4 raw_load_d4(int32x4 rs, int voff, int soff)
+{
+    doublex4 v;
+    bsr_floatx4 *f = reinterpret_cast<bsr_floatx4 *>(&v);
+    f[0] = raw_buffer_load_v4f32(rs, voff, soff, 0);
+    f[1] = raw_buffer_load_v4f32(rs, voff + 16, soff, 0);
+    return v;
+}
+
+template <bool BZ>
+__global__ __launch_bounds__(64 * BSR64_SR) __attribute__((amdgpu_waves_per_eu(3)))
+void bsr16_spmm_f64_strip_kernel(
+    int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
+    const int32_t *__restrict__ bcolind, const double *__restrict__ val, int64_t k, double alpha,
+    const double *__restrict__ B, int64_t ldb, double beta, double *__restrict__ C, int64_t ldc)
+{
+    __shared__ __align__(16) char win[BSR64_BUF];
+    __shared__ int32_t s_jmin[BSR64_SR], s_jmax[BSR64_SR], s_len[BSR64_SR];
+    __shared__ uint32_t s_used[BSR64_SPAN / 32];      // window block-rows some block of the strip uses
+    const int64_t per_xcd = (int64_t)gridDim.x / NUM_XCD;
+    const int64_t strip = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
+    const int64_t R0 = strip * BSR64_SR;
+    if (R0 >= mb) return;                  // whole workgroup
+    if (threadIdx.x < BSR64_SPAN / 32) s_used[threadIdx.x] = 0;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 15;
+    const int g = lane >> 4;
+    const int ar = 4 * (i & 3) + (i >> 2);     // the A row this lane feeds
+    const int64_t R = R0 + wave;
+    const bool live = R < mb;
+    const int64_t q0 = live ? (int64_t)__builtin_amdgcn_readfirstlane(browptr[R]) - origin : 0;
+    const int64_t q1 = live ? (int64_t)__builtin_amdgcn_readfirstlane(browptr[R + 1]) - origin : 0;
+    const int nq = (int)(q1 - q0);
+    const doublex4 zero = {0.0, 0.0, 0.0, 0.0};
+    {
+        int32_t jmin = INT32_MAX, jmax = INT32_MIN;
+        for (int64_t q = q0 + lane; q < q1; q += 64) {
+            const int32_t j = bcolind[q] - origin;
+            jmin = min(jmin, j);
+            jmax = max(jmax, j);
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) {
+            jmin = min(jmin, __shfl_xor(jmin, off, 64));
+            jmax = max(jmax, __shfl_xor(jmax, off, 64));
+        }
+        if (lane == 0) {
+            s_jmin[wave] = jmin;
+            s_jmax[wave] = jmax;
+            s_len[wave] = nq;
+        }
+    }
+    __syncthreads();
+    int32_t jw0 = INT32_MAX, jw1 = INT32_MIN, lmax = 0;
+#pragma unroll
+    for (int w = 0; w < BSR64_SR; ++w) {
+        jw0 = min(jw0, s_jmin[w]);
+        jw1 = max(jw1, s_jmax[w]);
+        lmax = max(lmax, s_len[w]);
+    }
+    jw0 = __builtin_amdgcn_readfirstlane(jw0);
+    jw1 = __builtin_amdgcn_readfirstlane(jw1);
+    lmax = __builtin_amdgcn_readfirstlane(lmax);
+    const int32_t nwin = jw1 >= jw0 ? jw1 - jw0 + 1 : 0;
+    const int c_lane = (4 * g + i * (int)ldc) * 8;   // C: this lane's byte offset in a tile
+    const int so_c = (int)(R * BSR_BS * 8);           // C: this wave's rows in a tile
+
+    // Only the window block-rows some block of the strip uses are copied (about
+    // three quarters of a +-32 band's), packed in order: slot s of a column is
+    // the s-th used row.  Each 128-byte row segment is one cache line, so no
+    // line is fetched for an unused row.
+    uint32_t used[BSR64_SPAN / 32];
+    int nu = 0;
+    const bool windowed = lmax <= BSR_QCHUNK && nwin <= BSR64_SPAN;
+    if (windowed) {
+        for (int64_t q = q0 + lane; q < q1; q += 64) {
+            const int32_t r = bcolind[q] - origin - jw0;
+            atomicOr(&s_used[r >> 5], 1u << (r & 31));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int w = 0; w < BSR64_SPAN / 32; ++w) {
+            used[w] = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_used[w]);
+            nu += __builtin_popcount(used[w]);
+        }
+    }
+
+    if (!windowed || nu > BSR64_WMAX) {
+        // Direct operand loads (any row length, any window).
+        if (!live) return;
+        for (int64_t c0 = 0; c0 < k; c0 += 16) {
+            const int64_t colc = c0 + i < k ? c0 + i : k - 1;
+            doublex4 acc = zero;
+            for (int64_t q = q0; q < q1; ++q) {
+                const doublex4 a = *reinterpret_cast<const doublex4 *>(val + q * 256 + ar * 16 + 4 * g);
+                const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
+                const doublex4 b = *reinterpret_cast<const doublex4 *>(B + brow + colc * ldb);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], b[u], acc, 0, 0, 0);
+            }
+            if (c0 + i < k) {
+                double *dst = C + R * BSR_BS + 4 * g + (c0 + i) * ldc;
+                doublex4 out = alpha * acc;
+                if (!BZ) out += beta * *reinterpret_cast<const doublex4 *>(dst);
+                *reinterpret_cast<doublex4 *>(dst) = out;
+            }
+        }
+        return;
+    }
+
+    // A operands, and the window slot of each block's B rows (wave-uniform).
+    doublex4 a[BSR_QCHUNK];
+    int32_t jrel[BSR_QCHUNK];
+#pragma unroll
+    for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+        a[qq] = qq < nq ? *reinterpret_cast<const doublex4 *>(val + (q0 + qq) * 256 + ar * 16 + 4 * g) : zero;
+        int32_t slot = 0;
+        if (qq < nq) {
+            const int32_t r = __builtin_amdgcn_readfirstlane(bcolind[q0 + qq] - origin - jw0);
+#pragma unroll
+            for (int w = 0; w < BSR64_SPAN / 32; ++w)
+                if (32 * w < r) slot += __builtin_popcount(32 * (w + 1) <= r ? used[w] : used[w] & ((1u << (r & 31)) - 1u));
+        }
+        jrel[qq] = slot;
+    }
+    // Window copies: wave w < npc moves part w -- slots [8 w, 8 w + 8), 1024
+    // bytes -- of every column's window (npc <= 10 for 76 used rows, so one
+    // part per wave).  Lane l moves bytes 16 (l % 8) .. +16 of slot
+    // 8 w + l / 8, whose used row it looks up once; lanes past the last slot,
+    // and columns past k, are masked off.
+    const int npc = (nu + 7) / 8;                // parts per column
+    const int pbyte = wave * 1024;
+    const bool copier = wave < npc;
+    const int my_slot = 8 * wave + (lane >> 3);
+    const bool lane_ok = my_slot < nu;
+    int my_row = 0;                              // the my_slot-th used row of the window
+    {
+        int t = my_slot;
+#pragma unroll
+        for (int w = 0; w < BSR64_SPAN / 32; ++w) {
+            const int c = __builtin_popcount(used[w]);
+            if (t >= 0 && t < c) {
+                uint32_t x = used[w];
+                for (int u = 0; u < t; ++u) x &= x - 1u;
+                my_row = 32 * w + __builtin_ctz(x);
+            }
+            t -= c;
+        }
+    }
+    const int lane_off = my_row * 128 + (lane & 7) * 16;   // bytes from the column's window start
+    const int ldb8 = (int)ldb * 8;
+    auto tile_b = [&](int64_t c0) { return buffer_resource(B + (int64_t)jw0 * BSR_BS + c0 * ldb); };
+    auto copy_col = [&](int32x4 rs, int64_t c0, int j) {
+        if (copier && c0 + j < k && lane_ok)
+            raw_buffer_load_lds(rs, (lds_void *)(win + j * BSR64_CS + pbyte), 16, lane_off, j * ldb8, 0, 0);
+    };
+    {
+        const int32x4 rs0 = tile_b(0);
+        for (int j = 0; j < 16; ++j) copy_col(rs0, 0, j);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    asm volatile("s_barrier" ::: "memory");
+    // C of tile t is formed and stored at tile t + 1's start, after its
+    // operand reads: the store needs no wait of its own before those reads,
+    // and the MFMA chain of tile t drains while they run.  With beta != 0 the
+    // old C of a tile is loaded at the tile's start, before its copies.
+    const uint32_t col_off = (uint32_t)(i * BSR64_CS + 32 * g);
+    doublex4 accp = zero, oldp = zero;
+    int64_t out_c0 = -1;
+    for (int64_t c0 = 0; c0 < k; c0 += 16) {
+        doublex4 b[BSR_QCHUNK];
+        uint32_t co = col_off;
+        asm volatile("" : "+v"(co));
+#pragma unroll
+        for (int qq = 0; qq < BSR_QCHUNK; ++qq)
+            b[qq] = *reinterpret_cast<const doublex4 *>(win + co + jrel[qq] * 128);
+        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+        if (live) {
+            if (out_c0 >= 0 && out_c0 + i < k) {
+                doublex4 out = alpha * accp;
+                if (!BZ) out += beta * oldp;
+                raw_store_d4(out, buffer_resource(C + out_c0 * ldc), c_lane, so_c);
+            }
+            if (!BZ && c0 + i < k) oldp = raw_load_d4(buffer_resource(C + c0 * ldc), c_lane, so_c);
+        }
+        asm volatile("" ::: "memory");
+        doublex4 acc = zero;
+        const bool more = c0 + 16 < k;
+        const int32x4 rsn = tile_b(more ? c0 + 16 : c0);
+        // The 16 copies of the next tile: BSR64_CFRONT before the first
+        // block's MFMAs, then BSR64_CPB before each later block's.
+        int jn = 0;
+        if (more) {
+#pragma unroll
+            for (int c = 0; c < BSR64_CFRONT; ++c) copy_col(rsn, c0 + 16, jn++);
+        }
+#pragma unroll
+        for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+            if (more && qq > 0) {
+#pragma unroll
+                for (int c = 0; c < BSR64_CPB; ++c)
+                    if (jn < 16) copy_col(rsn, c0 + 16, jn++);
+            }
+            asm volatile("" ::: "memory");
+            if (live && qq < nq) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[qq][u], b[qq][u], acc, 0, 0, 0);
+            }
+        }
+        if (more)
+            while (jn < 16) copy_col(rsn, c0 + 16, jn++);
+        accp = acc;
+        out_c0 = c0;
+        __builtin_amdgcn_s_waitcnt(0);
+        asm volatile("s_barrier" ::: "memory");
+    }
+    if (live && out_c0 >= 0 && out_c0 + i < k) {
+        doublex4 out = alpha * accp;
+        if (!BZ) out += beta * oldp;
+        raw_store_d4(out, buffer_resource(C + out_c0 * ldc), c_lane, so_c);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
 // JLUST_HIP_BSR_STRIP=0 keeps the row-wave kernel (read at each call, so a
 // test can run both kernels in one process; the row-wave kernel is also the
 // one for B or C whose byte offsets reach 2^31).
@@ -837,6 +1105,21 @@ int bsr_spmm_f64(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origi
     const int64_t grid = (mb + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
     hipStream_t s = (hipStream_t)stream;
     const int bz = beta == 0.0;
+    // The strip kernel addresses 16 columns of B (from the window's first row)
+    // and of C through 32-bit buffer offsets.
+    const bool strip_fits = (uint64_t)(16 * ldb + BSR64_SPAN * BSR_BS) * 8 < ((uint64_t)1 << 31) &&
+                            (uint64_t)(16 * ldc + mrows) * 8 < ((uint64_t)1 << 31);
+    if (row_major_blocks && vec && strip_fits && bsr_strip()) {
+        const int64_t strips = (mb + BSR64_SR - 1) / BSR64_SR;
+        const int64_t grids = (strips + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+        if (bz)
+            hipLaunchKernelGGL((bsr16_spmm_f64_strip_kernel<true>), dim3((unsigned)grids), dim3(64 * BSR64_SR), 0,
+                               s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
+        else
+            hipLaunchKernelGGL((bsr16_spmm_f64_strip_kernel<false>), dim3((unsigned)grids), dim3(64 * BSR64_SR),
+                               0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
+        return check_launch("bsr16_spmm_f64_strip_kernel");
+    }
 #define JLUST_BSR64_LAUNCH(RM, V)                                                                   \
     hipLaunchKernelGGL((bsr16_spmm_f64_kernel<RM, V>), dim3((unsigned)grid), dim3(64 * BSR_WAVES), \
                        0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, bz, C, ldc)

@@ -136,3 +136,54 @@ def test_bsr_f64_banded_scaled(J, O):
     A = _bsr64(J, cfg["browptr"], cfg["bcolind"], val, cfg["mb"], cfg["nb"])
     C = _run(J, A, B)
     _check(O, C, cfg["browptr"], cfg["bcolind"], val, B, 1.0, 0.0, None, cfg["name"] + " f64 /32")
+
+
+@pytest.mark.parametrize("beta", [0.0, -0.5])
+@pytest.mark.parametrize("strip", ["1", "0"])
+def test_bsr_f64_strip_paths(J, O, beta, strip, monkeypatch):
+    """Row-major aligned Float64 blocks run the strip kernel (LDS windows of
+    B); a strip whose rows hold more than 8 blocks, or whose window spans more
+    than 76 block-rows, computes with direct operand loads; a banded strip
+    uses the window.  Every kind of strip in one matrix, k not a multiple of
+    16, against the oracle; JLUST_HIP_BSR_STRIP=0 runs the per-row kernel on
+    the same input."""
+    monkeypatch.setenv("JLUST_HIP_BSR_STRIP", strip)
+    mb, nb, k = 60, 200, 40
+    rng = np.random.default_rng(11)
+    bcols = []
+    for R in range(mb):
+        if R < 12:                                   # long rows: up to 12 blocks
+            c = rng.choice(nb, int(rng.integers(6, 13)), replace=False)
+        elif R < 24:                                 # a window wider than 76 block-rows
+            c = rng.choice(nb, 5, replace=False)
+        elif R % 7 == 0:
+            c = np.zeros(0, np.int64)                # empty rows inside banded strips
+        else:                                        # banded: within +-10 of the diagonal
+            lo, hi = max(0, R - 10), min(nb, R + 11)
+            c = rng.choice(np.arange(lo, hi), 6, replace=False)
+        bcols.append(np.sort(c))
+    browptr = (np.r_[0, np.cumsum([c.size for c in bcols])] + 1).astype(np.int32)
+    bcolind = (np.concatenate(bcols) + 1).astype(np.int32)
+    val = rng.standard_normal(bcolind.size * 256)
+    A = _bsr64(J, browptr, bcolind, val, mb, nb)
+    B = np.asfortranarray(rng.standard_normal((nb * 16, k)))
+    C0 = np.asfortranarray(rng.standard_normal((mb * 16, k))) if beta else None
+    C = _run(J, A, B, C0, 1.5, beta)
+    _check(O, C, browptr, bcolind, val, B, 1.5, beta, C0, f"f64 strip paths (strip={strip})")
+
+
+def test_bsr_f64_banded_quarter_every_output(J, O):
+    """Config 5's banded pattern at 1/4 scale (16,384 block-rows, 8 blocks
+    within +-32, k = 256) in Float64 through the strip kernel, every output."""
+    from jlust_amd import workloads as W
+    cfg = W.make(5, scale=4)
+    val = cfg["val"].astype(np.float64)
+    B = np.asfortranarray(cfg["B"].astype(np.float64))
+    A = _bsr64(J, cfg["browptr"], cfg["bcolind"], val, cfg["mb"], cfg["nb"])
+    C = _run(J, A, B)
+    rp, ci, v = O.bsr_to_csr(cfg["browptr"], cfg["bcolind"], val, 16)
+    for c0 in range(0, B.shape[1], 64):
+        Bs = np.asfortranarray(B[:, c0:c0 + 64])
+        ref, _ = O.csr_spmm(rp, ci, v, Bs)
+        absref = O.csr_spmm_absref(rp, ci, v, Bs)
+        assert_within(C[:, c0:c0 + 64], ref, absref, np.float64, cfg["name"] + f" f64 /4 cols {c0}..")
