@@ -522,10 +522,11 @@ def spmv_parts():
 
 def bsr_f64():
     """Config 5's banded BSR pattern (65,536 block-rows of 16 x 16 blocks,
-    8 per block-row within +-32, k = 256) in Float64: the fp64 MFMA kernel
-    (jlust_hip_bsr_spmm_f64_i32) against the same product through the
-    device CSR expansion and the CSR SpMM, which is how Float64 BSR ran before
-    that kernel.  HIP events over 10 calls after 2 warm-up calls."""
+    8 per block-row within +-32, k = 256) in Float64: the fp64 MFMA strip
+    kernel (jlust_hip_bsr_spmm_f64_i32, LDS windows of B) against the
+    per-row fp64 kernel it replaced (JLUST_HIP_BSR_STRIP=0) and the same
+    product through the device CSR expansion and the CSR SpMM.  HIP events
+    over 10 calls after 2 warm-up calls."""
     import torch
     import jlust_amd as J
     from jlust_amd import workloads as W

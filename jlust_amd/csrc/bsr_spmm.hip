@@ -572,7 +572,11 @@ void bsr16_spmm_strip_kernel(
 // and B rows 4g .. 4g+3 of column i, and holds C rows 4g .. 4g+3 of column i.
 // The buffer resources of B and C are rebased per tile (B at the window's
 // first row of column c0, C at column c0), so 32-bit offsets cover 16 columns
-// of any height.
+// of any height.  One workgroup per CU walks its XCD's strips (persistent),
+// and a strip's set-up -- its rows' block ranges and columns, window and
+// slots, and A operands -- is loaded during the previous strip's last tiles,
+// so that the CU's MFMAs do not wait for it (set up at a strip's start, it
+// took about a sixth of the time).
 constexpr int BSR64_SR = 12;                      // block-rows (waves) per workgroup
 constexpr int BSR64_WMAX = BSR64_SR + 64;         // used window block-rows held in LDS
 constexpr int BSR64_SPAN = 128;                   // window block-rows the used-row mask covers
@@ -584,7 +588,7 @@ constexpr int BSR64_PAD = JLUST_BSR64_PAD;        // bytes after each window col
 #define JLUST_BSR64_CFRONT 0
 #endif
 #ifndef JLUST_BSR64_CPB
-#define JLUST_BSR64_CPB 4
+#define JLUST_BSR64_CPB 3
 #endif
 constexpr int BSR64_CFRONT = JLUST_BSR64_CFRONT;  // window copies issued before the first block's MFMAs
 constexpr int BSR64_CPB = JLUST_BSR64_CPB;        // window copies issued before each later block's MFMAs
@@ -615,128 +619,169 @@ void bsr16_spmm_f64_strip_kernel(
     const double *__restrict__ B, int64_t ldb, double beta, double *__restrict__ C, int64_t ldc)
 {
     __shared__ __align__(16) char win[BSR64_BUF];
-    __shared__ int32_t s_jmin[BSR64_SR], s_jmax[BSR64_SR], s_len[BSR64_SR];
-    __shared__ uint32_t s_used[BSR64_SPAN / 32];      // window block-rows some block of the strip uses
-    const int64_t per_xcd = (int64_t)gridDim.x / NUM_XCD;
-    const int64_t strip = (int64_t)(blockIdx.x % NUM_XCD) * per_xcd + blockIdx.x / NUM_XCD;
-    const int64_t R0 = strip * BSR64_SR;
-    if (R0 >= mb) return;                  // whole workgroup
-    if (threadIdx.x < BSR64_SPAN / 32) s_used[threadIdx.x] = 0;
+    // Set-up of a strip, double-buffered by strip parity: per wave its row's
+    // first and last window block-row and block count, and the mask of the
+    // window block-rows some block of the strip uses.
+    __shared__ int32_t s_jmin[2][BSR64_SR], s_jmax[2][BSR64_SR], s_len[2][BSR64_SR];
+    __shared__ uint32_t s_used[2][BSR64_SPAN / 32];
+    // Persistent workgroups: XCD x = blockIdx % 8 owns strips [lo, hi), a
+    // contiguous run, and its G workgroups take lo + w, lo + w + G, ... so
+    // the strips in flight on an XCD are neighbours sharing B rows in its L2.
+    // A last round of r <= G / 2 strips is cut into f = G / r column ranges
+    // each, so that it takes 1 / f of a round.
+    const int nstrips = (int)((mb + BSR64_SR - 1) / BSR64_SR);
+    const int G = (int)gridDim.x / NUM_XCD;
+    const int xcd = (int)blockIdx.x % NUM_XCD;
+    const int wl = (int)blockIdx.x / NUM_XCD;
+    const int lo = (int)((int64_t)xcd * nstrips / NUM_XCD), hi = (int)((int64_t)(xcd + 1) * nstrips / NUM_XCD);
+    if (hi <= lo) return;                  // whole workgroup
+    const int kk = (int)k;                      // k < 2^31 - 16 (checked by the host)
+    const int ntiles = (kk + 15) / 16;
+    const int rounds = (hi - lo + G - 1) / G;
+    const int rlast = hi - lo - (rounds - 1) * G;          // strips in the last round, 1..G
+    const int fsplit = min(2 * rlast <= G ? G / rlast : 1, ntiles);
+    // Work unit it of this workgroup: strip s, tiles [t0, t1).
+    auto unit = [&](int it, int &s, int &t0, int &t1) -> bool {
+        if (it < rounds - 1) {
+            s = lo + wl + it * G;
+            t0 = 0;
+            t1 = ntiles;
+            return true;
+        }
+        if (it > rounds - 1 || wl >= rlast * fsplit) return false;
+        s = lo + (rounds - 1) * G + wl / fsplit;
+        const int c = wl % fsplit;
+        t0 = c * ntiles / fsplit;
+        t1 = (c + 1) * ntiles / fsplit;
+        return true;
+    };
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int i = lane & 15;
     const int g = lane >> 4;
     const int ar = 4 * (i & 3) + (i >> 2);     // the A row this lane feeds
-    const int64_t R = R0 + wave;
-    const bool live = R < mb;
-    const int64_t q0 = live ? (int64_t)__builtin_amdgcn_readfirstlane(browptr[R]) - origin : 0;
-    const int64_t q1 = live ? (int64_t)__builtin_amdgcn_readfirstlane(browptr[R + 1]) - origin : 0;
-    const int nq = (int)(q1 - q0);
+    const int c_lane = (4 * g + i * (int)ldc) * 8;   // C: this lane's byte offset in a tile
+    const int ldb8 = (int)ldb * 8;
+    const int pbyte = wave * 1024;
+    // A unit of four or more tiles sets up the next unit's strip during its
+    // last four tiles; otherwise a strip is set up at its unit's start.
     const doublex4 zero = {0.0, 0.0, 0.0, 0.0};
-    {
-        int32_t jmin = INT32_MAX, jmax = INT32_MIN;
-        for (int64_t q = q0 + lane; q < q1; q += 64) {
-            const int32_t j = bcolind[q] - origin;
-            jmin = min(jmin, j);
-            jmax = max(jmax, j);
-        }
+    const uint32_t col_off = (uint32_t)(i * BSR64_CS + 32 * g);
+    auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    auto tile_b = [&](int32_t jw, int c0) { return buffer_resource(B + (int64_t)jw * BSR_BS + (int64_t)c0 * ldb); };
+
+    // ---- the strip being computed.
+    bool live = false, windowed = false, copier = false, lane_ok = false;
+    int q0 = 0, nq = 0, lane_off = 0, so_c = 0;
+    int32_t jw0 = 0;
+    uint32_t jrel[2] = {0u, 0u};           // window slots of the row's blocks, 8 bits each
+
+    // ---- set-up of a strip in five steps: 1-4 write the *n variables (the
+    // strip being set up), 5 adopts them as the strip being computed.
+    int Rn = 0;
+    bool liven = false;
+    int32_t p0n = 0, p1n = 0, bcoln = 0, jw0n = 0;
+    int q0n = 0, nqn = 0;
+    bool windowedn = false;
+    // 1: the row's block range.
+    auto setup1 = [&](int sn) {
+        Rn = sn * BSR64_SR + wave;
+        liven = Rn < mb;
+        p0n = liven ? browptr[Rn] : 0;
+        p1n = liven ? browptr[Rn + 1] : 0;
+    };
+    // 2: the row's block columns (one per lane), for rows short enough to
+    // be held as operands.
+    auto setup2 = [&]() {
+        q0n = __builtin_amdgcn_readfirstlane(p0n) - origin;
+        const int q1n = __builtin_amdgcn_readfirstlane(p1n) - origin;
+        nqn = liven ? q1n - q0n : 0;
+        bcoln = 0;
+        if (nqn <= BSR_QCHUNK && lane < nqn) bcoln = bcolind[q0n + lane] - origin;
+    };
+    // 3: per wave the row's column range and length; the used mask cleared.
+    auto setup3 = [&](int par) {
+        const bool has = nqn <= BSR_QCHUNK && lane < nqn;
+        int32_t jmin = has ? bcoln : INT32_MAX, jmax = has ? bcoln : INT32_MIN;
 #pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
+        for (int off = 4; off > 0; off >>= 1) {    // the columns sit in lanes 0..7
             jmin = min(jmin, __shfl_xor(jmin, off, 64));
             jmax = max(jmax, __shfl_xor(jmax, off, 64));
         }
         if (lane == 0) {
-            s_jmin[wave] = jmin;
-            s_jmax[wave] = jmax;
-            s_len[wave] = nq;
+            s_jmin[par][wave] = jmin;
+            s_jmax[par][wave] = jmax;
+            s_len[par][wave] = nqn;
         }
-    }
-    __syncthreads();
-    int32_t jw0 = INT32_MAX, jw1 = INT32_MIN, lmax = 0;
+        if (threadIdx.x < BSR64_SPAN / 32) s_used[par][threadIdx.x] = 0;
+    };
+    // 4 (after a barrier): the strip's window; its used block-rows marked.
+    auto setup4 = [&](int par) {
+        // Lane w < BSR64_SR reads wave w's entries; a 16-lane reduction.
+        int32_t jw0 = INT32_MAX, jw1 = INT32_MIN, lmax = 0;
+        if (lane < BSR64_SR) {
+            jw0 = s_jmin[par][lane];
+            jw1 = s_jmax[par][lane];
+            lmax = s_len[par][lane];
+        }
 #pragma unroll
-    for (int w = 0; w < BSR64_SR; ++w) {
-        jw0 = min(jw0, s_jmin[w]);
-        jw1 = max(jw1, s_jmax[w]);
-        lmax = max(lmax, s_len[w]);
-    }
-    jw0 = __builtin_amdgcn_readfirstlane(jw0);
-    jw1 = __builtin_amdgcn_readfirstlane(jw1);
-    lmax = __builtin_amdgcn_readfirstlane(lmax);
-    const int32_t nwin = jw1 >= jw0 ? jw1 - jw0 + 1 : 0;
-    const int c_lane = (4 * g + i * (int)ldc) * 8;   // C: this lane's byte offset in a tile
-    const int so_c = (int)(R * BSR_BS * 8);           // C: this wave's rows in a tile
-
-    // Only the window block-rows some block of the strip uses are copied (about
-    // three quarters of a +-32 band's), packed in order: slot s of a column is
-    // the s-th used row.  Each 128-byte row segment is one cache line, so no
-    // line is fetched for an unused row.
-    uint32_t used[BSR64_SPAN / 32];
-    int nu = 0;
-    const bool windowed = lmax <= BSR_QCHUNK && nwin <= BSR64_SPAN;
-    if (windowed) {
-        for (int64_t q = q0 + lane; q < q1; q += 64) {
-            const int32_t r = bcolind[q] - origin - jw0;
-            atomicOr(&s_used[r >> 5], 1u << (r & 31));
+        for (int off = 8; off > 0; off >>= 1) {
+            jw0 = min(jw0, __shfl_xor(jw0, off, 64));
+            jw1 = max(jw1, __shfl_xor(jw1, off, 64));
+            lmax = max(lmax, __shfl_xor(lmax, off, 64));
         }
-        __syncthreads();
+        jw0 = __builtin_amdgcn_readfirstlane(jw0);
+        jw1 = __builtin_amdgcn_readfirstlane(jw1);
+        lmax = __builtin_amdgcn_readfirstlane(lmax);
+        const int32_t nwin = jw1 >= jw0 ? jw1 - jw0 + 1 : 0;
+        jw0n = nwin > 0 ? jw0 : 0;
+        windowedn = lmax <= BSR_QCHUNK && nwin <= BSR64_SPAN;
+        if (windowedn && lane < nqn) {
+            const int32_t r = bcoln - jw0n;
+            atomicOr(&s_used[par][r >> 5], 1u << (r & 31));
+        }
+    };
+    // 5 (after a barrier): adopt the strip; its window slots.  Only the used
+    // window block-rows (about three quarters of a +-32 band's) are copied,
+    // packed in order: slot s of a column is the s-th used row, so no line is
+    // fetched for an unused row.  Each block's B rows sit at its row's slot
+    // (wave-uniform).  Copies: wave w < npc moves part w -- slots [8 w,
+    // 8 w + 8), 1024 bytes -- of every column (npc <= 10 for 76 used rows, one
+    // part per wave); lane l moves bytes 16 (l % 8) .. +16 of slot
+    // 8 w + l / 8, whose used row it looks up once; lanes past the last slot
+    // are masked off.
+    auto setup5 = [&](int par) {
+        live = liven;
+        q0 = q0n;
+        nq = nqn;
+        jw0 = jw0n;
+        so_c = Rn * BSR_BS * 8;            // C: this wave's rows in a tile
+        uint32_t used[BSR64_SPAN / 32];
+        int nu = 0;
 #pragma unroll
         for (int w = 0; w < BSR64_SPAN / 32; ++w) {
-            used[w] = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_used[w]);
+            used[w] = (uint32_t)__builtin_amdgcn_readfirstlane((int)s_used[par][w]);
             nu += __builtin_popcount(used[w]);
         }
-    }
-
-    if (!windowed || nu > BSR64_WMAX) {
-        // Direct operand loads (any row length, any window).
-        if (!live) return;
-        for (int64_t c0 = 0; c0 < k; c0 += 16) {
-            const int64_t colc = c0 + i < k ? c0 + i : k - 1;
-            doublex4 acc = zero;
-            for (int64_t q = q0; q < q1; ++q) {
-                const doublex4 a = *reinterpret_cast<const doublex4 *>(val + q * 256 + ar * 16 + 4 * g);
-                const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
-                const doublex4 b = *reinterpret_cast<const doublex4 *>(B + brow + colc * ldb);
+        windowed = windowedn && nu <= BSR64_WMAX;
+        jrel[0] = jrel[1] = 0u;
 #pragma unroll
-                for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], b[u], acc, 0, 0, 0);
+        for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+            uint32_t slot = 0;
+            if (qq < nqn) {
+                const int32_t r = __builtin_amdgcn_readlane(bcoln, qq) - jw0n;
+#pragma unroll
+                for (int w = 0; w < BSR64_SPAN / 32; ++w)
+                    if (32 * w < r)
+                        slot += __builtin_popcount(32 * (w + 1) <= r ? used[w] : used[w] & ((1u << (r & 31)) - 1u));
             }
-            if (c0 + i < k) {
-                double *dst = C + R * BSR_BS + 4 * g + (c0 + i) * ldc;
-                doublex4 out = alpha * acc;
-                if (!BZ) out += beta * *reinterpret_cast<const doublex4 *>(dst);
-                *reinterpret_cast<doublex4 *>(dst) = out;
-            }
+            jrel[qq >> 2] |= slot << (8 * (qq & 3));
         }
-        return;
-    }
-
-    // A operands, and the window slot of each block's B rows (wave-uniform).
-    doublex4 a[BSR_QCHUNK];
-    int32_t jrel[BSR_QCHUNK];
-#pragma unroll
-    for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
-        a[qq] = qq < nq ? *reinterpret_cast<const doublex4 *>(val + (q0 + qq) * 256 + ar * 16 + 4 * g) : zero;
-        int32_t slot = 0;
-        if (qq < nq) {
-            const int32_t r = __builtin_amdgcn_readfirstlane(bcolind[q0 + qq] - origin - jw0);
-#pragma unroll
-            for (int w = 0; w < BSR64_SPAN / 32; ++w)
-                if (32 * w < r) slot += __builtin_popcount(32 * (w + 1) <= r ? used[w] : used[w] & ((1u << (r & 31)) - 1u));
-        }
-        jrel[qq] = slot;
-    }
-    // Window copies: wave w < npc moves part w -- slots [8 w, 8 w + 8), 1024
-    // bytes -- of every column's window (npc <= 10 for 76 used rows, so one
-    // part per wave).  Lane l moves bytes 16 (l % 8) .. +16 of slot
-    // 8 w + l / 8, whose used row it looks up once; lanes past the last slot,
-    // and columns past k, are masked off.
-    const int npc = (nu + 7) / 8;                // parts per column
-    const int pbyte = wave * 1024;
-    const bool copier = wave < npc;
-    const int my_slot = 8 * wave + (lane >> 3);
-    const bool lane_ok = my_slot < nu;
-    int my_row = 0;                              // the my_slot-th used row of the window
-    {
-        int t = my_slot;
+        const int npc = (nu + 7) / 8;
+        copier = wave < npc;
+        const int my_slot = 8 * wave + (lane >> 3);
+        lane_ok = my_slot < nu;
+        int my_row = 0, t = my_slot;
 #pragma unroll
         for (int w = 0; w < BSR64_SPAN / 32; ++w) {
             const int c = __builtin_popcount(used[w]);
@@ -747,80 +792,166 @@ void bsr16_spmm_f64_strip_kernel(
             }
             t -= c;
         }
-    }
-    const int lane_off = my_row * 128 + (lane & 7) * 16;   // bytes from the column's window start
-    const int ldb8 = (int)ldb * 8;
-    auto tile_b = [&](int64_t c0) { return buffer_resource(B + (int64_t)jw0 * BSR_BS + c0 * ldb); };
-    auto copy_col = [&](int32x4 rs, int64_t c0, int j) {
-        if (copier && c0 + j < k && lane_ok)
-            raw_buffer_load_lds(rs, (lds_void *)(win + j * BSR64_CS + pbyte), 16, lane_off, j * ldb8, 0, 0);
+        lane_off = my_row * 128 + (lane & 7) * 16;
     };
-    {
-        const int32x4 rs0 = tile_b(0);
-        for (int j = 0; j < 16; ++j) copy_col(rs0, 0, j);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    asm volatile("s_barrier" ::: "memory");
-    // C of tile t is formed and stored at tile t + 1's start, after its
-    // operand reads: the store needs no wait of its own before those reads,
-    // and the MFMA chain of tile t drains while they run.  With beta != 0 the
-    // old C of a tile is loaded at the tile's start, before its copies.
-    const uint32_t col_off = (uint32_t)(i * BSR64_CS + 32 * g);
+    auto load_a = [&](doublex4 &dst, int qq) {
+        dst = *reinterpret_cast<const doublex4 *>(val + ((int64_t)q0n + qq) * 256 + ar * 16 + 4 * g);
+    };
+    // Column j of the window of the tile at column cb; the copy's LDS
+    // address and B offset advance column by column from values made opaque
+    // per tile (sd, so), so the compiler keeps two SGPRs, not 32.
+    auto copy_col = [&](int32x4 rs, int cb, int j, uint32_t &sd, int &so) {
+        if (copier && cb + j < kk && lane_ok)
+            raw_buffer_load_lds(rs, (lds_void *)(win + sd), 16, lane_off, so, 0, 0);
+        sd += BSR64_CS;
+        so += ldb8;
+    };
+
+    doublex4 a[BSR_QCHUNK];                // the row's blocks, A operands for all of k
+#pragma unroll
+    for (int qq = 0; qq < BSR_QCHUNK; ++qq) a[qq] = zero;
+    // C of a tile is formed and stored at the next tile's start (possibly
+    // the next strip's), after that tile's operand reads: the store needs no
+    // wait of its own before them, and the MFMA chain drains while they run.
+    // With beta != 0 the old C of a tile is loaded at the tile's start.
     doublex4 accp = zero, oldp = zero;
-    int64_t out_c0 = -1;
-    for (int64_t c0 = 0; c0 < k; c0 += 16) {
-        doublex4 b[BSR_QCHUNK];
-        uint32_t co = col_off;
-        asm volatile("" : "+v"(co));
-#pragma unroll
-        for (int qq = 0; qq < BSR_QCHUNK; ++qq)
-            b[qq] = *reinterpret_cast<const doublex4 *>(win + co + jrel[qq] * 128);
-        asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-        if (live) {
-            if (out_c0 >= 0 && out_c0 + i < k) {
-                doublex4 out = alpha * accp;
-                if (!BZ) out += beta * oldp;
-                raw_store_d4(out, buffer_resource(C + out_c0 * ldc), c_lane, so_c);
-            }
-            if (!BZ && c0 + i < k) oldp = raw_load_d4(buffer_resource(C + c0 * ldc), c_lane, so_c);
+    int out_c0 = -1;
+    int out_so = 0;
+    bool out_live = false;
+    auto flush = [&]() {
+        if (out_live && out_c0 >= 0 && out_c0 + i < kk) {
+            doublex4 out = alpha * accp;
+            if (!BZ) out += beta * oldp;
+            raw_store_d4(out, buffer_resource(C + (int64_t)out_c0 * ldc), c_lane, out_so);
         }
-        asm volatile("" ::: "memory");
-        doublex4 acc = zero;
-        const bool more = c0 + 16 < k;
-        const int32x4 rsn = tile_b(more ? c0 + 16 : c0);
-        // The 16 copies of the next tile: BSR64_CFRONT before the first
-        // block's MFMAs, then BSR64_CPB before each later block's.
-        int jn = 0;
-        if (more) {
+        out_c0 = -1;
+    };
+
+    // ready: steps 1-4 and the A operand loads of strip s were done during
+    // the previous strip's tiles (step 4 in its last tile, before its final
+    // barrier).
+    bool ready = false;
+    int par = 0;
+    int s = 0, t0 = 0, t1 = 0, sn = 0, t0n = 0, t1n = 0;
+    bool has = unit(0, s, t0, t1), hasn = false;
+    for (int it = 0; has; ++it, par ^= 1, has = hasn, s = sn, t0 = t0n, t1 = t1n) {
+        hasn = unit(it + 1, sn, t0n, t1n);
+        const bool pre = hasn && t1 - t0 >= 4;  // steps 1-4 of strip sn run during this unit's tiles
+        if (!ready) {
+            setup1(s);
+            setup2();
+            setup3(par);
+            barrier();
+            setup4(par);
 #pragma unroll
-            for (int c = 0; c < BSR64_CFRONT; ++c) copy_col(rsn, c0 + 16, jn++);
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq)
+                if (liven && qq < nqn) load_a(a[qq], qq);
+            barrier();
         }
+        setup5(par);
+        ready = false;
+
+        if (!windowed) {
+            // Direct operand loads (any row length, any window).
+            flush();
+            if (live) {
+                for (int64_t c0 = (int64_t)t0 * 16; c0 < k && c0 < (int64_t)t1 * 16; c0 += 16) {
+                    const int64_t colc = c0 + i < k ? c0 + i : k - 1;
+                    doublex4 acc = zero;
+                    for (int64_t q = q0; q < (int64_t)q0 + nq; ++q) {
+                        const doublex4 av = *reinterpret_cast<const doublex4 *>(val + q * 256 + ar * 16 + 4 * g);
+                        const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
+                        const doublex4 bv = *reinterpret_cast<const doublex4 *>(B + brow + colc * ldb);
 #pragma unroll
-        for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
-            if (more && qq > 0) {
-#pragma unroll
-                for (int c = 0; c < BSR64_CPB; ++c)
-                    if (jn < 16) copy_col(rsn, c0 + 16, jn++);
+                        for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av[u], bv[u], acc, 0, 0, 0);
+                    }
+                    if (c0 + i < k) {
+                        double *dst = C + (int64_t)Rn * BSR_BS + 4 * g + (c0 + i) * ldc;
+                        doublex4 out = alpha * acc;
+                        if (!BZ) out += beta * *reinterpret_cast<const doublex4 *>(dst);
+                        *reinterpret_cast<doublex4 *>(dst) = out;
+                    }
+                }
             }
-            asm volatile("" ::: "memory");
-            if (live && qq < nq) {
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[qq][u], b[qq][u], acc, 0, 0, 0);
-            }
+            __builtin_amdgcn_s_waitcnt(0);
+            asm volatile("s_barrier" ::: "memory");   // every wave is past step 5's reads
+            continue;
         }
-        if (more)
-            while (jn < 16) copy_col(rsn, c0 + 16, jn++);
-        accp = acc;
-        out_c0 = c0;
+        {
+            const int32x4 rs0 = tile_b(jw0, t0 * 16);
+            uint32_t sd = pbyte;
+            int so = 0;
+            for (int j = 0; j < 16; ++j) copy_col(rs0, t0 * 16, j, sd, so);
+        }
         __builtin_amdgcn_s_waitcnt(0);
         asm volatile("s_barrier" ::: "memory");
+
+        for (int t = t0; t < t1; ++t) {
+            const int c0 = t * 16;
+            const bool last = t == t1 - 1;
+            doublex4 b[BSR_QCHUNK];
+            uint32_t co = col_off, jr0 = jrel[0], jr1 = jrel[1];
+            asm volatile("" : "+v"(co), "+s"(jr0), "+s"(jr1));
+#pragma unroll
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq)
+                b[qq] = *reinterpret_cast<const doublex4 *>(win + co + (((qq < 4 ? jr0 : jr1) >> (8 * (qq & 3))) & 0xffu) * 128);
+            barrier();                     // the window is free
+            flush();
+            if (!BZ && live && c0 + i < kk) oldp = raw_load_d4(buffer_resource(C + (int64_t)c0 * ldc), c_lane, so_c);
+            if (pre && t == t1 - 4) setup1(sn);
+            if (pre && t == t1 - 3) setup2();
+            if (pre && last) setup4(par ^ 1);
+            asm volatile("" ::: "memory");
+            // The 16 copies of the next tile: BSR64_CFRONT before the first
+            // block's MFMAs, then BSR64_CPB before each later block's.  In
+            // the last tile the next strip's A operands are loaded instead,
+            // each after its block's MFMAs have read this strip's.
+            const bool more = !last;
+            const int32x4 rsn = tile_b(jw0, more ? c0 + 16 : c0);
+            const bool nxa = last && pre && liven;
+            doublex4 acc = zero;
+            int jn = 0;
+            uint32_t sd = pbyte;
+            int so = 0;
+            asm volatile("" : "+s"(sd), "+s"(so));
+            if (more) {
+#pragma unroll
+                for (int c = 0; c < BSR64_CFRONT; ++c) copy_col(rsn, c0 + 16, jn++, sd, so);
+            }
+#pragma unroll
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+                if (more && qq > 0) {
+#pragma unroll
+                    for (int c = 0; c < BSR64_CPB; ++c)
+                        if (jn < 16) copy_col(rsn, c0 + 16, jn++, sd, so);
+                }
+                asm volatile("" ::: "memory");
+                if (live && qq < nq) {
+#pragma unroll
+                    for (int u = 0; u < 4; ++u)
+                        acc = __builtin_amdgcn_mfma_f64_16x16x4f64(a[qq][u], b[qq][u], acc, 0, 0, 0);
+                }
+                if (nxa && qq < nqn) load_a(a[qq], qq);
+            }
+            if (more)
+                while (jn < 16) copy_col(rsn, c0 + 16, jn++, sd, so);
+            if (pre && t == t1 - 2) setup3(par ^ 1);
+            accp = acc;
+            out_c0 = c0;
+            out_so = so_c;
+            out_live = live;
+            if (last) {
+                // No window copies are in flight: the next strip's A operand
+                // loads stay in flight into its first window's copies.
+                barrier();
+            } else {
+                __builtin_amdgcn_s_waitcnt(0);
+                asm volatile("s_barrier" ::: "memory");
+            }
+        }
+        ready = pre;
     }
-    if (live && out_c0 >= 0 && out_c0 + i < k) {
-        doublex4 out = alpha * accp;
-        if (!BZ) out += beta * oldp;
-        raw_store_d4(out, buffer_resource(C + out_c0 * ldc), c_lane, so_c);
-    }
+    flush();
     __builtin_amdgcn_s_waitcnt(0);
 }
 
@@ -1108,10 +1239,15 @@ int bsr_spmm_f64(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origi
     // The strip kernel addresses 16 columns of B (from the window's first row)
     // and of C through 32-bit buffer offsets.
     const bool strip_fits = (uint64_t)(16 * ldb + BSR64_SPAN * BSR_BS) * 8 < ((uint64_t)1 << 31) &&
-                            (uint64_t)(16 * ldc + mrows) * 8 < ((uint64_t)1 << 31);
+                            (uint64_t)(16 * ldc + mrows) * 8 < ((uint64_t)1 << 31) && k < INT32_MAX - 16;
     if (row_major_blocks && vec && strip_fits && bsr_strip()) {
+        // One resident workgroup per CU (the window takes its LDS), each
+        // walking its XCD's strips.
+        int dev = 0;
+        if (int st = require_device(&dev)) return st;
         const int64_t strips = (mb + BSR64_SR - 1) / BSR64_SR;
-        const int64_t grids = (strips + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+        const int64_t per_xcd = std::max<int64_t>(1, device_info(dev).cu_count / NUM_XCD);
+        const int64_t grids = std::min((strips + NUM_XCD - 1) / NUM_XCD, per_xcd) * NUM_XCD;
         if (bz)
             hipLaunchKernelGGL((bsr16_spmm_f64_strip_kernel<true>), dim3((unsigned)grids), dim3(64 * BSR64_SR), 0,
                                s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);

@@ -187,3 +187,37 @@ def test_bsr_f64_banded_quarter_every_output(J, O):
         ref, _ = O.csr_spmm(rp, ci, v, Bs)
         absref = O.csr_spmm_absref(rp, ci, v, Bs)
         assert_within(C[:, c0:c0 + 64], ref, absref, np.float64, cfg["name"] + f" f64 /4 cols {c0}..")
+
+
+@pytest.mark.parametrize("k,beta", [(40, 0.0), (64, 0.0), (100, -0.5), (256, 1.0)])
+def test_bsr_f64_persistent_schedule(J, O, k, beta):
+    """A matrix of 3,100 block-rows (259 strips of 12): with one workgroup per
+    CU each XCD's workgroups take several strips in turn, setting up the next
+    strip during a strip's last tiles (4 tiles or more: k = 64, 100, 256) or
+    at its start (k = 40); an XCD's last round of one strip is cut into column
+    ranges.  Strips of long rows or wide windows (direct operand loads) sit
+    between banded ones, some rows are empty and the last strip is partial;
+    every output against the oracle."""
+    mb = nb = 3100
+    rng = np.random.default_rng(k)
+    bcols = []
+    for R in range(mb):
+        s = R // 12
+        if s % 17 == 5:                               # long rows: up to 11 blocks
+            c = rng.choice(nb, int(rng.integers(9, 12)), replace=False)
+        elif s % 23 == 9:                             # a window wider than 128 block-rows
+            c = rng.choice(nb, 4, replace=False)
+        elif R % 13 == 0:
+            c = np.zeros(0, np.int64)
+        else:
+            lo, hi = max(0, R - 32), min(nb, R + 33)
+            c = rng.choice(np.arange(lo, hi), int(rng.integers(1, 9)), replace=False)
+        bcols.append(np.sort(c))
+    browptr = (np.r_[0, np.cumsum([c.size for c in bcols])] + 1).astype(np.int32)
+    bcolind = (np.concatenate(bcols) + 1).astype(np.int32)
+    val = rng.standard_normal(bcolind.size * 256)
+    A = _bsr64(J, browptr, bcolind, val, mb, nb)
+    B = np.asfortranarray(rng.standard_normal((nb * 16, k)))
+    C0 = np.asfortranarray(rng.standard_normal((mb * 16, k))) if beta else None
+    C = _run(J, A, B, C0, 0.75, beta)
+    _check(O, C, browptr, bcolind, val, B, 0.75, beta, C0, f"f64 persistent k={k} beta={beta}")
