@@ -525,8 +525,9 @@ def bsr_f64():
     8 per block-row within +-32, k = 256) in Float64: the fp64 MFMA strip
     kernel (jlust_hip_bsr_spmm_f64_i32, LDS windows of B) against the
     per-row fp64 kernel it replaced (JLUST_HIP_BSR_STRIP=0) and the same
-    product through the device CSR expansion and the CSR SpMM.  HIP events
-    over 10 calls after 2 warm-up calls."""
+    product through the device CSR expansion and the CSR SpMM.  HIP events:
+    the median of 5 runs of 10 calls after 3 warm-up calls (the expansion:
+    one run of 3 calls)."""
     import torch
     import jlust_amd as J
     from jlust_amd import workloads as W
@@ -541,17 +542,20 @@ def bsr_f64():
     flops = 2.0 * 16 * 16 * k * int(A.crd_buffers[1].numel())
     stream = torch.cuda.current_stream()
 
-    def ms(fn, reps=10):
-        for _ in range(2):
+    def ms(fn, reps=10, trials=5):
+        for _ in range(3):
             fn()
         torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        s.record(stream)
-        for _ in range(reps):
-            fn()
-        e.record(stream)
-        torch.cuda.synchronize()
-        return s.elapsed_time(e) / reps
+        ts = []
+        for _ in range(trials):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            for _ in range(reps):
+                fn()
+            e.record(stream)
+            torch.cuda.synchronize()
+            ts.append(s.elapsed_time(e) / reps)
+        return sorted(ts)[len(ts) // 2]
 
     t_mfma = ms(lambda: J.execute(J.SpMMOp, A, B, C))
     old = os.environ.get("JLUST_HIP_BSR_STRIP")
@@ -564,7 +568,7 @@ def bsr_f64():
         else:
             os.environ["JLUST_HIP_BSR_STRIP"] = old
     Acsr = _bsr_as_csr(A)
-    t_csr = ms(lambda: J.execute(J.SpMMOp, Acsr, B, C), reps=3)
+    t_csr = ms(lambda: J.execute(J.SpMMOp, Acsr, B, C), reps=3, trials=1)
     tf = lambda t: round(flops / (t * 1e-3) / 1e12, 2)  # noqa: E731
     res = {"workload": "bsr16_spmm_f64_banded_65536x8_k256", "flops": flops,
            "kernel": "bsr16_spmm_f64_strip_kernel",

@@ -569,7 +569,9 @@ void bsr16_spmm_strip_kernel(
 // fp32 one (156 KB for a +-32 band), so one workgroup holds the CU's LDS and
 // there are twice the VGPRs per wave (three waves per SIMD).  Operand layout
 // (see bsr16_spmm_f64_kernel): lane (i, g) feeds A's row 4 (i % 4) + i / 4
-// and B rows 4g .. 4g+3 of column i, and holds C rows 4g .. 4g+3 of column i.
+// and holds C rows 4g .. 4g+3 of column i; the contraction rows it feeds
+// (A's columns, B's rows) are kg, kg+1, kg+4, kg+5 with kg = 2 (g % 2) +
+// 8 (g / 2), an order whose window reads meet no LDS bank conflict (below).
 // The buffer resources of B and C are rebased per tile (B at the window's
 // first row of column c0, C at column c0), so 32-bit offsets cover 16 columns
 // of any height.  One workgroup per CU walks its XCD's strips (persistent),
@@ -600,6 +602,16 @@ __device__ __forceinline__ void raw_store_d4(doublex4 v, int32x4 rs, int voff, i
     const bsr_floatx4 *f = reinterpret_cast<const bsr_floatx4 *>(&v);
     raw_buffer_store_v4f32(f[0], rs, voff, soff, 0);
     raw_buffer_store_v4f32(f[1], rs, voff + 16, soff, 0);
+}
+
+// Four doubles from two 16-byte LDS pieces 32 bytes apart.
+__device__ __forceinline__ doublex4 lds_read_pieces(const char *p)
+{
+    doublex4 v;
+    bsr_floatx4 *f = reinterpret_cast<bsr_floatx4 *>(&v);
+    f[0] = *reinterpret_cast<const bsr_floatx4 *>(p);
+    f[1] = *reinterpret_cast<const bsr_floatx4 *>(p + 32);
+    return v;
 }
 
 __device__ __forceinline__ doublex4 raw_load_d4(int32x4 rs, int voff, int soff)
@@ -666,7 +678,15 @@ void bsr16_spmm_f64_strip_kernel(
     // A unit of four or more tiles sets up the next unit's strip during its
     // last four tiles; otherwise a strip is set up at its unit's start.
     const doublex4 zero = {0.0, 0.0, 0.0, 0.0};
-    const uint32_t col_off = (uint32_t)(i * BSR64_CS + 32 * g);
+    // Contraction split: lane (i, g) holds rows kg, kg + 1, kg + 4, kg + 5
+    // of the block (kg = 2 (g % 2) + 8 (g / 2)) -- A's columns and B's rows,
+    // MFMA u taking the u-th of them -- so it reads two 16-byte pieces of a
+    // window row, 32 bytes apart, at byte 8 kg.  With window columns
+    // BSR64_CS = 32 mod 512 bytes apart, the 32 lanes of a half-wave then
+    // read distinct LDS banks in each 8-byte pass of a ds_read_b128
+    // (SQ_LDS_BANK_CONFLICT: 0 cycles per read; 3.7 with rows 4g .. 4g + 3).
+    const int kg = 2 * (g & 1) + 8 * (g >> 1);
+    const uint32_t col_off = (uint32_t)(i * BSR64_CS + 8 * kg);
     auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
     auto tile_b = [&](int32_t jw, int c0) { return buffer_resource(B + (int64_t)jw * BSR_BS + (int64_t)c0 * ldb); };
 
@@ -795,7 +815,10 @@ void bsr16_spmm_f64_strip_kernel(
         lane_off = my_row * 128 + (lane & 7) * 16;
     };
     auto load_a = [&](doublex4 &dst, int qq) {
-        dst = *reinterpret_cast<const doublex4 *>(val + ((int64_t)q0n + qq) * 256 + ar * 16 + 4 * g);
+        const double *p = val + ((int64_t)q0n + qq) * 256 + ar * 16 + kg;
+        bsr_floatx4 *f = reinterpret_cast<bsr_floatx4 *>(&dst);
+        f[0] = *reinterpret_cast<const bsr_floatx4 *>(p);
+        f[1] = *reinterpret_cast<const bsr_floatx4 *>(p + 4);
     };
     // Column j of the window of the tile at column cb; the copy's LDS
     // address and B offset advance column by column from values made opaque
@@ -889,12 +912,17 @@ void bsr16_spmm_f64_strip_kernel(
         for (int t = t0; t < t1; ++t) {
             const int c0 = t * 16;
             const bool last = t == t1 - 1;
+            // Nothing is in flight here (the previous tile or the strip's start
+            // waited for everything); said explicitly, so that the compiler
+            // adds no waits of its own before this tile's MFMAs for the next
+            // strip's A loads of a last tile.
+            __builtin_amdgcn_s_waitcnt(0);
             doublex4 b[BSR_QCHUNK];
             uint32_t co = col_off, jr0 = jrel[0], jr1 = jrel[1];
             asm volatile("" : "+v"(co), "+s"(jr0), "+s"(jr1));
 #pragma unroll
             for (int qq = 0; qq < BSR_QCHUNK; ++qq)
-                b[qq] = *reinterpret_cast<const doublex4 *>(win + co + (((qq < 4 ? jr0 : jr1) >> (8 * (qq & 3))) & 0xffu) * 128);
+                b[qq] = lds_read_pieces(win + co + (((qq < 4 ? jr0 : jr1) >> (8 * (qq & 3))) & 0xffu) * 128);
             barrier();                     // the window is free
             flush();
             if (!BZ && live && c0 + i < kk) oldp = raw_load_d4(buffer_resource(C + (int64_t)c0 * ldc), c_lane, so_c);
