@@ -992,6 +992,14 @@ bool bsr_strip()
     return !(e && e[0] == '0');
 }
 
+// JLUST_HIP_BSR_SPMV_SEGMENTS=0 keeps 16 x 16 BSR SpMV on the one-thread-per-
+// row kernel (read at each call, for tests and timing beside it).
+bool bsr_spmv_segments()
+{
+    const char *e = getenv("JLUST_HIP_BSR_SPMV_SEGMENTS");
+    return !(e && e[0] == '0');
+}
+
 // ------------------------------------------------------------- BSR SpMV
 
 // y = alpha*A*x + beta*y for BSR of any b1 x b2 blocks: one thread per
@@ -1023,6 +1031,207 @@ __global__ __launch_bounds__(256) void bsr_spmv_kernel(int64_t mb, int64_t nb, i
     y[row] = BZ ? alpha * acc : alpha * acc + beta * y[row];
 }
 
+// 16 x 16 blocks: segments of at most BSRMV_SEG blocks of one block-row, a
+// wave each, so that a long block-row is spread over many waves and a short
+// one costs one wave (one thread per scalar row leaves a power-law row
+// pattern to its longest row: 12 ms for what the segments do in 0.2 ms).
+// A block-row of n blocks has max(1, ceil(n / BSRMV_SEG)) segments (an empty
+// one is a segment of no blocks, which writes beta*y).  Each lane holds a
+// partial sum of one scalar row over 4 of the block's 16 columns, blocks in
+// storage order; the 4 partials combine in a fixed order; a block-row of one
+// segment writes y, one of several writes each segment's 16 sums to part[],
+// and a second kernel adds them in segment order.  The result is the same
+// on every call; its summation order differs from the CSR expansion's.
+constexpr int BSRMV_SEG = 32;              // blocks per segment
+#ifndef JLUST_BSRMV_UNROLL
+#define JLUST_BSRMV_UNROLL 8
+#endif
+constexpr int BSRMV_UNROLL = JLUST_BSRMV_UNROLL;
+
+// Segment counts: segstart[R] = max(1, ceil(n_R / BSRMV_SEG)) for R < mb and
+// segstart[mb] = 0; an exclusive scan then makes segstart[R] the first
+// segment of block-row R and segstart[mb] the count.  Block ranges are
+// clamped as in bsr_spmv_kernel.
+__global__ __launch_bounds__(256) void bsr16_spmv_count_kernel(int64_t mb, int64_t nnzb, int32_t origin,
+                                                               const int32_t *__restrict__ browptr,
+                                                               int32_t *__restrict__ segstart)
+{
+    const int64_t R = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (R > mb) return;
+    if (R == mb) {
+        segstart[mb] = 0;
+        return;
+    }
+    const int64_t q0 = min(max((int64_t)browptr[R] - origin, (int64_t)0), nnzb);
+    const int64_t q1 = min(max((int64_t)browptr[R + 1] - origin, q0), nnzb);
+    segstart[R] = (int32_t)max((int64_t)1, (q1 - q0 + BSRMV_SEG - 1) / BSRMV_SEG);
+}
+
+// segrow[s] = the block-row of segment s, one thread per block-row.  Segment
+// numbers are clamped to [0, nsegmax) (a canonical browptr has at most
+// nsegmax segments), and every reader clamps what it reads, so a malformed
+// browptr cannot take an access out of bounds.
+__global__ __launch_bounds__(256) void bsr16_spmv_rows_kernel(int64_t mb, const int32_t *__restrict__ segstart,
+                                                              int32_t *__restrict__ segrow, int64_t nsegmax)
+{
+    const int64_t R = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (R >= mb) return;
+    const int64_t s0 = min(max((int64_t)segstart[R], (int64_t)0), nsegmax);
+    const int64_t s1 = min(max((int64_t)segstart[R + 1], s0), nsegmax);
+    for (int64_t s = s0; s < s1; ++s) segrow[s] = (int32_t)R;
+}
+
+template <typename T, bool RM, bool VEC, bool BZ>
+__global__ __launch_bounds__(256) void bsr16_spmv_seg_kernel(int64_t mb, int64_t nb, int64_t nnzb, int32_t origin,
+                                                             const int32_t *__restrict__ browptr,
+                                                             const int32_t *__restrict__ bcolind,
+                                                             const T *__restrict__ val, T alpha,
+                                                             const T *__restrict__ x, T beta, T *__restrict__ y,
+                                                             const int32_t *__restrict__ segstart,
+                                                             const int32_t *__restrict__ segrow,
+                                                             T *__restrict__ part, int64_t nsegmax)
+{
+    const int64_t sg_id = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (sg_id >= nsegmax || sg_id >= (int64_t)segstart[mb]) return;   // whole waves
+    const int lane = threadIdx.x & 63;
+    // Row-major blocks: lane (r, c4) = (lane / 4, lane % 4), 16 contiguous
+    // bytes of row r; column-major: (lane % 16, lane / 16), one element of
+    // each of 4 columns (16 lanes read 64 contiguous bytes).
+    const int r = RM ? lane >> 2 : lane & 15;
+    const int c4 = RM ? lane & 3 : lane >> 4;
+    const int64_t R = min(max((int64_t)segrow[sg_id], (int64_t)0), mb - 1);
+    const int64_t k = sg_id - segstart[R];
+    const int64_t nsR = (int64_t)segstart[R + 1] - segstart[R];
+    const int64_t rb = min(max((int64_t)browptr[R] - origin, (int64_t)0), nnzb);
+    const int64_t re = min(max((int64_t)browptr[R + 1] - origin, rb), nnzb);
+    const int64_t q0 = min(max(rb + k * BSRMV_SEG, rb), re), q1 = min(q0 + BSRMV_SEG, re);
+    // Blocks in groups of BSRMV_UNROLL: the group's column indices, then its
+    // value and x loads, then the products in storage order, so that a
+    // wave keeps that many blocks' loads in flight.
+    T acc = T(0);
+    auto load = [&](int64_t q, T (&vv)[4], T (&xx)[4]) {
+        const int64_t c = min(max((int64_t)bcolind[q] - origin, (int64_t)0), nb - 1) * 16 + 4 * c4;
+        const T *v = val + q * 256;
+        if (RM && VEC) {
+            typedef T T2 __attribute__((ext_vector_type(2)));
+            const T *vr = v + r * 16 + 4 * c4;
+            const T2 v0 = *reinterpret_cast<const T2 *>(vr), v1 = *reinterpret_cast<const T2 *>(vr + 2);
+            const T2 x0 = *reinterpret_cast<const T2 *>(x + c), x1 = *reinterpret_cast<const T2 *>(x + c + 2);
+            vv[0] = v0.x; vv[1] = v0.y; vv[2] = v1.x; vv[3] = v1.y;
+            xx[0] = x0.x; xx[1] = x0.y; xx[2] = x1.x; xx[3] = x1.y;
+        } else {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                vv[u] = RM ? v[r * 16 + 4 * c4 + u] : v[(4 * c4 + u) * 16 + r];
+                xx[u] = x[c + u];
+            }
+        }
+    };
+    int64_t q = q0;
+    for (; q + BSRMV_UNROLL <= q1; q += BSRMV_UNROLL) {
+        T vv[BSRMV_UNROLL][4], xx[BSRMV_UNROLL][4];
+#pragma unroll
+        for (int b = 0; b < BSRMV_UNROLL; ++b) load(q + b, vv[b], xx[b]);
+#pragma unroll
+        for (int b = 0; b < BSRMV_UNROLL; ++b)
+#pragma unroll
+            for (int u = 0; u < 4; ++u) acc += vv[b][u] * xx[b][u];
+    }
+    for (; q < q1; ++q) {
+        T vv[4], xx[4];
+        load(q, vv, xx);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc += vv[u] * xx[u];
+    }
+    // The 4 column groups of a row, in the order (0 + 1) + (2 + 3).
+    const int m1 = RM ? 1 : 16, m2 = RM ? 2 : 32;
+    acc += __shfl_xor(acc, m1, 64);
+    acc += __shfl_xor(acc, m2, 64);
+    if (c4 != 0) return;
+    if (nsR == 1) {
+        T *yr = y + R * 16 + r;
+        *yr = BZ ? alpha * acc : alpha * acc + beta * *yr;
+    } else {
+        part[sg_id * 16 + r] = acc;
+    }
+}
+
+// y of the block-rows of several segments: their sums added in segment order.
+template <typename T, bool BZ>
+__global__ __launch_bounds__(256) void bsr16_spmv_fix_kernel(int64_t mb, const int32_t *__restrict__ segstart,
+                                                             const T *__restrict__ part, int64_t nsegmax,
+                                                             T alpha, T beta, T *__restrict__ y)
+{
+    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= mb * 16) return;
+    const int64_t R = row / 16, r = row % 16;
+    const int64_t s0 = segstart[R], s1 = segstart[R + 1];
+    if (s1 - s0 <= 1 || s0 < 0 || s1 > nsegmax) return;
+    // Eight partial sums loaded at a time, added in segment order.
+    T acc = T(0);
+    int64_t s = s0;
+    for (; s + 8 <= s1; s += 8) {
+        T p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p[u] = part[(s + u) * 16 + r];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += p[u];
+    }
+    for (; s < s1; ++s) acc += part[s * 16 + r];
+    y[row] = BZ ? alpha * acc : alpha * acc + beta * y[row];
+}
+
+template <typename T>
+int bsr16_spmv(int64_t mb, int64_t nb, int64_t nnzb, int32_t origin, const int32_t *browptr,
+               const int32_t *bcolind, const T *val, int row_major_blocks, T alpha, const T *x, T beta, T *y,
+               jlust_stream_t stream)
+{
+    // Scratch: the scan's own part, then segstart (mb + 1), segrow (at most
+    // mb + nnzb / BSRMV_SEG segments), part (16 sums per segment).
+    const int64_t nsegmax = mb + (nnzb + BSRMV_SEG - 1) / BSRMV_SEG;
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t start_off = up(exclusive_scan_scratch_bytes(mb + 1));
+    const size_t row_off = start_off + up((size_t)(mb + 1) * sizeof(int32_t));
+    const size_t part_off = row_off + up((size_t)nsegmax * sizeof(int32_t));
+    void *ws = nullptr;
+    if (int st = scratch(stream, part_off + (size_t)nsegmax * 16 * sizeof(T), &ws)) return st;
+    int32_t *segstart = (int32_t *)((char *)ws + start_off), *segrow = (int32_t *)((char *)ws + row_off);
+    T *part = (T *)((char *)ws + part_off);
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(bsr16_spmv_count_kernel, dim3((unsigned)((mb + 1 + 255) / 256)), dim3(256), 0, s, mb, nnzb,
+                       origin, browptr, segstart);
+    if (int st = check_launch("bsr16_spmv_count_kernel")) return st;
+    if (int st = exclusive_scan_i32(segstart, segstart, mb + 1, stream)) return st;
+    hipLaunchKernelGGL(bsr16_spmv_rows_kernel, dim3((unsigned)((mb + 255) / 256)), dim3(256), 0, s, mb, segstart,
+                       segrow, nsegmax);
+    if (int st = check_launch("bsr16_spmv_rows_kernel")) return st;
+    const bool bz = beta == T(0);
+    const bool vec = ((uintptr_t)val % (2 * sizeof(T)) == 0) && ((uintptr_t)x % (2 * sizeof(T)) == 0);
+    const dim3 grid((unsigned)((nsegmax + 3) / 4));
+#define JLUST_BSRMV16(RM, V, Z)                                                                             \
+    hipLaunchKernelGGL((bsr16_spmv_seg_kernel<T, RM, V, Z>), grid, dim3(256), 0, s, mb, nb, nnzb, origin,  \
+                       browptr, bcolind, val, alpha, x, beta, y, segstart, segrow, part, nsegmax)
+    if (row_major_blocks) {
+        if (vec) {
+            if (bz) JLUST_BSRMV16(true, true, true); else JLUST_BSRMV16(true, true, false);
+        } else {
+            if (bz) JLUST_BSRMV16(true, false, true); else JLUST_BSRMV16(true, false, false);
+        }
+    } else {
+        if (bz) JLUST_BSRMV16(false, false, true); else JLUST_BSRMV16(false, false, false);
+    }
+#undef JLUST_BSRMV16
+    if (int st = check_launch("bsr16_spmv_seg_kernel")) return st;
+    const dim3 gfix((unsigned)((mb * 16 + 255) / 256));
+    if (bz)
+        hipLaunchKernelGGL((bsr16_spmv_fix_kernel<T, true>), gfix, dim3(256), 0, s, mb, segstart, part, nsegmax, alpha,
+                           beta, y);
+    else
+        hipLaunchKernelGGL((bsr16_spmv_fix_kernel<T, false>), gfix, dim3(256), 0, s, mb, segstart, part, nsegmax, alpha,
+                           beta, y);
+    return check_launch("bsr16_spmv_fix_kernel");
+}
+
 template <typename T>
 int bsr_spmv(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
              const int32_t *browptr, const int32_t *bcolind, const T *val, int row_major_blocks, T alpha,
@@ -1042,6 +1251,9 @@ int bsr_spmv(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32
     if (int st = require_device(nullptr)) return st;
     const int64_t m = mb * b1;
     if (m == 0) return JLUST_STATUS_SUCCESS;
+    if (b1 == 16 && b2 == 16 && bsr_spmv_segments())
+        return bsr16_spmv<T>(mb, nb, nnzb, origin, browptr, bcolind, val, row_major_blocks, alpha, x, beta, y,
+                             stream);
     const dim3 grid((unsigned)((m + 255) / 256));
     hipStream_t s = (hipStream_t)stream;
 #define JLUST_BSRMV(RM, Z)                                                                             \
@@ -1524,6 +1736,7 @@ namespace jlust {
 int preload_bsr()
 {
     JLUST_PRELOAD_KERNEL(bsr_expand_rowptr_kernel);
+    JLUST_PRELOAD_KERNEL(bsr16_spmv_count_kernel);
     return JLUST_STATUS_SUCCESS;
 }
 }  // namespace jlust

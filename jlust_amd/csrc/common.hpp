@@ -76,6 +76,10 @@ int scratch(jlust_stream_t stream, size_t bytes, void **out);
 // out[i] = sum(in[0..i)) over n int32 counts (in == out allowed); stream-ordered.
 // Uses the stream's scratch buffer for chunk sums.
 int exclusive_scan_i32(const int32_t *in, int32_t *out, int64_t n, jlust_stream_t stream);
+// The first bytes of the stream's scratch buffer that exclusive_scan_i32 over
+// n counts uses; a caller keeping data of its own in that buffer across the
+// scan places it after them.
+size_t exclusive_scan_scratch_bytes(int64_t n);
 
 constexpr int NUM_XCD = 8;   // MI355X: workgroup b runs on XCD b % 8
 

@@ -96,6 +96,11 @@ __global__ __launch_bounds__(SCAN_BLOCK) void scan_apply(const int32_t *in, int3
 
 }  // namespace
 
+size_t exclusive_scan_scratch_bytes(int64_t n)
+{
+    return n <= 0 ? 0 : sizeof(int64_t) * (size_t)((n + SCAN_CHUNK - 1) / SCAN_CHUNK);
+}
+
 int exclusive_scan_i32(const int32_t *in, int32_t *out, int64_t n, jlust_stream_t stream)
 {
     if (n <= 0) return JLUST_STATUS_SUCCESS;
