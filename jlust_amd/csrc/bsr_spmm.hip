@@ -992,9 +992,9 @@ bool bsr_strip()
     return !(e && e[0] == '0');
 }
 
-// JLUST_HIP_BSR_SPMV_SEGMENTS=0 keeps 16 x 16 BSR SpMV on the one-thread-per-
-// row kernel (read at each call, for tests and timing beside it).
-bool bsr_spmv_segments()
+// JLUST_HIP_BSR_SPMV_SEGMENTS=0 keeps BSR SpMV on the one-thread-per-row
+// kernel (read at each call, for tests and timing beside it).
+bool bsr_spmv_segmented()
 {
     const char *e = getenv("JLUST_HIP_BSR_SPMV_SEGMENTS");
     return !(e && e[0] == '0');
@@ -1156,15 +1156,54 @@ __global__ __launch_bounds__(256) void bsr16_spmv_seg_kernel(int64_t mb, int64_t
     }
 }
 
+// Blocks of any other shape: a thread per (segment, scalar row), blocks in
+// storage order and each block's row in column order, as bsr_spmv_kernel
+// (a block-row of one segment gets that kernel's sum).
+template <typename T, bool RM, bool BZ>
+__global__ __launch_bounds__(256) void bsr_spmv_seg_kernel(int64_t mb, int64_t nb, int64_t b1, int64_t b2,
+                                                           int64_t nnzb, int32_t origin,
+                                                           const int32_t *__restrict__ browptr,
+                                                           const int32_t *__restrict__ bcolind,
+                                                           const T *__restrict__ val, T alpha,
+                                                           const T *__restrict__ x, T beta, T *__restrict__ y,
+                                                           const int32_t *__restrict__ segstart,
+                                                           const int32_t *__restrict__ segrow,
+                                                           T *__restrict__ part, int64_t nsegmax)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t sg_id = t / b1, r = t % b1;
+    if (sg_id >= nsegmax || sg_id >= (int64_t)segstart[mb]) return;
+    const int64_t R = min(max((int64_t)segrow[sg_id], (int64_t)0), mb - 1);
+    const int64_t k = sg_id - segstart[R];
+    const int64_t nsR = (int64_t)segstart[R + 1] - segstart[R];
+    const int64_t rb = min(max((int64_t)browptr[R] - origin, (int64_t)0), nnzb);
+    const int64_t re = min(max((int64_t)browptr[R + 1] - origin, rb), nnzb);
+    const int64_t q0 = min(max(rb + k * BSRMV_SEG, rb), re), q1 = min(q0 + BSRMV_SEG, re);
+    const int64_t bb = b1 * b2;
+    T acc = T(0);
+    for (int64_t q = q0; q < q1; ++q) {
+        const int64_t c = min(max((int64_t)bcolind[q] - origin, (int64_t)0), nb - 1) * b2;
+        const T *v = val + q * bb + (RM ? r * b2 : r);
+        for (int64_t s = 0; s < b2; ++s) acc += v[RM ? s : s * b1] * x[c + s];
+    }
+    if (nsR == 1) {
+        T *yr = y + R * b1 + r;
+        *yr = BZ ? alpha * acc : alpha * acc + beta * *yr;
+    } else {
+        part[sg_id * b1 + r] = acc;
+    }
+}
+
 // y of the block-rows of several segments: their sums added in segment order.
 template <typename T, bool BZ>
-__global__ __launch_bounds__(256) void bsr16_spmv_fix_kernel(int64_t mb, const int32_t *__restrict__ segstart,
-                                                             const T *__restrict__ part, int64_t nsegmax,
-                                                             T alpha, T beta, T *__restrict__ y)
+__global__ __launch_bounds__(256) void bsr_spmv_fix_kernel(int64_t mb, int64_t b1,
+                                                           const int32_t *__restrict__ segstart,
+                                                           const T *__restrict__ part, int64_t nsegmax,
+                                                           T alpha, T beta, T *__restrict__ y)
 {
     const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (row >= mb * 16) return;
-    const int64_t R = row / 16, r = row % 16;
+    if (row >= mb * b1) return;
+    const int64_t R = row / b1, r = row % b1;
     const int64_t s0 = segstart[R], s1 = segstart[R + 1];
     if (s1 - s0 <= 1 || s0 < 0 || s1 > nsegmax) return;
     // Eight partial sums loaded at a time, added in segment order.
@@ -1173,28 +1212,28 @@ __global__ __launch_bounds__(256) void bsr16_spmv_fix_kernel(int64_t mb, const i
     for (; s + 8 <= s1; s += 8) {
         T p[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) p[u] = part[(s + u) * 16 + r];
+        for (int u = 0; u < 8; ++u) p[u] = part[(s + u) * b1 + r];
 #pragma unroll
         for (int u = 0; u < 8; ++u) acc += p[u];
     }
-    for (; s < s1; ++s) acc += part[s * 16 + r];
+    for (; s < s1; ++s) acc += part[s * b1 + r];
     y[row] = BZ ? alpha * acc : alpha * acc + beta * y[row];
 }
 
 template <typename T>
-int bsr16_spmv(int64_t mb, int64_t nb, int64_t nnzb, int32_t origin, const int32_t *browptr,
-               const int32_t *bcolind, const T *val, int row_major_blocks, T alpha, const T *x, T beta, T *y,
-               jlust_stream_t stream)
+int bsr_spmv_segments(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
+                      const int32_t *browptr, const int32_t *bcolind, const T *val, int row_major_blocks, T alpha,
+                      const T *x, T beta, T *y, jlust_stream_t stream)
 {
     // Scratch: the scan's own part, then segstart (mb + 1), segrow (at most
-    // mb + nnzb / BSRMV_SEG segments), part (16 sums per segment).
+    // mb + nnzb / BSRMV_SEG segments), part (b1 sums per segment).
     const int64_t nsegmax = mb + (nnzb + BSRMV_SEG - 1) / BSRMV_SEG;
     auto up = [](size_t b) { return (b + 255) / 256 * 256; };
     const size_t start_off = up(exclusive_scan_scratch_bytes(mb + 1));
     const size_t row_off = start_off + up((size_t)(mb + 1) * sizeof(int32_t));
     const size_t part_off = row_off + up((size_t)nsegmax * sizeof(int32_t));
     void *ws = nullptr;
-    if (int st = scratch(stream, part_off + (size_t)nsegmax * 16 * sizeof(T), &ws)) return st;
+    if (int st = scratch(stream, part_off + (size_t)(nsegmax * b1) * sizeof(T), &ws)) return st;
     int32_t *segstart = (int32_t *)((char *)ws + start_off), *segrow = (int32_t *)((char *)ws + row_off);
     T *part = (T *)((char *)ws + part_off);
     hipStream_t s = (hipStream_t)stream;
@@ -1206,30 +1245,44 @@ int bsr16_spmv(int64_t mb, int64_t nb, int64_t nnzb, int32_t origin, const int32
                        segrow, nsegmax);
     if (int st = check_launch("bsr16_spmv_rows_kernel")) return st;
     const bool bz = beta == T(0);
-    const bool vec = ((uintptr_t)val % (2 * sizeof(T)) == 0) && ((uintptr_t)x % (2 * sizeof(T)) == 0);
-    const dim3 grid((unsigned)((nsegmax + 3) / 4));
-#define JLUST_BSRMV16(RM, V, Z)                                                                             \
-    hipLaunchKernelGGL((bsr16_spmv_seg_kernel<T, RM, V, Z>), grid, dim3(256), 0, s, mb, nb, nnzb, origin,  \
-                       browptr, bcolind, val, alpha, x, beta, y, segstart, segrow, part, nsegmax)
-    if (row_major_blocks) {
-        if (vec) {
-            if (bz) JLUST_BSRMV16(true, true, true); else JLUST_BSRMV16(true, true, false);
+    if (b1 != 16 || b2 != 16) {
+        const dim3 g((unsigned)((nsegmax * b1 + 255) / 256));
+#define JLUST_BSRMVG(RM, Z)                                                                              \
+        hipLaunchKernelGGL((bsr_spmv_seg_kernel<T, RM, Z>), g, dim3(256), 0, s, mb, nb, b1, b2, nnzb, origin, \
+                           browptr, bcolind, val, alpha, x, beta, y, segstart, segrow, part, nsegmax)
+        if (row_major_blocks) {
+            if (bz) JLUST_BSRMVG(true, true); else JLUST_BSRMVG(true, false);
         } else {
-            if (bz) JLUST_BSRMV16(true, false, true); else JLUST_BSRMV16(true, false, false);
+            if (bz) JLUST_BSRMVG(false, true); else JLUST_BSRMVG(false, false);
         }
+#undef JLUST_BSRMVG
+        if (int st = check_launch("bsr_spmv_seg_kernel")) return st;
     } else {
-        if (bz) JLUST_BSRMV16(false, false, true); else JLUST_BSRMV16(false, false, false);
-    }
+        const bool vec = ((uintptr_t)val % (2 * sizeof(T)) == 0) && ((uintptr_t)x % (2 * sizeof(T)) == 0);
+        const dim3 grid((unsigned)((nsegmax + 3) / 4));
+#define JLUST_BSRMV16(RM, V, Z)                                                                             \
+        hipLaunchKernelGGL((bsr16_spmv_seg_kernel<T, RM, V, Z>), grid, dim3(256), 0, s, mb, nb, nnzb, origin,  \
+                           browptr, bcolind, val, alpha, x, beta, y, segstart, segrow, part, nsegmax)
+        if (row_major_blocks) {
+            if (vec) {
+                if (bz) JLUST_BSRMV16(true, true, true); else JLUST_BSRMV16(true, true, false);
+            } else {
+                if (bz) JLUST_BSRMV16(true, false, true); else JLUST_BSRMV16(true, false, false);
+            }
+        } else {
+            if (bz) JLUST_BSRMV16(false, false, true); else JLUST_BSRMV16(false, false, false);
+        }
 #undef JLUST_BSRMV16
-    if (int st = check_launch("bsr16_spmv_seg_kernel")) return st;
-    const dim3 gfix((unsigned)((mb * 16 + 255) / 256));
+        if (int st = check_launch("bsr16_spmv_seg_kernel")) return st;
+    }
+    const dim3 gfix((unsigned)((mb * b1 + 255) / 256));
     if (bz)
-        hipLaunchKernelGGL((bsr16_spmv_fix_kernel<T, true>), gfix, dim3(256), 0, s, mb, segstart, part, nsegmax, alpha,
-                           beta, y);
+        hipLaunchKernelGGL((bsr_spmv_fix_kernel<T, true>), gfix, dim3(256), 0, s, mb, b1, segstart, part, nsegmax,
+                           alpha, beta, y);
     else
-        hipLaunchKernelGGL((bsr16_spmv_fix_kernel<T, false>), gfix, dim3(256), 0, s, mb, segstart, part, nsegmax, alpha,
-                           beta, y);
-    return check_launch("bsr16_spmv_fix_kernel");
+        hipLaunchKernelGGL((bsr_spmv_fix_kernel<T, false>), gfix, dim3(256), 0, s, mb, b1, segstart, part, nsegmax,
+                           alpha, beta, y);
+    return check_launch("bsr_spmv_fix_kernel");
 }
 
 template <typename T>
@@ -1251,9 +1304,9 @@ int bsr_spmv(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32
     if (int st = require_device(nullptr)) return st;
     const int64_t m = mb * b1;
     if (m == 0) return JLUST_STATUS_SUCCESS;
-    if (b1 == 16 && b2 == 16 && bsr_spmv_segments())
-        return bsr16_spmv<T>(mb, nb, nnzb, origin, browptr, bcolind, val, row_major_blocks, alpha, x, beta, y,
-                             stream);
+    if (bsr_spmv_segmented())
+        return bsr_spmv_segments<T>(mb, nb, b1, b2, nnzb, origin, browptr, bcolind, val, row_major_blocks, alpha, x,
+                                    beta, y, stream);
     const dim3 grid((unsigned)((m + 255) / 256));
     hipStream_t s = (hipStream_t)stream;
 #define JLUST_BSRMV(RM, Z)                                                                             \

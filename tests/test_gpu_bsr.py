@@ -414,20 +414,21 @@ def test_bsr_f32_unaligned_values_plain_and_plan(J, O):
     assert_within(host(C2), ref, absref, np.float32, "unaligned plan")
 
 
+@pytest.mark.parametrize("b1,b2", [(16, 16), (3, 5)])
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("row_major", [True, False])
 @pytest.mark.parametrize("segments", ["1", "0"])
-def test_bsr16_spmv_power_law_rows(J, O, dtype, row_major, segments, monkeypatch):
-    """16 x 16 BSR SpMV over power-law block-rows (one of 700 blocks, several
-    past the 32-block segment, empty ones): the segmented kernel spreads a
-    block-row over waves and adds the segments' sums in order
-    (JLUST_HIP_BSR_SPMV_SEGMENTS=0: the one-thread-per-row kernel).  Against
-    the oracle's expansion + CSR SpMV, alpha/beta, values viewed at an odd
-    offset too (element loads)."""
+def test_bsr_spmv_power_law_rows(J, O, b1, b2, dtype, row_major, segments, monkeypatch):
+    """BSR SpMV over power-law block-rows (one of 700 blocks, several past
+    the 32-block segment, empty ones): the segmented kernels spread a
+    block-row over waves (16 x 16) or threads (other shapes) and add the
+    segments' sums in order (JLUST_HIP_BSR_SPMV_SEGMENTS=0: the
+    one-thread-per-row kernel).  Against the oracle's expansion + CSR SpMV,
+    alpha/beta, values viewed at an odd offset too (element loads)."""
     import torch
     monkeypatch.setenv("JLUST_HIP_BSR_SPMV_SEGMENTS", segments)
     mb, nb = 300, 900
-    rng = np.random.default_rng(17 + row_major)
+    rng = np.random.default_rng(17 + row_major + b1)
     lens = np.minimum((rng.pareto(1.3, mb) + 1) * 3, nb).astype(np.int64)
     lens[::11] = 0
     lens[5], lens[6], lens[7] = 700, 33, 32
@@ -435,18 +436,18 @@ def test_bsr16_spmv_power_law_rows(J, O, dtype, row_major, segments, monkeypatch
     origin = 1 if row_major else 0
     bp = (np.r_[0, np.cumsum(lens)] + origin).astype(np.int32)
     bc = (np.concatenate(bcols) + origin).astype(np.int32)
-    flat = rng.standard_normal(bc.size * 256).astype(dtype)
-    x = rng.uniform(-1, 1, nb * 16).astype(dtype)
-    y0 = rng.uniform(-1, 1, mb * 16).astype(dtype)
-    rp, ci, v = O.bsr_to_csr(bp, bc, flat, 16, origin, row_major, 16)
+    flat = rng.standard_normal(bc.size * b1 * b2).astype(dtype)
+    x = rng.uniform(-1, 1, nb * b2).astype(dtype)
+    y0 = rng.uniform(-1, 1, mb * b1).astype(dtype)
+    rp, ci, v = O.bsr_to_csr(bp, bc, flat, b1, origin, row_major, b2)
     og = J.OneBased() if origin == 1 else J.ZeroBased()
     vbuf = dev(np.r_[np.zeros(1, dtype), flat])
     for vals in (dev(flat), vbuf[1:]):
-        A = J.bsr_tensor(dev(bp), dev(bc), vals, (mb * 16, nb * 16), (16, 16), row_major, og)
+        A = J.bsr_tensor(dev(bp), dev(bc), vals, (mb * b1, nb * b2), (b1, b2), row_major, og)
         for alpha, beta in ((1.0, 0.0), (-0.5, 1.5)):
-            y = dev(y0.copy()) if beta else torch.full((mb * 16,), float("nan"), dtype=A.dtype, device="cuda")
+            y = dev(y0.copy()) if beta else torch.full((mb * b1,), float("nan"), dtype=A.dtype, device="cuda")
             J.execute(J.SpMVOp, A, dev(x), y, alpha=alpha, beta=beta)
             yb = y0 if beta else None
             ref = O.csr_spmv(rp, ci, v, x, alpha, beta, yb, origin)
             absref = O.csr_spmv_absref(rp, ci, v, x, alpha, beta, yb, origin)
-            assert_within(host(y), ref, absref, dtype, f"bsr16 spmv power-law beta={beta}")
+            assert_within(host(y), ref, absref, dtype, f"bsr {b1}x{b2} spmv power-law beta={beta}")
