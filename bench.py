@@ -82,6 +82,9 @@ def parse():
     p.add_argument("--bsr-f64", action="store_true",
                    help="config 5's BSR pattern in Float64: the fp64 MFMA kernel against the CSR "
                         "expansion path")
+    p.add_argument("--bsr-spmv", action="store_true",
+                   help="16 x 16 BSR SpMV over power-law block-rows: the segmented kernel, the "
+                        "one-thread-per-row kernel and the CSR expansion route")
     p.add_argument("--gather-overlap", action="store_true",
                    help="only time config 3's chunk gathers alone, a 256 MB transpose alone, and the "
                         "two on two streams at once")
@@ -578,6 +581,77 @@ def bsr_f64():
            "csr_expansion_ms": round(t_csr, 3), "csr_expansion_tflops": tf(t_csr)}
     log(f"bsr f64: {res}")
     return res
+
+
+def bsr_spmv_powerlaw():
+    """16 x 16 BSR SpMV (jlust_hip_bsr_spmv_*) over power-law block-rows:
+    65,536 block-rows whose lengths follow a Pareto law (mean about 8 blocks,
+    capped at 8,192), random block columns, values N(0, 1).  The segmented
+    kernel (default), the one-thread-per-row kernel
+    (JLUST_HIP_BSR_SPMV_SEGMENTS=0), and the CSR expansion route (expansion,
+    then CSR SpMV on the expanded matrix).  HIP events: the median of 5 runs
+    of 20 calls after 3 warm-up calls; bytes = values + block columns +
+    browptr + x + y."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd.hip_backend import _bsr_as_csr
+    stream = torch.cuda.current_stream()
+
+    def ms(fn, reps=20, trials=5):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(trials):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            for _ in range(reps):
+                fn()
+            e.record(stream)
+            torch.cuda.synchronize()
+            ts.append(s.elapsed_time(e) / reps)
+        return sorted(ts)[len(ts) // 2]
+
+    out = []
+    mb = nb = 65536
+    rng = np.random.default_rng(1)
+    lens = np.maximum(np.minimum((rng.pareto(1.5, mb) + 1) * 8 / 3, 8192).astype(np.int64), 1)
+    bcolind = np.concatenate([np.sort(rng.choice(nb, int(n), replace=False)) for n in lens]).astype(np.int32)
+    browptr = np.r_[0, np.cumsum(lens)].astype(np.int32)
+    nnzb = int(bcolind.size)
+    for dt in (np.float32, np.float64):
+        val = np.random.default_rng(2).standard_normal(nnzb * 256).astype(dt)
+        A = J.bsr_tensor(dev(browptr), dev(bcolind), dev(val), (mb * 16, nb * 16), (16, 16),
+                         origin=J.ZeroBased())
+        del val
+        x = dev(np.random.default_rng(3).standard_normal(nb * 16).astype(dt))
+        y = torch.zeros(mb * 16, dtype=x.dtype, device="cuda")
+        t_seg = ms(lambda: J.execute(J.SpMVOp, A, x, y))
+        old = os.environ.get("JLUST_HIP_BSR_SPMV_SEGMENTS")
+        os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"] = "0"
+        try:
+            t_row = ms(lambda: J.execute(J.SpMVOp, A, x, y), reps=3, trials=1)
+        finally:
+            if old is None:
+                del os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"]
+            else:
+                os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"] = old
+        t_exp = ms(lambda: _bsr_as_csr(A), reps=3, trials=1)
+        Acsr = _bsr_as_csr(A)
+        t_csr = ms(lambda: J.execute(J.SpMVOp, Acsr, x, y))
+        isz = np.dtype(dt).itemsize
+        nbytes = nnzb * 256 * isz + nnzb * 4 + (mb + 1) * 4 + (nb + mb) * 16 * isz
+        gbs = lambda t: round(nbytes / (t * 1e-3) / 1e9, 1)  # noqa: E731
+        r = {"workload": f"bsr16_spmv_powerlaw_65536_{np.dtype(dt).name}", "nnzb": nnzb,
+             "max_blocks_per_row": int(lens.max()), "bytes": nbytes,
+             "segments_ms": round(t_seg, 4), "segments_GBps": gbs(t_seg),
+             "row_kernel_ms": round(t_row, 3), "row_kernel_GBps": gbs(t_row),
+             "expansion_ms": round(t_exp, 3), "csr_spmv_on_expansion_ms": round(t_csr, 4)}
+        log(f"bsr spmv: {r}")
+        out.append(r)
+        del A, Acsr, x, y
+        torch.cuda.empty_cache()
+    return out
 
 
 def gather_overlap():
@@ -1445,6 +1519,9 @@ def main():
         return
     if args.bsr_f64:
         print(json.dumps({"bsr_f64": bsr_f64()}), flush=True)
+        return
+    if args.bsr_spmv:
+        print(json.dumps({"bsr_spmv": bsr_spmv_powerlaw()}), flush=True)
         return
     if args.spmv_parts:
         print(json.dumps({"spmv_parts": spmv_parts()}), flush=True)
