@@ -82,6 +82,9 @@ def parse():
     p.add_argument("--bsr-f64", action="store_true",
                    help="config 5's BSR pattern in Float64: the fp64 MFMA kernel against the CSR "
                         "expansion path")
+    p.add_argument("--plan-build", action="store_true",
+                   help="config 2's SpMV plan built six times: wall time per build, the first "
+                        "included, after jlust_amd.preload()")
     p.add_argument("--bsr-spmv", action="store_true",
                    help="16 x 16 BSR SpMV over power-law block-rows: the segmented kernel, the "
                         "one-thread-per-row kernel and the CSR expansion route")
@@ -581,6 +584,39 @@ def bsr_f64():
            "csr_expansion_ms": round(t_csr, 3), "csr_expansion_tflops": tf(t_csr)}
     log(f"bsr f64: {res}")
     return res
+
+
+def plan_build():
+    """Config 2's prepared SpMV plan (`prepare(HIPBackend(), SpMVOp, A)`, the
+    LDS-binned layout) built six times in one process after
+    jlust_amd.preload(): wall time of each build from the call to the
+    device's completion, the plan's kind and its device bytes.  Under
+    `rocprofv3 --kernel-trace` the same command gives the build's kernels."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    t0 = time.perf_counter()
+    J.preload()
+    torch.cuda.synchronize()
+    preload_ms = (time.perf_counter() - t0) * 1e3
+    cfg = W.make(2)
+    A = J.csr_tensor(dev(cfg["rowptr"]), dev(cfg["colind"]), dev(cfg["val"]), (cfg["m"], cfg["n"]))
+    del cfg
+    builds, kind, nbytes = [], None, None
+    for _ in range(6):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+        torch.cuda.synchronize()
+        builds.append(round((time.perf_counter() - t0) * 1e3, 2))
+        kind, nbytes = h.kernel(), h.device_bytes()
+        del h
+        torch.cuda.synchronize()
+    r = {"workload": "csr_spmv_f64_powerlaw_4M_mean16 plan", "kind": kind, "device_bytes": nbytes,
+         "preload_ms": round(preload_ms, 2), "build_ms": builds, "first_ms": builds[0],
+         "steady_ms": sorted(builds[1:])[len(builds[1:]) // 2]}
+    log(f"plan build: {r}")
+    return r
 
 
 def bsr_spmv_powerlaw():
@@ -1522,6 +1558,9 @@ def main():
         return
     if args.bsr_spmv:
         print(json.dumps({"bsr_spmv": bsr_spmv_powerlaw()}), flush=True)
+        return
+    if args.plan_build:
+        print(json.dumps({"plan_build": plan_build()}), flush=True)
         return
     if args.spmv_parts:
         print(json.dumps({"spmv_parts": spmv_parts()}), flush=True)

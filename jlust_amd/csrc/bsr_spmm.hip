@@ -1615,11 +1615,11 @@ extern "C" int jlust_hip_bsr_expand_csr_i32(int64_t mb, int64_t b1, int64_t b2, 
 // ------------------------------------------------------------------- plans
 
 // A prepared BSR SpMM (the analyse-once handle of the C ABI; the cuSPARSE SpMM
-// handle contract, ext/CUDAExt/ops/spmm.jl:8-70, for BSR).  16 x 16 fp32
-// blocks keep the MFMA kernels and the caller's buffers.  Any other block
-// shape, or Float64, is expanded to CSR once (the plan owns the expansion)
-// and runs through a CSR SpMM plan over it; update_values re-expands the
-// values only, on the stream.
+// handle contract, ext/CUDAExt/ops/spmm.jl:8-70, for BSR).  16 x 16 blocks,
+// Float32 or Float64, keep the MFMA kernels and the caller's buffers
+// (update_values swaps the value pointer).  Any other block shape is
+// expanded to CSR once (the plan owns the expansion) and runs through a CSR
+// SpMM plan over it; update_values re-expands the values only, on the stream.
 static size_t bsr_align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 struct jlust_bsr_plan {
