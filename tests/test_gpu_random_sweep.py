@@ -12,10 +12,13 @@ The paths:
   slices, LDS bins, the plan's own choice);
 - COO SpMV (storage order shuffled, some entries duplicated) plain and prepared;
 - CSC SpMV;
-- CSR SpMM plain and prepared, for a random column count;
-- SDDMM over the CSR mask, a shuffled COO mask, and the prepared plan, for a
-  random inner dimension;
-- BSR SpMM and SpMV for a random block shape and block order.
+- CSR SpMM plain and prepared, for a random column count; COO SpMM (shuffled,
+  some entries duplicated) and CSC SpMM, plain and prepared;
+- SDDMM over the CSR mask, a shuffled COO mask, a DCSR mask of the non-empty
+  rows, a CSC mask, and the prepared plans, for a random inner dimension;
+- BSR SpMM and SpMV for a random block shape, block order and value type
+  (16 x 16 blocks in both precisions), with a block-row of nb blocks in every
+  third draw (several SpMV segments).
 
 Every output is compared with the oracle (oracle/jlust_cpu.c) under the parity
 bar: |got - ref| <= tol * (|alpha| |A| |x| + |beta| |y0|), tol 1e-12 (f64) and
@@ -187,6 +190,46 @@ def test_sweep_spmm(J, O, seed):
     J.execute(h, dev(B), C, alpha=alpha, beta=beta)
     assert_within(host(C), ref, absref, dtype, f"seed {seed} CSR SpMM plan {what}")
 
+    # COO: storage order shuffled, a few entries stored twice (their scale in
+    # the bound counts each stored copy).
+    rows0 = np.repeat(np.arange(m), np.diff(rowptr))
+    cols0 = colind.astype(np.int64) - origin
+    dup = rng.random(val.size) < 0.05
+    r = np.concatenate([rows0, rows0[dup]])
+    c = np.concatenate([cols0, cols0[dup]])
+    v = np.concatenate([val, val[dup] * dtype(0.5)]).astype(dtype)
+    perm = rng.permutation(v.size)
+    r, c, v = r[perm], c[perm], v[perm]
+    rows_o, cols_o = (r + origin).astype(np.int32), (c + origin).astype(np.int32)
+    cref = O.coo_spmm(rows_o, cols_o, v, B, m, alpha, beta, c0, origin=origin)
+    crp = np.r_[0, np.cumsum(np.bincount(r, minlength=m))].astype(np.int64)
+    order = np.argsort(r, kind="stable")
+    cabs = O.csr_spmm_absref((crp + origin).astype(np.int32), cols_o[order], v[order], B, alpha, beta, c0,
+                             origin=origin)
+    Ac = J.coo_tensor(dev(rows_o), dev(cols_o), dev(v), (m, n), origin=_org(J, origin))
+    _say(seed, f"COO SpMM plain nnz={v.size} {what}")
+    C = out()
+    J.execute(J.SpMMOp, Ac, dev(B), C, alpha=alpha, beta=beta)
+    assert_within(host(C), cref, cabs, dtype, f"seed {seed} COO SpMM plain {what}")
+    _say(seed, f"COO SpMM plan {what}")
+    hc = J.prepare(J.HIPBackend(), J.SpMMOp, Ac, n_cols=k)
+    C = out()
+    J.execute(hc, dev(B), C, alpha=alpha, beta=beta)
+    assert_within(host(C), cref, cabs, dtype, f"seed {seed} COO SpMM plan {what}")
+
+    colptr, rowind, cval = O.csr_to_csc(rowptr, colind, val, n, origin=origin)
+    sref = O.csc_spmm(colptr, rowind, cval, B, m, alpha, beta, c0, origin=origin)
+    As = J.csc_tensor(dev(colptr), dev(rowind), dev(cval), (m, n), origin=_org(J, origin))
+    _say(seed, f"CSC SpMM plain {what}")
+    C = out()
+    J.execute(J.SpMMOp, As, dev(B), C, alpha=alpha, beta=beta)
+    assert_within(host(C), sref, absref, dtype, f"seed {seed} CSC SpMM plain {what}")
+    _say(seed, f"CSC SpMM plan {what}")
+    hs = J.prepare(J.HIPBackend(), J.SpMMOp, As, n_cols=k)
+    C = out()
+    J.execute(hs, dev(B), C, alpha=alpha, beta=beta)
+    assert_within(host(C), sref, absref, dtype, f"seed {seed} CSC SpMM plan {what}")
+
 
 @pytest.mark.parametrize("seed", SEEDS)
 def test_sweep_sddmm(J, O, seed):
@@ -231,16 +274,55 @@ def test_sweep_sddmm(J, O, seed):
     J.execute(J.SDDMMOp, dev(A), dev(Bm), Cc, alpha=alpha, beta=beta)
     assert_within(host(cv), cref, absref[perm], dtype, f"seed {seed} SDDMM COO {what}")
 
+    # DCSR: the non-empty rows of the CSR mask, entries in the same order.
+    keep = np.flatnonzero(np.diff(rowptr) > 0)
+    outer = (keep + origin).astype(np.int32)
+    dpos = (np.r_[0, np.cumsum(np.diff(rowptr)[keep])] + origin).astype(np.int32)
+    dref = O.dcsr_sddmm(outer, dpos, colind, A, Bm, alpha, beta, c0 if beta else None, origin=origin)
+    _say(seed, f"SDDMM DCSR mask {what}")
+    cv = cvals(c0)
+    Cd = J.dcsr_tensor(dev(outer), dev(dpos), dev(colind), cv, (m, n), origin=_org(J, origin))
+    J.execute(J.SDDMMOp, dev(A), dev(Bm), Cd, alpha=alpha, beta=beta)
+    assert_within(host(cv), dref, absref, dtype, f"seed {seed} SDDMM DCSR {what}")
+    _say(seed, f"SDDMM DCSR plan {what}")
+    cv = cvals(c0)
+    Cd = J.dcsr_tensor(dev(outer), dev(dpos), dev(colind), cv, (m, n), origin=_org(J, origin))
+    hd = J.prepare(J.HIPBackend(), J.SDDMMOp, Cd, n_inner=K)
+    J.execute(hd, dev(A), dev(Bm), alpha=alpha, beta=beta)
+    assert_within(host(cv), dref, absref, dtype, f"seed {seed} SDDMM DCSR plan {what}")
+
+    # CSC: the mask's entries in column order.
+    idx = np.arange(val.size, dtype=np.float64) + 1.0
+    cp, ri, ci = O.csr_to_csc(rowptr, colind, idx, n, origin=origin)
+    cperm = (ci - 1.0).astype(np.int64)
+    sref = O.csc_sddmm(cp, ri, A, Bm, alpha, beta, c0[cperm] if beta else None, origin=origin)
+    _say(seed, f"SDDMM CSC mask {what}")
+    cv = cvals(c0[cperm])
+    Cs = J.csc_tensor(dev(cp), dev(ri), cv, (m, n), origin=_org(J, origin))
+    J.execute(J.SDDMMOp, dev(A), dev(Bm), Cs, alpha=alpha, beta=beta)
+    assert_within(host(cv), sref, absref[cperm], dtype, f"seed {seed} SDDMM CSC {what}")
+    _say(seed, f"SDDMM CSC plan {what}")
+    cv = cvals(c0[cperm])
+    Cs = J.csc_tensor(dev(cp), dev(ri), cv, (m, n), origin=_org(J, origin))
+    hs = J.prepare(J.HIPBackend(), J.SDDMMOp, Cs, n_inner=K)
+    J.execute(hs, dev(A), dev(Bm), alpha=alpha, beta=beta)
+    assert_within(host(cv), sref, absref[cperm], dtype, f"seed {seed} SDDMM CSC plan {what}")
+
 
 @pytest.mark.parametrize("seed", SEEDS)
 def test_sweep_bsr(J, O, seed):
     rng = np.random.default_rng(5000 + seed)
     b1, b2 = [(16, 16), (16, 16), (1, 1), (2, 3), (4, 4), (3, 5), (8, 2), (1, 7)][seed % 8]
-    dtype = np.float32 if (b1, b2) == (16, 16) or rng.random() < 0.5 else np.float64
+    if (b1, b2) == (16, 16):
+        dtype = np.float64 if seed % 16 >= 8 else np.float32
+    else:
+        dtype = np.float32 if rng.random() < 0.5 else np.float64
     row_major = bool(rng.random() < 0.75)
     origin = int(rng.integers(0, 2))
     mb, nb = int(rng.integers(1, 60)), int(rng.integers(1, 60))
     counts = np.minimum(rng.integers(0, 12, mb), nb)
+    if seed % 3 == 0:                                 # one block-row of nb blocks
+        counts[int(rng.integers(0, mb))] = nb
     bcols = [np.sort(rng.choice(nb, int(cn), replace=False)) for cn in counts]
     browptr = (np.r_[0, np.cumsum(counts)] + origin).astype(np.int32)
     bcolind = ((np.concatenate(bcols) if counts.sum() else np.zeros(0, np.int64)) + origin).astype(np.int32)
