@@ -382,12 +382,31 @@ __global__ void bn_chunk_kernel(int64_t nnz, int32_t S, int32_t B, int32_t nch,
     cpi[q] = fpre[e];
 }
 
+// New values into the layout: sval[e] = val[perm[e]], run by run.  Workgroup
+// w takes run (slice c, bin b); bins are dealt to the XCDs round-robin (XCD
+// w % 8 takes bins b = 8 j + w % 8) and each XCD's workgroups walk its bins
+// one at a time, every slice of a bin before the next bin.  A bin's entries
+// come from one contiguous range of rows, so the gathers of the XCD's
+// workgroups in flight fall in one bin's values (about nnz / B entries), which
+// its L2 keeps, instead of anywhere in val.  Run bounds are clamped.
 template <typename T>
-__global__ void bn_gather_kernel(int64_t nnz, const int32_t *__restrict__ perm, const T *__restrict__ src,
-                                 T *__restrict__ dst)
+__global__ __launch_bounds__(256) void bn_refresh_kernel(int64_t nnz, int32_t S, int32_t B,
+                                                         const int32_t *__restrict__ est,
+                                                         const int32_t *__restrict__ perm,
+                                                         const T *__restrict__ src, T *__restrict__ dst)
 {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e < nnz) dst[e] = src[perm[e]];
+    const int64_t j = blockIdx.x / NUM_XCD;                  // rank within the XCD
+    const int64_t b = (j / S) * NUM_XCD + blockIdx.x % NUM_XCD;
+    const int64_t c = j % S;
+    if (b >= B) return;
+    const int64_t r = c * B + b;
+    const int64_t e0 = min(max((int64_t)est[r], (int64_t)0), nnz);
+    const int64_t e1 = min(max((int64_t)est[r + 1], e0), nnz);
+    for (int64_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {
+        int64_t k = perm[e];
+        k = k < 0 ? 0 : (k >= nnz ? nnz - 1 : k);
+        dst[e] = src[k];
+    }
 }
 
 unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
@@ -407,9 +426,10 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     const size_t sz_pr = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
     const size_t sz_rw = align_up(sizeof(uint16_t) * (size_t)(nnz + 1), 256);
     const size_t sz_pv = align_up(sizeof(T) * (size_t)(nnz + 1), 256);
-    const size_t persistent = sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_rw + sz_pv;
+    const size_t sz_es = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
+    const size_t persistent = sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_es + sz_rw + sz_pv;
     // Temporaries: row counts / rows (nnz + 1), keys, sorted keys, iota,
-    // flags / partial indices (nnz + 1), run starts, sort storage.
+    // flags / partial indices (nnz + 1), sort storage.
     uint32_t *nk = nullptr;
     size_t sort_bytes = 0;
     int bits = 1;
@@ -417,8 +437,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, sort_bytes, nk, nk, (int32_t *)nullptr,
                                             (int32_t *)nullptr, (size_t)nnz, 0, bits, s));
     const size_t sz_i = align_up(sizeof(int32_t) * (size_t)(nnz + 1), 256);
-    const size_t sz_r = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
-    const size_t temporary = 5 * sz_i + sz_r + align_up(sort_bytes, 256);
+    const size_t temporary = 5 * sz_i + align_up(sort_bytes, 256);
     if (max_bytes > 0 && (int64_t)(persistent + temporary) > max_bytes)
         return fail(JLUST_STATUS_OUT_OF_MEMORY,
                     "binned spmv layout: %lld + %lld build bytes above JLUST_HIP_PLAN_MAX_BYTES (%lld)",
@@ -432,6 +451,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     L->cst = (int32_t *)p;       p += sz_ch;
     L->cpi = (int32_t *)p;       p += sz_ch;
     L->pr = (int32_t *)p;        p += sz_pr;
+    L->est = (int32_t *)p;       p += sz_es;
     L->prow = (uint16_t *)p;     p += sz_rw;
     L->pval = p;
 
@@ -443,7 +463,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     uint32_t *skey = (uint32_t *)q; q += sz_i;
     int32_t *iota = (int32_t *)q;   q += sz_i;
     int32_t *fpre = (int32_t *)q;   q += sz_i;
-    int32_t *est = (int32_t *)q;    q += sz_r;
+    int32_t *est = L->est;
     void *sort_tmp = q;
     const int32_t *erow = cnt + 1;
 
@@ -594,13 +614,16 @@ int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64
 
 int binned_update(BinnedLayout *L, const void *val, hipStream_t s)
 {
+    // One workgroup per run, bins padded to a multiple of the XCD count.
+    const int64_t bins = ((int64_t)L->B + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
+    const dim3 grid((unsigned)(bins * L->S));
     if (L->value_type == 0)
-        hipLaunchKernelGGL((bn_gather_kernel<double>), dim3(blocks256(L->nnz)), dim3(256), 0, s, L->nnz,
+        hipLaunchKernelGGL((bn_refresh_kernel<double>), grid, dim3(256), 0, s, L->nnz, L->S, L->B, L->est,
                            L->perm, (const double *)val, (double *)L->sval);
     else
-        hipLaunchKernelGGL((bn_gather_kernel<float>), dim3(blocks256(L->nnz)), dim3(256), 0, s, L->nnz,
+        hipLaunchKernelGGL((bn_refresh_kernel<float>), grid, dim3(256), 0, s, L->nnz, L->S, L->B, L->est,
                            L->perm, (const float *)val, (float *)L->sval);
-    return check_launch("bn_gather_kernel");
+    return check_launch("bn_refresh_kernel");
 }
 
 int binned_execute_f64(const BinnedLayout *L, double alpha, const double *x, double beta, double *y,

@@ -22,6 +22,7 @@ struct BinnedLayout {
     int32_t *cst = nullptr;    // [S*nch + 1] entry start of each chunk
     int32_t *cpi = nullptr;    // [S*nch] index of the chunk's first partial
     int32_t *pr = nullptr;     // [S*B + 1] first partial of run (slice c, bin b) at c*B + b
+    int32_t *est = nullptr;    // [S*B + 1] first entry of run (slice c, bin b) at c*B + b
     uint16_t *prow = nullptr;  // [P + 1] bin-local row of each partial
     void *pval = nullptr;      // [P + 1] partial sums, rewritten by every execute
     int64_t bytes = 0;         // size of mem
