@@ -36,6 +36,7 @@
 // flags, their prefix count (= partial indices), run and chunk boundaries.
 #include <algorithm>
 #include <cstdlib>
+#include <vector>
 
 #include <rocprim/device/device_radix_sort.hpp>
 
@@ -382,30 +383,160 @@ __global__ void bn_chunk_kernel(int64_t nnz, int32_t S, int32_t B, int32_t nch,
     cpi[q] = fpre[e];
 }
 
-// New values into the layout: sval[e] = val[perm[e]], run by run.  Workgroup
-// w takes run (slice c, bin b); bins are dealt to the XCDs round-robin (XCD
-// w % 8 takes bins b = 8 j + w % 8) and each XCD's workgroups walk its bins
-// one at a time, every slice of a bin before the next bin.  A bin's entries
-// come from one contiguous range of rows, so the gathers of the XCD's
-// workgroups in flight fall in one bin's values (about nnz / B entries), which
-// its L2 keeps, instead of anywhere in val.  Run bounds are clamped.
-template <typename T>
-__global__ __launch_bounds__(256) void bn_refresh_kernel(int64_t nnz, int32_t S, int32_t B,
-                                                         const int32_t *__restrict__ est,
-                                                         const int32_t *__restrict__ perm,
-                                                         const T *__restrict__ src, T *__restrict__ dst)
+// First CSR entry of each bin: bst[b] = rowptr[min(b H, m)] - origin, clamped.
+__global__ void bn_binstart_kernel(int64_t m, int64_t nnz, int32_t origin, int32_t H, int32_t B,
+                                   const int32_t *__restrict__ rowptr, int32_t *__restrict__ bst)
 {
-    const int64_t j = blockIdx.x / NUM_XCD;                  // rank within the XCD
-    const int64_t b = (j / S) * NUM_XCD + blockIdx.x % NUM_XCD;
-    const int64_t c = j % S;
-    if (b >= B) return;
-    const int64_t r = c * B + b;
-    const int64_t e0 = min(max((int64_t)est[r], (int64_t)0), nnz);
-    const int64_t e1 = min(max((int64_t)est[r + 1], e0), nnz);
-    for (int64_t e = e0 + threadIdx.x; e < e1; e += blockDim.x) {
-        int64_t k = perm[e];
-        k = k < 0 ? 0 : (k >= nnz ? nnz - 1 : k);
-        dst[e] = src[k];
+    const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (b > B) return;
+    int64_t v = (int64_t)rowptr[min(b * H, m)] - origin;
+    bst[b] = (int32_t)(v < 0 ? 0 : (v > nnz ? nnz : v));
+}
+
+// rtab[row * S + c] for row = rtb[b] + k: the first entry e of run (c, b)
+// with perm[e] >= bst[b] + k * chunk (a run's entries are in CSR order, so
+// perm increases along it), by binary search.  One thread per (row, c).
+__global__ void bn_rtable_kernel(int64_t nrows, int32_t S, int32_t B, int64_t chunk,
+                                 const int32_t *__restrict__ rtb, const int32_t *__restrict__ bst,
+                                 const int32_t *__restrict__ est, const int32_t *__restrict__ perm,
+                                 int32_t *__restrict__ rtab)
+{
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nrows * S) return;
+    const int64_t row = t / S, c = t % S;
+    int lo = 0, hi = B;                   // the bin b with rtb[b] <= row < rtb[b + 1]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (rtb[mid] <= row) lo = mid; else hi = mid;
+    }
+    const int64_t b = lo;
+    const int64_t want = (int64_t)bst[b] + (row - rtb[b]) * chunk;
+    int64_t a = est[c * B + b], z = est[c * B + b + 1];
+    while (a < z) {
+        const int64_t mid = (a + z) / 2;
+        if ((int64_t)perm[mid] < want) a = mid + 1; else z = mid;
+    }
+    rtab[t] = (int32_t)a;
+}
+
+// New values into the layout by chunks: workgroup g holds chunk k of bin b,
+// CSR entries [c0, c1) = [bst[b] + k L, min(bst[b] + (k+1) L, bst[b+1])), in
+// LDS (L = RF_LDS / sizeof(T)), read once and coalesced; every run (c, b)
+// holds those entries as one contiguous range [rtab[row][c], rtab[row+1][c]),
+// so the workgroup writes the ranges of all S runs, each entry e taking
+// v[perm[e] - c0] from LDS; the outputs are the chunk's S ranges laid end to
+// end.  Indices are clamped into the chunk and the layout.
+constexpr int RF_THREADS = 512;           // refresh workgroup: two per CU
+constexpr int RF_LDS = 64 * 1024;         // values of a refresh chunk in LDS
+constexpr int RF_SPT = (BN_SMAX + RF_THREADS - 1) / RF_THREADS;   // runs per thread in the scan
+
+template <typename T>
+__global__ __launch_bounds__(RF_THREADS) void bn_refresh_lds_kernel(int64_t nnz, int32_t S, int32_t B,
+                                                                    const int32_t *__restrict__ rch,
+                                                                    const int32_t *__restrict__ bst,
+                                                                    const int32_t *__restrict__ rtb,
+                                                                    const int32_t *__restrict__ rtab,
+                                                                    const int32_t *__restrict__ perm,
+                                                                    const T *__restrict__ src,
+                                                                    T *__restrict__ dst)
+{
+    constexpr int L = RF_LDS / sizeof(T);
+    constexpr int PER = L / RF_THREADS;   // values (and outputs) per thread
+    __shared__ T v[L];
+    __shared__ int32_t pre[BN_SMAX + 1], beg[BN_SMAX], tsum[RF_THREADS];
+    const int t = threadIdx.x;
+    const int64_t b = rch[2 * blockIdx.x], k = rch[2 * blockIdx.x + 1];
+    const int64_t lo = bst[b], hi = bst[b + 1];
+    const int64_t c0 = min(lo + k * L, hi), c1 = min(c0 + L, hi);
+    const int nv = (int)(c1 - c0);
+    // The runs' range bounds are loaded first, then the chunk's values, every
+    // load issued before any is used.
+    const int64_t row = (int64_t)rtb[b] + k;
+    int32_t rb0[RF_SPT], rb1[RF_SPT];
+#pragma unroll
+    for (int j = 0; j < RF_SPT; ++j) {
+        const int c = t * RF_SPT + j;
+        rb0[j] = c < S ? rtab[row * S + c] : 0;
+        rb1[j] = c < S ? rtab[(row + 1) * S + c] : 0;
+    }
+    {
+        T tmp[PER];
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = t + u * RF_THREADS;
+            tmp[u] = i < nv ? src[c0 + i] : T(0);
+        }
+#pragma unroll
+        for (int u = 0; u < PER; ++u) {
+            const int i = t + u * RF_THREADS;
+            if (i < nv) v[i] = tmp[u];
+        }
+    }
+    // Range starts and lengths of the S runs; pre[c] = outputs before run c.
+    int32_t lens[RF_SPT], local = 0;
+#pragma unroll
+    for (int j = 0; j < RF_SPT; ++j) {
+        const int c = t * RF_SPT + j;
+        lens[j] = 0;
+        if (c < S) {
+            const int64_t e0 = min(max((int64_t)rb0[j], (int64_t)0), nnz);
+            const int64_t e1 = min(max((int64_t)rb1[j], e0), nnz);
+            beg[c] = (int32_t)e0;
+            lens[j] = (int32_t)(e1 - e0);
+        }
+        local += lens[j];
+    }
+    tsum[t] = local;
+    __syncthreads();
+    for (int off = 1; off < RF_THREADS; off <<= 1) {   // inclusive scan of the per-thread sums
+        const int32_t x = t >= off ? tsum[t - off] : 0;
+        __syncthreads();
+        tsum[t] += x;
+        __syncthreads();
+    }
+    {
+        int32_t run = tsum[t] - local;
+#pragma unroll
+        for (int j = 0; j < RF_SPT; ++j) {
+            const int c = t * RF_SPT + j;
+            if (c < S) pre[c] = run;
+            run += lens[j];
+        }
+        if (t == RF_THREADS - 1) pre[S] = tsum[t];
+    }
+    __syncthreads();
+    // At most nv <= L outputs.  Wave w owns outputs [w PER 64, (w+1) PER 64),
+    // lane l takes every 64th of them from l, so a wave's step covers 64
+    // consecutive outputs (consecutive entries of one or two runs); a lane
+    // finds its first run by binary search and later ones by stepping
+    // forward.  All the permutation loads are issued before the LDS reads and
+    // stores.
+    const int32_t total = min(pre[S], (int32_t)L);
+    const int32_t o0 = (t >> 6) * (PER * 64) + (t & 63);
+    int c = 0;                             // the run with pre[c] <= o < pre[c + 1]
+    {
+        int z = S;
+        while (z - c > 1) {
+            const int mid = (c + z) / 2;
+            if (pre[mid] <= o0) c = mid; else z = mid;
+        }
+    }
+    int32_t ev[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        const int32_t o = o0 + u * 64;
+        while (c + 1 < S && pre[c + 1] <= o) ++c;
+        ev[u] = o < total ? beg[c] + (o - pre[c]) : -1;
+    }
+    int32_t pk[PER];
+#pragma unroll
+    for (int u = 0; u < PER; ++u) pk[u] = ev[u] >= 0 ? perm[ev[u]] : 0;
+#pragma unroll
+    for (int u = 0; u < PER; ++u) {
+        if (ev[u] < 0) continue;
+        int64_t kk = (int64_t)pk[u] - c0;
+        kk = kk < 0 ? 0 : (kk >= nv ? nv - 1 : kk);
+        dst[ev[u]] = v[kk];
     }
 }
 
@@ -427,7 +558,14 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     const size_t sz_rw = align_up(sizeof(uint16_t) * (size_t)(nnz + 1), 256);
     const size_t sz_pv = align_up(sizeof(T) * (size_t)(nnz + 1), 256);
     const size_t sz_es = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
-    const size_t persistent = sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_es + sz_rw + sz_pv;
+    // Refresh tables, sized for at most nnz / chunk + B chunks.
+    const int64_t chunk = RF_LDS / (int64_t)sizeof(T);
+    const int64_t nrch_max = nnz / chunk + L->B + 1;
+    const size_t sz_rch = align_up(sizeof(int32_t) * (size_t)(2 * nrch_max), 256);
+    const size_t sz_bb = align_up(sizeof(int32_t) * (size_t)(L->B + 1), 256);
+    const size_t sz_rt = align_up(sizeof(int32_t) * (size_t)((nrch_max + L->B) * L->S), 256);
+    const size_t persistent = sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_es + sz_rw + sz_pv + sz_rch + 2 * sz_bb +
+                              sz_rt;
     // Temporaries: row counts / rows (nnz + 1), keys, sorted keys, iota,
     // flags / partial indices (nnz + 1), sort storage.
     uint32_t *nk = nullptr;
@@ -452,6 +590,10 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     L->cpi = (int32_t *)p;       p += sz_ch;
     L->pr = (int32_t *)p;        p += sz_pr;
     L->est = (int32_t *)p;       p += sz_es;
+    L->rch = (int32_t *)p;       p += sz_rch;
+    L->bst = (int32_t *)p;       p += sz_bb;
+    L->rtb = (int32_t *)p;       p += sz_bb;
+    L->rtab = (int32_t *)p;      p += sz_rt;
     L->prow = (uint16_t *)p;     p += sz_rw;
     L->pval = p;
 
@@ -467,6 +609,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     void *sort_tmp = q;
     const int32_t *erow = cnt + 1;
 
+    std::vector<int32_t> h_bst, h_rch, h_rtb;      // host side of the refresh tables
     int st = JLUST_STATUS_SUCCESS;
     hipError_t e = hipMemsetAsync(cnt, 0, sizeof(int32_t) * (size_t)(nnz + 1), s);
     if (e != hipSuccess) st = hip_fail(e, "hipMemsetAsync(binned row counts)");
@@ -506,6 +649,50 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
         hipLaunchKernelGGL(bn_chunk_kernel, dim3(blocks256(nchunks + 1)), dim3(256), 0, s, nnz, L->S, L->B,
                            L->nch, est, fpre, L->cst, L->cpi);
         st = check_launch("bn_chunk_kernel");
+    }
+    // Refresh tables: the bins' first entries, their chunks (host), and the
+    // first entry of every run at every chunk boundary of its bin.
+    if (!st) {
+        hipLaunchKernelGGL(bn_binstart_kernel, dim3(blocks256(L->B + 1)), dim3(256), 0, s, m, nnz, origin, L->H,
+                           L->B, rowptr, L->bst);
+        st = check_launch("bn_binstart_kernel");
+    }
+    if (!st) {
+        h_bst.resize((size_t)L->B + 1);
+        e = hipMemcpyAsync(h_bst.data(), L->bst, sizeof(int32_t) * h_bst.size(), hipMemcpyDeviceToHost, s);
+        if (e == hipSuccess) e = hipStreamSynchronize(s);
+        if (e != hipSuccess) st = hip_fail(e, "binned refresh tables (bin starts)");
+    }
+    int64_t nrows = 0;
+    if (!st) {
+        h_rtb.resize((size_t)L->B + 1);
+        for (int32_t b = 0; b < L->B; ++b) {
+            h_rtb[b] = (int32_t)nrows;
+            const int64_t nb = std::max<int64_t>(0, (int64_t)h_bst[b + 1] - h_bst[b]);
+            const int64_t q = (nb + chunk - 1) / chunk;
+            for (int64_t k = 0; k < q; ++k) {
+                h_rch.push_back(b);
+                h_rch.push_back((int32_t)k);
+            }
+            nrows += q + 1;
+        }
+        h_rtb[L->B] = (int32_t)nrows;
+        L->nrch = (int32_t)(h_rch.size() / 2);
+        if ((int64_t)L->nrch > nrch_max)
+            st = fail(JLUST_STATUS_NONCANONICAL_STORAGE,
+                      "binned spmv layout: rowptr not non-decreasing (%d value chunks, at most %lld)", L->nrch,
+                      (long long)nrch_max);
+    }
+    if (!st && L->nrch > 0) {
+        e = hipMemcpyAsync(L->rch, h_rch.data(), sizeof(int32_t) * h_rch.size(), hipMemcpyHostToDevice, s);
+        if (e == hipSuccess)
+            e = hipMemcpyAsync(L->rtb, h_rtb.data(), sizeof(int32_t) * h_rtb.size(), hipMemcpyHostToDevice, s);
+        if (e != hipSuccess) st = hip_fail(e, "binned refresh tables (chunks)");
+        if (!st) {
+            hipLaunchKernelGGL(bn_rtable_kernel, dim3(blocks256(nrows * L->S)), dim3(256), 0, s, nrows, L->S, L->B,
+                               chunk, L->rtb, L->bst, est, L->perm, L->rtab);
+            st = check_launch("bn_rtable_kernel");
+        }
     }
     // cnt is free again: cnt[0] receives the longest run.
     if (!st) {
@@ -614,16 +801,16 @@ int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64
 
 int binned_update(BinnedLayout *L, const void *val, hipStream_t s)
 {
-    // One workgroup per run, bins padded to a multiple of the XCD count.
-    const int64_t bins = ((int64_t)L->B + NUM_XCD - 1) / NUM_XCD * NUM_XCD;
-    const dim3 grid((unsigned)(bins * L->S));
+    if (L->nrch <= 0) return JLUST_STATUS_SUCCESS;
     if (L->value_type == 0)
-        hipLaunchKernelGGL((bn_refresh_kernel<double>), grid, dim3(256), 0, s, L->nnz, L->S, L->B, L->est,
-                           L->perm, (const double *)val, (double *)L->sval);
+        hipLaunchKernelGGL((bn_refresh_lds_kernel<double>), dim3((unsigned)L->nrch), dim3(RF_THREADS), 0, s, L->nnz,
+                           L->S, L->B, L->rch, L->bst, L->rtb, L->rtab, L->perm, (const double *)val,
+                           (double *)L->sval);
     else
-        hipLaunchKernelGGL((bn_refresh_kernel<float>), grid, dim3(256), 0, s, L->nnz, L->S, L->B, L->est,
-                           L->perm, (const float *)val, (float *)L->sval);
-    return check_launch("bn_refresh_kernel");
+        hipLaunchKernelGGL((bn_refresh_lds_kernel<float>), dim3((unsigned)L->nrch), dim3(RF_THREADS), 0, s, L->nnz,
+                           L->S, L->B, L->rch, L->bst, L->rtb, L->rtab, L->perm, (const float *)val,
+                           (float *)L->sval);
+    return check_launch("bn_refresh_lds_kernel");
 }
 
 int binned_execute_f64(const BinnedLayout *L, double alpha, const double *x, double beta, double *y,

@@ -23,6 +23,13 @@ struct BinnedLayout {
     int32_t *cpi = nullptr;    // [S*nch] index of the chunk's first partial
     int32_t *pr = nullptr;     // [S*B + 1] first partial of run (slice c, bin b) at c*B + b
     int32_t *est = nullptr;    // [S*B + 1] first entry of run (slice c, bin b) at c*B + b
+    // Value refresh by chunks of a bin's CSR entries held in LDS (BN_LDS bytes):
+    int32_t nrch = 0;          // chunks
+    int32_t *rch = nullptr;    // [2*nrch] (bin, chunk index within the bin) of each chunk
+    int32_t *bst = nullptr;    // [B + 1] first CSR entry of each bin
+    int32_t *rtb = nullptr;    // [B + 1] first row of each bin in rtab
+    int32_t *rtab = nullptr;   // [(nrch + B) * S]: row rtb[b] + k, column c = first entry of run
+                               // (c, b) taken from CSR entries bst[b] + k * chunk or later
     uint16_t *prow = nullptr;  // [P + 1] bin-local row of each partial
     void *pval = nullptr;      // [P + 1] partial sums, rewritten by every execute
     int64_t bytes = 0;         // size of mem
