@@ -237,3 +237,33 @@ def test_copied_layout_falls_back_to_merge_when_over_budget(J, O, mode, monkeypa
     assert h2.device_bytes() > 12 * rowptr[-1]
     J.execute(h2, dev(x), y)
     assert_within(host(y), ref, absref, np.float64, "layout plan")
+
+
+@pytest.mark.parametrize("dtype", [np.float64, np.float32])
+def test_binned_refresh_uneven_bins(J, O, dtype, monkeypatch):
+    """update_values on a binned plan re-gathers the values chunk by chunk of
+    consecutive CSR entries (8,192 f64 / 16,384 f32 per chunk): a bin holding
+    one 300,000-entry row spans dozens of chunks, runs of empty rows leave
+    bins without entries.  After the update the plan's product is
+    bit-identical to a plan built on the new values (the same layout and sums)
+    and within the bar of the oracle."""
+    import torch
+    monkeypatch.setenv("JLUST_HIP_SPMV_SLICE", "2")
+    m, n = 600_000, 2_000_000
+    rng = np.random.default_rng(41)
+    lens = rng.integers(0, 12, m)
+    lens[100_000:260_000] = 0                     # empty bins
+    lens[400_123] = 300_000                       # one bin of many chunks
+    rowptr, colind, val = random_csr(m, n, lengths=lens, seed=42, dtype=dtype)
+    x = rng.uniform(-1, 1, n).astype(dtype)
+    y, h, A = check(J, O, rowptr, colind, val, x, m, n, dtype, "binned uneven bins")
+    val2 = rng.uniform(-2, 2, val.size).astype(dtype)
+    J.update_values_(h, J.csr_tensor(A.pos_buffers[1], A.crd_buffers[1], dev(val2), (m, n)))
+    yt = torch.full((m,), float("nan"), dtype=A.dtype, device="cuda")
+    J.execute(h, dev(x), yt)
+    fresh, hf, _ = run_binned(J, rowptr, colind, val2, x, m, n)
+    assert hf.kernel() == "binned"
+    np.testing.assert_array_equal(host(yt), fresh)
+    ref2 = O.csr_spmv(rowptr, colind, val2, x)
+    absref2 = O.csr_spmv_absref(rowptr, colind, val2, x)
+    assert_within(host(yt), ref2, absref2, dtype, "binned uneven bins after update_values!")
