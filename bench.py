@@ -1183,7 +1183,7 @@ def build_step(cfg, use_plan=False):
         A = J.bsr_tensor(dev(cfg["browptr"]), dev(cfg["bcolind"]), dev(cfg["val"]), (m, n))
         B = dev(cfg["B"])
         C = J.dense_matrix(m, cfg["k"], dtype=torch.float32)
-        return (lambda: J.execute(J.SpMMOp, A, B, C)), "bsr16_spmm_strip_kernel", "mfma", (A, B, C)
+        return (lambda: J.execute(J.SpMMOp, A, B, C)), "bsr16_spmm_wide_strip_kernel", "mfma", (A, B, C)
     raise ValueError(kind)
 
 

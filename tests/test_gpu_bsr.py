@@ -451,3 +451,42 @@ def test_bsr_spmv_power_law_rows(J, O, b1, b2, dtype, row_major, segments, monke
             ref = O.csr_spmv(rp, ci, v, x, alpha, beta, yb, origin)
             absref = O.csr_spmv_absref(rp, ci, v, x, alpha, beta, yb, origin)
             assert_within(host(y), ref, absref, dtype, f"bsr {b1}x{b2} spmv power-law beta={beta}")
+
+
+@pytest.mark.parametrize("wide", ["1", "0"])
+@pytest.mark.parametrize("k,beta", [(40, 0.0), (64, 0.0), (100, -0.5), (256, 1.0)])
+def test_bsr_strip_schedule(J, O, k, beta, wide, monkeypatch):
+    """A matrix of 6,900 block-rows (288 strips of 24; 575 of 12) through the
+    24-row persistent strip kernel (JLUST_HIP_BSR_WIDE=1) and the 12-row one:
+    each XCD's workgroups take several strips in turn, setting up the next
+    strip during a strip's last tiles (4 tiles or more: k = 64, 100, 256) or
+    at its start (k = 40), and an XCD's last round of 4 strips is cut into
+    column ranges.  Strips of long rows or wide windows (direct operand loads)
+    sit between banded ones, some rows are empty and the last strip is
+    partial; every output against the oracle."""
+    monkeypatch.setenv("JLUST_HIP_BSR_WIDE", wide)
+    mb = nb = 6900
+    rng = np.random.default_rng(k)
+    bcols = []
+    for R in range(mb):
+        s = R // 24
+        if s % 17 == 5 and R % 3 == 0:                # long rows: up to 11 blocks
+            c = rng.choice(nb, int(rng.integers(9, 12)), replace=False)
+        elif s % 23 == 9 and R % 5 == 0:              # a window wider than 88 block-rows
+            c = rng.choice(nb, 4, replace=False)
+        elif R % 13 == 0:
+            c = np.zeros(0, np.int64)
+        else:
+            lo, hi = max(0, R - 32), min(nb, R + 33)
+            c = rng.choice(np.arange(lo, hi), int(rng.integers(1, 9)), replace=False)
+        bcols.append(np.sort(c))
+    browptr = (np.r_[0, np.cumsum([c.size for c in bcols])] + 1).astype(np.int32)
+    bcolind = (np.concatenate(bcols) + 1).astype(np.int32)
+    val = rng.standard_normal(bcolind.size * 256).astype(np.float32)
+    B = np.asfortranarray(rng.standard_normal((nb * 16, k)).astype(np.float32))
+    C0 = np.asfortranarray(rng.standard_normal((mb * 16, k)).astype(np.float32)) if beta else None
+    C = run_bsr(J, browptr, bcolind, val, B, mb, nb, alpha=0.75, beta=beta, C0=C0)
+    ref = O.bsr_spmm(browptr, bcolind, val, 16, B, 0.75, beta, C0)
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
+    absref = O.csr_spmm_absref(rp, ci, v, B, 0.75, beta, C0)
+    assert_within(C, ref, absref, np.float32, f"strip schedule wide={wide} k={k} beta={beta}")
