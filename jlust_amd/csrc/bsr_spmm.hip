@@ -26,6 +26,7 @@
 
 #include <cstdlib>
 #include <memory>
+#include <type_traits>
 
 // Raw buffer intrinsics (MUBUF with a 128-bit resource in SGPRs), bound to
 // the LLVM intrinsics by name; declared at file scope, since a declaration
@@ -830,13 +831,13 @@ void bsr16_spmm_wide_strip_kernel(
             continue;
         }
 
-        for (int t = t0; t < t1; ++t) {
+        // One tile; the unit's last tile is a separate instance, the only one
+        // that loads A operands, so that the compiler sees none in flight in
+        // the other tiles and adds no wait before their MFMAs: the C stores of
+        // a tile stay in flight into the next.
+        auto tile = [&](int t, auto last_tag) {
+            constexpr bool last = decltype(last_tag)::value;
             const int c0 = t * 16;
-            const bool last = t == t1 - 1;
-            // Nothing is in flight here (the previous tile waited for
-            // everything); said explicitly, so that the compiler adds no waits
-            // of its own before the MFMAs for the next strip's A loads.
-            __builtin_amdgcn_s_waitcnt(0);
             floatx4 b0[BSR_QCHUNK], b1[BSR_QCHUNK];
             uint32_t co = col_off, j0 = jp[0], j1 = jp[1], j2 = jp[2], j3 = jp[3];
             asm volatile("" : "+v"(co), "+s"(j0), "+s"(j1), "+s"(j2), "+s"(j3));
@@ -850,17 +851,16 @@ void bsr16_spmm_wide_strip_kernel(
             barrier();                     // the window is free
             if (pre && t == t1 - 4) setup1(sn);
             if (pre && t == t1 - 3) setup2();
-            if (pre && last) setup4(par ^ 1);
+            if (last && pre) setup4(par ^ 1);
             asm volatile("" ::: "memory");
             // The copies of the next tile of this strip or, in the last tile,
             // of the next strip's first tile; and in the last tile the next
             // strip's A operands, each after its block's MFMAs.
-            const bool more = !last;
             const bool nxt = last && pre && windowedn;
-            const bool cv = more ? cvalid : (nxt && cvalidn);
-            const bool lok = more ? lane_ok : lane_okn;
-            const int32x4 rsn = more ? rs_b : buffer_resource(B + (int64_t)jw0n * BSR_BS);
-            const int cn = more ? c0 + 16 : t0n * 16;
+            const bool cv = last ? nxt && cvalidn : cvalid;
+            const bool lok = last ? lane_okn : lane_ok;
+            const int32x4 rsn = last ? buffer_resource(B + (int64_t)jw0n * BSR_BS) : rs_b;
+            const int cn = last ? t0n * 16 : c0 + 16;
             floatx4 acc0 = zero, acc1 = zero;
 #pragma unroll
             for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
@@ -873,11 +873,11 @@ void bsr16_spmm_wide_strip_kernel(
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
                     acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[qq][u], b0[qq][u], acc0, 0, 0, 0);
-                if (__builtin_expect(nxt, 0)) load_a0(a0[qq], qq);
+                if (last && nxt) load_a0(a0[qq], qq);
 #pragma unroll
                 for (int u = 0; u < 4; ++u)
                     acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[qq][u], b1[qq][u], acc1, 0, 0, 0);
-                if (__builtin_expect(nxt, 0)) load_a1(a1[qq], qq);
+                if (last && nxt) load_a1(a1[qq], qq);
             }
             asm volatile("" ::: "memory");
             if (c0 + i < kk) {
@@ -895,13 +895,16 @@ void bsr16_spmm_wide_strip_kernel(
                 }
             }
             if (pre && t == t1 - 2) setup3(par ^ 1);
-            // Every copy (and A load) landed; the C stores may be in flight.
+            // Every copy (and A load) landed; the C stores of a tile before
+            // the last may be in flight.
             if (last) __builtin_amdgcn_s_waitcnt(0);
             else if (live1) __builtin_amdgcn_s_waitcnt(0x0002);       // vmcnt(2)
             else if (live0) __builtin_amdgcn_s_waitcnt(0x0001);       // vmcnt(1)
             else __builtin_amdgcn_s_waitcnt(0);
             asm volatile("s_barrier" ::: "memory");
-        }
+        };
+        for (int t = t0; t < t1 - 1; ++t) tile(t, std::false_type{});
+        tile(t1 - 1, std::true_type{});
         ready = pre;
     }
     __builtin_amdgcn_s_waitcnt(0);
