@@ -623,7 +623,8 @@ def bsr_spmv_powerlaw():
     """16 x 16 BSR SpMV (jlust_hip_bsr_spmv_*) over power-law block-rows:
     65,536 block-rows whose lengths follow a Pareto law (mean about 8 blocks,
     capped at 8,192), random block columns, values N(0, 1).  The segmented
-    kernel (default), the one-thread-per-row kernel
+    kernel (default; plain calls, and a prepared plan that keeps the segment
+    table), the one-thread-per-row kernel
     (JLUST_HIP_BSR_SPMV_SEGMENTS=0), and the CSR expansion route (expansion,
     then CSR SpMV on the expanded matrix).  HIP events: the median of 5 runs
     of 20 calls after 3 warm-up calls; bytes = values + block columns +
@@ -663,6 +664,9 @@ def bsr_spmv_powerlaw():
         x = dev(np.random.default_rng(3).standard_normal(nb * 16).astype(dt))
         y = torch.zeros(mb * 16, dtype=x.dtype, device="cuda")
         t_seg = ms(lambda: J.execute(J.SpMVOp, A, x, y))
+        h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+        t_plan = ms(lambda: J.execute(h, x, y))
+        del h
         old = os.environ.get("JLUST_HIP_BSR_SPMV_SEGMENTS")
         os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"] = "0"
         try:
@@ -681,6 +685,7 @@ def bsr_spmv_powerlaw():
         r = {"workload": f"bsr16_spmv_powerlaw_65536_{np.dtype(dt).name}", "nnzb": nnzb,
              "max_blocks_per_row": int(lens.max()), "bytes": nbytes,
              "segments_ms": round(t_seg, 4), "segments_GBps": gbs(t_seg),
+             "plan_ms": round(t_plan, 4), "plan_GBps": gbs(t_plan),
              "row_kernel_ms": round(t_row, 3), "row_kernel_GBps": gbs(t_row),
              "expansion_ms": round(t_exp, 3), "csr_spmv_on_expansion_ms": round(t_csr, 4)}
         log(f"bsr spmv: {r}")

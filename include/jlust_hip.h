@@ -55,6 +55,7 @@ typedef struct jlust_convert *jlust_convert_t;
 typedef struct jlust_spmm_plan *jlust_spmm_plan_t;
 typedef struct jlust_sddmm_plan *jlust_sddmm_plan_t;
 typedef struct jlust_bsr_plan *jlust_bsr_plan_t;
+typedef struct jlust_bsr_spmv_plan *jlust_bsr_spmv_plan_t;
 
 /*
  * Status codes.  The Julia side maps them onto the reference's exception
@@ -812,6 +813,42 @@ int jlust_hip_bsr_spmm_plan_execute_f64(jlust_bsr_plan_t plan, double alpha,
 int jlust_hip_bsr_spmm_plan_info(jlust_bsr_plan_t plan, int32_t *path);
 /* Drains the device, then frees the plan's expansion and CSR plan. */
 int jlust_hip_bsr_spmm_plan_destroy(jlust_bsr_plan_t plan);
+
+/*
+ * Prepared BSR SpMV: prepare(EmitterBackend, SpMVOp, u_A) on a BSR matrix
+ * (ext/KernelAbstractionsExt/ops/spmv.jl:518-544, the handle execute(h, x, y)
+ * and update_values! run on; the reference analyses nothing for it).  Any
+ * block shape, either block order, Float64 or Float32 (value_type 0 / 1).
+ * create builds the segment table of jlust_hip_bsr_spmv_*_i32 once (block-
+ * rows cut into segments of at most 32 blocks; the plan owns it and the
+ * per-segment sums) and synchronises `stream`; it reads browptr's ends back
+ * and returns JLUST_STATUS_NONCANONICAL_STORAGE unless they are origin and
+ * nnzb + origin.  execute: y = alpha*A*x + beta*y (beta == 0: y write-only),
+ * stream-ordered; one plan must not run on two streams at once (the partial
+ * sums are the plan's).  update_values: new values of the same pattern, a
+ * pointer swap.  The plan keeps browptr, bcolind and the values by pointer:
+ * the caller keeps them alive.
+ */
+int jlust_hip_bsr_spmv_plan_create(int64_t mb, int64_t nb, int64_t b1,
+                                   int64_t b2, int64_t nnzb, int32_t origin,
+                                   int value_type, int row_major_blocks,
+                                   const int32_t *browptr,
+                                   const int32_t *bcolind, const void *val,
+                                   jlust_stream_t stream,
+                                   jlust_bsr_spmv_plan_t *plan_out);
+int jlust_hip_bsr_spmv_plan_update_values(jlust_bsr_spmv_plan_t plan,
+                                          const void *val,
+                                          jlust_stream_t stream);
+int jlust_hip_bsr_spmv_plan_execute_f64(jlust_bsr_spmv_plan_t plan,
+                                        double alpha, const double *x,
+                                        double beta, double *y,
+                                        jlust_stream_t stream);
+int jlust_hip_bsr_spmv_plan_execute_f32(jlust_bsr_spmv_plan_t plan,
+                                        float alpha, const float *x,
+                                        float beta, float *y,
+                                        jlust_stream_t stream);
+/* Drains the device, then frees the plan's segment table. */
+int jlust_hip_bsr_spmv_plan_destroy(jlust_bsr_spmv_plan_t plan);
 
 /* ----------------------------------------------------------- conversions */
 

@@ -128,6 +128,12 @@ SIGNATURES = {
     "jlust_hip_bsr_spmm_plan_execute_f64": (_INT, [_P, _D, _P, _I64, _D, _P, _I64, _P]),
     "jlust_hip_bsr_spmm_plan_info": (_INT, [_P, ctypes.POINTER(_I32)]),
     "jlust_hip_bsr_spmm_plan_destroy": (_INT, [_P]),
+    "jlust_hip_bsr_spmv_plan_create": (_INT, [_I64, _I64, _I64, _I64, _I64, _I32, _INT, _INT, _P, _P, _P, _P,
+                                              ctypes.POINTER(_P)]),
+    "jlust_hip_bsr_spmv_plan_update_values": (_INT, [_P, _P, _P]),
+    "jlust_hip_bsr_spmv_plan_execute_f64": (_INT, [_P, _D, _P, _D, _P, _P]),
+    "jlust_hip_bsr_spmv_plan_execute_f32": (_INT, [_P, _F, _P, _F, _P, _P]),
+    "jlust_hip_bsr_spmv_plan_destroy": (_INT, [_P]),
     "jlust_hip_convert_analyze": (_INT, [_P, _I32, _I32, _I32, _I32, _INT, _P, ctypes.POINTER(_P),
                                          ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "jlust_hip_convert_fill": (_INT, [_P, _P, _P]),

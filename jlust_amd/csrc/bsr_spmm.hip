@@ -1587,22 +1587,15 @@ __global__ __launch_bounds__(256) void bsr_spmv_fix_kernel(int64_t mb, int64_t b
     y[row] = BZ ? alpha * acc : alpha * acc + beta * y[row];
 }
 
-template <typename T>
-int bsr_spmv_segments(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
-                      const int32_t *browptr, const int32_t *bcolind, const T *val, int row_major_blocks, T alpha,
-                      const T *x, T beta, T *y, jlust_stream_t stream)
+// Segments of at most BSRMV_SEG blocks (a block-row of L blocks is ceil(L /
+// BSRMV_SEG) of them, an empty one still one): nsegmax bounds their count.
+int64_t bsr_spmv_nsegmax(int64_t mb, int64_t nnzb) { return mb + (nnzb + BSRMV_SEG - 1) / BSRMV_SEG; }
+
+// The segment table: segstart (mb + 1, the first segment of each block-row)
+// and segrow (nsegmax, the block-row of each segment).
+int bsr_spmv_table(int64_t mb, int64_t nnzb, int32_t origin, const int32_t *browptr, int32_t *segstart,
+                   int32_t *segrow, int64_t nsegmax, jlust_stream_t stream)
 {
-    // Scratch: the scan's own part, then segstart (mb + 1), segrow (at most
-    // mb + nnzb / BSRMV_SEG segments), part (b1 sums per segment).
-    const int64_t nsegmax = mb + (nnzb + BSRMV_SEG - 1) / BSRMV_SEG;
-    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
-    const size_t start_off = up(exclusive_scan_scratch_bytes(mb + 1));
-    const size_t row_off = start_off + up((size_t)(mb + 1) * sizeof(int32_t));
-    const size_t part_off = row_off + up((size_t)nsegmax * sizeof(int32_t));
-    void *ws = nullptr;
-    if (int st = scratch(stream, part_off + (size_t)(nsegmax * b1) * sizeof(T), &ws)) return st;
-    int32_t *segstart = (int32_t *)((char *)ws + start_off), *segrow = (int32_t *)((char *)ws + row_off);
-    T *part = (T *)((char *)ws + part_off);
     hipStream_t s = (hipStream_t)stream;
     hipLaunchKernelGGL(bsr16_spmv_count_kernel, dim3((unsigned)((mb + 1 + 255) / 256)), dim3(256), 0, s, mb, nnzb,
                        origin, browptr, segstart);
@@ -1610,7 +1603,18 @@ int bsr_spmv_segments(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nn
     if (int st = exclusive_scan_i32(segstart, segstart, mb + 1, stream)) return st;
     hipLaunchKernelGGL(bsr16_spmv_rows_kernel, dim3((unsigned)((mb + 255) / 256)), dim3(256), 0, s, mb, segstart,
                        segrow, nsegmax);
-    if (int st = check_launch("bsr16_spmv_rows_kernel")) return st;
+    return check_launch("bsr16_spmv_rows_kernel");
+}
+
+// The product over a segment table: per-segment partial sums (part, nsegmax
+// x b1), then each block-row's sum of its segments into y.
+template <typename T>
+int bsr_spmv_run(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
+                 const int32_t *browptr, const int32_t *bcolind, const T *val, int row_major_blocks, T alpha,
+                 const T *x, T beta, T *y, const int32_t *segstart, const int32_t *segrow, T *part, int64_t nsegmax,
+                 jlust_stream_t stream)
+{
+    hipStream_t s = (hipStream_t)stream;
     const bool bz = beta == T(0);
     if (b1 != 16 || b2 != 16) {
         const dim3 g((unsigned)((nsegmax * b1 + 255) / 256));
@@ -1650,6 +1654,27 @@ int bsr_spmv_segments(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nn
         hipLaunchKernelGGL((bsr_spmv_fix_kernel<T, false>), gfix, dim3(256), 0, s, mb, b1, segstart, part, nsegmax,
                            alpha, beta, y);
     return check_launch("bsr_spmv_fix_kernel");
+}
+
+template <typename T>
+int bsr_spmv_segments(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb, int32_t origin,
+                      const int32_t *browptr, const int32_t *bcolind, const T *val, int row_major_blocks, T alpha,
+                      const T *x, T beta, T *y, jlust_stream_t stream)
+{
+    // Scratch: the scan's own part, then segstart (mb + 1), segrow (nsegmax),
+    // part (b1 sums per segment).
+    const int64_t nsegmax = bsr_spmv_nsegmax(mb, nnzb);
+    auto up = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t start_off = up(exclusive_scan_scratch_bytes(mb + 1));
+    const size_t row_off = start_off + up((size_t)(mb + 1) * sizeof(int32_t));
+    const size_t part_off = row_off + up((size_t)nsegmax * sizeof(int32_t));
+    void *ws = nullptr;
+    if (int st = scratch(stream, part_off + (size_t)(nsegmax * b1) * sizeof(T), &ws)) return st;
+    int32_t *segstart = (int32_t *)((char *)ws + start_off), *segrow = (int32_t *)((char *)ws + row_off);
+    T *part = (T *)((char *)ws + part_off);
+    if (int st = bsr_spmv_table(mb, nnzb, origin, browptr, segstart, segrow, nsegmax, stream)) return st;
+    return bsr_spmv_run<T>(mb, nb, b1, b2, nnzb, origin, browptr, bcolind, val, row_major_blocks, alpha, x, beta, y,
+                           segstart, segrow, part, nsegmax, stream);
 }
 
 template <typename T>
@@ -2166,6 +2191,166 @@ extern "C" int jlust_hip_bsr_spmm_plan_destroy(jlust_bsr_plan_t plan)
     delete plan;
     if (e != hipSuccess) return jlust::hip_fail(e, "bsr_spmm_plan_destroy");
     return st;
+}
+
+// ---- prepared BSR SpMV: the segment table built once.
+struct jlust_bsr_spmv_plan {
+    int64_t mb = 0, nb = 0, b1 = 0, b2 = 0, nnzb = 0, nsegmax = 0;
+    int32_t origin = 0;
+    int value_type = 0, row_major = 1, device = 0;
+    const int32_t *browptr = nullptr;
+    const int32_t *bcolind = nullptr;
+    const void *val = nullptr;
+    void *mem = nullptr;                // segstart | segrow | partial sums
+    int32_t *segstart = nullptr;
+    int32_t *segrow = nullptr;
+    void *part = nullptr;
+};
+
+static int bsr_spmv_plan_create_body(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
+                                     int32_t origin, int value_type, int row_major_blocks,
+                                     const int32_t *browptr, const int32_t *bcolind, const void *val,
+                                     jlust_stream_t stream, jlust_bsr_spmv_plan_t *plan_out)
+{
+    using namespace jlust;
+    clear_error();
+    if (!plan_out) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_create: null plan_out");
+    *plan_out = nullptr;
+    if (mb < 0 || nb < 0 || b1 <= 0 || b2 <= 0 || nnzb < 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_create: negative extent or block size");
+    if (value_type != 0 && value_type != 1)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE,
+                    "bsr_spmv_plan_create: value_type %d (0 = Float64, 1 = Float32)", value_type);
+    if (int st = check_origin(origin)) return st;
+    if (mb * b1 > INT32_MAX || nb * b2 > INT32_MAX || nnzb * b1 * b2 > INT32_MAX)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_create: extents exceed the Int32 index range");
+    if ((mb > 0 && !browptr) || bad_ptr(bcolind, nnzb) || bad_ptr(val, nnzb * b1 * b2))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_create: null device pointer");
+    if (nnzb > 0 && nb == 0)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_create: blocks stored in a matrix with no columns");
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    std::unique_ptr<jlust_bsr_spmv_plan> p(new jlust_bsr_spmv_plan());
+    p->mb = mb;
+    p->nb = nb;
+    p->b1 = b1;
+    p->b2 = b2;
+    p->nnzb = nnzb;
+    p->origin = origin;
+    p->value_type = value_type;
+    p->row_major = row_major_blocks ? 1 : 0;
+    p->device = dev;
+    p->browptr = browptr;
+    p->bcolind = bcolind;
+    p->val = val;
+    if (mb > 0) {
+        // browptr's ends, read back: the table's kernels would only clamp a
+        // malformed pointer array.
+        hipStream_t s = (hipStream_t)stream;
+        int32_t ends[2] = {0, 0};
+        JLUST_HIP_TRY(hipMemcpyAsync(&ends[0], browptr, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+        JLUST_HIP_TRY(hipMemcpyAsync(&ends[1], browptr + mb, sizeof(int32_t), hipMemcpyDeviceToHost, s));
+        JLUST_HIP_TRY(hipStreamSynchronize(s));
+        if (ends[0] != origin || (int64_t)ends[1] != nnzb + origin)
+            return fail(JLUST_STATUS_NONCANONICAL_STORAGE,
+                        "bsr_spmv_plan_create: browptr runs from %d to %d, expected %d to %lld", ends[0], ends[1],
+                        origin, (long long)(nnzb + origin));
+        const size_t tsz = value_type == 0 ? sizeof(double) : sizeof(float);
+        p->nsegmax = bsr_spmv_nsegmax(mb, nnzb);
+        const size_t sz_st = bsr_align_up(sizeof(int32_t) * (size_t)(mb + 1), 256);
+        const size_t sz_rw = bsr_align_up(sizeof(int32_t) * (size_t)p->nsegmax, 256);
+        JLUST_HIP_TRY(hipMalloc(&p->mem, sz_st + sz_rw + bsr_align_up(tsz * (size_t)(p->nsegmax * b1), 256)));
+        char *b = (char *)p->mem;
+        p->segstart = (int32_t *)b;
+        p->segrow = (int32_t *)(b + sz_st);
+        p->part = b + sz_st + sz_rw;
+        int st = bsr_spmv_table(mb, nnzb, origin, browptr, p->segstart, p->segrow, p->nsegmax, stream);
+        if (!st) {
+            const hipError_t e = hipStreamSynchronize(s);  // the plan may then run on any stream
+            if (e != hipSuccess) st = hip_fail(e, "bsr_spmv_plan_create");
+        }
+        if (st) {
+            (void)hipStreamSynchronize(s);
+            (void)hipFree(p->mem);
+            return st;
+        }
+    }
+    *plan_out = p.release();
+    return JLUST_STATUS_SUCCESS;
+}
+
+extern "C" int jlust_hip_bsr_spmv_plan_create(int64_t mb, int64_t nb, int64_t b1, int64_t b2, int64_t nnzb,
+                                              int32_t origin, int value_type, int row_major_blocks,
+                                              const int32_t *browptr, const int32_t *bcolind, const void *val,
+                                              jlust_stream_t stream, jlust_bsr_spmv_plan_t *plan_out)
+{
+    return jlust::host_guard("bsr_spmv_plan_create", [&] {
+        return bsr_spmv_plan_create_body(mb, nb, b1, b2, nnzb, origin, value_type, row_major_blocks, browptr,
+                                         bcolind, val, stream, plan_out);
+    });
+}
+
+extern "C" int jlust_hip_bsr_spmv_plan_update_values(jlust_bsr_spmv_plan_t plan, const void *val,
+                                                     jlust_stream_t stream)
+{
+    using namespace jlust;
+    (void)stream;                           // a pointer swap: nothing to enqueue
+    clear_error();
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_update_values: null plan");
+    if (bad_ptr(val, plan->nnzb * plan->b1 * plan->b2))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_update_values: null values");
+    plan->val = val;
+    return JLUST_STATUS_SUCCESS;
+}
+
+template <typename T>
+static int bsr_spmv_plan_execute(jlust_bsr_spmv_plan_t plan, int value_type, T alpha, const T *x, T beta, T *y,
+                                 jlust_stream_t stream)
+{
+    using namespace jlust;
+    clear_error();
+    if (!plan) return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_execute: null plan");
+    if (plan->value_type != value_type)
+        return fail(JLUST_STATUS_UNSUPPORTED_VALUE_TYPE, "bsr_spmv_plan_execute: plan was created for %s values",
+                    plan->value_type == 0 ? "Float64" : "Float32");
+    if ((plan->nnzb > 0 && !x) || bad_ptr(y, plan->mb * plan->b1))
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_execute: null device pointer");
+    int dev = 0;
+    if (int st = require_device(&dev)) return st;
+    if (dev != plan->device)
+        return fail(JLUST_STATUS_INVALID_ARGUMENT, "bsr_spmv_plan_execute: plan belongs to device %d, current device is %d",
+                    plan->device, dev);
+    if (plan->mb == 0) return JLUST_STATUS_SUCCESS;
+    return bsr_spmv_run<T>(plan->mb, plan->nb, plan->b1, plan->b2, plan->nnzb, plan->origin, plan->browptr,
+                           plan->bcolind, (const T *)plan->val, plan->row_major, alpha, x, beta, y, plan->segstart,
+                           plan->segrow, (T *)plan->part, plan->nsegmax, stream);
+}
+
+extern "C" int jlust_hip_bsr_spmv_plan_execute_f64(jlust_bsr_spmv_plan_t plan, double alpha, const double *x,
+                                                   double beta, double *y, jlust_stream_t stream)
+{
+    return bsr_spmv_plan_execute<double>(plan, 0, alpha, x, beta, y, stream);
+}
+
+extern "C" int jlust_hip_bsr_spmv_plan_execute_f32(jlust_bsr_spmv_plan_t plan, float alpha, const float *x,
+                                                   float beta, float *y, jlust_stream_t stream)
+{
+    return bsr_spmv_plan_execute<float>(plan, 1, alpha, x, beta, y, stream);
+}
+
+extern "C" int jlust_hip_bsr_spmv_plan_destroy(jlust_bsr_spmv_plan_t plan)
+{
+    jlust::clear_error();
+    if (!plan) return JLUST_STATUS_SUCCESS;
+    // Work queued on any stream may still read the plan's buffers.
+    hipError_t e = hipDeviceSynchronize();
+    if (plan->mem) {
+        const hipError_t e2 = hipFree(plan->mem);
+        if (e == hipSuccess) e = e2;
+    }
+    delete plan;
+    if (e != hipSuccess) return jlust::hip_fail(e, "bsr_spmv_plan_destroy");
+    return JLUST_STATUS_SUCCESS;
 }
 
 namespace jlust {

@@ -1371,6 +1371,112 @@ class HIPBSRSpMMHandle(AbstractKernelHandle):
         self._destroy()
 
 
+class HIPBSRSpMVHandle(AbstractKernelHandle):
+    """Prepared BSR SpMV (jlust_hip_bsr_spmv_plan_*): prepare(HIPBackend(),
+    SpMVOp, A::BSR) -> execute(h, x, y) or execute(h, A, x, y) ->
+    update_values!(h, A), the EmitterSpMVHandle contract (ext/
+    KernelAbstractionsExt/ops/spmv.jl:518-544) with the block-rows' segment
+    table built once instead of at every call.  The plan reads A's values in
+    place, so a product sees them as they are at the call; an A with another
+    value tensor becomes the plan's values (update_values! semantics).  Index
+    buffers written in place through torch since the plan was built are
+    checked and the table rebuilt.  input_fn/output_fn apply as in plain
+    execute."""
+
+    takes_raw = True
+
+    def __init__(self, u_A: USTensor, input_fn=None, output_fn=None):
+        if not is_bsr(u_A.format):
+            raise UnsupportedFormat(u_A.format, _BE, "prepared BSR SpMV plans take BSR")
+        self.input_fn, self.output_fn = input_fn, output_fn
+        self.suf = _value_suffix(u_A)
+        self.T = nonzeros(u_A).dtype
+        b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
+        _check_values(u_A, self.T)
+        self.dev = _check_same_device(browptr, bcolind, nonzeros(u_A))
+        self.u_A = u_A                      # keeps the buffers alive (GC anchor)
+        self._vals = nonzeros(u_A)
+        self._plan = ctypes.c_void_p(0)
+        self._make()
+
+    def _make(self):
+        self._destroy()
+        b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(self.u_A)
+        _check_pos_once(self.u_A, browptr, mb, bcolind.numel(), self.dev)
+        _check_crd_once(self.u_A, bcolind, nb, False, self.dev)
+        plan = ctypes.c_void_p(0)
+        with _on(self.dev):
+            st = _lib.lib().jlust_hip_bsr_spmv_plan_create(
+                mb, nb, b1, b2, bcolind.numel(), self.u_A.origin.offset, 0 if self.suf == "f64" else 1,
+                int(row_major), _ptr(browptr), _ptr(bcolind), _ptr(self._vals), _stream(self.dev),
+                ctypes.byref(plan))
+        _lib.check(st, "bsr_spmv_plan_create", self.u_A.format, _BE, self.T)
+        self._plan = plan
+        self._iver = (browptr._version, bcolind._version)
+
+    def _current(self):
+        """Rebuild the table if A's index buffers were written in place."""
+        browptr, bcolind = self.u_A.pos_buffers[1], self.u_A.crd_buffers[1]
+        if (browptr._version, bcolind._version) != self._iver:
+            self._make()
+
+    def execute(self, *ts, alpha=1.0, beta=0.0):
+        """execute(h, x, y) or execute(h, A, x, y); with plain device tensors
+        x, y the call returns y, with USTensors u_y."""
+        if len(ts) == 2 and isinstance(ts[0], torch.Tensor) and isinstance(ts[1], torch.Tensor):
+            self.execute(ust(ts[0]), ust(ts[1]), alpha=alpha, beta=beta)
+            return ts[1]
+        ts = tuple(t if isinstance(t, USTensor) else ust(t) for t in ts)
+        if len(ts) == 3:
+            u_A, u_x, u_y = ts
+            if nonzeros(u_A) is not self._vals:
+                self.update_values(u_A)
+        elif len(ts) == 2:
+            u_x, u_y = ts
+        else:
+            raise TypeError("execute(handle, [A,] x, y)")
+        self._current()
+        return spmv_with_fns(self._execute_plain, self.u_A, u_x, u_y, alpha, beta,
+                             self.input_fn, self.output_fn)
+
+    def _execute_plain(self, u_A, u_x: USTensor, u_y: USTensor, alpha=1.0, beta=0.0):
+        x, y = _vec_checks(self.u_A, u_x, u_y)
+        _check_same_device(self._vals, x, y)
+        with _on(self.dev):
+            st = getattr(_lib.lib(), f"jlust_hip_bsr_spmv_plan_execute_{self.suf}")(
+                self._plan, float(alpha), _ptr(x), float(beta), _ptr(y), _stream(self.dev))
+        _lib.check(st, "bsr_spmv_plan_execute", self.u_A.format, _BE, self.T)
+        return u_y
+
+    def update_values(self, u_A: USTensor):
+        if u_A.extents != self.u_A.extents or nnz(u_A) != nnz(self.u_A) or u_A.format != self.u_A.format:
+            raise IncompatibleExtents("update_values!: the sparsity structure must not change")
+        _check_values(u_A, self.T)
+        _check_same_device(nonzeros(u_A), self._vals)
+        self.u_A = USTensor(self.u_A.extents, self.u_A.format, self.u_A.pos_buffers,
+                            self.u_A.crd_buffers, nonzeros(u_A), self.u_A.owner, self.u_A.origin)
+        self._vals = nonzeros(u_A)
+        with _on(self.dev):
+            st = _lib.lib().jlust_hip_bsr_spmv_plan_update_values(self._plan, _ptr(self._vals),
+                                                                  _stream(self.dev))
+        _lib.check(st, "bsr_spmv_plan_update_values", self.u_A.format, _BE, self.T)
+        return self
+
+    def kernel(self) -> str:
+        return "bsr_segments"
+
+    def _destroy(self):
+        plan, self._plan = getattr(self, "_plan", None), ctypes.c_void_p(0)
+        if plan is not None and plan.value:
+            try:
+                _lib.lib().jlust_hip_bsr_spmv_plan_destroy(plan)
+            except Exception:
+                pass
+
+    def __del__(self):
+        self._destroy()
+
+
 class HIPSDDMMHandle(AbstractKernelHandle):
     """Prepared SDDMM (jlust_hip_sddmm_plan_*): prepare(HIPBackend(), SDDMMOp,
     A, B, C) -> execute(h, A, B, C) -> update_values!(h, C), the cuSPARSE
@@ -1489,6 +1595,8 @@ def prepare(optype, u_A: USTensor, *more, **kw):
             raise TypeError(f"prepare(SpMVOp): unexpected keywords {sorted(bad)} or tensors ({len(more)})")
         if is_csr_shaped(u_A.format) or is_coo_shaped(u_A.format):
             return HIPSpMVHandle(u_A, kw.get("input_fn"), kw.get("output_fn"))
+        if is_bsr(u_A.format):
+            return HIPBSRSpMVHandle(u_A, kw.get("input_fn"), kw.get("output_fn"))
         return HIPOpHandle(SpMVOp, u_A, **kw)
     if tag == "SpMM":
         bad = set(kw) - {"n_cols", "skip_empty_rows"}

@@ -490,3 +490,113 @@ def test_bsr_strip_schedule(J, O, k, beta, wide, monkeypatch):
     rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
     absref = O.csr_spmm_absref(rp, ci, v, B, 0.75, beta, C0)
     assert_within(C, ref, absref, np.float32, f"strip schedule wide={wide} k={k} beta={beta}")
+
+
+@pytest.mark.parametrize("wide", ["1", "0"])
+def test_bsr_nonfinite_b_rows_reach_only_their_blocks(J, O, wide, monkeypatch):
+    """B rows holding NaN and Inf inside the strips' windows: only the
+    block-rows with a block in those B rows may see them.  The 24-row kernel
+    runs the MFMAs of absent blocks on a zero row of its window rather than
+    on B, so no other output may turn non-finite; rows of 1 to 8 blocks (the
+    absent blocks in between) within a +-32 band, through both strip kernels."""
+    monkeypatch.setenv("JLUST_HIP_BSR_WIDE", wide)
+    mb = nb = 600
+    k = 48
+    rng = np.random.default_rng(77)
+    bcols = []
+    for R in range(mb):
+        lo, hi = max(0, R - 32), min(nb, R + 33)
+        bcols.append(np.sort(rng.choice(np.arange(lo, hi), int(rng.integers(1, 9)), replace=False)))
+    browptr = (np.r_[0, np.cumsum([c.size for c in bcols])] + 1).astype(np.int32)
+    bcolind = (np.concatenate(bcols) + 1).astype(np.int32)
+    val = rng.standard_normal(bcolind.size * 256).astype(np.float32)
+    B = np.asfortranarray(rng.standard_normal((nb * 16, k)).astype(np.float32))
+    bad_blocks = rng.choice(nb, 40, replace=False)
+    B[bad_blocks[:20] * 16 + 3, :] = np.nan
+    B[bad_blocks[20:] * 16 + 11, :] = np.inf
+    C = run_bsr(J, browptr, bcolind, val, B, mb, nb, alpha=1.0, beta=0.0)
+    touched = np.array([np.isin(c, bad_blocks).any() for c in bcols])
+    rows_ok = np.repeat(~touched, 16)
+    assert rows_ok.any() and (~rows_ok).any()
+    assert np.isfinite(C[rows_ok]).all(), f"wide={wide}: a non-finite B row reached a row without its block"
+    keep = ~touched
+    sel = np.flatnonzero(keep)
+    sub_bp = np.r_[0, np.cumsum([bcols[R].size for R in sel])] + 1
+    sub_bc = np.concatenate([bcols[R] for R in sel]) + 1
+    sub_val = np.concatenate([val[(browptr[R] - 1) * 256:(browptr[R + 1] - 1) * 256] for R in sel])
+    Bf = np.where(np.isfinite(B), B, 0).astype(np.float32)
+    ref = O.bsr_spmm(sub_bp.astype(np.int32), sub_bc.astype(np.int32), sub_val, 16, Bf, 1.0, 0.0, None)
+    rp, ci, v = O.bsr_to_csr(sub_bp.astype(np.int32), sub_bc.astype(np.int32), sub_val, 16)
+    absref = O.csr_spmm_absref(rp, ci, v, Bf, 1.0, 0.0, None)
+    assert_within(C[rows_ok], ref, absref, np.float32, f"wide={wide}: finite rows")
+
+
+@pytest.mark.parametrize("b1,b2", [(16, 16), (3, 5)])
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("row_major", [True, False])
+def test_bsr_spmv_plan(J, O, b1, b2, dtype, row_major):
+    """prepare(HIPBackend(), SpMVOp, A::BSR) builds the segment table once
+    (jlust_hip_bsr_spmv_plan_*): products on power-law block-rows (empty
+    ones, one past many segments) against the oracle, repeated with new x;
+    values written in place are seen; another value tensor through
+    update_values! and through execute(h, A, x, y); a block column written in
+    place rebuilds the table, a malformed one raises NonCanonicalStorage."""
+    import torch
+    from jlust_amd.hip_backend import HIPBSRSpMVHandle
+    mb, nb = 200, 300
+    rng = np.random.default_rng(41 + b1 + row_major)
+    lens = np.minimum((rng.pareto(1.3, mb) + 1) * 2, nb).astype(np.int64)
+    lens[::9] = 0
+    lens[3] = 250
+    bcols = [np.sort(rng.choice(nb, int(n), replace=False)) for n in lens]
+    origin = 1 if row_major else 0
+    bp = (np.r_[0, np.cumsum(lens)] + origin).astype(np.int32)
+    bc = (np.concatenate(bcols) + origin).astype(np.int32)
+    flat = rng.standard_normal(bc.size * b1 * b2).astype(dtype)
+    og = J.OneBased() if origin == 1 else J.ZeroBased()
+    A = J.bsr_tensor(dev(bp), dev(bc), dev(flat), (mb * b1, nb * b2), (b1, b2), row_major, og)
+    h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
+    assert isinstance(h, HIPBSRSpMVHandle)
+    y0 = rng.uniform(-1, 1, mb * b1).astype(dtype)
+
+    def check(vals, bcv, what):
+        rp, ci, v = O.bsr_to_csr(bp, bcv, vals, b1, origin, row_major, b2)
+        for alpha, beta in ((1.0, 0.0), (-0.5, 1.5)):
+            x = rng.uniform(-1, 1, nb * b2).astype(dtype)
+            y = dev(y0.copy()) if beta else torch.full((mb * b1,), float("nan"), dtype=A.dtype, device="cuda")
+            J.execute(h, dev(x), y, alpha=alpha, beta=beta)
+            yb = y0 if beta else None
+            ref = O.csr_spmv(rp, ci, v, x, alpha, beta, yb, origin)
+            absref = O.csr_spmv_absref(rp, ci, v, x, alpha, beta, yb, origin)
+            assert_within(host(y), ref, absref, dtype, f"bsr {b1}x{b2} spmv plan, {what}, beta={beta}")
+
+    check(flat, bc, "first")
+    A.val.mul_(-2.0)                                     # in place: the plan reads the values at the call
+    check(flat * -2, bc, "values scaled in place")
+    flat2 = rng.standard_normal(flat.size).astype(dtype)
+    J.update_values_(h, J.bsr_tensor(A.pos_buffers[1], A.crd_buffers[1], dev(flat2), A.extents,
+                                     (b1, b2), row_major, og))
+    check(flat2, bc, "update_values!")
+    flat3 = rng.standard_normal(flat.size).astype(dtype)
+    A3 = J.bsr_tensor(A.pos_buffers[1], A.crd_buffers[1], dev(flat3), A.extents, (b1, b2), row_major, og)
+    x = rng.uniform(-1, 1, nb * b2).astype(dtype)
+    y = dev(np.zeros(mb * b1, dtype))
+    J.execute(h, A3, dev(x), y)
+    rp, ci, v = O.bsr_to_csr(bp, bc, flat3, b1, origin, row_major, b2)
+    assert_within(host(y), O.csr_spmv(rp, ci, v, x, 1.0, 0.0, None, origin),
+                  O.csr_spmv_absref(rp, ci, v, x, 1.0, 0.0, None, origin), dtype, "execute(h, A, x, y)")
+    # the first block of block-row 3 moved to a column the row does not use
+    bc2 = bc.copy()
+    q = bp[3] - origin
+    free = np.setdiff1d(np.arange(nb), bcols[3])
+    bc2[q] = free[0] + origin
+    order = np.argsort(bc2[q:q + lens[3]], kind="stable")
+    bc2[q:q + lens[3]] = bc2[q:q + lens[3]][order]
+    blocks = flat3.reshape(-1, b1 * b2).copy()
+    blocks[q:q + lens[3]] = blocks[q:q + lens[3]][order]
+    h.u_A.crd_buffers[1].copy_(dev(bc2))
+    h.u_A.val.copy_(dev(blocks.reshape(-1)))
+    check(blocks.reshape(-1), bc2, "block columns written in place")
+    h.u_A.crd_buffers[1][0] = nb + origin                # past the last block column
+    with pytest.raises(J.NonCanonicalStorage):
+        J.execute(h, dev(x), y)
