@@ -76,7 +76,8 @@ enum jlust_status {
     JLUST_STATUS_HIP_ERROR = 6,
     JLUST_STATUS_NO_DEVICE = 7,
     JLUST_STATUS_OUT_OF_MEMORY = 8,
-    JLUST_STATUS_STREAM_CAPTURING = 9   /* graph launch onto a capturing stream */
+    JLUST_STATUS_STREAM_CAPTURING = 9,  /* graph launch onto a capturing stream */
+    JLUST_STATUS_UNSUPPORTED_INDEX_TYPE = 10  /* an index beyond the Int32 kernels' range */
 };
 
 /* ---------------------------------------------------------------- library */
@@ -127,6 +128,16 @@ int jlust_hip_check_csr(int64_t m, int64_t n, int64_t nnz, int32_t origin,
  */
 int jlust_hip_check_pos_i32(int64_t nouter, int64_t nnz, int32_t origin,
                             const int32_t *pos, jlust_stream_t stream);
+/*
+ * Int64 index buffers (the walker keeps the index type as stored,
+ * ext/KernelAbstractionsExt/ops/_walker.jl:105-110) narrowed to the Int32
+ * the kernels take: dst[i] = src[i] for n entries.  An index outside Int32's
+ * range, or n >= 2^31, returns JLUST_STATUS_UNSUPPORTED_INDEX_TYPE (the
+ * reference's UnsupportedIndexType, src/errors.jl:4).  Synchronises `stream`
+ * (one flag word read back).
+ */
+int jlust_hip_narrow_index_i64(int64_t n, const int64_t *src, int32_t *dst,
+                               jlust_stream_t stream);
 int jlust_hip_check_crd_i32(int64_t len, int64_t extent, int32_t origin,
                             int strictly_increasing, const int32_t *crd,
                             jlust_stream_t stream);

@@ -134,6 +134,7 @@ SIGNATURES = {
     "jlust_hip_bsr_spmv_plan_execute_f64": (_INT, [_P, _D, _P, _D, _P, _P]),
     "jlust_hip_bsr_spmv_plan_execute_f32": (_INT, [_P, _F, _P, _F, _P, _P]),
     "jlust_hip_bsr_spmv_plan_destroy": (_INT, [_P]),
+    "jlust_hip_narrow_index_i64": (_INT, [_I64, _P, _P, _P]),
     "jlust_hip_convert_analyze": (_INT, [_P, _I32, _I32, _I32, _I32, _INT, _P, ctypes.POINTER(_P),
                                          ctypes.POINTER(_I64), ctypes.POINTER(_I64)]),
     "jlust_hip_convert_fill": (_INT, [_P, _P, _P]),
@@ -161,7 +162,7 @@ SIGNATURES = {
 STATUS = {
     0: "SUCCESS", 1: "INVALID_ARGUMENT", 2: "UNSUPPORTED_VALUE_TYPE", 3: "UNSUPPORTED_FORMAT",
     4: "NONCANONICAL_STORAGE", 5: "INDEX_ORIGIN", 6: "HIP_ERROR", 7: "NO_DEVICE",
-    8: "OUT_OF_MEMORY", 9: "STREAM_CAPTURING",
+    8: "OUT_OF_MEMORY", 9: "STREAM_CAPTURING", 10: "UNSUPPORTED_INDEX_TYPE",
 }
 STREAM_CAPTURING = 9
 
@@ -232,6 +233,8 @@ def check(status: int, what: str, fmt=None, backend=None, T=None):
         raise errors.NoDevice(msg)
     if status == 8:
         raise MemoryError(msg)
+    if status == 10:
+        raise errors.UnsupportedIndexType(T, backend, msg)
     raise errors.HIPError(f"{STATUS.get(status, status)}: {msg}")
 
 

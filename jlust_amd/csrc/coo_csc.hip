@@ -69,6 +69,19 @@ __global__ void crd_check_kernel(int64_t len, int64_t extent, int32_t origin, in
     if (f) atomicOr(flag, f);
 }
 
+// dst[i] = src[i] narrowed to Int32; a value outside Int32's range sets flag
+// bit 32 (and leaves 0).
+__global__ void narrow_index_kernel(int64_t n, const int64_t *__restrict__ src, int32_t *__restrict__ dst,
+                                    int32_t *__restrict__ flag)
+{
+    const int64_t i = (int64_t)blockIdx.x * XB + threadIdx.x;
+    if (i >= n) return;
+    const int64_t v = src[i];
+    const bool ok = v >= INT32_MIN && v <= INT32_MAX;
+    dst[i] = ok ? (int32_t)v : 0;
+    if (!ok) atomicOr(flag, 32);
+}
+
 // crd_out[p] = outer ? outer[s] : s + origin, for the segment s holding entry
 // p: the last s < nouter with pos[s] - origin <= p (pos checked canonical, so
 // empty segments before it are skipped).
@@ -329,6 +342,28 @@ extern "C" int jlust_hip_check_crd_i32(int64_t len, int64_t extent, int32_t orig
         }))
         return st;
     return pos_status("check_crd", f);
+}
+
+extern "C" int jlust_hip_narrow_index_i64(int64_t n, const int64_t *src, int32_t *dst, jlust_stream_t stream)
+{
+    clear_error();
+    if (n < 0) return fail(JLUST_STATUS_INVALID_ARGUMENT, "narrow_index: negative length");
+    if (n >= (int64_t)1 << 31)
+        return fail(JLUST_STATUS_UNSUPPORTED_INDEX_TYPE, "narrow_index: %lld entries exceed the Int32 index range",
+                    (long long)n);
+    if (bad_ptr(src, n) || bad_ptr(dst, n)) return fail(JLUST_STATUS_INVALID_ARGUMENT, "narrow_index: null device pointer");
+    if (int st = require_device(nullptr)) return st;
+    if (n == 0) return JLUST_STATUS_SUCCESS;
+    hipStream_t s = (hipStream_t)stream;
+    int32_t f = 0;
+    if (int st = run_checks(s, &f, [&](int32_t *flag) {
+            hipLaunchKernelGGL(narrow_index_kernel, dim3(xgrid(n)), dim3(XB), 0, s, n, src, dst, flag);
+            return check_launch("narrow_index_kernel");
+        }))
+        return st;
+    if (f & 32)
+        return fail(JLUST_STATUS_UNSUPPORTED_INDEX_TYPE, "narrow_index: an index is outside the Int32 range");
+    return JLUST_STATUS_SUCCESS;
 }
 
 extern "C" int jlust_hip_expand_pos_i32(int64_t nouter, int64_t nnz, int32_t origin, const int32_t *pos,

@@ -22,9 +22,10 @@ class UnsupportedFormat(JLUSTError):
 
 
 class UnsupportedIndexType(JLUSTError):
-    def __init__(self, T, backend):
+    def __init__(self, T, backend, detail=""):
         self.T, self.backend = T, backend
-        super().__init__(f"UnsupportedIndexType: {T} not supported by {backend}")
+        msg = f"UnsupportedIndexType: {T} not supported by {backend}"
+        super().__init__(msg + (f" ({detail})" if detail else ""))
 
 
 class UnsupportedValueType(JLUSTError):

@@ -90,6 +90,49 @@ def _check_index(u: USTensor, *bufs):
             raise NonCanonicalStorage(f"{u.format} index buffers must be contiguous")
 
 
+def _narrow_buffer(u: USTensor, b):
+    """An Int64 index buffer narrowed to Int32 on the device
+    (jlust_hip_narrow_index_i64), once per torch version of it: the copy is
+    kept on the buffer object, so it lives as long as the buffer does."""
+    if b is None or b.dtype != torch.int64:
+        return b
+    c = b.__dict__.get("_jlust_i32")
+    if c is not None and c[0] == b._version:
+        return c[1]
+    if not b.is_contiguous():
+        raise NonCanonicalStorage(f"{u.format} index buffers must be contiguous")
+    dev = _check_same_device(b)
+    out = torch.empty(b.shape, dtype=torch.int32, device=dev)
+    with _on(dev):
+        st = _lib.lib().jlust_hip_narrow_index_i64(b.numel(), _ptr(b), _ptr(out), _stream(dev))
+    _lib.check(st, "narrow_index", u.format, _BE, b.dtype)
+    b.__dict__["_jlust_i32"] = (b._version, out)
+    return out
+
+
+def _narrowed(u):
+    """u itself, or, when it holds Int64 index buffers, the same tensor over
+    their Int32 narrowing (the walker keeps the index type as stored,
+    ext/KernelAbstractionsExt/ops/_walker.jl:105-110; the kernels take
+    Int32).  The values are shared, so results written into them are the
+    caller's.  The wrapper is kept on u while its Int64 buffers are unchanged
+    (plans and checks cached on it keep applying); an index beyond Int32
+    raises UnsupportedIndexType."""
+    if not isinstance(u, USTensor):
+        return u
+    bufs = [b for b in (*u.pos_buffers, *u.crd_buffers) if b is not None and b.dtype == torch.int64]
+    if not bufs:
+        return u
+    key = tuple((id(b), b._version) for b in bufs) + (id(u.val),)
+    c = u.__dict__.get("_jlust_narrowed")
+    if c is not None and c[0] == key:
+        return c[1]
+    n = USTensor(u.extents, u.format, tuple(_narrow_buffer(u, b) for b in u.pos_buffers),
+                 tuple(_narrow_buffer(u, b) for b in u.crd_buffers), u.val, u.owner, u.origin)
+    u.__dict__["_jlust_narrowed"] = (key, n)
+    return n
+
+
 def _check_same_device(*ts):
     devs = {t.device for t in ts if t is not None}
     if len(devs) != 1:
@@ -164,6 +207,19 @@ def execute(op: Op, *ts, alpha=1.0, beta=0.0, input_fn=None, output_fn=None,
     from .elementwise import is_identity
     if not supports(op):
         raise UnsupportedFormat(op.formats, _BE)
+    nts = tuple(_narrowed(t) for t in ts)
+    if any(a is not b for a, b in zip(nts, ts)):
+        # Int64 index buffers: the product runs on their Int32 narrowing; an
+        # operand returned is the caller's own tensor.
+        r = execute(op, *nts, alpha=alpha, beta=beta, input_fn=input_fn, output_fn=output_fn,
+                    skip_empty_rows=skip_empty_rows, mask=_narrowed(mask))
+        for a, b in zip(nts, ts):
+            if r is a:
+                return b
+        return r
+    if mask is not None and _narrowed(mask) is not mask:
+        return execute(op, *ts, alpha=alpha, beta=beta, input_fn=input_fn, output_fn=output_fn,
+                       skip_empty_rows=skip_empty_rows, mask=_narrowed(mask))
     if op.tag == "SpMV":
         return spmv_with_fns(_spmv, *ts, alpha=alpha, beta=beta, input_fn=input_fn,
                              output_fn=output_fn)
@@ -753,6 +809,7 @@ def spmv_fast(u_A: USTensor, x: torch.Tensor, y: torch.Tensor, alpha, beta):
     attribute compares, the plan cache consulted directly.  Returns the
     output USTensor, or None when the call needs the general path (which then
     raises or handles what this one does not)."""
+    u_A = _narrowed(u_A)
     st = u_A.__dict__.get("_hip_spmv")
     if st is None or not st.matches(u_A):
         st = _spmv_fast_state(u_A)
@@ -1587,7 +1644,11 @@ class HIPSDDMMHandle(AbstractKernelHandle):
 def prepare(optype, u_A: USTensor, *more, **kw):
     """prepare(HIPBackend(), OpType, A; kw...) (src/ops.jl:163-177).  SpMV:
     input_fn/output_fn; SpMM: n_cols, skip_empty_rows; SDDMM: (A, B, C) as
-    the cuSPARSE handle takes them, or the mask C alone (n_inner = K)."""
+    the cuSPARSE handle takes them, or the mask C alone (n_inner = K).  A
+    sparse operand with Int64 index buffers is prepared over their Int32
+    narrowing as it is at this call."""
+    u_A = _narrowed(u_A)
+    more = tuple(_narrowed(t) for t in more)
     tag = getattr(optype, "tag", None)
     if tag == "SpMV":
         bad = set(kw) - {"input_fn", "output_fn"}

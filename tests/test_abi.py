@@ -76,7 +76,8 @@ def test_status_mapping_to_reference_exceptions():
     from jlust_amd import _lib
     for code, exc in ((1, J.IncompatibleExtents), (2, J.UnsupportedValueType),
                       (3, J.UnsupportedFormat), (4, J.NonCanonicalStorage),
-                      (5, J.IndexOriginMismatch), (7, J.NoDevice), (6, J.HIPError)):
+                      (5, J.IndexOriginMismatch), (7, J.NoDevice), (6, J.HIPError),
+                      (10, J.UnsupportedIndexType)):
         with pytest.raises(exc):
             _lib.check(code, "test")
     _lib.check(0, "ok")

@@ -187,10 +187,17 @@ def test_errors(J):
     with pytest.raises(J.UnsupportedFormat, match="belong to SpMV"):
         J.execute(J.SpMMOp, A, J.dense_matrix(3, 2, fill=1.0), J.dense_matrix(3, 2),
                   input_fn=lambda v: 2 * v)
+    # Int64 indices run on their Int32 narrowing (the golden answer); other
+    # index types are UnsupportedIndexType
     A64 = J.csr_tensor(dev(np.array(c["rowptr"], np.int64)), dev(np.array(c["colind"], np.int64)),
                        dev(np.array(c["val"])), (3, 3))
+    y64 = dev(np.zeros(3))
+    J.execute(J.SpMVOp, A64, dev(np.ones(3)), y64)
+    assert host(y64).tolist() == [3.0, 3.0, 9.0]
+    A16 = J.csr_tensor(dev(np.array(c["rowptr"], np.int16)), dev(np.array(c["colind"], np.int16)),
+                       dev(np.array(c["val"])), (3, 3))
     with pytest.raises(J.UnsupportedIndexType):
-        J.execute(J.SpMVOp, A64, dev(np.ones(3)), dev(np.zeros(3)))
+        J.execute(J.SpMVOp, A16, dev(np.ones(3)), dev(np.zeros(3)))
     Ah = J.csr_tensor(torch.tensor(c["rowptr"], dtype=torch.int32),
                       torch.tensor(c["colind"], dtype=torch.int32), torch.tensor(c["val"]), (3, 3))
     with pytest.raises(J.UnsupportedFormat):
