@@ -426,8 +426,14 @@ __global__ void bn_rtable_kernel(int64_t nrows, int32_t S, int32_t B, int64_t ch
 // so the workgroup writes the ranges of all S runs, each entry e taking
 // v[perm[e] - c0] from LDS; the outputs are the chunk's S ranges laid end to
 // end.  Indices are clamped into the chunk and the layout.
-constexpr int RF_THREADS = 512;           // refresh workgroup: two per CU
-constexpr int RF_LDS = 64 * 1024;         // values of a refresh chunk in LDS
+#ifndef JLUST_RF_THREADS
+#define JLUST_RF_THREADS 1024
+#endif
+#ifndef JLUST_RF_LDS_KB
+#define JLUST_RF_LDS_KB 64
+#endif
+constexpr int RF_THREADS = JLUST_RF_THREADS;        // refresh workgroup (two per CU)
+constexpr int RF_LDS = JLUST_RF_LDS_KB * 1024;      // values of a refresh chunk in LDS
 constexpr int RF_SPT = (BN_SMAX + RF_THREADS - 1) / RF_THREADS;   // runs per thread in the scan
 
 template <typename T>
