@@ -85,6 +85,9 @@ def parse():
     p.add_argument("--plan-build", action="store_true",
                    help="config 2's SpMV plan built six times: wall time per build, the first "
                         "included, after jlust_amd.preload()")
+    p.add_argument("--bsr-long-rows", action="store_true",
+                   help="config 5's band at a quarter of its block-rows with 8, 9, 12 and 16 blocks a "
+                        "row: the fp32 strip kernels against the CSR expansion path")
     p.add_argument("--bsr-spmv", action="store_true",
                    help="16 x 16 BSR SpMV over power-law block-rows: the segmented kernel, the "
                         "one-thread-per-row kernel and the CSR expansion route")
@@ -617,6 +620,59 @@ def plan_build():
          "steady_ms": sorted(builds[1:])[len(builds[1:]) // 2]}
     log(f"plan build: {r}")
     return r
+
+
+def bsr_long_rows():
+    """16 x 16 fp32 BSR SpMM (k = 256) on config 5's +-32 band at a quarter of
+    its block-rows (16,384) with 8, 9, 12 and 16 blocks a row: up to 8 the
+    windowed strip kernels hold a row's A operands in registers; a strip with a
+    longer row takes the direct operand loads.  Beside it the same product
+    through the device CSR expansion and the CSR SpMM.  HIP events: the median
+    of 5 runs of 5 calls after 2 warm-up calls (the expansion path: one run of
+    3 calls)."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd import workloads as W
+    from jlust_amd.hip_backend import _bsr_as_csr
+    stream = torch.cuda.current_stream()
+
+    def ms(fn, reps=5, trials=5):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(trials):
+            s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            for _ in range(reps):
+                fn()
+            e.record(stream)
+            torch.cuda.synchronize()
+            ts.append(s.elapsed_time(e) / reps)
+        return sorted(ts)[len(ts) // 2]
+
+    out = []
+    mb = nb = 16384
+    k = 256
+    for per_row in (8, 9, 12, 16):
+        browptr = W.rowptr_from_lengths(np.full(mb, per_row, dtype=np.int64), origin=1)
+        bcolind = W.columns(browptr, mb, 7, band=32)
+        val = np.random.default_rng(1).standard_normal(bcolind.size * 256).astype(np.float32)
+        A = J.bsr_tensor(dev(browptr), dev(bcolind), dev(val), (mb * 16, nb * 16))
+        B = dev(np.asfortranarray(np.random.default_rng(2).standard_normal((nb * 16, k)).astype(np.float32)))
+        C = J.dense_matrix(mb * 16, k, dtype=torch.float32)
+        flops = 2.0 * 256 * k * bcolind.size
+        t = ms(lambda: J.execute(J.SpMMOp, A, B, C))
+        Ac = _bsr_as_csr(A)
+        Cc = J.dense_matrix(mb * 16, k, dtype=torch.float32)
+        tc = ms(lambda: J.execute(J.SpMMOp, Ac, B, Cc), reps=3, trials=1)
+        r = {"blocks_per_row": per_row, "bsr_ms": round(t, 4), "bsr_TFLOPs": round(flops / t / 1e9, 2),
+             "csr_expansion_spmm_ms": round(tc, 3)}
+        log(f"bsr long rows: {r}")
+        out.append(r)
+        del A, B, C, Ac, Cc
+        torch.cuda.empty_cache()
+    return out
 
 
 def bsr_spmv_powerlaw():
@@ -1563,6 +1619,9 @@ def main():
         return
     if args.bsr_spmv:
         print(json.dumps({"bsr_spmv": bsr_spmv_powerlaw()}), flush=True)
+        return
+    if args.bsr_long_rows:
+        print(json.dumps({"bsr_long_rows": bsr_long_rows()}), flush=True)
         return
     if args.plan_build:
         print(json.dumps({"plan_build": plan_build()}), flush=True)
