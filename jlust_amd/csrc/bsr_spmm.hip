@@ -910,6 +910,385 @@ void bsr16_spmm_wide_strip_kernel(
     __builtin_amdgcn_s_waitcnt(0);
 }
 
+// Long-row kernel: the 24-row kernel above, and strips whose rows hold 9 to
+// 16 blocks.  Such a strip runs as two halves of 12 rows, one row a wave,
+// the row's blocks in two groups of up to 8 that take the register slots of
+// the 24-row kernel's two rows (a0: blocks 0..7, a1: 8..15); the copies,
+// operand reads and MFMAs are the same, and a tile's C is the two groups'
+// sums.  Each half is set up at its start.  Strips of rows of at most 8
+// blocks run as in the 24-row kernel.  Taken when the rows hold more than 8
+// blocks on average; a function of its own because the extra state, as a
+// branch of the 24-row kernel, changed that kernel's register assignment and
+// cost its 8-block strips about 3 %.
+template <bool BZ>
+__global__ __launch_bounds__(64 * BSRW_WAVES) __attribute__((amdgpu_waves_per_eu(3)))
+void bsr16_spmm_wide_long_kernel(
+    int64_t mb, int32_t origin, const int32_t *__restrict__ browptr,
+    const int32_t *__restrict__ bcolind, const float *__restrict__ val, int64_t k, float alpha,
+    const float *__restrict__ B, int64_t ldb, float beta, float *__restrict__ C, int64_t ldc)
+{
+    __shared__ __align__(16) char win[BSRW_BUF];
+    __shared__ int32_t s_jmin[2][BSRW_WAVES], s_jmax[2][BSRW_WAVES], s_len[2][BSRW_WAVES];
+    const int nstrips = (int)((mb + BSRW_SR - 1) / BSRW_SR);
+    const int G = (int)gridDim.x / NUM_XCD;
+    const int xcd = (int)blockIdx.x % NUM_XCD;
+    const int wl = (int)blockIdx.x / NUM_XCD;
+    const int lo = (int)((int64_t)xcd * nstrips / NUM_XCD), hi = (int)((int64_t)(xcd + 1) * nstrips / NUM_XCD);
+    if (hi <= lo) return;                  // whole workgroup
+    const int kk = (int)k;                 // k < 2^31 - 16 (checked by the host)
+    const int ntiles = (kk + 15) / 16;
+    const int rounds = (hi - lo + G - 1) / G;
+    const int rlast = hi - lo - (rounds - 1) * G;          // strips in the last round, 1..G
+    const int fsplit = min(2 * rlast <= G ? G / rlast : 1, ntiles);
+    // Work unit it of this workgroup: strip s, tiles [t0, t1).
+    auto unit = [&](int it, int &s, int &t0, int &t1) -> bool {
+        if (it < rounds - 1) {
+            s = lo + wl + it * G;
+            t0 = 0;
+            t1 = ntiles;
+            return true;
+        }
+        if (it > rounds - 1 || wl >= rlast * fsplit) return false;
+        s = lo + (rounds - 1) * G + wl / fsplit;
+        const int c = wl % fsplit;
+        t0 = c * ntiles / fsplit;
+        t1 = (c + 1) * ntiles / fsplit;
+        return true;
+    };
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 15;               // MFMA: A row / B, C column in the tile
+    const int g = lane >> 4;               // MFMA: contraction group / C row group
+    const floatx4 zero = {0.f, 0.f, 0.f, 0.f};
+    const uint32_t col_off = (uint32_t)(i * BSRW_CS + 16 * g);
+    const int lane16 = lane * 16;
+    const int c_lane = (4 * g + i * (int)ldc) * 4;
+    const int32x4 rs_c = buffer_resource(C);
+    // Window copies: a tile's window is 16 columns x 6 parts of 1024 bytes
+    // (nwin <= 88 block-rows, 5,632 bytes a column), 96 instructions, 8 per
+    // wave: wave w moves part w % 6 of columns 2t + w / 6, t = 0..7.  Lanes
+    // past the window's end are masked off, and a part wholly past it, or a
+    // column past k, is skipped.
+    static_assert(16 * 6 == 8 * BSRW_WAVES && BSRW_WMAX * 64 <= 6 * 1024, "wide strip copy split");
+    const int cpar = wave / 6, cpart = wave % 6;
+    const uint32_t lds_base = (uint32_t)(cpar * BSRW_CS + cpart * 1024);
+    const int g_base = (int)((cpart * 256 + cpar * ldb) * 4);   // bytes, wave-uniform
+    auto barrier = [] { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); };
+    // The zero row of each window column, in the column's pad, which no copy
+    // writes (the first unit's set-up barriers precede every read).
+    if (threadIdx.x < 64)
+        *reinterpret_cast<floatx4 *>(win + (threadIdx.x >> 2) * BSRW_CS + BSRW_ZROW * 64 + (threadIdx.x & 3) * 16) = zero;
+
+    // ---- the strip being computed.  In long mode (longm; rows of 9 to 16
+    // blocks) a wave owns one row, its blocks in two groups of up to 8 (a0:
+    // blocks 0..7, a1: 8..15), and the 24 rows run as two halves of 12.
+    bool live0 = false, live1 = false, windowed = false, cvalid = false, lane_ok = false, longm = false;
+    int Ra = 0, nq0 = 0, nq1 = 0, lmaxs = 0;
+    int64_t qa = 0, qb = 0;
+    int32x4 rs_b = buffer_resource(B);
+    uint32_t jp[4] = {0u, 0u, 0u, 0u};     // window rows of the blocks, 8 bits each
+    // ---- set-up of a strip in five steps: 1-4 write the *n variables (the
+    // strip being set up), 5 adopts them.
+    int Ran = 0;
+    bool live0n = false, live1n = false, windowedn = false, cvalidn = false, lane_okn = false, longn = false;
+    int32_t pa = 0, pb = 0, pc = 0, bcoln = 0, jw0n = 0;
+    int qan = 0, qbn = 0, nq0n = 0, nq1n = 0, lmaxn = 0;
+    uint32_t jpn[4] = {0u, 0u, 0u, 0u};
+    // 1: the rows' block ranges (long mode: half h's row of this wave).
+    auto setup1 = [&](int sn, int h, bool lg) {
+        longn = lg;
+        Ran = sn * BSRW_SR + (lg ? BSRW_WAVES * h + wave : 2 * wave);
+        live0n = Ran < mb;
+        live1n = lg ? live0n : Ran + 1 < mb;
+        pa = live0n ? browptr[Ran] : 0;
+        pb = live0n ? browptr[Ran + 1] : 0;
+        pc = !lg && live1n ? browptr[Ran + 2] : pb;
+    };
+    // 2: the two block groups' ranges [qan, qbn) and [qbn, qcn) -- the two
+    // rows, or a long row's first 8 blocks and the rest -- and their block
+    // columns, one per lane, when both groups are short enough to be held as
+    // operands.
+    auto setup2 = [&]() {
+        qan = __builtin_amdgcn_readfirstlane(pa) - origin;
+        const int q1 = __builtin_amdgcn_readfirstlane(pb) - origin;
+        const int qcn = longn ? q1 : __builtin_amdgcn_readfirstlane(pc) - origin;
+        qbn = longn ? min(qan + BSR_QCHUNK, q1) : q1;
+        nq0n = qbn - qan;
+        nq1n = qcn - qbn;
+        bcoln = 0;
+        if (nq0n <= BSR_QCHUNK && nq1n <= BSR_QCHUNK && lane < qcn - qan) bcoln = bcolind[qan + lane] - origin;
+    };
+    // 3: per wave the rows' column range and longer length.
+    auto setup3 = [&](int par) {
+        const bool has = nq0n <= BSR_QCHUNK && nq1n <= BSR_QCHUNK && lane < nq0n + nq1n;
+        int32_t jmin = has ? bcoln : INT32_MAX, jmax = has ? bcoln : INT32_MIN;
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {    // the columns sit in lanes 0..15
+            jmin = min(jmin, __shfl_xor(jmin, off, 64));
+            jmax = max(jmax, __shfl_xor(jmax, off, 64));
+        }
+        if (lane == 0) {
+            s_jmin[par][wave] = jmin;
+            s_jmax[par][wave] = jmax;
+            s_len[par][wave] = max(nq0n, nq1n);
+        }
+    };
+    // 4 (after a barrier): the strip's window, the blocks' window rows and
+    // this wave's copy masks.
+    auto setup4 = [&](int par) {
+        int32_t jw0 = INT32_MAX, jw1 = INT32_MIN, lmax = 0;
+        if (lane < BSRW_WAVES) {
+            jw0 = s_jmin[par][lane];
+            jw1 = s_jmax[par][lane];
+            lmax = s_len[par][lane];
+        }
+#pragma unroll
+        for (int off = 8; off > 0; off >>= 1) {
+            jw0 = min(jw0, __shfl_xor(jw0, off, 64));
+            jw1 = max(jw1, __shfl_xor(jw1, off, 64));
+            lmax = max(lmax, __shfl_xor(lmax, off, 64));
+        }
+        jw0 = __builtin_amdgcn_readfirstlane(jw0);
+        jw1 = __builtin_amdgcn_readfirstlane(jw1);
+        lmax = __builtin_amdgcn_readfirstlane(lmax);
+        lmaxn = lmax;
+        const int32_t nwin = jw1 >= jw0 ? jw1 - jw0 + 1 : 0;
+        jw0n = nwin > 0 ? jw0 : 0;
+        windowedn = lmax <= BSR_QCHUNK && nwin <= BSRW_WMAX;
+        const int wfloats = nwin * 16;
+        cvalidn = cpart * 256 < wfloats;
+        lane_okn = cpart * 256 + 4 * lane < wfloats;
+        // A block a row does not have reads the zero row (its A operand is
+        // zero too), so every wave runs all 16 blocks' MFMAs unguarded.
+#pragma unroll
+        for (int x = 0; x < 4; ++x) jpn[x] = BSRW_ZROW * 0x01010101u;
+        if (windowedn) {
+#pragma unroll
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+                const uint32_t sh = 8 * (qq & 3);
+                if (qq < nq0n)
+                    jpn[qq >> 2] ^= ((uint32_t)(__builtin_amdgcn_readlane(bcoln, qq) - jw0n) ^ BSRW_ZROW) << sh;
+                if (qq < nq1n)
+                    jpn[2 + (qq >> 2)] ^= ((uint32_t)(__builtin_amdgcn_readlane(bcoln, nq0n + qq) - jw0n) ^ BSRW_ZROW) << sh;
+            }
+        }
+    };
+    // 5: adopt the strip set up.
+    auto setup5 = [&]() {
+        longm = longn;
+        lmaxs = lmaxn;
+        Ra = Ran;
+        live0 = live0n;
+        live1 = live1n;
+        qa = qan;
+        qb = qbn;
+        nq0 = live0n ? nq0n : 0;
+        nq1 = live1n ? nq1n : 0;
+        windowed = windowedn;
+        cvalid = cvalidn;
+        lane_ok = lane_okn;
+        rs_b = buffer_resource(B + (int64_t)jw0n * BSR_BS);
+#pragma unroll
+        for (int x = 0; x < 4; ++x) jp[x] = jpn[x];
+    };
+    auto load_a0 = [&](floatx4 &dst, int qq) {
+        dst = live0n && qq < nq0n ? *reinterpret_cast<const floatx4 *>(val + ((int64_t)qan + qq) * 256 + i * 16 + 4 * g) : zero;
+    };
+    auto load_a1 = [&](floatx4 &dst, int qq) {
+        dst = live1n && qq < nq1n ? *reinterpret_cast<const floatx4 *>(val + ((int64_t)qbn + qq) * 256 + i * 16 + 4 * g) : zero;
+    };
+    // Copy t (0..7) of this wave for the tile at column c0 of a window at rs.
+    auto copy_t = [&](int32x4 rs, bool cv, bool lok, int c0, int t) {
+        if (!cv || c0 + 2 * t + cpar >= kk) return;
+        const int so = g_base + (int)((int64_t)(c0 + 2 * t) * ldb * 4);
+        if (lok) raw_buffer_load_lds(rs, (lds_void *)(win + lds_base + t * 2 * BSRW_CS), 16, lane16, so, 0, 0);
+    };
+
+    floatx4 a0[BSR_QCHUNK], a1[BSR_QCHUNK];
+#pragma unroll
+    for (int qq = 0; qq < BSR_QCHUNK; ++qq) a0[qq] = a1[qq] = zero;
+    // ready: steps 1-4, the A operand loads and the first window's copies of
+    // strip s were done during the previous unit's tiles.
+    bool ready = false;
+    int par = 0;
+    int s = 0, t0 = 0, t1 = 0, sn = 0, t0n = 0, t1n = 0;
+    bool has = unit(0, s, t0, t1), hasn = false;
+    for (int it = 0; has; ++it, par ^= 1, has = hasn, s = sn, t0 = t0n, t1 = t1n) {
+        hasn = unit(it + 1, sn, t0n, t1n);
+        // Steps 1-4 of strip sn run during this unit's tiles if it has four
+        // and its strip is windowed (the direct loads and long mode run no
+        // set-up stage; a unit they take leaves ready false).
+        const bool pre = hasn && t1 - t0 >= 4;
+        if (!ready) {
+            setup1(s, 0, false);
+            setup2();
+            setup3(par);
+            barrier();
+            setup4(par);
+            if (windowedn) {
+#pragma unroll
+                for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+                    load_a0(a0[qq], qq);
+                    load_a1(a1[qq], qq);
+                }
+                const int32x4 rsn = buffer_resource(B + (int64_t)jw0n * BSR_BS);
+#pragma unroll
+                for (int t = 0; t < 8; ++t) copy_t(rsn, cvalidn, lane_okn, t0 * 16, t);
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            asm volatile("s_barrier" ::: "memory");
+        }
+        setup5();
+        ready = false;
+
+        // Direct operand loads (any row length, any window), row by row.
+        auto direct = [&]() {
+            for (int r = 0; r < (longm ? 1 : 2); ++r) {
+                if (!(r ? live1 : live0)) break;
+                const int64_t q0 = r ? qb : qa, q1 = longm || r ? qb + nq1 : qa + nq0;
+                const int64_t crow = (int64_t)(Ra + r) * BSR_BS + 4 * g;
+                for (int64_t c0 = (int64_t)t0 * 16; c0 < k && c0 < (int64_t)t1 * 16; c0 += 16) {
+                    const int64_t colc = c0 + i < k ? c0 + i : k - 1;
+                    floatx4 acc = zero;
+                    for (int64_t q = q0; q < q1; ++q) {
+                        const floatx4 a = *reinterpret_cast<const floatx4 *>(val + q * 256 + i * 16 + 4 * g);
+                        const int64_t brow = ((int64_t)bcolind[q] - origin) * BSR_BS + 4 * g;
+                        const floatx4 b = *reinterpret_cast<const floatx4 *>(B + brow + colc * ldb);
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u], b[u], acc, 0, 0, 0);
+                    }
+                    if (c0 + i < k) {
+                        floatx4 *dst = reinterpret_cast<floatx4 *>(C + crow + (c0 + i) * ldc);
+                        floatx4 out = alpha * acc;
+                        if (!BZ) out += beta * *dst;
+                        *dst = out;
+                    }
+                }
+            }
+            __builtin_amdgcn_s_waitcnt(0);
+            asm volatile("s_barrier" ::: "memory");   // every wave is past step 5
+        };
+
+        // One tile; the unit's last tile is a separate instance, the only one
+        // that loads A operands, so that the compiler sees none in flight in
+        // the other tiles and adds no wait before their MFMAs: the C stores of
+        // a tile stay in flight into the next.
+        auto tile = [&](int t, auto last_tag) {
+            constexpr bool last = decltype(last_tag)::value;
+            const int c0 = t * 16;
+            floatx4 b0[BSR_QCHUNK], b1[BSR_QCHUNK];
+            uint32_t co = col_off, j0 = jp[0], j1 = jp[1], j2 = jp[2], j3 = jp[3];
+            asm volatile("" : "+v"(co), "+s"(j0), "+s"(j1), "+s"(j2), "+s"(j3));
+#pragma unroll
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+                const uint32_t r0 = ((qq < 4 ? j0 : j1) >> (8 * (qq & 3))) & 0xffu;
+                const uint32_t r1 = ((qq < 4 ? j2 : j3) >> (8 * (qq & 3))) & 0xffu;
+                b0[qq] = *reinterpret_cast<const floatx4 *>(win + co + r0 * 64);
+                b1[qq] = *reinterpret_cast<const floatx4 *>(win + co + r1 * 64);
+            }
+            barrier();                     // the window is free
+            if (pre && t == t1 - 4) setup1(sn, 0, false);
+            if (pre && t == t1 - 3) setup2();
+            if (last && pre) setup4(par ^ 1);
+            asm volatile("" ::: "memory");
+            // The copies of the next tile of this strip or, in the last tile,
+            // of the next strip's first tile; and in the last tile the next
+            // strip's A operands, each after its block's MFMAs.
+            const bool nxt = last && pre && windowedn;
+            const bool cv = last ? nxt && cvalidn : cvalid;
+            const bool lok = last ? lane_okn : lane_ok;
+            const int32x4 rsn = last ? buffer_resource(B + (int64_t)jw0n * BSR_BS) : rs_b;
+            const int cn = last ? t0n * 16 : c0 + 16;
+            floatx4 acc0 = zero, acc1 = zero;
+#pragma unroll
+            for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+#pragma unroll
+                for (int cc = 0; cc < BSRW_CPQ; ++cc) {
+                    const int tt = qq * BSRW_CPQ + cc;
+                    if (tt < 8) copy_t(rsn, cv, lok, cn, tt);
+                }
+                asm volatile("" ::: "memory");
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a0[qq][u], b0[qq][u], acc0, 0, 0, 0);
+                if (last && nxt) load_a0(a0[qq], qq);
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a1[qq][u], b1[qq][u], acc1, 0, 0, 0);
+                if (last && nxt) load_a1(a1[qq], qq);
+            }
+            asm volatile("" ::: "memory");
+            if (longm) {
+                // One row: its two block groups' sums.
+                if (c0 + i < kk && live0) {
+                    const int so_c = (int)(((int64_t)Ra * BSR_BS + (int64_t)c0 * ldc) * 4);
+                    floatx4 out = alpha * (acc0 + acc1);
+                    if (!BZ) out += beta * raw_buffer_load_v4f32(rs_c, c_lane, so_c, 0);
+                    raw_buffer_store_v4f32(out, rs_c, c_lane, so_c, 0);
+                }
+            } else if (c0 + i < kk) {
+                if (live0) {
+                    const int so_c = (int)(((int64_t)Ra * BSR_BS + (int64_t)c0 * ldc) * 4);
+                    floatx4 out = alpha * acc0;
+                    if (!BZ) out += beta * raw_buffer_load_v4f32(rs_c, c_lane, so_c, 0);
+                    raw_buffer_store_v4f32(out, rs_c, c_lane, so_c, 0);
+                }
+                if (live1) {
+                    const int so_c = (int)(((int64_t)Ra * BSR_BS + BSR_BS + (int64_t)c0 * ldc) * 4);
+                    floatx4 out = alpha * acc1;
+                    if (!BZ) out += beta * raw_buffer_load_v4f32(rs_c, c_lane, so_c, 0);
+                    raw_buffer_store_v4f32(out, rs_c, c_lane, so_c, 0);
+                }
+            }
+            if (pre && t == t1 - 2) setup3(par ^ 1);
+            // Every copy (and A load) landed; the C stores of a tile before
+            // the last may be in flight.
+            if (last) __builtin_amdgcn_s_waitcnt(0);
+            else if (live1 && !longm) __builtin_amdgcn_s_waitcnt(0x0002);   // vmcnt(2)
+            else if (live0) __builtin_amdgcn_s_waitcnt(0x0001);             // vmcnt(1)
+            else __builtin_amdgcn_s_waitcnt(0);
+            asm volatile("s_barrier" ::: "memory");
+        };
+        // Rows of 9 to 16 blocks: the strip as two halves of 12 rows, one
+        // row a wave, each set up at its start; otherwise one pass over
+        // the strip set up above.  (One call site of the tile code: two
+        // would double its register pressure.)
+        const bool first_windowed = windowed;
+        const bool lng = !windowed && lmaxs > BSR_QCHUNK && lmaxs <= 2 * BSR_QCHUNK;
+        for (int h = 0; h < (lng ? 2 : 1); ++h) {
+            if (lng) {
+                setup1(s, h, true);
+                setup2();
+                setup3(par);
+                barrier();
+                setup4(par);
+                if (windowedn) {
+#pragma unroll
+                    for (int qq = 0; qq < BSR_QCHUNK; ++qq) {
+                        load_a0(a0[qq], qq);
+                        load_a1(a1[qq], qq);
+                    }
+                    const int32x4 rsn = buffer_resource(B + (int64_t)jw0n * BSR_BS);
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) copy_t(rsn, cvalidn, lane_okn, t0 * 16, t);
+                }
+                __builtin_amdgcn_s_waitcnt(0);
+                asm volatile("s_barrier" ::: "memory");
+                setup5();
+            }
+            if (windowed) {
+                for (int t = t0; t < t1 - 1; ++t) tile(t, std::false_type{});
+                tile(t1 - 1, std::true_type{});
+            } else {
+                direct();
+            }
+        }
+        if (!first_windowed) continue;     // no next-strip set-up ran
+        ready = pre;
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+}
+
 // Float64 strip kernel (row-major blocks; values, B and C 32-byte aligned,
 // ldb and ldc multiples of 4; 16 columns of B or C span less than 2^31 bytes).
 // The fp32 strip kernel's design on v_mfma_f64_16x16x4_f64: a workgroup of
@@ -1869,13 +2248,23 @@ int bsr_spmm(int64_t mb, int64_t nb, int64_t bs, int64_t nnzb, int32_t origin,
         const int64_t strips = (mb + BSRW_SR - 1) / BSRW_SR;
         const int64_t per_xcd = std::max<int64_t>(1, device_info(dev).cu_count / NUM_XCD);
         const int64_t grids = std::min((strips + NUM_XCD - 1) / NUM_XCD, per_xcd) * NUM_XCD;
-        if (beta == 0.f)
-            hipLaunchKernelGGL((bsr16_spmm_wide_strip_kernel<true>), dim3((unsigned)grids), dim3(64 * BSRW_WAVES),
-                               0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
-        else
-            hipLaunchKernelGGL((bsr16_spmm_wide_strip_kernel<false>), dim3((unsigned)grids), dim3(64 * BSRW_WAVES),
-                               0, s, mb, origin, browptr, bcolind, val, k, alpha, B, ldb, beta, C, ldc);
-        return check_launch("bsr16_spmm_wide_strip_kernel");
+        // Rows of more than 8 blocks on average: the long-row kernel, which
+        // also runs strips of 9 to 16 blocks a row in registers (two halves
+        // of 12 rows); the 24-row kernel leaves such strips to the direct
+        // operand loads.
+#define JLUST_BSRW_LAUNCH(KERNEL)                                                                        \
+        hipLaunchKernelGGL(KERNEL, dim3((unsigned)grids), dim3(64 * BSRW_WAVES), 0, s, mb, origin, browptr, \
+                           bcolind, val, k, alpha, B, ldb, beta, C, ldc)
+        const bool lg = nnzb > (int64_t)BSR_QCHUNK * mb;
+        if (beta == 0.f) {
+            if (lg) JLUST_BSRW_LAUNCH(bsr16_spmm_wide_long_kernel<true>);
+            else JLUST_BSRW_LAUNCH(bsr16_spmm_wide_strip_kernel<true>);
+        } else {
+            if (lg) JLUST_BSRW_LAUNCH(bsr16_spmm_wide_long_kernel<false>);
+            else JLUST_BSRW_LAUNCH(bsr16_spmm_wide_strip_kernel<false>);
+        }
+#undef JLUST_BSRW_LAUNCH
+        return check_launch(lg ? "bsr16_spmm_wide_long_kernel" : "bsr16_spmm_wide_strip_kernel");
     }
     if (rm && vec && offsets_fit && bsr_strip()) {
         const int64_t strips = (mb + BSR_SR - 1) / BSR_SR;

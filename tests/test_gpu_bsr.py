@@ -600,3 +600,42 @@ def test_bsr_spmv_plan(J, O, b1, b2, dtype, row_major):
     h.u_A.crd_buffers[1][0] = nb + origin                # past the last block column
     with pytest.raises(J.NonCanonicalStorage):
         J.execute(h, dev(x), y)
+
+
+@pytest.mark.parametrize("k,beta", [(40, 0.0), (100, -0.5), (256, 1.0)])
+def test_bsr_long_rows_two_halves(J, O, k, beta):
+    """Rows of 9 to 16 blocks, more than 8 on average (the long-row kernel:
+    a strip as two halves of 12 rows, a row's blocks in two groups of 8):
+    mixed with strips of 8-block rows, rows of 17 to 20 blocks (direct
+    operand loads), empty rows, a window wider than 88 block-rows in one
+    half, and a partial last strip; every output against the oracle."""
+    mb = nb = 2000
+    rng = np.random.default_rng(k + 5)
+    bcols = []
+    for R in range(mb):
+        s = R // 24
+        lo, hi = max(0, R - 32), min(nb, R + 33)
+        if s % 7 == 3:
+            n = 8
+        elif s % 11 == 6 and R % 5 == 0:
+            n = int(rng.integers(17, 21))
+        elif s % 13 == 2 and R % 24 == 14:               # second half: a block far away
+            c = np.r_[rng.choice(np.arange(lo, hi), 10, replace=False), (R + 500) % nb]
+            bcols.append(np.sort(np.unique(c)))
+            continue
+        elif R % 17 == 0:
+            n = 0
+        else:
+            n = int(rng.integers(9, 17))
+        bcols.append(np.sort(rng.choice(np.arange(lo, hi), min(n, hi - lo), replace=False)))
+    browptr = (np.r_[0, np.cumsum([c.size for c in bcols])] + 1).astype(np.int32)
+    bcolind = (np.concatenate(bcols) + 1).astype(np.int32)
+    assert bcolind.size > 8 * mb
+    val = rng.standard_normal(bcolind.size * 256).astype(np.float32)
+    B = np.asfortranarray(rng.standard_normal((nb * 16, k)).astype(np.float32))
+    C0 = np.asfortranarray(rng.standard_normal((mb * 16, k)).astype(np.float32)) if beta else None
+    C = run_bsr(J, browptr, bcolind, val, B, mb, nb, alpha=0.75, beta=beta, C0=C0)
+    ref = O.bsr_spmm(browptr, bcolind, val, 16, B, 0.75, beta, C0)
+    rp, ci, v = O.bsr_to_csr(browptr, bcolind, val, 16)
+    absref = O.csr_spmm_absref(rp, ci, v, B, 0.75, beta, C0)
+    assert_within(C, ref, absref, np.float32, f"long rows k={k} beta={beta}")
