@@ -1355,10 +1355,10 @@ def plain_call_timings(cfg, steps, warmup):
 
 def emitter_handle_timing(cfg, keep, steps, warmup):
     """The emitter-form handle call execute(h, A, x, y) as a binding without
-    torch's version counters makes it (the Julia ccall of INTEGRATION.md):
-    every call re-reads A's values into the plan -- a gather through the
-    plan's permutation for the copying layouts, a pointer for the others --
-    then runs the product (jlust_hip_csr_spmv_plan_execute_values_*)."""
+    torch's version counters makes it (a Julia ccall binding): every call
+    re-reads A's values into the plan -- a refresh of the copy for the
+    copying layouts, a pointer for the others -- then runs the product
+    (jlust_hip_csr_spmv_plan_execute_values_*)."""
     import torch
     from jlust_amd import _lib
     from jlust_amd import workloads as W
@@ -1378,8 +1378,9 @@ def emitter_handle_timing(cfg, keep, steps, warmup):
     nbytes = W.algorithmic_bytes(cfg)
     return {"value": round(nbytes / (e_ms * 1e-3) / 1e9, 3), "ms_per_step": round(e_ms, 6),
             "per_launch_ms": round(e_launch, 6), "kernel": h.kernel(),
-            "refresh": "values re-read on every call (a gather through the plan's permutation for "
-                       "the binned and sliced layouts; nothing to copy for merge and vector plans)"}
+            "refresh": "values re-read on every call (the binned layout: CSR values in LDS chunks "
+                       "written out by run; the sliced layout: a gather through the plan's "
+                       "permutation; nothing to copy for merge and vector plans)"}
 
 
 def timed(step, steps, warmup):

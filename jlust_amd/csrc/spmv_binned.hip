@@ -419,13 +419,28 @@ __global__ void bn_rtable_kernel(int64_t nrows, int32_t S, int32_t B, int64_t ch
     rtab[t] = (int32_t)a;
 }
 
+// loff[e]: the offset of sorted entry e's CSR entry perm[e] within its
+// bin's refresh chunk, (perm[e] - bst[b]) mod chunk, b = the bin of its key.
+__global__ void bn_loff_kernel(int64_t nnz, int32_t B, int32_t chunk, const uint32_t *__restrict__ skey,
+                               const int32_t *__restrict__ bst, const int32_t *__restrict__ perm,
+                               uint16_t *__restrict__ loff)
+{
+    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= nnz) return;
+    const int64_t d = (int64_t)perm[e] - bst[skey[e] % (uint32_t)B];
+    loff[e] = (uint16_t)(d < 0 ? 0 : d % chunk);
+}
+
 // New values into the layout by chunks: workgroup g holds chunk k of bin b,
 // CSR entries [c0, c1) = [bst[b] + k L, min(bst[b] + (k+1) L, bst[b+1])), in
 // LDS (L = RF_LDS / sizeof(T)), read once and coalesced; every run (c, b)
 // holds those entries as one contiguous range [rtab[row][c], rtab[row+1][c]),
 // so the workgroup writes the ranges of all S runs, each entry e taking
-// v[perm[e] - c0] from LDS; the outputs are the chunk's S ranges laid end to
-// end.  Indices are clamped into the chunk and the layout.
+// v[loff[e]] from LDS; the outputs are the chunk's S ranges laid end to end.
+// Indices are clamped into the chunk and the layout.  The chunks are dealt
+// to the XCDs in contiguous ranges (workgroup g, on XCD g % 8, takes chunk
+// (g % 8) * per + g / 8): a bin's neighbouring chunks then write the two ends
+// of their shared output lines into one L2, which writes each line back once.
 #ifndef JLUST_RF_THREADS
 #define JLUST_RF_THREADS 1024
 #endif
@@ -435,14 +450,16 @@ __global__ void bn_rtable_kernel(int64_t nrows, int32_t S, int32_t B, int64_t ch
 constexpr int RF_THREADS = JLUST_RF_THREADS;        // refresh workgroup (two per CU)
 constexpr int RF_LDS = JLUST_RF_LDS_KB * 1024;      // values of a refresh chunk in LDS
 constexpr int RF_SPT = (BN_SMAX + RF_THREADS - 1) / RF_THREADS;   // runs per thread in the scan
+static_assert(RF_LDS / sizeof(float) <= 65536, "a refresh chunk's offsets must fit 16 bits (loff)");
 
 template <typename T>
 __global__ __launch_bounds__(RF_THREADS) void bn_refresh_lds_kernel(int64_t nnz, int32_t S, int32_t B,
+                                                                    int32_t nrch,
                                                                     const int32_t *__restrict__ rch,
                                                                     const int32_t *__restrict__ bst,
                                                                     const int32_t *__restrict__ rtb,
                                                                     const int32_t *__restrict__ rtab,
-                                                                    const int32_t *__restrict__ perm,
+                                                                    const uint16_t *__restrict__ loff,
                                                                     const T *__restrict__ src,
                                                                     T *__restrict__ dst)
 {
@@ -451,7 +468,10 @@ __global__ __launch_bounds__(RF_THREADS) void bn_refresh_lds_kernel(int64_t nnz,
     __shared__ T v[L];
     __shared__ int32_t pre[BN_SMAX + 1], beg[BN_SMAX], tsum[RF_THREADS];
     const int t = threadIdx.x;
-    const int64_t b = rch[2 * blockIdx.x], k = rch[2 * blockIdx.x + 1];
+    const int per = (nrch + NUM_XCD - 1) / NUM_XCD;
+    const int g = (int)(blockIdx.x % NUM_XCD) * per + (int)(blockIdx.x / NUM_XCD);
+    if (g >= nrch) return;                // whole workgroup
+    const int64_t b = rch[2 * g], k = rch[2 * g + 1];
     const int64_t lo = bst[b], hi = bst[b + 1];
     const int64_t c0 = min(lo + k * L, hi), c1 = min(c0 + L, hi);
     const int nv = (int)(c1 - c0);
@@ -515,7 +535,7 @@ __global__ __launch_bounds__(RF_THREADS) void bn_refresh_lds_kernel(int64_t nnz,
     // lane l takes every 64th of them from l, so a wave's step covers 64
     // consecutive outputs (consecutive entries of one or two runs); a lane
     // finds its first run by binary search and later ones by stepping
-    // forward.  All the permutation loads are issued before the LDS reads and
+    // forward.  All the offset loads are issued before the LDS reads and
     // stores.
     const int32_t total = min(pre[S], (int32_t)L);
     const int32_t o0 = (t >> 6) * (PER * 64) + (t & 63);
@@ -536,13 +556,11 @@ __global__ __launch_bounds__(RF_THREADS) void bn_refresh_lds_kernel(int64_t nnz,
     }
     int32_t pk[PER];
 #pragma unroll
-    for (int u = 0; u < PER; ++u) pk[u] = ev[u] >= 0 ? perm[ev[u]] : 0;
+    for (int u = 0; u < PER; ++u) pk[u] = ev[u] >= 0 ? loff[ev[u]] : 0;
 #pragma unroll
     for (int u = 0; u < PER; ++u) {
         if (ev[u] < 0) continue;
-        int64_t kk = (int64_t)pk[u] - c0;
-        kk = kk < 0 ? 0 : (kk >= nv ? nv - 1 : kk);
-        dst[ev[u]] = v[kk];
+        dst[ev[u]] = v[pk[u] >= nv ? nv - 1 : pk[u]];
     }
 }
 
@@ -558,7 +576,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     // Persistent arrays.
     const size_t sz_v = align_up(sizeof(T) * (size_t)nnz, 256);
     const size_t sz_c = align_up(sizeof(uint16_t) * (size_t)nnz, 256);
-    const size_t sz_p = align_up(sizeof(int32_t) * (size_t)nnz, 256);
+    const size_t sz_lo = align_up(sizeof(uint16_t) * (size_t)nnz, 256);
     const size_t sz_ch = align_up(sizeof(int32_t) * (size_t)(nchunks + 1), 256);
     const size_t sz_pr = align_up(sizeof(int32_t) * (size_t)(R + 1), 256);
     const size_t sz_rw = align_up(sizeof(uint16_t) * (size_t)(nnz + 1), 256);
@@ -570,10 +588,10 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     const size_t sz_rch = align_up(sizeof(int32_t) * (size_t)(2 * nrch_max), 256);
     const size_t sz_bb = align_up(sizeof(int32_t) * (size_t)(L->B + 1), 256);
     const size_t sz_rt = align_up(sizeof(int32_t) * (size_t)((nrch_max + L->B) * L->S), 256);
-    const size_t persistent = sz_v + sz_c + sz_p + 2 * sz_ch + sz_pr + sz_es + sz_rw + sz_pv + sz_rch + 2 * sz_bb +
+    const size_t persistent = sz_v + sz_c + sz_lo + 2 * sz_ch + sz_pr + sz_es + sz_rw + sz_pv + sz_rch + 2 * sz_bb +
                               sz_rt;
     // Temporaries: row counts / rows (nnz + 1), keys, sorted keys, iota,
-    // flags / partial indices (nnz + 1), sort storage.
+    // the sort permutation, flags / partial indices (nnz + 1), sort storage.
     uint32_t *nk = nullptr;
     size_t sort_bytes = 0;
     int bits = 1;
@@ -581,7 +599,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, sort_bytes, nk, nk, (int32_t *)nullptr,
                                             (int32_t *)nullptr, (size_t)nnz, 0, bits, s));
     const size_t sz_i = align_up(sizeof(int32_t) * (size_t)(nnz + 1), 256);
-    const size_t temporary = 5 * sz_i + align_up(sort_bytes, 256);
+    const size_t temporary = 6 * sz_i + align_up(sort_bytes, 256);
     if (max_bytes > 0 && (int64_t)(persistent + temporary) > max_bytes)
         return fail(JLUST_STATUS_OUT_OF_MEMORY,
                     "binned spmv layout: %lld + %lld build bytes above JLUST_HIP_PLAN_MAX_BYTES (%lld)",
@@ -591,7 +609,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     char *p = (char *)L->mem;
     L->sval = p;                 p += sz_v;
     L->scol = (uint16_t *)p;     p += sz_c;
-    L->perm = (int32_t *)p;      p += sz_p;
+    L->loff = (uint16_t *)p;     p += sz_lo;
     L->cst = (int32_t *)p;       p += sz_ch;
     L->cpi = (int32_t *)p;       p += sz_ch;
     L->pr = (int32_t *)p;        p += sz_pr;
@@ -610,6 +628,7 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
     uint32_t *key = (uint32_t *)q;  q += sz_i;
     uint32_t *skey = (uint32_t *)q; q += sz_i;
     int32_t *iota = (int32_t *)q;   q += sz_i;
+    int32_t *perm = (int32_t *)q;   q += sz_i;   // sorted entry e holds CSR entry perm[e]
     int32_t *fpre = (int32_t *)q;   q += sz_i;
     int32_t *est = L->est;
     void *sort_tmp = q;
@@ -631,19 +650,19 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
         st = check_launch("bn_key_kernel");
     }
     if (!st) {
-        e = rocprim::radix_sort_pairs(sort_tmp, sort_bytes, key, skey, iota, L->perm, (size_t)nnz, 0, bits,
+        e = rocprim::radix_sort_pairs(sort_tmp, sort_bytes, key, skey, iota, perm, (size_t)nnz, 0, bits,
                                       s);
         if (e != hipSuccess) st = hip_fail(e, "rocprim::radix_sort_pairs(binned keys)");
     }
     if (!st) {
         hipLaunchKernelGGL((bn_fill_kernel<T>), dim3(blocks256(nnz + 1)), dim3(256), 0, s, nnz, m, origin,
-                           colind, val, erow, L->W, L->B, skey, L->perm, (T *)L->sval, L->scol, fpre);
+                           colind, val, erow, L->W, L->B, skey, perm, (T *)L->sval, L->scol, fpre);
         st = check_launch("bn_fill_kernel");
     }
     if (!st) st = exclusive_scan_i32(fpre, fpre, nnz + 1, (jlust_stream_t)s);
     if (!st) {
         hipLaunchKernelGGL(bn_prow_kernel, dim3(blocks256(nnz)), dim3(256), 0, s, nnz, m, erow, L->H, L->B,
-                           skey, L->perm, L->scol, fpre, L->prow);
+                           skey, perm, L->scol, fpre, L->prow);
         st = check_launch("bn_prow_kernel");
     }
     if (!st) {
@@ -696,8 +715,13 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
         if (e != hipSuccess) st = hip_fail(e, "binned refresh tables (chunks)");
         if (!st) {
             hipLaunchKernelGGL(bn_rtable_kernel, dim3(blocks256(nrows * L->S)), dim3(256), 0, s, nrows, L->S, L->B,
-                               chunk, L->rtb, L->bst, est, L->perm, L->rtab);
+                               chunk, L->rtb, L->bst, est, perm, L->rtab);
             st = check_launch("bn_rtable_kernel");
+        }
+        if (!st) {
+            hipLaunchKernelGGL(bn_loff_kernel, dim3(blocks256(nnz)), dim3(256), 0, s, nnz, L->B, (int32_t)chunk,
+                               skey, L->bst, perm, L->loff);
+            st = check_launch("bn_loff_kernel");
         }
     }
     // cnt is free again: cnt[0] receives the longest run.
@@ -808,13 +832,14 @@ int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64
 int binned_update(BinnedLayout *L, const void *val, hipStream_t s)
 {
     if (L->nrch <= 0) return JLUST_STATUS_SUCCESS;
+    const unsigned grid = (unsigned)((L->nrch + NUM_XCD - 1) / NUM_XCD * NUM_XCD);
     if (L->value_type == 0)
-        hipLaunchKernelGGL((bn_refresh_lds_kernel<double>), dim3((unsigned)L->nrch), dim3(RF_THREADS), 0, s, L->nnz,
-                           L->S, L->B, L->rch, L->bst, L->rtb, L->rtab, L->perm, (const double *)val,
+        hipLaunchKernelGGL((bn_refresh_lds_kernel<double>), dim3(grid), dim3(RF_THREADS), 0, s, L->nnz, L->S, L->B,
+                           L->nrch, L->rch, L->bst, L->rtb, L->rtab, L->loff, (const double *)val,
                            (double *)L->sval);
     else
-        hipLaunchKernelGGL((bn_refresh_lds_kernel<float>), dim3((unsigned)L->nrch), dim3(RF_THREADS), 0, s, L->nnz,
-                           L->S, L->B, L->rch, L->bst, L->rtb, L->rtab, L->perm, (const float *)val,
+        hipLaunchKernelGGL((bn_refresh_lds_kernel<float>), dim3(grid), dim3(RF_THREADS), 0, s, L->nnz, L->S, L->B,
+                           L->nrch, L->rch, L->bst, L->rtb, L->rtab, L->loff, (const float *)val,
                            (float *)L->sval);
     return check_launch("bn_refresh_lds_kernel");
 }

@@ -18,7 +18,8 @@ struct BinnedLayout {
     void *mem = nullptr;     // one allocation holds everything below
     void *sval = nullptr;    // values in slice-major (slice, bin, row, k) order
     uint16_t *scol = nullptr;  // slice-local column | (last entry of a partial) << 15
-    int32_t *perm = nullptr;   // sval[e] = val[perm[e]]
+    uint16_t *loff = nullptr;  // sval[e] = val[bst[b] + k * chunk + loff[e]]: entry e of bin b sits
+                               // at offset loff[e] of the bin's refresh chunk k
     int32_t *cst = nullptr;    // [S*nch + 1] entry start of each chunk
     int32_t *cpi = nullptr;    // [S*nch] index of the chunk's first partial
     int32_t *pr = nullptr;     // [S*B + 1] first partial of run (slice c, bin b) at c*B + b
