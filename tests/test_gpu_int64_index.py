@@ -63,16 +63,15 @@ def test_int64_index_written_in_place_is_narrowed_again(J):
     A64 = J.csr_tensor(_i64(rp), _i64(ci), dev(v), (m, n))
     y = torch.zeros(m, dtype=torch.float64, device="cuda")
     J.execute(J.SpMVOp, A64, x, y)
-    # row 0's first column moved to a column the row does not hold (columns stay sorted)
-    lo, hi = rp[0] - 1, rp[1] - 1
-    assert hi > lo
-    row_cols = set(ci[lo:hi].tolist())
-    new = next(c for c in range(1, int(ci[lo])) if c not in row_cols) if int(ci[lo]) > 1 else None
-    if new is None:
-        pytest.skip("row 0 starts at column 1")
+    # the first entry of the row whose first column is largest moves to
+    # column 1, which that row does not hold (its columns stay sorted)
+    firsts = [(int(ci[rp[r] - 1]), r) for r in range(m) if rp[r + 1] > rp[r]]
+    first_col, r = max(firsts)
+    assert first_col > 1
+    lo = rp[r] - 1
     ci2 = ci.copy()
-    ci2[lo] = new
-    A64.crd_buffers[1][lo] = new
+    ci2[lo] = 1
+    A64.crd_buffers[1][lo] = 1
     y2 = torch.zeros(m, dtype=torch.float64, device="cuda")
     J.execute(J.SpMVOp, A64, x, y2)
     ref = torch.zeros(m, dtype=torch.float64, device="cuda")
