@@ -304,59 +304,33 @@ __global__ void bn_key_kernel(int64_t nnz, int64_t m, int32_t origin, const int3
     iota[k] = (int32_t)k;
 }
 
-// Per sorted entry e: value, local column, and whether it ends its partial
-// (the next entry is in another run or another row).  flag[nnz] = 0.
-template <typename T>
-__global__ void bn_fill_kernel(int64_t nnz, int64_t m, int32_t origin, const int32_t *__restrict__ colind,
-                               const T *__restrict__ val, const int32_t *__restrict__ erow, int32_t W,
-                               int32_t B, const uint32_t *__restrict__ skey,
-                               const int32_t *__restrict__ perm, T *__restrict__ sval,
-                               uint16_t *__restrict__ scol, int32_t *__restrict__ flag)
-{
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e > nnz) return;
-    if (e == nnz) {
-        flag[e] = 0;
-        return;
-    }
-    const int32_t k = perm[e];
-    const uint32_t key = skey[e];
-    bool last = e == nnz - 1;
-    if (!last) last = skey[e + 1] != key || bn_row(erow, perm[e + 1], m) != bn_row(erow, k, m);
-    const int64_t c = key / (uint32_t)B;
-    int64_t lc = (int64_t)colind[k] - origin - c * W;
-    lc = lc < 0 ? 0 : (lc >= W ? W - 1 : lc);
-    scol[e] = (uint16_t)(lc | (last ? BN_END : 0u));
-    sval[e] = val[k];
-    flag[e] = last ? 1 : 0;
-}
-
 // prow[partial] = bin-local row, for the entry that ends each partial.
-__global__ void bn_prow_kernel(int64_t nnz, int64_t m, const int32_t *__restrict__ erow, int32_t H,
-                               int32_t B, const uint32_t *__restrict__ skey,
-                               const int32_t *__restrict__ perm, const uint16_t *__restrict__ scol,
+__global__ void bn_prow_kernel(int64_t nnz, const uint16_t *__restrict__ erl, const uint16_t *__restrict__ scol,
                                const int32_t *__restrict__ fpre, uint16_t *__restrict__ prow)
 {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= nnz || !(scol[e] & BN_END)) return;
-    const int32_t b = (int32_t)(skey[e] % (uint32_t)B);
-    prow[fpre[e]] = (uint16_t)(bn_row(erow, perm[e], m) - b * H);
+    prow[fpre[e]] = erl[e];
 }
 
-// Run bounds from the sorted keys: est[r] = first entry with key >= r and
-// pr[r] = its partial index, for r in [0, R]; every r is written once.
-__global__ void bn_runs_kernel(int64_t nnz, int64_t R, const uint32_t *__restrict__ skey,
-                               const int32_t *__restrict__ fpre, int32_t *__restrict__ est,
-                               int32_t *__restrict__ pr)
+// Run bounds from the sorted keys: est[r] = first entry with key >= r, for
+// r in [0, R]; every r is written once.
+__global__ void bn_est_kernel(int64_t nnz, int64_t R, const uint32_t *__restrict__ skey,
+                              int32_t *__restrict__ est)
 {
     const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e > nnz) return;
     const int64_t prev = e == 0 ? -1 : (int64_t)skey[e - 1];
     const int64_t cur = e == nnz ? R : (int64_t)skey[e];
-    for (int64_t r = prev + 1; r <= cur; ++r) {
-        est[r] = (int32_t)e;
-        pr[r] = fpre[e];
-    }
+    for (int64_t r = prev + 1; r <= cur; ++r) est[r] = (int32_t)e;
+}
+
+// pr[r] = the partial index of run r's first entry, r in [0, R].
+__global__ void bn_pr_kernel(int64_t R, const int32_t *__restrict__ est, const int32_t *__restrict__ fpre,
+                             int32_t *__restrict__ pr)
+{
+    const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (r <= R) pr[r] = fpre[est[r]];
 }
 
 // Longest run, in partials.
@@ -564,7 +538,133 @@ __global__ __launch_bounds__(RF_THREADS) void bn_refresh_lds_kernel(int64_t nnz,
     }
 }
 
+// Layout columns, end bits and rows by the refresh's chunks: workgroup g
+// holds chunk k of bin b -- the columns and bin-local rows of CSR entries
+// [c0, c1) in LDS -- and, for every layout entry e of the chunk's S ranges
+// (entry e of run c at LDS slot loff[e]), writes
+//   scol[e] = slice-local column | BN_END if e ends its partial,
+//   flag[e] = that end bit, erl[e] = its bin-local row.
+// e ends its partial when e + 1 starts another run or holds another row.
+// Within the chunk's range of run c the next entry's row is in LDS; past it,
+// the run's next entry lies in a later chunk and its row is read through
+// perm.  Slots, rows and columns are clamped into range; entries no chunk
+// reaches (a malformed rowptr) keep the zeros the caller cleared.
+template <int L>
+__global__ __launch_bounds__(RF_THREADS) void bn_fill_lds_kernel(
+    int64_t nnz, int64_t m, int32_t origin, int32_t S, int32_t B, int32_t W, int32_t H, int32_t nrch,
+    const int32_t *__restrict__ rch, const int32_t *__restrict__ bst, const int32_t *__restrict__ rtb,
+    const int32_t *__restrict__ rtab, const int32_t *__restrict__ est, const uint16_t *__restrict__ loff,
+    const int32_t *__restrict__ perm, const int32_t *__restrict__ colind, const int32_t *__restrict__ erow,
+    uint16_t *__restrict__ scol, int32_t *__restrict__ flag, uint16_t *__restrict__ erl)
+{
+    constexpr int PER = L / RF_THREADS;   // outputs per thread
+    __shared__ int32_t col[L];
+    __shared__ uint16_t lrow[L];
+    __shared__ int32_t pre[BN_SMAX + 1], beg[BN_SMAX], rend[BN_SMAX], tsum[RF_THREADS];
+    const int t = threadIdx.x;
+    const int per = (nrch + NUM_XCD - 1) / NUM_XCD;
+    const int g = (int)(blockIdx.x % NUM_XCD) * per + (int)(blockIdx.x / NUM_XCD);
+    if (g >= nrch) return;                // whole workgroup
+    const int64_t b = rch[2 * g], k = rch[2 * g + 1];
+    const int64_t lo = bst[b], hi = bst[b + 1];
+    const int64_t c0 = min(lo + k * L, hi), c1 = min(c0 + L, hi);
+    const int nv = (int)(c1 - c0);
+    const int64_t row = (int64_t)rtb[b] + k;
+    const int64_t r0 = b * H;             // the bin's first row
+    int32_t rb0[RF_SPT], rb1[RF_SPT], re[RF_SPT];
+#pragma unroll
+    for (int j = 0; j < RF_SPT; ++j) {
+        const int c = t * RF_SPT + j;
+        rb0[j] = c < S ? rtab[row * S + c] : 0;
+        rb1[j] = c < S ? rtab[(row + 1) * S + c] : 0;
+        re[j] = c < S ? est[(int64_t)c * B + b + 1] : 0;
+    }
+    for (int i = t; i < nv; i += RF_THREADS) {
+        col[i] = colind[c0 + i] - origin;
+        const int64_t lr = (int64_t)bn_row(erow, c0 + i, m) - r0;
+        lrow[i] = (uint16_t)(lr < 0 ? 0 : (lr >= H ? H - 1 : lr));
+    }
+    int32_t lens[RF_SPT], local = 0;
+#pragma unroll
+    for (int j = 0; j < RF_SPT; ++j) {
+        const int c = t * RF_SPT + j;
+        lens[j] = 0;
+        if (c < S) {
+            const int64_t e0 = min(max((int64_t)rb0[j], (int64_t)0), nnz);
+            const int64_t e1 = min(max((int64_t)rb1[j], e0), nnz);
+            beg[c] = (int32_t)e0;
+            rend[c] = min(max(re[j], 0), (int32_t)nnz);
+            lens[j] = (int32_t)(e1 - e0);
+        }
+        local += lens[j];
+    }
+    tsum[t] = local;
+    __syncthreads();
+    for (int off = 1; off < RF_THREADS; off <<= 1) {   // inclusive scan of the per-thread sums
+        const int32_t x = t >= off ? tsum[t - off] : 0;
+        __syncthreads();
+        tsum[t] += x;
+        __syncthreads();
+    }
+    {
+        int32_t run = tsum[t] - local;
+#pragma unroll
+        for (int j = 0; j < RF_SPT; ++j) {
+            const int c = t * RF_SPT + j;
+            if (c < S) pre[c] = run;
+            run += lens[j];
+        }
+        if (t == RF_THREADS - 1) pre[S] = tsum[t];
+    }
+    __syncthreads();
+    // Outputs as in the refresh: wave w owns [w PER 64, (w+1) PER 64), lane l
+    // every 64th of them from l.
+    const int32_t total = min(pre[S], (int32_t)L);
+    const int32_t o0 = (t >> 6) * (PER * 64) + (t & 63);
+    int c = 0;                             // the run with pre[c] <= o < pre[c + 1]
+    {
+        int z = S;
+        while (z - c > 1) {
+            const int mid = (c + z) / 2;
+            if (pre[mid] <= o0) c = mid; else z = mid;
+        }
+    }
+#pragma unroll 4
+    for (int u = 0; u < PER; ++u) {
+        const int32_t o = o0 + u * 64;
+        while (c + 1 < S && pre[c + 1] <= o) ++c;
+        if (o >= total) continue;
+        const int64_t e = (int64_t)beg[c] + (o - pre[c]);
+        const int kk = min((int)loff[e], nv - 1);
+        const int rowe = lrow[kk];
+        bool end;
+        if (e + 1 >= rend[c]) end = true;
+        else if (o + 1 < pre[c + 1]) end = lrow[min((int)loff[e + 1], nv - 1)] != rowe;
+        else end = (int64_t)bn_row(erow, perm[e + 1], m) - r0 != rowe;
+        int64_t lc = (int64_t)col[kk] - (int64_t)c * W;
+        lc = lc < 0 ? 0 : (lc >= W ? W - 1 : lc);
+        scol[e] = (uint16_t)(lc | (end ? BN_END : 0u));
+        flag[e] = end ? 1 : 0;
+        erl[e] = (uint16_t)rowe;
+    }
+}
+
 unsigned blocks256(int64_t n) { return (unsigned)((n + 255) / 256); }
+
+// The value refresh over every chunk: sval from val (CSR order).
+int launch_refresh(const BinnedLayout *L, const void *val, hipStream_t s)
+{
+    const unsigned grid = (unsigned)((L->nrch + NUM_XCD - 1) / NUM_XCD * NUM_XCD);
+    if (L->value_type == 0)
+        hipLaunchKernelGGL((bn_refresh_lds_kernel<double>), dim3(grid), dim3(RF_THREADS), 0, s, L->nnz, L->S, L->B,
+                           L->nrch, L->rch, L->bst, L->rtb, L->rtab, L->loff, (const double *)val,
+                           (double *)L->sval);
+    else
+        hipLaunchKernelGGL((bn_refresh_lds_kernel<float>), dim3(grid), dim3(RF_THREADS), 0, s, L->nnz, L->S, L->B,
+                           L->nrch, L->rch, L->bst, L->rtb, L->rtab, L->loff, (const float *)val,
+                           (float *)L->sval);
+    return check_launch("bn_refresh_lds_kernel");
+}
 
 template <typename T>
 int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t *colind, const T *val,
@@ -654,26 +754,12 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
                                       s);
         if (e != hipSuccess) st = hip_fail(e, "rocprim::radix_sort_pairs(binned keys)");
     }
+    // Run starts; then the refresh tables; then the layout by the refresh's
+    // chunks: the values through the refresh kernel, and the columns, end
+    // bits and rows through bn_fill_lds_kernel.
     if (!st) {
-        hipLaunchKernelGGL((bn_fill_kernel<T>), dim3(blocks256(nnz + 1)), dim3(256), 0, s, nnz, m, origin,
-                           colind, val, erow, L->W, L->B, skey, perm, (T *)L->sval, L->scol, fpre);
-        st = check_launch("bn_fill_kernel");
-    }
-    if (!st) st = exclusive_scan_i32(fpre, fpre, nnz + 1, (jlust_stream_t)s);
-    if (!st) {
-        hipLaunchKernelGGL(bn_prow_kernel, dim3(blocks256(nnz)), dim3(256), 0, s, nnz, m, erow, L->H, L->B,
-                           skey, perm, L->scol, fpre, L->prow);
-        st = check_launch("bn_prow_kernel");
-    }
-    if (!st) {
-        hipLaunchKernelGGL(bn_runs_kernel, dim3(blocks256(nnz + 1)), dim3(256), 0, s, nnz, R, skey, fpre,
-                           est, L->pr);
-        st = check_launch("bn_runs_kernel");
-    }
-    if (!st) {
-        hipLaunchKernelGGL(bn_chunk_kernel, dim3(blocks256(nchunks + 1)), dim3(256), 0, s, nnz, L->S, L->B,
-                           L->nch, est, fpre, L->cst, L->cpi);
-        st = check_launch("bn_chunk_kernel");
+        hipLaunchKernelGGL(bn_est_kernel, dim3(blocks256(nnz + 1)), dim3(256), 0, s, nnz, R, skey, est);
+        st = check_launch("bn_est_kernel");
     }
     // Refresh tables: the bins' first entries, their chunks (host), and the
     // first entry of every run at every chunk boundary of its bin.
@@ -723,6 +809,37 @@ int build(BinnedLayout *L, int32_t origin, const int32_t *rowptr, const int32_t 
                                skey, L->bst, perm, L->loff);
             st = check_launch("bn_loff_kernel");
         }
+        if (!st) st = launch_refresh(L, val, s);
+    }
+    // Every entry's column and end bit start at zero, so that entries no chunk
+    // reaches (a malformed rowptr) still give partial indices in range.
+    if (!st) {
+        e = hipMemsetAsync(L->scol, 0, sizeof(uint16_t) * (size_t)nnz, s);
+        if (e == hipSuccess) e = hipMemsetAsync(fpre, 0, sizeof(int32_t) * (size_t)(nnz + 1), s);
+        if (e != hipSuccess) st = hip_fail(e, "hipMemsetAsync(binned columns and end bits)");
+    }
+    uint16_t *erl = reinterpret_cast<uint16_t *>(key);   // keys are dead after the sort
+    if (!st && L->nrch > 0) {
+        constexpr int CH = RF_LDS / (int)sizeof(T);
+        const unsigned grid = (unsigned)((L->nrch + NUM_XCD - 1) / NUM_XCD * NUM_XCD);
+        hipLaunchKernelGGL((bn_fill_lds_kernel<CH>), dim3(grid), dim3(RF_THREADS), 0, s, nnz, m, origin, L->S, L->B,
+                           L->W, L->H, L->nrch, L->rch, L->bst, L->rtb, L->rtab, est, L->loff, perm, colind, erow,
+                           L->scol, fpre, erl);
+        st = check_launch("bn_fill_lds_kernel");
+    }
+    if (!st) st = exclusive_scan_i32(fpre, fpre, nnz + 1, (jlust_stream_t)s);
+    if (!st) {
+        hipLaunchKernelGGL(bn_prow_kernel, dim3(blocks256(nnz)), dim3(256), 0, s, nnz, erl, L->scol, fpre, L->prow);
+        st = check_launch("bn_prow_kernel");
+    }
+    if (!st) {
+        hipLaunchKernelGGL(bn_pr_kernel, dim3(blocks256(R + 1)), dim3(256), 0, s, R, est, fpre, L->pr);
+        st = check_launch("bn_pr_kernel");
+    }
+    if (!st) {
+        hipLaunchKernelGGL(bn_chunk_kernel, dim3(blocks256(nchunks + 1)), dim3(256), 0, s, nnz, L->S, L->B,
+                           L->nch, est, fpre, L->cst, L->cpi);
+        st = check_launch("bn_chunk_kernel");
     }
     // cnt is free again: cnt[0] receives the longest run.
     if (!st) {
@@ -832,16 +949,7 @@ int binned_build(BinnedLayout **out, int value_type, int64_t m, int64_t n, int64
 int binned_update(BinnedLayout *L, const void *val, hipStream_t s)
 {
     if (L->nrch <= 0) return JLUST_STATUS_SUCCESS;
-    const unsigned grid = (unsigned)((L->nrch + NUM_XCD - 1) / NUM_XCD * NUM_XCD);
-    if (L->value_type == 0)
-        hipLaunchKernelGGL((bn_refresh_lds_kernel<double>), dim3(grid), dim3(RF_THREADS), 0, s, L->nnz, L->S, L->B,
-                           L->nrch, L->rch, L->bst, L->rtb, L->rtab, L->loff, (const double *)val,
-                           (double *)L->sval);
-    else
-        hipLaunchKernelGGL((bn_refresh_lds_kernel<float>), dim3(grid), dim3(RF_THREADS), 0, s, L->nnz, L->S, L->B,
-                           L->nrch, L->rch, L->bst, L->rtb, L->rtab, L->loff, (const float *)val,
-                           (float *)L->sval);
-    return check_launch("bn_refresh_lds_kernel");
+    return launch_refresh(L, val, s);
 }
 
 int binned_execute_f64(const BinnedLayout *L, double alpha, const double *x, double beta, double *y,
