@@ -37,7 +37,12 @@ __global__ void coo_rows_check_kernel(int64_t nnz, const int32_t *__restrict__ r
     int32_t f = 0;
     if (r < 0 || r >= m) f |= 1;
     if (i > 0 && rows[i] < rows[i - 1]) f |= 2;
-    if (f) atomicOr(flags, f);
+    // One atomic per wave, and none once the flags hold the wave's bits: the
+    // rows of a shuffled COO set bit 2 in about half of the entries.
+    const int32_t wf = (__ballot(f & 1) ? 1 : 0) | (__ballot(f & 2) ? 2 : 0);
+    if (wf && __lane_id() == (int)__builtin_ctzll(__ballot(1)) &&
+        (__hip_atomic_load(flags, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & wf) != wf)
+        atomicOr(flags, wf);
     keys[i] = (uint32_t)(r < 0 ? 0 : (r >= m ? m - 1 : r));
     iota[i] = (int32_t)i;
 }

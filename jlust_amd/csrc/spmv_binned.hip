@@ -333,11 +333,14 @@ __global__ void bn_pr_kernel(int64_t R, const int32_t *__restrict__ est, const i
     if (r <= R) pr[r] = fpre[est[r]];
 }
 
-// Longest run, in partials.
+// Longest run, in partials: a wave's maximum, one atomic per wave.
 __global__ void bn_maxrun_kernel(int64_t R, const int32_t *__restrict__ pr, int32_t *__restrict__ out)
 {
     const int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (r < R) atomicMax(out, pr[r + 1] - pr[r]);
+    int32_t v = r < R ? pr[r + 1] - pr[r] : 0;
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+    if (__lane_id() == 0 && v > 0) atomicMax(out, v);
 }
 
 // Chunk q = c*nch + w of slice c starts at the first partial start at or after
