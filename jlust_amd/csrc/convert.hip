@@ -104,11 +104,13 @@ __global__ void seg_mark_kernel(const int32_t *__restrict__ ptr, int64_t nseg, i
     if (b > a && a >= 0 && a < len) mark[a] = (int32_t)s;
 }
 
-// Per stored value p: its (row, col), a keep flag (value != 0) and its key.
+// Per stored value p: its (row, col), a keep flag (value != 0) and its key;
+// *dropped (if given) counts the values not kept, one atomic per wave that
+// drops any.
 template <typename T>
 __global__ void decompose_kernel(jlust_sparse src, const int32_t *__restrict__ seg, KeyLayout L,
                                  uint64_t *__restrict__ keys, int32_t *__restrict__ keep,
-                                 int32_t *__restrict__ bad)
+                                 int32_t *__restrict__ bad, int32_t *__restrict__ dropped)
 {
     const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= src.nnz) return;
@@ -131,8 +133,19 @@ __global__ void decompose_kernel(jlust_sparse src, const int32_t *__restrict__ s
     const bool inb = row >= 0 && row < src.m && col >= 0 && col < src.n;
     if (!inb) bad[0] = 1;
     const T v = static_cast<const T *>(src.val)[p];
-    keep[p] = (inb && v != T(0)) ? 1 : 0;       // -0.0 == 0 is dropped, NaN kept
+    const bool kp = inb && v != T(0);           // -0.0 == 0 is dropped, NaN kept
+    keep[p] = kp ? 1 : 0;
     keys[p] = inb ? make_key(L, row, col) : 0;
+    if (dropped) {
+        const uint64_t d = __ballot(!kp);
+        if (d && __lane_id() == (int)__builtin_ctzll(__ballot(1))) atomicAdd(dropped, (int32_t)__popcll(d));
+    }
+}
+
+__global__ void iota_kernel(int64_t n, int32_t *__restrict__ p)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = (int32_t)i;
 }
 
 // out[idx[i]] = in[i] for flagged i, idx = exclusive scan of the flags.
@@ -185,7 +198,7 @@ __global__ void lower_bound_ptr_kernel(int64_t n, const uint64_t *__restrict__ k
     ptr[r] = (int32_t)(lo + origin);
 }
 
-// Entry arrays of CSR/CSC/COO/DCSR targets.
+// Entry arrays of CSR/CSC/COO/DCSR targets (pos null: entry i is stored value i).
 template <typename T>
 __global__ void fill_entries_kernel(int64_t n, const uint64_t *__restrict__ k,
                                     const int32_t *__restrict__ pos, KeyLayout L, int32_t origin,
@@ -196,7 +209,7 @@ __global__ void fill_entries_kernel(int64_t n, const uint64_t *__restrict__ k,
     if (i >= n) return;
     if (major_out) major_out[i] = (int32_t)(key_major(L, k[i]) + origin);
     minor_out[i] = (int32_t)(key_minor(L, k[i]) + origin);
-    val_out[i] = sval[pos[i]];
+    val_out[i] = sval[pos ? pos[i] : i];
 }
 
 // DCSR: at run heads of the row, crd1[run] = row + origin and pos2[run] = i + origin.
@@ -220,7 +233,7 @@ __global__ void fill_runs_kernel(int64_t n, const uint64_t *__restrict__ k,
 }
 
 // BSR target: block b = run[i] of entry i; at block heads the block column
-// and block row; every entry's value into its block slot.
+// and block row; every entry's value into its block slot (pos as above).
 template <typename T>
 __global__ void fill_bsr_kernel(int64_t n, const uint64_t *__restrict__ k,
                                 const int32_t *__restrict__ pos, const int32_t *__restrict__ head,
@@ -235,7 +248,7 @@ __global__ void fill_bsr_kernel(int64_t n, const uint64_t *__restrict__ k,
         bcol[b] = (int32_t)(key_minor(L, k[i]) + origin);
         brow[b] = (int32_t)key_major(L, k[i]);
     }
-    val_out[b * L.b1 * L.b2 + key_inner(L, k[i])] = sval[pos[i]];
+    val_out[b * L.b1 * L.b2 + key_inner(L, k[i])] = sval[pos ? pos[i] : i];
 }
 
 template <typename T>
@@ -374,9 +387,9 @@ struct jlust_convert {
     int64_t count = 0;          // entries after drop + dedup
     int64_t nruns = 0;          // DCSR rows / BSR blocks
     const void *src_val = nullptr;
-    void *mem = nullptr;        // keys | pos | head | run
+    void *mem = nullptr;        // the analysis workspace: keys, pos, head and run point into it
     uint64_t *keys = nullptr;
-    int32_t *pos = nullptr, *head = nullptr, *run = nullptr;
+    int32_t *pos = nullptr, *head = nullptr, *run = nullptr;   // pos null: the identity
 };
 
 namespace {
@@ -407,13 +420,13 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
     int32_t *flag = (int32_t *)b;     b += 4 * n;
     int32_t *idx = (int32_t *)b;      b += 4 * n;
     int32_t *seg = (int32_t *)b;      b += 4 * nseg_len;
-    int32_t *bad = (int32_t *)b;
-    JLUST_HIP_TRY(hipMemsetAsync(bad, 0, sizeof(int32_t), st));
+    int32_t *bad = (int32_t *)b;      // bad[0]: a coordinate out of range; bad[1]: values dropped
+    JLUST_HIP_TRY(hipMemsetAsync(bad, 0, 2 * sizeof(int32_t), st));
 
     int64_t seglen = 0;
     if (int e = segments(src, seg, seglen, tmpw.p, tmp_bytes, st)) return e;
     hipLaunchKernelGGL((decompose_kernel<T>), dim3(cv_grid(N)), dim3(CV_BLOCK), 0, st, *src, seg, L, k0,
-                       flag, bad);
+                       flag, bad, bad + 1);
     if (int e = check_launch("decompose_kernel")) return e;
 
     auto ensure = [&](size_t need) -> int {
@@ -441,33 +454,45 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
         return JLUST_STATUS_SUCCESS;
     };
 
-    // 1. drop explicit zeros (stable).
-    int64_t K = 0;
-    if (int e = count_flags(N, &K)) return e;
-    int32_t badh = 0;
-    JLUST_HIP_TRY(hipMemcpy(&badh, bad, 4, hipMemcpyDeviceToHost));
-    if (badh)
+    // 1. drop explicit zeros (stable).  With none dropped the keys stay in
+    // place and an entry's position is its index (pc null).
+    int32_t flags_h[2] = {0, 0};
+    JLUST_HIP_TRY(hipMemcpyAsync(flags_h, bad, sizeof(flags_h), hipMemcpyDeviceToHost, st));
+    JLUST_HIP_TRY(hipStreamSynchronize(st));
+    if (flags_h[0])
         return fail(JLUST_STATUS_INVALID_ARGUMENT,
                     "convert: a stored coordinate lies outside the %lld x %lld extents",
                     (long long)src->m, (long long)src->n);
-    hipLaunchKernelGGL(compact_kernel, dim3(cv_grid(N)), dim3(CV_BLOCK), 0, st, N, flag, idx, k0,
-                       (const int32_t *)nullptr, k1, p1);
-    if (int e = check_launch("compact_kernel")) return e;
-    uint64_t *kc = k1;
-    int32_t *pc = p1;
+    uint64_t *kc = k0;
+    int32_t *pc = nullptr;
+    int64_t K = N;
+    if (flags_h[1] > 0) {
+        if (int e = count_flags(N, &K)) return e;
+        hipLaunchKernelGGL(compact_kernel, dim3(cv_grid(N)), dim3(CV_BLOCK), 0, st, N, flag, idx, k0,
+                           (const int32_t *)nullptr, k1, p1);
+        if (int e = check_launch("compact_kernel")) return e;
+        kc = k1;
+        pc = p1;
+    }
     if (K == 0) return JLUST_STATUS_SUCCESS;
 
     // 2. sort by level coordinates unless target and source share the
     // identity ordering (convert.jl:331-349).
     const bool sort = !(dst_identity(h->dst_format) && src_ordered_identity(src->format));
     if (sort) {
+        if (!pc) {                                  // the positions to carry: 0..K-1
+            hipLaunchKernelGGL(iota_kernel, dim3(cv_grid(K)), dim3(CV_BLOCK), 0, st, K, p1);
+            if (int e = check_launch("iota_kernel")) return e;
+            pc = p1;
+        }
+        uint64_t *ko = kc == k0 ? k1 : k0;
         size_t need = 0;
-        JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, need, kc, k0, pc, p0, (size_t)K, 0,
+        JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, need, kc, ko, pc, p0, (size_t)K, 0,
                                                 L.total_bits > 0 ? L.total_bits : 1, st));
         if (int e = ensure(need)) return e;
-        JLUST_HIP_TRY(rocprim::radix_sort_pairs(tmpw.p, need, kc, k0, pc, p0, (size_t)K, 0,
+        JLUST_HIP_TRY(rocprim::radix_sort_pairs(tmpw.p, need, kc, ko, pc, p0, (size_t)K, 0,
                                                 L.total_bits > 0 ? L.total_bits : 1, st));
-        kc = k0;
+        kc = ko;
         pc = p0;
     } else if (h->dst_format == JLUST_FORMAT_CSR) {
         // CSR's Dense row level needs non-decreasing rows; the reference
@@ -475,6 +500,7 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
         JLUST_HIP_TRY(hipMemsetAsync(bad, 0, sizeof(int32_t), st));
         hipLaunchKernelGGL(major_order_kernel, dim3(cv_grid(K)), dim3(CV_BLOCK), 0, st, K, kc, L, bad);
         if (int e = check_launch("major_order_kernel")) return e;
+        int32_t badh = 0;
         JLUST_HIP_TRY(hipMemcpyAsync(&badh, bad, 4, hipMemcpyDeviceToHost, st));
         JLUST_HIP_TRY(hipStreamSynchronize(st));
         if (badh)
@@ -489,7 +515,7 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
         if (int e = check_launch("head_kernel")) return e;
         if (int e = count_flags(K, &C)) return e;
         uint64_t *ko = kc == k1 ? k0 : k1;
-        int32_t *po = pc == p1 ? p0 : p1;
+        int32_t *po = pc == p1 ? p0 : p1;           // pc null: positions are indices
         hipLaunchKernelGGL(compact_kernel, dim3(cv_grid(K)), dim3(CV_BLOCK), 0, st, K, flag, idx, kc, pc,
                            ko, po);
         if (int e = check_launch("compact_kernel")) return e;
@@ -497,15 +523,15 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
         pc = po;
     }
 
-    // 4. keep keys, positions and (DCSR rows / BSR blocks) run ids.
+    // 4. the handle keeps the workspace: keys, positions, and (DCSR rows /
+    // BSR blocks) run heads and ids in the flag and index arrays, free now.
     const size_t c = (size_t)C;
-    JLUST_HIP_TRY(hipMalloc(&h->mem, 8 * c + 4 * c * 3));
-    h->keys = (uint64_t *)h->mem;
-    h->pos = (int32_t *)((char *)h->mem + 8 * c);
-    h->head = h->pos + c;
-    h->run = h->head + c;
-    JLUST_HIP_TRY(hipMemcpyAsync(h->keys, kc, 8 * c, hipMemcpyDeviceToDevice, st));
-    JLUST_HIP_TRY(hipMemcpyAsync(h->pos, pc, 4 * c, hipMemcpyDeviceToDevice, st));
+    h->mem = ws.p;
+    ws.p = nullptr;
+    h->keys = kc;
+    h->pos = pc;
+    h->head = flag;
+    h->run = idx;
     h->count = C;
     if (h->dst_format == JLUST_FORMAT_DCSR || h->dst_format == JLUST_FORMAT_BSR) {
         KeyLayout Lr = L;
@@ -738,10 +764,10 @@ extern "C" int jlust_hip_sparse_to_dense(const jlust_sparse *src, int value_type
     if (int st = segments(src, seg, seglen, tmpw.p, tmp_bytes, s)) return st;
     if (value_type == 0)
         hipLaunchKernelGGL((decompose_kernel<double>), dim3(cv_grid(N)), dim3(CV_BLOCK), 0, s, *src, seg, L, k,
-                           keep, bad);
+                           keep, bad, nullptr);
     else
         hipLaunchKernelGGL((decompose_kernel<float>), dim3(cv_grid(N)), dim3(CV_BLOCK), 0, s, *src, seg, L, k,
-                           keep, bad);
+                           keep, bad, nullptr);
     if (int st = check_launch("decompose_kernel")) return st;
     int32_t badh = 0;
     JLUST_HIP_TRY(hipMemcpyAsync(&badh, bad, 4, hipMemcpyDeviceToHost, s));
