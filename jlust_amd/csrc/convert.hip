@@ -486,12 +486,18 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
             pc = p1;
         }
         uint64_t *ko = kc == k0 ? k1 : k0;
+        // A source whose segments run in the order of the target's minor
+        // coordinate (CSR rows to a CSC target, CSC columns to a row-major
+        // one) holds equal majors in ascending minor order already, so the
+        // stable sort need only order the major bits.
+        const bool major_only = (src->format == JLUST_FORMAT_CSR && h->dst_format == JLUST_FORMAT_CSC) ||
+                                (src->format == JLUST_FORMAT_CSC && dst_identity(h->dst_format));
+        const int end_bit = L.total_bits > 0 ? L.total_bits : 1;
+        const int begin_bit = major_only && L.minor_bits + L.inner_bits < end_bit ? L.minor_bits + L.inner_bits : 0;
         size_t need = 0;
-        JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, need, kc, ko, pc, p0, (size_t)K, 0,
-                                                L.total_bits > 0 ? L.total_bits : 1, st));
+        JLUST_HIP_TRY(rocprim::radix_sort_pairs(nullptr, need, kc, ko, pc, p0, (size_t)K, begin_bit, end_bit, st));
         if (int e = ensure(need)) return e;
-        JLUST_HIP_TRY(rocprim::radix_sort_pairs(tmpw.p, need, kc, ko, pc, p0, (size_t)K, 0,
-                                                L.total_bits > 0 ? L.total_bits : 1, st));
+        JLUST_HIP_TRY(rocprim::radix_sort_pairs(tmpw.p, need, kc, ko, pc, p0, (size_t)K, begin_bit, end_bit, st));
         kc = ko;
         pc = p0;
     } else if (h->dst_format == JLUST_FORMAT_CSR) {
