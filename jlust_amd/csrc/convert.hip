@@ -160,15 +160,20 @@ __global__ void compact_kernel(int64_t n, const int32_t *__restrict__ flag,
     pout[idx[i]] = pin ? pin[i] : (int32_t)i;
 }
 
-// head[i] = 1 where key (or, with block_only, its block) differs from i-1.
+// head[i] = 1 where key (or, with block_only, its block) differs from i-1;
+// *repeats (if given) counts the others, one atomic per wave that has any.
 __global__ void head_kernel(int64_t n, const uint64_t *__restrict__ k, KeyLayout L, int block_only,
-                            int32_t *__restrict__ head)
+                            int32_t *__restrict__ head, int32_t *__restrict__ repeats)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
     bool h = i == 0;
     if (!h) h = block_only ? key_block(L, k[i]) != key_block(L, k[i - 1]) : k[i] != k[i - 1];
     head[i] = h ? 1 : 0;
+    if (repeats) {
+        const uint64_t r = __ballot(!h);
+        if (r && __lane_id() == (int)__builtin_ctzll(__ballot(1))) atomicAdd(repeats, (int32_t)__popcll(r));
+    }
 }
 
 // Sets bad[0] when the major coordinate decreases (an unsorted "ordered" source).
@@ -514,19 +519,26 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
                         "convert: the source's rows are not in non-decreasing order");
     }
 
-    // 3. merge adjacent equal coordinates on unique levels (keep the first).
+    // 3. merge adjacent equal coordinates on unique levels (keep the first);
+    // nothing to do when no key repeats.
     int64_t C = K;
     if (h->dst_format != JLUST_FORMAT_COO) {
-        hipLaunchKernelGGL(head_kernel, dim3(cv_grid(K)), dim3(CV_BLOCK), 0, st, K, kc, L, 0, flag);
+        JLUST_HIP_TRY(hipMemsetAsync(bad + 1, 0, sizeof(int32_t), st));
+        hipLaunchKernelGGL(head_kernel, dim3(cv_grid(K)), dim3(CV_BLOCK), 0, st, K, kc, L, 0, flag, bad + 1);
         if (int e = check_launch("head_kernel")) return e;
-        if (int e = count_flags(K, &C)) return e;
-        uint64_t *ko = kc == k1 ? k0 : k1;
-        int32_t *po = pc == p1 ? p0 : p1;           // pc null: positions are indices
-        hipLaunchKernelGGL(compact_kernel, dim3(cv_grid(K)), dim3(CV_BLOCK), 0, st, K, flag, idx, kc, pc,
-                           ko, po);
-        if (int e = check_launch("compact_kernel")) return e;
-        kc = ko;
-        pc = po;
+        int32_t repeats = 0;
+        JLUST_HIP_TRY(hipMemcpyAsync(&repeats, bad + 1, sizeof(int32_t), hipMemcpyDeviceToHost, st));
+        JLUST_HIP_TRY(hipStreamSynchronize(st));
+        if (repeats > 0) {
+            if (int e = count_flags(K, &C)) return e;
+            uint64_t *ko = kc == k1 ? k0 : k1;
+            int32_t *po = pc == p1 ? p0 : p1;       // pc null: positions are indices
+            hipLaunchKernelGGL(compact_kernel, dim3(cv_grid(K)), dim3(CV_BLOCK), 0, st, K, flag, idx, kc, pc,
+                               ko, po);
+            if (int e = check_launch("compact_kernel")) return e;
+            kc = ko;
+            pc = po;
+        }
     }
 
     // 4. the handle keeps the workspace: keys, positions, and (DCSR rows /
@@ -546,7 +558,7 @@ int analyze(const jlust_sparse *src, jlust_convert *h, hipStream_t st)
             Lr.minor_bits = 0;
         }
         hipLaunchKernelGGL(head_kernel, dim3(cv_grid(C)), dim3(CV_BLOCK), 0, st, C, h->keys, Lr, 1,
-                           h->head);
+                           h->head, nullptr);
         if (int e = check_launch("head_kernel")) return e;
         size_t need = 0;
         JLUST_HIP_TRY(rocprim::inclusive_scan(nullptr, need, h->head, h->run, c, rocprim::plus<int32_t>(), st));
