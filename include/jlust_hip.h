@@ -906,8 +906,9 @@ typedef struct jlust_sparse {
  * coordinates on unique levels keeping the first value (convert.jl:232-250).
  * Reports the target's sizes: *dst_nnz values and *dst_nouter (DCSR stored
  * rows, BSR blocks; 0 otherwise).  Synchronises `stream`.  The handle owns
- * the analysed entries until jlust_hip_convert_destroy; src must stay valid
- * until jlust_hip_convert_fill.  dst_b1/dst_b2/dst_row_major_blocks describe
+ * the analysed entries (its analysis workspace, about 32 bytes of device
+ * memory per stored source value) until jlust_hip_convert_destroy; src must
+ * stay valid until jlust_hip_convert_fill.  dst_b1/dst_b2/dst_row_major_blocks describe
  * a BSR target.  Returns NONCANONICAL_STORAGE where the reference asserts
  * (a CSR target built from rows in decreasing order).
  */
