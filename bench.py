@@ -684,10 +684,11 @@ def bsr_spmv_powerlaw():
     (JLUST_HIP_BSR_SPMV_SEGMENTS=0), and the CSR expansion route (expansion,
     then CSR SpMV on the expanded matrix).  HIP events: the median of 5 runs
     of 20 calls after 3 warm-up calls; bytes = values + block columns +
-    browptr + x + y."""
+    browptr + x + y.  Plain calls are timed both as they run by default (a
+    cached plan from the third call on a matrix) and on the plain kernels."""
     import torch
     import jlust_amd as J
-    from jlust_amd.hip_backend import _bsr_as_csr
+    from jlust_amd.hip_backend import _bsr_as_csr, PLAN_CACHE
     stream = torch.cuda.current_stream()
 
     def ms(fn, reps=20, trials=5):
@@ -719,17 +720,23 @@ def bsr_spmv_powerlaw():
         del val
         x = dev(np.random.default_rng(3).standard_normal(nb * 16).astype(dt))
         y = torch.zeros(mb * 16, dtype=x.dtype, device="cuda")
-        t_seg = ms(lambda: J.execute(J.SpMVOp, A, x, y))
+        # Plain calls switch to a cached plan at the third call on a matrix;
+        # the plain kernels are timed with the cache off.
+        t_cached = ms(lambda: J.execute(J.SpMVOp, A, x, y))
         h = J.prepare(J.HIPBackend(), J.SpMVOp, A)
         t_plan = ms(lambda: J.execute(h, x, y))
         del h
+        PLAN_CACHE.clear()
+        cache_on, PLAN_CACHE.enabled = PLAN_CACHE.enabled, False
         old = os.environ.get("JLUST_HIP_BSR_SPMV_SEGMENTS")
-        os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"] = "0"
         try:
+            t_seg = ms(lambda: J.execute(J.SpMVOp, A, x, y))
+            os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"] = "0"
             t_row = ms(lambda: J.execute(J.SpMVOp, A, x, y), reps=3, trials=1)
         finally:
+            PLAN_CACHE.enabled = cache_on
             if old is None:
-                del os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"]
+                os.environ.pop("JLUST_HIP_BSR_SPMV_SEGMENTS", None)
             else:
                 os.environ["JLUST_HIP_BSR_SPMV_SEGMENTS"] = old
         t_exp = ms(lambda: _bsr_as_csr(A), reps=3, trials=1)
@@ -741,6 +748,7 @@ def bsr_spmv_powerlaw():
         r = {"workload": f"bsr16_spmv_powerlaw_65536_{np.dtype(dt).name}", "nnzb": nnzb,
              "max_blocks_per_row": int(lens.max()), "bytes": nbytes,
              "segments_ms": round(t_seg, 4), "segments_GBps": gbs(t_seg),
+             "plain_cached_ms": round(t_cached, 4), "plain_cached_GBps": gbs(t_cached),
              "plan_ms": round(t_plan, 4), "plan_GBps": gbs(t_plan),
              "row_kernel_ms": round(t_row, 3), "row_kernel_GBps": gbs(t_row),
              "expansion_ms": round(t_exp, 3), "csr_spmv_on_expansion_ms": round(t_csr, 4)}

@@ -299,6 +299,8 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
         # rejected here instead, once per version of the index buffers.
         _check_pos_once(u_A, browptr, mb, bcolind.numel(), dev)
         _check_crd_once(u_A, bcolind, nb, False, dev)
+        if PLAN_CACHE.enabled and PLAN_CACHE.run(u_A, browptr, bcolind, dev, alpha, x, beta, y):
+            return u_y
         with _on(dev):
             st = getattr(L, f"jlust_hip_bsr_spmv_{suf}_i32")(
                 mb, nb, b1, b2, bcolind.numel(), u_A.origin.offset, _ptr(browptr), _ptr(bcolind),
@@ -620,7 +622,7 @@ class _CachedPlan:
     holds weak references to the matrix's buffers only, so the caller's
     tensors are freed as usual; the plan is dropped when any of them is."""
 
-    __slots__ = ("plan", "suf", "copies", "refs", "pat_ver", "val_ver", "bytes", "dev", "kind",
+    __slots__ = ("plan", "suf", "copies", "refs", "pat_ver", "val_ver", "bytes", "dev", "kind", "what",
                  "_exec", "_exec_values", "__weakref__")
 
     def __init__(self, u_A: USTensor, idx1, idx2, dev):
@@ -640,6 +642,7 @@ class _CachedPlan:
         _lib.check(_lib.lib().jlust_hip_csr_spmv_plan_info(self.plan, ctypes.byref(k), ctypes.byref(lpr),
                                                             ctypes.byref(nb)), "csr_spmv_plan_info")
         self.kind = ("merge", "vector", "sliced", "binned")[k.value]
+        self.what = "csr_spmv_plan_execute"
         self.bytes = nb.value
         # Sliced and binned layouts, and COO plans, run on a copy of the values.
         self.copies = coo or self.kind in ("sliced", "binned")
@@ -676,11 +679,55 @@ class _CachedPlan:
                 pass
 
 
+class _CachedBSRPlan:
+    """A BSR SpMV plan (jlust_hip_bsr_spmv_plan_*: the block-rows' segment
+    table, built once) for repeated plain calls on one matrix, with
+    _CachedPlan's interface and weak references only.  The plan reads the
+    values in place at every call."""
+
+    __slots__ = ("plan", "refs", "pat_ver", "bytes", "dev", "kind", "what", "_exec", "__weakref__")
+
+    def __init__(self, u_A: USTensor, idx1, idx2, dev):
+        vals = nonzeros(u_A)
+        b1, b2, row_major, browptr, bcolind, mb, nb = _bsr_parts(u_A)
+        suf = _value_suffix(u_A)
+        self.dev = dev
+        self.plan = ctypes.c_void_p(0)
+        with _on(dev):
+            st = _lib.lib().jlust_hip_bsr_spmv_plan_create(
+                mb, nb, b1, b2, bcolind.numel(), u_A.origin.offset, 0 if suf == "f64" else 1, int(row_major),
+                _ptr(browptr), _ptr(bcolind), _ptr(vals), _stream(dev), ctypes.byref(self.plan))
+        _lib.check(st, "bsr_spmv_plan_create", u_A.format, _BE, vals.dtype)
+        nseg = mb + (bcolind.numel() + 31) // 32         # segments of at most 32 blocks
+        self.bytes = 4 * (mb + 1) + 4 * nseg + nseg * b1 * vals.element_size()
+        self.kind = "bsr_segments"
+        self.what = "bsr_spmv_plan_execute"
+        self.refs = (weakref.ref(idx1), weakref.ref(idx2), weakref.ref(vals))
+        self.pat_ver = (idx1._version, idx2._version)
+        self._exec = getattr(_lib.lib(), f"jlust_hip_bsr_spmv_plan_execute_{suf}")
+
+    def valid(self, idx1, idx2, vals) -> bool:
+        r1, r2, r3 = self.refs
+        return (r1() is idx1 and r2() is idx2 and r3() is vals and
+                (idx1._version, idx2._version) == self.pat_ver)
+
+    def launch(self, alpha, x, beta, y, stream) -> int:
+        return self._exec(self.plan, alpha, x, beta, y, stream)
+
+    def destroy(self):
+        plan, self.plan = self.plan, ctypes.c_void_p(0)
+        if plan.value:
+            try:
+                _lib.lib().jlust_hip_bsr_spmv_plan_destroy(plan)
+            except Exception:
+                pass
+
+
 class PlanCache:
     """Prepared plans for repeated plain SpMV calls, execute(SpMVOp, A, x, y)
-    with a CSR or COO A -- the counterpart of the reference's per-matrix cache
-    of compiled views in its GPU mul! (ext/CUDAExt/ops/block_mul.jl:53,227,
-    327-357).  A matrix is recognised by its index and value tensors (the same
+    with a CSR, COO or BSR A (for BSR, the block-rows' segment table) -- the
+    counterpart of the reference's per-matrix cache of compiled views in its
+    GPU mul! (ext/CUDAExt/ops/block_mul.jl:53,227,327-357).  A matrix is recognised by its index and value tensors (the same
     objects and device addresses, index tensors not written since: torch's
     version counters).  Its first `after` plain calls run the plain kernels;
     the next one builds a plan (the analysis a prepare would do) and every
@@ -708,8 +755,9 @@ class PlanCache:
     def _key(u_A, idx1, idx2, vals, dev, stream):
         # The stream is part of the key: a plan's partial sums are not shared
         # between streams, as the plain call's scratch is not.
+        blocks = _bsr_parts(u_A)[:3] if is_bsr(u_A.format) else None
         return (idx1.data_ptr(), idx2.data_ptr(), vals.data_ptr(), u_A.extents, nnz(u_A),
-                u_A.origin.offset, vals.dtype, dev.index, is_coo_shaped(u_A.format), stream.value)
+                u_A.origin.offset, vals.dtype, dev.index, is_coo_shaped(u_A.format), blocks, stream.value)
 
     def run(self, u_A: USTensor, idx1, idx2, dev, alpha, x, beta, y, fast=None) -> bool:
         """Run the product through a cached plan and return True, or return
@@ -739,7 +787,7 @@ class PlanCache:
                 self._seen[key] = (count, refs, seen[2])
                 return False
             del self._seen[key]
-            ent = _CachedPlan(u_A, idx1, idx2, dev)
+            ent = (_CachedBSRPlan if is_bsr(u_A.format) else _CachedPlan)(u_A, idx1, idx2, dev)
             self._plans[key] = ent
             self._bytes += ent.bytes
             for t in (idx1, idx2, vals):
@@ -752,7 +800,7 @@ class PlanCache:
             fast.key, fast.ent = key, ent
         with _on(dev):
             st = ent.launch(float(alpha), x.data_ptr(), float(beta), y.data_ptr(), stream)
-        _lib.check(st, "csr_spmv_plan_execute", u_A.format, _BE, vals.dtype)
+        _lib.check(st, ent.what, u_A.format, _BE, vals.dtype)
         return True
 
     def _trim_seen(self):

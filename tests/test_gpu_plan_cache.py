@@ -154,3 +154,50 @@ def test_coo_plain_calls_switch_to_a_plan(J, O, cache):
         J.execute(J.SpMVOp, A, dev(x), y)
         assert_within(host(y), ref, absref, np.float64, f"COO call {call}")
     assert len(cache.info()) == 1
+
+
+@pytest.mark.parametrize("b1,b2,dtype", [(4, 3, np.float64), (16, 16, np.float32)])
+def test_bsr_plain_calls_switch_to_a_plan(J, O, cache, b1, b2, dtype):
+    """BSR SpMV plain calls: the third on a matrix builds its segment table
+    once (a BSR SpMV plan, jlust_hip_bsr_spmv_plan_*); every product matches
+    the oracle before and after the switch; values written in place are seen;
+    a block column written in place drops the plan."""
+    import torch
+    mb, nb = 300, 200
+    rng = np.random.default_rng(102 + b1)
+    lens = np.minimum((rng.pareto(1.3, mb) + 1) * 2, nb).astype(np.int64)
+    lens[::7] = 0
+    lens[5] = 120                                        # several segments of 32 blocks
+    bcols = [np.sort(rng.choice(nb, int(n), replace=False)) for n in lens]
+    bp = (np.r_[0, np.cumsum(lens)] + 1).astype(np.int32)
+    bc = (np.concatenate(bcols) + 1).astype(np.int32)
+    flat = rng.standard_normal(bc.size * b1 * b2).astype(dtype)
+    A = J.bsr_tensor(dev(bp), dev(bc), dev(flat), (mb * b1, nb * b2), (b1, b2), True, J.OneBased())
+
+    def check(vals, bcv, what):
+        rp, ci, v = O.bsr_to_csr(bp, bcv, vals, b1, 1, True, b2)
+        x = rng.uniform(-1, 1, nb * b2).astype(dtype)
+        y0 = rng.uniform(-1, 1, mb * b1).astype(dtype)
+        y = dev(y0.copy())
+        J.execute(J.SpMVOp, A, dev(x), y, alpha=1.5, beta=-0.5)
+        ref = O.csr_spmv(rp, ci, v, x, 1.5, -0.5, y0)
+        absref = O.csr_spmv_absref(rp, ci, v, x, 1.5, -0.5, y0)
+        assert_within(host(y), ref, absref, dtype, f"bsr {b1}x{b2} {what}")
+
+    for call in range(4):
+        check(flat, bc, f"call {call}")
+        assert len(cache.info()) == (1 if call >= 2 else 0), (call, cache.info())
+    assert cache.info()[0]["kernel"] == "bsr_segments"
+    A.val.mul_(-2.0)                                     # in place: the plan reads the values at the call
+    check(flat * -2, bc, "values scaled in place")
+    assert len(cache.info()) == 1
+    bc2 = bc.copy()                                      # a block column moved within its row's range
+    r = int(np.flatnonzero(lens > 0)[0])
+    lo, hi = bp[r] - 1, bp[r + 1] - 1
+    free = np.setdiff1d(np.arange(1, nb + 1), bc[lo:hi])
+    bc2[lo] = free[0]
+    bc2[lo:hi] = np.sort(bc2[lo:hi])
+    A.crd_buffers[1].copy_(dev(bc2))
+    check(flat * -2, bc2, "block column written in place")
+    assert cache.info() == []
+    torch.cuda.synchronize()
