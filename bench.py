@@ -91,6 +91,9 @@ def parse():
     p.add_argument("--bsr-spmv", action="store_true",
                    help="16 x 16 BSR SpMV over power-law block-rows: the segmented kernel, the "
                         "one-thread-per-row kernel and the CSR expansion route")
+    p.add_argument("--coo-spmm", action="store_true",
+                   help="plain SpMM calls with a COO (shuffled) or CSC A: with the plan cache, on the "
+                        "plain path (cache off), and a prepared plan")
     p.add_argument("--gather-overlap", action="store_true",
                    help="only time config 3's chunk gathers alone, a 256 MB transpose alone, and the "
                         "two on two streams at once")
@@ -756,6 +759,62 @@ def bsr_spmv_powerlaw():
         out.append(r)
         del A, Acsr, x, y
         torch.cuda.empty_cache()
+    return out
+
+
+def coo_csc_spmm():
+    """Repeated plain SpMM calls execute(SpMMOp, A, B, C) with a COO A whose
+    entries are shuffled, and with the same matrix as CSC: 1M x 1M, 8 random
+    columns a row, f32, k = 32 columns of B.  Timed as they run by default
+    (the plan cache's COO/CSC SpMM plan from the third call on a matrix), on
+    the plain path (the cache off: the entries put in row order at every
+    call), and through a prepared plan.  HIP events over 10 calls after 3
+    warm-up calls."""
+    import torch
+    import jlust_amd as J
+    from jlust_amd.hip_backend import PLAN_CACHE
+    m = n = 1_000_000
+    per, k = 8, 32
+    rng = np.random.default_rng(1)
+    rows = np.repeat(np.arange(1, m + 1, dtype=np.int32), per)
+    cols = rng.integers(1, n + 1, rows.size).astype(np.int32)
+    val = rng.standard_normal(rows.size).astype(np.float32)
+    p = rng.permutation(rows.size)
+    A = J.coo_tensor(dev(rows[p]), dev(cols[p]), dev(val[p]), (m, n))
+    o = np.lexsort((rows, cols))
+    colptr = (np.r_[0, np.cumsum(np.bincount(cols - 1, minlength=n))] + 1).astype(np.int32)
+    Acsc = J.csc_tensor(dev(colptr), dev(rows[o]), dev(val[o]), (m, n))
+    B = torch.randn(k, n, device="cuda").t()
+    C = torch.zeros(k, m, device="cuda").t()
+    stream = torch.cuda.current_stream()
+
+    def ms(fn, reps=10):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(reps):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return round(s.elapsed_time(e) / reps, 4)
+
+    out = []
+    for name, M in (("coo_shuffled", A), ("csc", Acsc)):
+        r = {"matrix": name, "m": m, "n": n, "nnz": int(rows.size), "k": k}
+        r["plain_cached_ms"] = ms(lambda: J.execute(J.SpMMOp, M, B, C))
+        PLAN_CACHE.clear()
+        cache_on, PLAN_CACHE.enabled = PLAN_CACHE.enabled, False
+        try:
+            r["plain_uncached_ms"] = ms(lambda: J.execute(J.SpMMOp, M, B, C))
+        finally:
+            PLAN_CACHE.enabled = cache_on
+        h = J.prepare(J.HIPBackend(), J.SpMMOp, M, n_cols=k)
+        r["plan_ms"] = ms(lambda: J.execute(h, B, C))
+        del h
+        log(f"coo/csc spmm: {r}")
+        out.append(r)
     return out
 
 
@@ -1628,6 +1687,9 @@ def main():
         return
     if args.bsr_spmv:
         print(json.dumps({"bsr_spmv": bsr_spmv_powerlaw()}), flush=True)
+        return
+    if args.coo_spmm:
+        print(json.dumps({"coo_spmm": coo_csc_spmm()}), flush=True)
         return
     if args.bsr_long_rows:
         print(json.dumps({"bsr_long_rows": bsr_long_rows()}), flush=True)

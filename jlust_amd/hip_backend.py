@@ -500,6 +500,8 @@ def _spmm(u_A: USTensor, u_B: USTensor, u_C: USTensor, alpha, beta, skip_empty_r
         coo = is_coo_shaped(u_A.format)
         idx1, idx2 = _coo_parts(u_A) if coo else _csc_parts(u_A)
         dev = _check_same_device(idx1, idx2, nonzeros(u_A), B, C)
+        if PLAN_CACHE.enabled and k > 0 and PLAN_CACHE.run_spmm(u_A, idx1, idx2, dev, alpha, B, beta, C):
+            return u_C
         entry = f"jlust_hip_{'coo' if coo else 'csc'}_spmm_{suf}_i32"
         with _on(dev):
             st = getattr(L, entry)(m, n, k, nnz(u_A), u_A.origin.offset, _ptr(idx1), _ptr(idx2),
@@ -723,11 +725,72 @@ class _CachedBSRPlan:
                 pass
 
 
+class _CachedSpMMPlan:
+    """A COO or CSC SpMM plan (jlust_hip_coo_spmm_plan_create: the entries put
+    in row order once, the column chunking chosen for k) for repeated plain
+    SpMM calls on one matrix and column count, with _CachedPlan's interface
+    and weak references only.  A reordered plan holds the values in its row
+    order and gathers them again when A's value tensor was written since."""
+
+    __slots__ = ("plan", "suf", "refs", "pat_ver", "val_ver", "copies", "bytes", "dev", "kind", "what",
+                 "_exec", "__weakref__")
+
+    def __init__(self, u_A: USTensor, idx1, idx2, dev, k: int):
+        vals = nonzeros(u_A)
+        coo = is_coo_shaped(u_A.format)
+        m, n = u_A.extents
+        self.suf = _value_suffix(u_A)
+        self.dev = dev
+        self.plan = ctypes.c_void_p(0)
+        with _on(dev):
+            st = _lib.lib().jlust_hip_coo_spmm_plan_create(
+                2 if coo else 1, m, n, k, nnz(u_A), u_A.origin.offset, 0 if self.suf == "f64" else 1,
+                _ptr(idx1), _ptr(idx2), _ptr(vals), _stream(dev), ctypes.byref(self.plan))
+        _lib.check(st, "coo_spmm_plan_create", u_A.format, _BE, vals.dtype)
+        a, b, c, r = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int32()
+        _lib.check(_lib.lib().jlust_hip_csr_spmm_plan_info(self.plan, ctypes.byref(a), ctypes.byref(b),
+                                                            ctypes.byref(c), ctypes.byref(r)), "csr_spmm_plan_info")
+        self.copies = bool(r.value)
+        t = vals.element_size()
+        # its device memory, within padding: B's column chunk in row order, the
+        # entries in row order (and their values), the split rows' partial rows
+        self.bytes = n * c.value * t + 4 * (m + 1) + nnz(u_A) * (8 + t) + m + b.value * c.value * t
+        self.kind = "coo_spmm" if coo else "csc_spmm"
+        self.what = "csr_spmm_plan_execute"
+        self.refs = (weakref.ref(idx1), weakref.ref(idx2), weakref.ref(vals))
+        self.pat_ver = (idx1._version, idx2._version)
+        self.val_ver = vals._version
+        self._exec = getattr(_lib.lib(), f"jlust_hip_csr_spmm_plan_execute_{self.suf}")
+
+    def valid(self, idx1, idx2, vals) -> bool:
+        r1, r2, r3 = self.refs
+        return (r1() is idx1 and r2() is idx2 and r3() is vals and
+                (idx1._version, idx2._version) == self.pat_ver)
+
+    def launch(self, alpha, B, ldb, beta, C, ldc, stream) -> int:
+        vals = self.refs[2]()
+        if self.copies and vals._version != self.val_ver:
+            st = _lib.lib().jlust_hip_csr_spmm_plan_update_values(self.plan, vals.data_ptr(), stream)
+            if st:
+                return st
+            self.val_ver = vals._version
+        return self._exec(self.plan, alpha, B, ldb, beta, C, ldc, 0, stream)
+
+    def destroy(self):
+        plan, self.plan = self.plan, ctypes.c_void_p(0)
+        if plan.value:
+            try:
+                _lib.lib().jlust_hip_csr_spmm_plan_destroy(plan)
+            except Exception:
+                pass
+
+
 class PlanCache:
     """Prepared plans for repeated plain SpMV calls, execute(SpMVOp, A, x, y)
-    with a CSR, COO or BSR A (for BSR, the block-rows' segment table) -- the
-    counterpart of the reference's per-matrix cache of compiled views in its
-    GPU mul! (ext/CUDAExt/ops/block_mul.jl:53,227,327-357).  A matrix is recognised by its index and value tensors (the same
+    with a CSR, COO or BSR A (for BSR, the block-rows' segment table), and for
+    repeated plain SpMM calls with a COO or CSC A (one plan per column count)
+    -- the counterpart of the reference's per-matrix cache of compiled views
+    in its GPU mul! (ext/CUDAExt/ops/block_mul.jl:53,227,327-357).  A matrix is recognised by its index and value tensors (the same
     objects and device addresses, index tensors not written since: torch's
     version counters).  Its first `after` plain calls run the plain kernels;
     the next one builds a plan (the analysis a prepare would do) and every
@@ -759,13 +822,14 @@ class PlanCache:
         return (idx1.data_ptr(), idx2.data_ptr(), vals.data_ptr(), u_A.extents, nnz(u_A),
                 u_A.origin.offset, vals.dtype, dev.index, is_coo_shaped(u_A.format), blocks, stream.value)
 
-    def run(self, u_A: USTensor, idx1, idx2, dev, alpha, x, beta, y, fast=None) -> bool:
-        """Run the product through a cached plan and return True, or return
-        False (the caller makes the plain call).  `fast`: the fast path's
-        record of this matrix, which keeps the plan it runs."""
+    def _entry(self, u_A: USTensor, idx1, idx2, dev, extra, make):
+        """(key, the cached plan of this matrix and `extra`), built by `make`
+        at the call after the first `after` plain ones; the plan is None while
+        the caller should make the plain call."""
         vals = nonzeros(u_A)
         stream = _stream(dev)
-        key = self._key(u_A, idx1, idx2, vals, dev, stream)
+        base = self._key(u_A, idx1, idx2, vals, dev, stream)
+        key = base[:-1] + (extra,) + base[-1:]         # the stream stays last (the fast path reads it)
         ent = self._plans.get(key)
         if ent is not None:
             if not ent.valid(idx1, idx2, vals):
@@ -780,14 +844,14 @@ class PlanCache:
                     seen[2] != (idx1._version, idx2._version):
                 self._seen[key] = (1, refs, (idx1._version, idx2._version))
                 self._trim_seen()
-                return False
+                return key, None
             count = seen[0] + 1
             if count <= self.after or torch.cuda.is_current_stream_capturing():
                 # (no plan is built while the stream is captured: a build allocates and synchronises)
                 self._seen[key] = (count, refs, seen[2])
-                return False
+                return key, None
             del self._seen[key]
-            ent = (_CachedBSRPlan if is_bsr(u_A.format) else _CachedPlan)(u_A, idx1, idx2, dev)
+            ent = make()
             self._plans[key] = ent
             self._bytes += ent.bytes
             for t in (idx1, idx2, vals):
@@ -795,12 +859,36 @@ class PlanCache:
                 fin.atexit = False             # nothing to give back at interpreter exit
             self._trim()
             if key not in self._plans:         # larger than the whole budget
-                return False
+                return key, None
+        return key, ent
+
+    def run(self, u_A: USTensor, idx1, idx2, dev, alpha, x, beta, y, fast=None) -> bool:
+        """Run the product through a cached plan and return True, or return
+        False (the caller makes the plain call).  `fast`: the fast path's
+        record of this matrix, which keeps the plan it runs."""
+        kind = _CachedBSRPlan if is_bsr(u_A.format) else _CachedPlan
+        key, ent = self._entry(u_A, idx1, idx2, dev, None, lambda: kind(u_A, idx1, idx2, dev))
+        if ent is None:
+            return False
         if fast is not None:
             fast.key, fast.ent = key, ent
         with _on(dev):
-            st = ent.launch(float(alpha), x.data_ptr(), float(beta), y.data_ptr(), stream)
-        _lib.check(st, ent.what, u_A.format, _BE, vals.dtype)
+            st = ent.launch(float(alpha), x.data_ptr(), float(beta), y.data_ptr(), _stream(dev))
+        _lib.check(st, ent.what, u_A.format, _BE, nonzeros(u_A).dtype)
+        return True
+
+    def run_spmm(self, u_A: USTensor, idx1, idx2, dev, alpha, B, beta, C) -> bool:
+        """The same for a plain COO or CSC SpMM C = alpha A B + beta C, one plan
+        per matrix and column count k."""
+        k = B.shape[1]
+        key, ent = self._entry(u_A, idx1, idx2, dev, ("spmm", k),
+                               lambda: _CachedSpMMPlan(u_A, idx1, idx2, dev, k))
+        if ent is None:
+            return False
+        with _on(dev):
+            st = ent.launch(float(alpha), B.data_ptr(), leading_dim(B), float(beta), C.data_ptr(),
+                            leading_dim(C), _stream(dev))
+        _lib.check(st, ent.what, u_A.format, _BE, nonzeros(u_A).dtype)
         return True
 
     def _trim_seen(self):

@@ -201,3 +201,45 @@ def test_bsr_plain_calls_switch_to_a_plan(J, O, cache, b1, b2, dtype):
     check(flat * -2, bc2, "block column written in place")
     assert cache.info() == []
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("fmt", ["coo", "csc"])
+def test_coo_csc_spmm_plain_calls_switch_to_a_plan(J, O, cache, fmt):
+    """Plain SpMM calls with a COO (entries shuffled) or CSC A: the third on a
+    matrix and column count builds a COO/CSC SpMM plan (the entries put in row
+    order once); every product matches the oracle; values written in place
+    are gathered again; another column count is another plan; an index
+    tensor written in place drops the plan."""
+    m, n, k = 3000, 2500, 24
+    rowptr, colind, val = _powerlaw(m, n, 103)
+    rows = np.repeat(np.arange(1, m + 1, dtype=np.int32), np.diff(rowptr))
+    rng = np.random.default_rng(104)
+    if fmt == "coo":
+        p = rng.permutation(rows.size)
+        A = J.coo_tensor(dev(rows[p]), dev(colind[p]), dev(val[p]), (m, n))
+    else:
+        o = np.lexsort((rows, colind))                   # by column, rows ascending within one
+        colptr = (np.r_[0, np.cumsum(np.bincount(colind - 1, minlength=n))] + 1).astype(np.int32)
+        A = J.csc_tensor(dev(colptr), dev(rows[o]), dev(val[o]), (m, n))
+
+    def check(v, what, kk=k):
+        B = np.asfortranarray(rng.standard_normal((n, kk)))
+        C0 = np.asfortranarray(rng.standard_normal((m, kk)))
+        C = dev(C0)
+        J.execute(J.SpMMOp, A, dev(B), C, alpha=1.25, beta=-0.5)
+        ref, _ = O.csr_spmm(rowptr, colind, v, B, 1.25, -0.5, C0)
+        absref = O.csr_spmm_absref(rowptr, colind, v, B, 1.25, -0.5, C0)
+        assert_within(host(C), ref, absref, np.float64, f"{fmt} SpMM {what}")
+
+    for call in range(4):
+        check(val, f"call {call}")
+        assert len(cache.info()) == (1 if call >= 2 else 0), (call, cache.info())
+    assert cache.info()[0]["kernel"] == f"{fmt}_spmm"
+    J.nonzeros(A).mul_(-2.0)                             # in place: gathered again in row order
+    check(-2.0 * val, "values scaled in place")
+    for call in range(3):
+        check(-2.0 * val, f"k=40 call {call}", kk=40)
+    assert len(cache.info()) == 2                        # one plan per column count
+    A.crd_buffers[1].add_(0)                             # an index tensor written in place
+    check(-2.0 * val, "after an index write")
+    assert len(cache.info()) == 1                        # the k=24 plan is gone
