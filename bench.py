@@ -301,7 +301,8 @@ def coo_bench(steps, warmup, cpu_seconds):
     config 2's matrix: the plain entry point (atomics per row run) and the
     prepared plan (entries row-ordered once, then the CSR plan), with the
     entries in row order and randomly shuffled; DCSR SpMV of the same matrix
-    with every other row emptied.  Bytes: the COO compulsory bytes
+    with every other row emptied; CSC SpMV of it with and without the plan
+    cache.  Bytes: the COO compulsory bytes
     12*nnz + 4*nnz (rows) + 8(n + m).  CPU: the oracle's COO SpMV (C,
     sequential, oracle/jlust_cpu.c) on the box's host."""
     import torch
@@ -349,6 +350,23 @@ def coo_bench(steps, warmup, cpu_seconds):
     dpos = (np.concatenate([[0], np.cumsum(lens[stored])]) + 1).astype(np.int32)
     D = J.dcsr_tensor(dev((stored + 1).astype(np.int32)), dev(dpos), dev(dcols), dev(dval), (m, n))
     run("DCSR (every other row stored), plain call", lambda: J.execute(J.SpMVOp, D, x, y))
+    del D
+    # CSC of the same matrix: plain calls (the plan cache plans it as COO from
+    # the third call), and the plain path with the cache off.
+    from jlust_amd.hip_backend import PLAN_CACHE
+    o = np.lexsort((rows, cols))
+    colptr = (np.r_[0, np.cumsum(np.bincount(cols - 1, minlength=n))] + 1).astype(np.int32)
+    Acsc = J.csc_tensor(dev(colptr), dev(rows[o]), dev(val[o]), (m, n))
+    del o
+    run("CSC, plain call (cached plan)", lambda: J.execute(J.SpMVOp, Acsc, x, y))
+    PLAN_CACHE.clear()
+    cache_on, PLAN_CACHE.enabled = PLAN_CACHE.enabled, False
+    try:
+        run("CSC, plain call (plan cache off)", lambda: J.execute(J.SpMVOp, Acsc, x, y))
+    finally:
+        PLAN_CACHE.enabled = cache_on
+    del Acsc
+    torch.cuda.empty_cache()
     # CPU: the oracle's COO SpMV on a bounded sample (leading entries in row order).
     t0 = time.perf_counter()
     probe = max(1, nz // 50)

@@ -331,6 +331,8 @@ def _spmv(u_A: USTensor, u_x: USTensor, u_y: USTensor, alpha, beta):
         colptr, rowind = _csc_parts(u_A)
         dev = _check_same_device(colptr, rowind, nonzeros(u_A), x, y)
         _check_pos_once(u_A, colptr, n, nnz(u_A), dev)
+        if PLAN_CACHE.enabled and PLAN_CACHE.run(u_A, colptr, rowind, dev, alpha, x, beta, y):
+            return u_y
         with _on(dev):
             st = getattr(L, f"jlust_hip_csc_spmv_{suf}_i32")(
                 m, n, nnz(u_A), u_A.origin.offset, _ptr(colptr), _ptr(rowind), _ptr(nonzeros(u_A)),
@@ -625,19 +627,33 @@ class _CachedPlan:
     tensors are freed as usual; the plan is dropped when any of them is."""
 
     __slots__ = ("plan", "suf", "copies", "refs", "pat_ver", "val_ver", "bytes", "dev", "kind", "what",
-                 "_exec", "_exec_values", "__weakref__")
+                 "keep", "_exec", "_exec_values", "__weakref__")
 
     def __init__(self, u_A: USTensor, idx1, idx2, dev):
         vals = nonzeros(u_A)
-        coo = is_coo_shaped(u_A.format)
+        csc = is_csc_shaped(u_A.format)
+        coo = is_coo_shaped(u_A.format) or csc
         self.suf = _value_suffix(u_A)
         self.dev = dev
         self.plan = ctypes.c_void_p(0)
         m, n = u_A.extents
+        rows, cols = idx1, idx2
+        self.keep = None
+        if csc:
+            # A CSC matrix is planned as COO: its row indices, and each entry's
+            # column expanded from colptr (kept: a plan whose rows need no
+            # reordering reads its columns in place).
+            rows = idx2
+            cols = torch.empty(nnz(u_A), dtype=torch.int32, device=vals.device)
+            with _on(dev):
+                st = _lib.lib().jlust_hip_expand_pos_i32(n, nnz(u_A), u_A.origin.offset, _ptr(idx1), None,
+                                                         _ptr(cols), _stream(dev))
+            _lib.check(st, "expand_pos", u_A.format, _BE, vals.dtype)
+            self.keep = cols
         create = "jlust_hip_coo_spmv_plan_create" if coo else "jlust_hip_csr_spmv_plan_create"
         with _on(dev):
             st = getattr(_lib.lib(), create)(
-                m, n, nnz(u_A), u_A.origin.offset, 0 if self.suf == "f64" else 1, _ptr(idx1), _ptr(idx2),
+                m, n, nnz(u_A), u_A.origin.offset, 0 if self.suf == "f64" else 1, _ptr(rows), _ptr(cols),
                 _ptr(vals), _stream(dev), ctypes.byref(self.plan))
         _lib.check(st, create[10:], u_A.format, _BE, vals.dtype)
         k, lpr, nb = ctypes.c_int32(), ctypes.c_int32(), ctypes.c_int64()
@@ -787,7 +803,8 @@ class _CachedSpMMPlan:
 
 class PlanCache:
     """Prepared plans for repeated plain SpMV calls, execute(SpMVOp, A, x, y)
-    with a CSR, COO or BSR A (for BSR, the block-rows' segment table), and for
+    with a CSR, COO, CSC or BSR A (CSC planned as COO; for BSR, the
+    block-rows' segment table), and for
     repeated plain SpMM calls with a COO or CSC A (one plan per column count)
     -- the counterpart of the reference's per-matrix cache of compiled views
     in its GPU mul! (ext/CUDAExt/ops/block_mul.jl:53,227,327-357).  A matrix is recognised by its index and value tensors (the same
@@ -818,9 +835,13 @@ class PlanCache:
     def _key(u_A, idx1, idx2, vals, dev, stream):
         # The stream is part of the key: a plan's partial sums are not shared
         # between streams, as the plain call's scratch is not.
-        blocks = _bsr_parts(u_A)[:3] if is_bsr(u_A.format) else None
+        # The format: a CSC matrix and a CSR one on the same buffers are each
+        # other's transposes.
+        f = u_A.format
+        kind = ("bsr",) + tuple(_bsr_parts(u_A)[:3]) if is_bsr(f) else \
+            "coo" if is_coo_shaped(f) else "csc" if is_csc_shaped(f) else "csr"
         return (idx1.data_ptr(), idx2.data_ptr(), vals.data_ptr(), u_A.extents, nnz(u_A),
-                u_A.origin.offset, vals.dtype, dev.index, is_coo_shaped(u_A.format), blocks, stream.value)
+                u_A.origin.offset, vals.dtype, dev.index, kind, stream.value)
 
     def _entry(self, u_A: USTensor, idx1, idx2, dev, extra, make):
         """(key, the cached plan of this matrix and `extra`), built by `make`

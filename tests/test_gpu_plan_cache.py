@@ -243,3 +243,42 @@ def test_coo_csc_spmm_plain_calls_switch_to_a_plan(J, O, cache, fmt):
     A.crd_buffers[1].add_(0)                             # an index tensor written in place
     check(-2.0 * val, "after an index write")
     assert len(cache.info()) == 1                        # the k=24 plan is gone
+
+
+def test_csc_spmv_plain_calls_switch_to_a_plan(J, O, cache):
+    """Plain CSC SpMV calls: the third on a matrix builds a plan (CSC planned
+    as COO, each entry's column expanded from colptr); values written in place
+    are gathered again.  A square CSR matrix on the very same three tensors
+    is the CSC one's transpose: the two get plans of their own."""
+    import torch
+    n = 20000
+    rowptr, colind, val = _powerlaw(n, n, 105)
+    p, i, v = dev(rowptr), dev(colind), dev(val)
+    A_csr = J.csr_tensor(p, i, v, (n, n))
+    A_csc = J.csc_tensor(p, i, v, (n, n))               # the transpose of A_csr
+    rows = np.repeat(np.arange(1, n + 1, dtype=np.int32), np.diff(rowptr))
+    # A_csc as CSR: entry (colind, row) of A_csr is (row, col) of A_csc
+    t_order = np.lexsort((rows, colind))
+    t_rowptr = (np.r_[0, np.cumsum(np.bincount(colind - 1, minlength=n))] + 1).astype(np.int32)
+    t_cols, t_val = rows[t_order], val[t_order]
+    x = np.random.default_rng(106).uniform(-1, 1, n)
+    xd = dev(x)
+    y = torch.empty(n, dtype=torch.float64, device="cuda")
+
+    def check(A, scale, what):
+        J.execute(J.SpMVOp, A, xd, y)
+        if A is A_csr:
+            ref = O.csr_spmv(rowptr, colind, scale * val, x)
+            absref = O.csr_spmv_absref(rowptr, colind, scale * val, x)
+        else:
+            ref = O.csr_spmv(t_rowptr, t_cols, scale * t_val, x)
+            absref = O.csr_spmv_absref(t_rowptr, t_cols, scale * t_val, x)
+        assert_within(host(y), ref, absref, np.float64, what)
+
+    for call in range(4):
+        check(A_csc, 1.0, f"CSC call {call}")
+        check(A_csr, 1.0, f"CSR call {call}")
+    assert len(cache.info()) == 2
+    v.mul_(3.0)                                          # in place: both plans see it
+    check(A_csc, 3.0, "CSC values scaled in place")
+    check(A_csr, 3.0, "CSR values scaled in place")
